@@ -1,0 +1,235 @@
+"""Benchmark of the Q4_K_M x Q8 projection path on one MI355X.
+
+Headline (BASELINE.json metric): Q4_K x Q8 decode GEMV GB/s at M=1 on config
+2 (fused gate+up, N=2x17408=34816, K=5120), as a fraction of 8 TB/s HBM; the
+same JSON line carries the MMQ int8-equivalent TOPS at M=512 (config 4,
+Q4_K N=34816) and the other decode M values.
+
+A "step" is one projection launch over one weight copy with the Q8
+activations resident in HBM. Weight copies rotate (>= 1.2 GB in total) so
+MI355X's 256 MB Infinity Cache cannot serve repeats. Weights are seeded fp32
+~N(0, 0.02) quantized ON THE GPU by the library's Q4_K fitter (bit-exact with
+the reference's pinned llama.cpp fitter); activations ~N(0,1) with 1% of the
+channels x20, rounded to BF16 and Q8-packed by the library.
+
+The cpu_baseline leg times the oracle's C restatement of the same contraction
+(test infrastructure, OpenMP) on the host cores for a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA (AMD published)
+FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA (AMD published)
+METRIC = "Q4_K×Q8 GEMV GB/s (% of 8 TB/s) at M=1; MMQ int8 TOPS (% peak) at M=512"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def q4k_bytes(n, k):
+    return n * k // 256 * 144
+
+
+def make_weight(torch, ops, n, k, seed, layout):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn(n, k, generator=g, device="cuda", dtype=torch.float32) * 0.02
+    fail = torch.zeros(1, dtype=torch.int32, device="cuda")
+    blocks = ops.quantize_q4k_blocks(x, n, k, fail)
+    del x
+    w = ops.upload_q4k_blocks(blocks, n, k, layout=layout)
+    torch.cuda.synchronize()
+    assert int(fail.item()) == 0
+    return w, blocks
+
+
+def clone_weight(ops, w):
+    return ops.PrefillWeight(w.codes.clone(), w.scales.clone(), w.layout, w.quantizer, w.n, w.k,
+                             w.padded_n, w.padded_k)
+
+
+def make_q8(torch, ops, m, k, seed, outliers=True):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn(m, k, generator=g, device="cuda", dtype=torch.float32)
+    if outliers:
+        ch = torch.randperm(k, generator=g, device="cuda")[: max(1, round(0.01 * k))]
+        x[:, ch] *= 20.0
+    bf = x.to(torch.bfloat16).view(torch.int16).contiguous()
+    q = ops.Q8Input.empty(m, k)
+    fail = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ops.pack_q8(bf, q, fail)
+    torch.cuda.synchronize()
+    assert int(fail.item()) == 0
+    return q, bf
+
+
+def time_launches(torch, fn, copies, steps, warmup, use_graph=True):
+    """Runs `steps` launches rotating over `copies`; returns (ms_per_step, mode)."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn(i % copies)
+    torch.cuda.synchronize()
+    mode = "eager"
+    graph = None
+    if use_graph:
+        try:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, capture_error_mode="thread_local"):
+                for i in range(copies):
+                    fn(i)
+            graph.replay()
+            torch.cuda.synchronize()
+            mode = "hipgraph"
+        except Exception as e:  # fall back to eager launches
+            log(f"graph capture unavailable ({e}); timing eager launches")
+            graph = None
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    reps = max(1, steps // copies) if graph is not None else steps
+    torch.cuda.synchronize()
+    start.record(stream)
+    if graph is not None:
+        for _ in range(reps):
+            graph.replay()
+        n = reps * copies
+    else:
+        for i in range(steps):
+            fn(i % copies)
+        n = steps
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / n, n, mode
+
+
+def bench_decode(torch, ops, n, k, ms, steps, warmup, layout, seed=11):
+    wbytes = q4k_bytes(n, k)
+    copies = max(2, math.ceil(1.2e9 / wbytes))
+    base, _ = make_weight(torch, ops, n, k, seed, layout)
+    ws = [base] + [clone_weight(ops, base) for _ in range(copies - 1)]
+    res = {}
+    for m in ms:
+        q, _ = make_q8(torch, ops, m, k, seed + 100 + m)
+        outs = [torch.empty(m, n, device="cuda") for _ in range(copies)]
+        ms_step, nsteps, mode = time_launches(
+            torch, lambda i: ops.q4k_q8_project(ws[i], q, outs[i]), copies, steps, warmup)
+        algo = wbytes + m * k * 1.25 + m * n * 4  # weights + Q8 (1.25 B/elem) + fp32 out
+        res[m] = {"ms": ms_step, "gbs": algo / (ms_step * 1e-3) / 1e9, "bytes": algo,
+                  "steps": nsteps, "mode": mode}
+        log(f"decode N={n} K={k} M={m}: {ms_step*1e3:.2f} us/launch, "
+            f"{res[m]['gbs']:.0f} GB/s ({mode})")
+    return res, base
+
+
+def bench_mmq(torch, ops, n, k, m, steps, warmup, layout, seed=21):
+    w, _ = make_weight(torch, ops, n, k, seed, layout)
+    q, _ = make_q8(torch, ops, m, k, seed + 1)
+    out = torch.empty(m, n, device="cuda")
+    ms_step, nsteps, mode = time_launches(
+        torch, lambda i: ops.q4k_q8_project(w, q, out), 1, steps, warmup)
+    ops_count = 2.0 * m * n * k
+    tops = ops_count / (ms_step * 1e-3) / 1e12
+    log(f"mmq N={n} K={k} M={m}: {ms_step*1e3:.1f} us/launch, {tops:.1f} TOPS ({mode})")
+    return {"ms": ms_step, "tops": tops, "frac_int8_peak": tops / INT8_PEAK_TOPS,
+            "frac_fp16_mfma_peak": tops / FP16_PEAK_TFLOPS, "steps": nsteps, "mode": mode,
+            "m": m, "n": n, "k": k}
+
+
+def cpu_baseline(torch, blocks, n, k, m, budget_s):
+    """Oracle (C restatement, OpenMP) on the host cores: same contraction."""
+    import numpy as np
+
+    import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    w = oracle.Q4K.from_ggml(blocks.cpu().numpy(), n, k)
+    rng = np.random.Generator(np.random.PCG64(5))
+    x = oracle.fp32_to_bf16(rng.standard_normal((m, k), dtype=np.float32))
+    q = oracle.pack_q8(x, m, k)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.q4k_q8_contract(w, q, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    per = el / reps
+    algo = q4k_bytes(n, k) + m * k * 1.25 + m * n * 4
+    return {"value": algo / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} full passes of the N={n} K={k} M={m} Q4_K x Q8 contraction "
+                      f"(oracle/oracle.c, exact int32 K32 dots + affine), {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--layout", default="0x0240")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-mmq", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested); see DESIGN.md for how it would shard.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import qw38_amd.ops as ops
+    torch.cuda.set_device(0)
+    layout = int(args.layout, 16)
+    n, k = 34816, 5120
+    dec, base = bench_decode(torch, ops, n, k, [1, 2, 4, 8], args.steps, args.warmup, layout)
+    head = dec[1]
+    mmq = None if args.no_mmq else bench_mmq(torch, ops, n, k, 512, max(20, args.steps // 8),
+                                              max(3, args.warmup // 4), layout)
+    cpu = None
+    if not args.no_cpu:
+        _, blocks = make_weight(torch, ops, n, k, 11, layout)
+        cpu = cpu_baseline(torch, blocks, n, k, 1, args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(head["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded fp32 ~N(0,0.02) weights quantized to Q4_K on the GPU; "
+                "~N(0,1) activations with 1% channels x20 -> BF16 -> Q8)",
+        "config": {"workload": "config 2: fused gate+up Q4_K x Q8 decode GEMV, N=34816, "
+                               "K=5120, M=1", "layout": f"{layout:#06x}",
+                   "weight_copies_rotated": max(2, math.ceil(1.2e9 / q4k_bytes(n, k))),
+                   "timing": head["mode"]},
+        "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+        "decode_m": {str(m): {"gbs": round(v["gbs"], 1), "us": round(v["ms"] * 1e3, 3),
+                              "frac_hbm": round(v["gbs"] / HBM_PEAK_GBS, 4)}
+                     for m, v in dec.items()},
+        "mmq_m512": mmq,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,169 @@
+/*
+ * qw38_hip.h -- C-ABI boundary of the MI355X (gfx950) Q4_K_M x Q8 projection
+ * path. Plain pointers, sizes and a HIP stream handle passed as void*; no C++
+ * or torch types. Every entry point validates all operands before launching
+ * anything and returns a qw38_status; the details of the last failure on the
+ * calling thread are available from qw38_last_error().
+ *
+ * Each declaration names the reference interface it replaces (paths are in the
+ * Enucatl/qw38 tree). The C++ mirror of those interfaces (namespace
+ * qw38::cuda, headers under qw38_amd/cpp/cuda/) is implemented on top of this
+ * ABI.
+ */
+#ifndef QW38_HIP_H
+#define QW38_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: mirror qw38::cuda::ErrorCode (cuda/error.hpp:13-17). */
+enum qw38_status {
+  QW38_OK = 0,
+  QW38_STATUS = 1,           /* HIP runtime failure (hip status in last error) */
+  QW38_INVALID_ARGUMENT = 2, /* contract violation, rejected before launch */
+  QW38_OVERFLOW = 3          /* size/address arithmetic overflow */
+};
+
+/* Layout / quantizer wire IDs. 0x020D/0x0105 are the reference's
+ * (cuda/decode_mmv.hpp:195,205); 0x0240/0x0241/0x0140 are this build's
+ * repacked layouts (lossless byte reorders of GGML super-blocks). */
+#define QW38_LAYOUT_Q4K_CANDIDATE_V2 0x020D /* sequential nibbles, 8-row tiles */
+#define QW38_LAYOUT_Q4K_WAVE64 0x0240       /* 0x020D tiles, wave64 nibble order */
+#define QW38_LAYOUT_Q6K_WAVE64 0x0241       /* Q6_K 8-row tiles */
+#define QW38_QUANTIZER_Q4K 0x0105
+#define QW38_QUANTIZER_Q6K 0x0140
+
+/* Matrix operand: field-for-field cuda::PrefillWeight (cuda/prefill.hpp:33-44). */
+typedef struct qw38_weight {
+  const void* codes;
+  const void* scales;
+  uint16_t layout;
+  uint16_t quantizer;
+  uint32_t n;
+  uint32_t k;
+  uint32_t padded_n;
+  uint32_t padded_k;
+  uint64_t codes_bytes;
+  uint64_t scales_bytes;
+} qw38_weight;
+
+/* Q8 activation pack: cuda::Q8Input (cuda/q4k_q8.hpp:16-21) with each span as
+ * pointer + element count. codes int8 [m][padded_k], scales f32 and sums i32
+ * [m][padded_k/32]. */
+typedef struct qw38_q8_input {
+  int8_t* codes;
+  uint64_t codes_len;
+  float* scales;
+  uint64_t scales_len;
+  int32_t* sums;
+  uint64_t sums_len;
+  uint32_t m;
+  uint32_t k;
+  uint32_t padded_k;
+} qw38_q8_input;
+
+/* Limits (cuda/q4k_q8.hpp:23-25 and the larger shapes this build supports). */
+#define QW38_Q4K_Q8_DOT_BOUND (32 * 15 * 127)
+#define QW38_Q8_SUM_BOUND (32 * 127)
+#define QW38_Q8_MLP_MAX_TOKENS 512u
+#define QW38_PROJECT_MAX_TOKENS 4096u
+#define QW38_PROJECT_MAX_K 65536u
+#define QW38_PROJECT_MAX_N (1u << 20)
+
+/* Last failure on this thread: returns its status; copies the failing
+ * operation name and detail (NUL-terminated, truncated to the capacities). */
+int qw38_last_error(int* hip_status, char* operation, size_t operation_cap,
+                    char* detail, size_t detail_cap);
+
+/* Replaces qw38::cuda::pack_q8 (cuda/q4k_q8.hpp:32-34, cuda/q4k_q8.cu:318-330).
+ * BF16 rows [m][k] -> Q8 pack; *failure is set to 1 on a nonfinite group
+ * (that group's scale becomes NaN and its codes 0). failure_len must be 1. */
+int qw38_pack_q8(const uint16_t* input, uint64_t input_len, const qw38_q8_input* output,
+                 int* failure, uint64_t failure_len, void* stream);
+
+/* Replaces qw38::cuda::q4k_q8_project (cuda/q4k_q8.hpp:35-37,
+ * cuda/q4k_q8.cu:332-345). out [m][n] fp32 = W x^T (+ residual). Accepts
+ * layouts 0x020D and 0x0240 (Q4_K) and 0x0241 (Q6_K). residual may be NULL
+ * with residual_len 0. M <= 8 runs the HBM-streaming GEMV; larger M the MFMA
+ * MMQ kernels. */
+int qw38_q4k_q8_project(const qw38_weight* weight, const qw38_q8_input* input,
+                        float* output, uint64_t output_len, const float* residual,
+                        uint64_t residual_len, void* stream);
+
+/* Replaces cuda::q8_mlp_workspace_bytes (cuda/q4k_q8.hpp:28-30). */
+uint64_t qw38_q8_mlp_workspace_bytes(uint32_t m);
+
+/* Replaces qw38::cuda::q4k_q8_mlp (cuda/q4k_q8.hpp:44-49, cuda/q4k_q8.cu:
+ * 347-398): RMS->Q8, gate, up, SwiGLU->Q8, down + residual. *submitted is 0
+ * on prelaunch rejection and 1 once device work was enqueued. With
+ * pending_failure NULL the call waits and reports a nonfinite producer as
+ * QW38_INVALID_ARGUMENT ("q8.producer"); otherwise it only enqueues and the
+ * caller reads the sticky flag. */
+int qw38_q4k_q8_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
+                    const float* residual, const uint16_t* gamma, float eps, float* output,
+                    uint32_t m, void* workspace, uint64_t workspace_bytes, void* stream,
+                    int* submitted, int* pending_failure);
+
+/* Replaces launch_hidden_rms_q8 (cuda/activation.hpp:11-14,
+ * cuda/activation.cu:536-548): zero-centred RMS over hidden 5120 ->
+ * BF16 -> Q8 pack. codes [m][5120], scales/sums [m][160]. */
+int qw38_hidden_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                       int8_t* codes, float* scales, int32_t* sums, int* failure,
+                       void* stream);
+
+/* The SwiGLU->Q8 producer used inside q4k_q8_mlp (cuda/q4k_q8.cu:52-61),
+ * exposed on its own: BF16(SiLU(gate)*up) -> Q8 over [m][n], n % 256 == 0. */
+int qw38_swiglu_q8(const float* gate, const float* up, uint32_t m, uint32_t n,
+                   int8_t* codes, float* scales, int32_t* sums, int* failure, void* stream);
+
+/* Parity aid with no reference counterpart: the exact per-(token, row, K32
+ * group) int32 dots [m][n][padded_k/32] computed by the same device dot
+ * routines the projection kernels use (for Q6_K: sc0*dot0 + sc1*dot1). */
+int qw38_q8_group_dots(const qw38_weight* weight, const qw38_q8_input* input, int32_t* dots,
+                       uint64_t dots_len, void* stream);
+
+/* Load-time repack replacing the untyped cuda::upload of pre-tiled bytes
+ * (cuda/upload.hpp:16-17, cuda/upload.cpp:6-27) for GGML-order weights:
+ * n*(k/256) super-blocks (144 B Q4_K / 210 B Q6_K, row-major) already in
+ * device memory -> the tiled layout (0x020D or 0x0240 for Q4_K, 0x0241 for
+ * Q6_K). Lossless: only the byte order changes. k % 256 == 0. */
+int qw38_repack_q4k_blocks(const void* blocks, uint64_t blocks_bytes, uint32_t n, uint32_t k,
+                           uint16_t layout, void* codes, uint64_t codes_bytes, void* scales,
+                           uint64_t scales_bytes, void* stream);
+int qw38_repack_q6k_blocks(const void* blocks, uint64_t blocks_bytes, uint32_t n, uint32_t k,
+                           void* codes, uint64_t codes_bytes, void* scales,
+                           uint64_t scales_bytes, void* stream);
+
+/* On-device fitting of FP32 rows [n][k] (k % 256 == 0) into GGML-order
+ * super-blocks, replacing the offline compiler's quantize_bf16 / quantize_q4k_block
+ * (src/compiler/quantization/quantizer.cpp:173-183, q4k.cpp:186-278; Q6_K from
+ * llama.cpp quantize_row_q6_K_ref). Output bytes equal the pinned CPU fitter's.
+ * Q4_K: *failure is set to 1 for nonfinite or unrepresentable blocks (those
+ * blocks are left unwritten). Follow with qw38_repack_*_blocks. */
+int qw38_quantize_q4k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_t k,
+                             void* blocks, uint64_t blocks_bytes, int* failure, void* stream);
+int qw38_quantize_q6k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_t k,
+                             void* blocks, uint64_t blocks_bytes, void* stream);
+
+/* Byte sizes of a tiled weight (cuda/decode_mmv.hpp:330-369 for 0x020D,
+ * extended with this build's layouts). 0 for an unknown layout. */
+uint64_t qw38_code_bytes(uint16_t layout, uint32_t padded_n, uint32_t padded_k);
+uint64_t qw38_scale_bytes(uint16_t layout, uint32_t padded_n, uint32_t padded_k);
+
+/* Device allocation with the reference's instrumentation counters
+ * (cuda/alloc.hpp:9-15, cuda/buffer.hpp:212-215). */
+int qw38_device_malloc(void** pointer, uint64_t bytes);
+int qw38_device_free(void* pointer, uint64_t bytes);
+uint64_t qw38_malloc_count(void);
+uint64_t qw38_free_count(void);
+uint64_t qw38_live_bytes(void);
+uint64_t qw38_peak_live_bytes(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,833 @@
+/*
+ * CPU oracle for the Q4_K / Q6_K x Q8 projection path -- TEST INFRASTRUCTURE.
+ *
+ * Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg, as the checker or as the timed CPU baseline; never by the product.
+ *
+ * Restated reference algorithms and how each is pinned:
+ *   orc_fp16_to_fp32      src/format/floatcvt.hpp:17-41. Pinned: exhaustive
+ *                         65536-pattern equality against the pinned llama.cpp
+ *                         header (oracle/_ref) and fixtures.
+ *   orc_fp32_to_fp16      third_party/llama.cpp-q4k/reference.hpp:58-82 (IEEE
+ *                         round-to-nearest-even). Pinned: random + edge sweep vs
+ *                         oracle/_ref; fixture.
+ *   orc_fp32_to_bf16_rne  src/format/floatcvt.hpp:82-95. Pinned: closed form
+ *                         (ties, NaN quieting) in tests.
+ *   orc_nearest_int       reference.hpp:86-91. Pinned vs oracle/_ref and rint().
+ *   orc_pack_q8           cuda/q8_device.cuh:6-25, cuda/q4k_q8.cu:44-50.
+ *                         Pinned: the reference test's independent equation
+ *                         tests/q4k_q8_test.cpp:83-94 (ties, saturation, zero
+ *                         token, padding, NaN/Inf) as golden vectors.
+ *   orc_rms_q8            cuda/activation.cu:134-190 (block 256, warp-32 tree
+ *                         reductions, FMA contraction where nvcc contracts).
+ *                         Pinned: closed-form RMS in double within 1 bf16 ulp,
+ *                         invariants (scale invariance) -- exact tree order is
+ *                         this restatement's own claim.
+ *   orc_swiglu_q8         cuda/q4k_q8.cu:52-61 with orc_expf (Cody-Waite range
+ *                         reduction + degree-7 Taylor polynomial) in place of
+ *                         CUDA's expf. Pinned: orc_expf within 2 ulp of libm
+ *                         over a sweep; NaN propagation.
+ *   orc_quantize_q4k_*    src/compiler/quantization/q4k.cpp:186-278 and
+ *                         reference.hpp:93-252. Pinned: byte equality with the
+ *                         compiled pinned llama.cpp header (oracle/_ref) on the
+ *                         reference test's blocks (tests/q4k_reference_test.cpp
+ *                         :126-165) and committed fixtures.
+ *   orc_q4k_*ggml*        reference.hpp:244-248, tests/q4k_reference_test.cpp:
+ *                         55-59. Pinned: round trip + _ref dequantize equality.
+ *   orc_pack_q4k_layout   src/format/pack.cpp:216-262 (0x020D). Pinned: golden
+ *                         tile coordinates of tests/pack_layout_test.cpp:197-245
+ *                         and lossless round trip.
+ *   orc_quantize_q6k_*    llama.cpp quantize_row_q6_K_ref / make_qx_quants
+ *                         (ggml-quants.c at e6ab7c1a4, not vendored in the
+ *                         reference). PARITY UNPINNED: no reference code or
+ *                         vectors exist; only invariants are tested.
+ *   orc_q6k_*ggml*        ggml block_q6_K byte order (ggml-common.h). Pinned by
+ *                         round trip only.
+ *   orc_q4k_q8_contract   tests/q4k_q8_test.cpp:121-131 (double closed form),
+ *                         cuda/q4k_q8.cu:97,140 (FP32 K32 order). Pinned: brute
+ *                         force integer dots, closed form on the reference
+ *                         test's hash fixture, linearity.
+ *   orc_q6k_q8_contract   new (no reference code); closed form from the GGML
+ *                         Q6_K dequantization. Pinned: equals a dequantize-then-
+ *                         dot in double on random data.
+ *   orc_q4k_bf16_*        cuda/decode_mmv.cu:121-140 (BF16 operand rebuild).
+ *                         Pinned: one-hot operand fixture of
+ *                         tests/decode_mmv_unit_test.cpp:405-478 restated.
+ *
+ * Build with -ffp-contract=off -fno-fast-math: every FMA here is explicit.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <string.h>
+#include <stdlib.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ---- scalar conversions ------------------------------------------------ */
+float orc_fp16_to_fp32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 31u, mant = h & 1023u;
+  if (e == 0) {
+    if (mant == 0) return u2f(sign);
+    /* subnormal: value = mant * 2^-24 exactly representable in FP32 */
+    float v = (float)mant * 0x1p-24f;
+    return u2f(sign | f2u(v));
+  }
+  if (e == 31) return u2f(sign | 0x7f800000u | (mant << 13));
+  return u2f(sign | ((e + 112u) << 23) | (mant << 13));
+}
+
+uint16_t orc_fp32_to_fp16(float f) {
+  uint32_t u = f2u(f);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  uint32_t au = u & 0x7fffffffu;
+  if (au > 0x7f800000u) return sign | 0x7e00u; /* NaN */
+  if (au >= 0x477ff000u) return sign | 0x7c00u; /* rounds to >= 65520: Inf */
+  if (au < 0x38800000u) {
+    /* result is FP16 subnormal or zero: quantum 2^-24, RNE */
+    float a = u2f(au);
+    double q = (double)a * 16777216.0; /* exact */
+    double r = nearbyint(q);           /* RNE in default mode */
+    return sign | (uint16_t)r;
+  }
+  /* normal: keep 10 mantissa bits, RNE on the dropped 13 */
+  uint32_t exp = (au >> 23) - 112u;
+  uint32_t mant = au & 0x7fffffu;
+  uint32_t h = (exp << 10) | (mant >> 13);
+  uint32_t rem = mant & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;
+  return sign | (uint16_t)h;
+}
+
+float orc_bf16_to_fp32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t orc_fp32_to_bf16_rne(float x) {
+  uint32_t b = f2u(x);
+  if (((b >> 23) & 0xffu) == 0xffu) {
+    uint16_t h = (uint16_t)(b >> 16);
+    if (b & 0x7fffffu) h |= 0x40u;
+    return h;
+  }
+  return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+/* Magic-number rounding: adding 1.5*2^23 leaves the RNE integer in the low
+ * mantissa bits for |x| < 2^22. */
+int orc_nearest_int(float x) {
+  float v = x + 12582912.f;
+  int32_t i;
+  memcpy(&i, &v, 4);
+  return (i & 0x007fffff) - 0x00400000;
+}
+
+/* exp by Cody-Waite reduction x = n*ln2 + r, |r| <= ln2/2, and a degree-7
+ * Taylor polynomial in Horner form with explicit FMAs (Cephes constants for
+ * the two-part ln2). The device SwiGLU producer evaluates the same steps. */
+float orc_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return INFINITY;
+  if (x < -103.972084045410f) return 0.0f;
+  float n = rintf(x * 1.44269502162933349609375f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.98412698412698412698e-4f;        /* 1/5040 */
+  p = fmaf(p, r, 1.38888888888888888889e-3f);  /* 1/720 */
+  p = fmaf(p, r, 8.33333333333333333333e-3f);  /* 1/120 */
+  p = fmaf(p, r, 4.16666666666666666667e-2f);  /* 1/24 */
+  p = fmaf(p, r, 1.66666666666666666667e-1f);  /* 1/6 */
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)n);
+}
+
+/* ---- Q8 activation producers ------------------------------------------- */
+static int pack_group(const float* x /*32*/, int8_t* z, float* a_out, int32_t* s_out) {
+  float peak = 0.f;
+  int finite = 1;
+  for (int t = 0; t < 32; ++t) {
+    if (isfinite(x[t])) { float v = fabsf(x[t]); if (v > peak) peak = v; }
+    else finite = 0;
+  }
+  float a = peak == 0.f ? 1.f : peak / 127.f;
+  int valid = finite && isfinite(a) && a > 0.f;
+  int32_t sum = 0;
+  for (int t = 0; t < 32; ++t) {
+    int code = 0;
+    if (valid) {
+      float q = rintf(x[t] / a);
+      code = q > 127.f ? 127 : q < -127.f ? -127 : (int)q;
+    }
+    z[t] = (int8_t)code;
+    sum += code;
+  }
+  *a_out = valid ? a : u2f(0x7fc00000u);
+  *s_out = sum;
+  return !valid;
+}
+
+int orc_pack_q8_f32(const float* x, uint32_t m, uint32_t k, uint32_t pk,
+                    int8_t* codes, float* scales, int32_t* sums) {
+  int fail = 0;
+  float buf[32];
+  for (uint32_t r = 0; r < m; ++r)
+    for (uint32_t g = 0; g < pk / 32; ++g) {
+      for (int t = 0; t < 32; ++t) {
+        uint32_t c = g * 32 + t;
+        buf[t] = c < k ? x[(size_t)r * k + c] : 0.f;
+      }
+      size_t gi = (size_t)r * (pk / 32) + g;
+      fail |= pack_group(buf, codes + gi * 32, scales + gi, sums + gi);
+    }
+  return fail;
+}
+
+int orc_pack_q8(const uint16_t* bf16, uint32_t m, uint32_t k, uint32_t pk,
+                int8_t* codes, float* scales, int32_t* sums) {
+  int fail = 0;
+  float buf[32];
+  for (uint32_t r = 0; r < m; ++r)
+    for (uint32_t g = 0; g < pk / 32; ++g) {
+      for (int t = 0; t < 32; ++t) {
+        uint32_t c = g * 32 + t;
+        buf[t] = c < k ? orc_bf16_to_fp32(bf16[(size_t)r * k + c]) : 0.f;
+      }
+      size_t gi = (size_t)r * (pk / 32) + g;
+      fail |= pack_group(buf, codes + gi * 32, scales + gi, sums + gi);
+    }
+  return fail;
+}
+
+/* 32-lane shuffle-down tree: lane i adds lane i+off for off = 16..1. */
+static float tree32_sum(float* v) {
+  for (int off = 16; off; off >>= 1)
+    for (int i = 0; i < off; ++i) v[i] = v[i] + v[i + off];
+  return v[0];
+}
+static float tree32_max(float* v) {
+  for (int off = 16; off; off >>= 1)
+    for (int i = 0; i < off; ++i) v[i] = fmaxf(v[i], v[i + off]);
+  return v[0];
+}
+/* 256-thread block reduction: per-warp tree, then warp 0 over 8 partials
+ * padded with zeros to 32 lanes. */
+static float block256(float* per_thread, int is_max) {
+  float part[32];
+  for (int w = 0; w < 8; ++w) {
+    float lane[32];
+    memcpy(lane, per_thread + 32 * w, sizeof lane);
+    part[w] = is_max ? tree32_max(lane) : tree32_sum(lane);
+  }
+  for (int i = 8; i < 32; ++i) part[i] = 0.f;
+  return is_max ? tree32_max(part) : tree32_sum(part);
+}
+
+int orc_rms_q8(const float* residual, const uint16_t* gamma, float eps,
+               uint32_t m, int8_t* codes, float* scales, int32_t* sums,
+               uint16_t* bf16_out) {
+  enum { H = 5120, T = 256 };
+  int fail = 0;
+  float th[T];
+  float y[H];
+  for (uint32_t tok = 0; tok < m; ++tok) {
+    const float* x = residual + (size_t)tok * H;
+    for (int t = 0; t < T; ++t) {
+      float s = 0.f;
+      for (int i = t; i < H; i += T) s = fmaxf(s, fabsf(x[i]));
+      th[t] = s;
+    }
+    float scale = block256(th, 1);
+    float safe = scale == 0.f ? 1.f : scale;
+    for (int t = 0; t < T; ++t) {
+      float s = 0.f;
+      for (int i = t; i < H; i += T) { float q = x[i] / safe; s = fmaf(q, q, s); }
+      th[t] = s;
+    }
+    float sumsq = block256(th, 0);
+    float se = sqrtf(eps) / safe;
+    float inv = 1.0f / sqrtf(fmaf(se, se, sumsq / (float)H));
+    for (int i = 0; i < H; ++i) {
+      float g = orc_bf16_to_fp32(gamma[i]);
+      float v = (1.0f + g) * ((x[i] / safe) * inv);
+      uint16_t b = orc_fp32_to_bf16_rne(v);
+      y[i] = orc_bf16_to_fp32(b);
+      if (bf16_out) bf16_out[(size_t)tok * H + i] = b;
+    }
+    for (int g = 0; g < H / 32; ++g) {
+      size_t gi = (size_t)tok * (H / 32) + g;
+      fail |= pack_group(y + 32 * g, codes + gi * 32, scales + gi, sums + gi);
+    }
+  }
+  return fail;
+}
+
+int orc_swiglu_q8(const float* gate, const float* up, uint32_t m, uint32_t n,
+                  int8_t* codes, float* scales, int32_t* sums, uint16_t* bf16_out) {
+  int fail = 0;
+  float buf[32];
+  for (size_t gi = 0; gi < (size_t)m * n / 32; ++gi) {
+    for (int t = 0; t < 32; ++t) {
+      size_t i = gi * 32 + t;
+      float g = gate[i], u = up[i];
+      float v = (g / (1.f + orc_expf(-g))) * u;
+      if (!isfinite(g) || !isfinite(u)) v = u2f(0x7fc00000u);
+      uint16_t b = orc_fp32_to_bf16_rne(v);
+      if (bf16_out) bf16_out[i] = b;
+      buf[t] = orc_bf16_to_fp32(b);
+    }
+    fail |= pack_group(buf, codes + gi * 32, scales + gi, sums + gi);
+  }
+  return fail;
+}
+
+/* ---- Q4_K quantizer ----------------------------------------------------- */
+/* Weighted min/max affine fit over 32 values with a 21-step scale search
+ * (reference.hpp:93-172). Updates of the running minimum feed later search
+ * steps, exactly as the published routine does. */
+static float fit_qkx2(const float* x, const float* w, uint8_t* L, float* the_min,
+                      uint8_t* Laux) {
+  const int n = 32, nmax = 15, nstep = 20;
+  const float rmin = -1.f, rdelta = 0.1f;
+  float mn = x[0], mx = x[0];
+  float sum_w = w[0];
+  float sum_x = sum_w * x[0];
+  for (int i = 1; i < n; ++i) {
+    if (x[i] < mn) mn = x[i];
+    if (x[i] > mx) mx = x[i];
+    float wi = w[i];
+    sum_w += wi;
+    sum_x += wi * x[i];
+  }
+  if (mn > 0) mn = 0;
+  if (mx == mn) {
+    for (int i = 0; i < n; ++i) L[i] = 0;
+    *the_min = -mn;
+    return 0.f;
+  }
+  float iscale = nmax / (mx - mn);
+  float scale = 1 / iscale;
+  float best = 0;
+  for (int i = 0; i < n; ++i) {
+    int l = orc_nearest_int(iscale * (x[i] - mn));
+    L[i] = (uint8_t)(l < 0 ? 0 : l > nmax ? nmax : l);
+    float diff = scale * L[i] + mn - x[i];
+    diff = diff * diff;
+    best += w[i] * diff;
+  }
+  for (int is = 0; is <= nstep; ++is) {
+    iscale = (rmin + rdelta * is + nmax) / (mx - mn);
+    float sl = 0, sl2 = 0, sxl = 0;
+    for (int i = 0; i < n; ++i) {
+      int l = orc_nearest_int(iscale * (x[i] - mn));
+      l = l < 0 ? 0 : l > nmax ? nmax : l;
+      Laux[i] = (uint8_t)l;
+      float wi = w[i];
+      sl += wi * l;
+      sl2 += wi * l * l;
+      sxl += wi * l * x[i];
+    }
+    float D = sum_w * sl2 - sl * sl;
+    if (D > 0) {
+      float ts = (sum_w * sxl - sum_x * sl) / D;
+      float tm = (sl2 * sum_x - sl * sxl) / D;
+      if (tm > 0) { tm = 0; ts = sxl / sl2; }
+      float cur = 0;
+      for (int i = 0; i < n; ++i) {
+        float diff = ts * Laux[i] + tm - x[i];
+        diff = diff * diff;
+        cur += w[i] * diff;
+      }
+      if (cur < best) {
+        for (int i = 0; i < n; ++i) L[i] = Laux[i];
+        best = cur;
+        scale = ts;
+        mn = tm;
+      }
+    }
+  }
+  *the_min = -mn;
+  return scale;
+}
+
+void orc_q4k_scale_min(const uint8_t* meta, unsigned g, unsigned* s, unsigned* m) {
+  const uint8_t* p = meta + 4;
+  if (g < 4) { *s = p[g] & 63u; *m = p[g + 4] & 63u; }
+  else {
+    *s = (p[g + 4] & 15u) | ((unsigned)(p[g - 4] >> 6) << 4);
+    *m = (unsigned)(p[g + 4] >> 4) | ((unsigned)(p[g] >> 6) << 4);
+  }
+}
+
+int orc_quantize_q4k_block(const float* x, uint8_t* codes, uint8_t* meta) {
+  for (int i = 0; i < 256; ++i) {
+    if (!isfinite(x[i])) return 1;
+    if (fabsf(x[i]) > 1.0e10f) return 2;
+  }
+  uint8_t L[256], aux[32];
+  float w[32], mins[8], scl[8];
+  float max_scale = 0, max_min = 0;
+  for (int j = 0; j < 8; ++j) {
+    const float* xj = x + 32 * j;
+    float lo = 0, hi = xj[0];
+    for (int i = 0; i < 32; ++i) { lo = fminf(lo, xj[i]); hi = fmaxf(hi, xj[i]); }
+    if (hi != lo && !isfinite(16.f / (hi - lo))) return 2;
+    float sx2 = 0;
+    for (int i = 0; i < 32; ++i) sx2 += xj[i] * xj[i];
+    float av = sqrtf(sx2 / 32);
+    for (int i = 0; i < 32; ++i) w[i] = av + fabsf(xj[i]);
+    scl[j] = fit_qkx2(xj, w, L + 32 * j, &mins[j], aux);
+    if (scl[j] > max_scale) max_scale = scl[j];
+    if (mins[j] > max_min) max_min = mins[j];
+  }
+  float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+  float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+  if (!isfinite(inv_scale) || !isfinite(inv_min)) return 2;
+  uint8_t* p = meta + 4;
+  memset(p, 0, 12);
+  for (int j = 0; j < 8; ++j) {
+    uint8_t ls = (uint8_t)orc_nearest_int(inv_scale * scl[j]);
+    uint8_t lm = (uint8_t)orc_nearest_int(inv_min * mins[j]);
+    if (ls > 63) ls = 63;
+    if (lm > 63) lm = 63;
+    if (j < 4) { p[j] = ls; p[j + 4] = lm; }
+    else {
+      p[j + 4] = (uint8_t)((ls & 15) | ((lm & 15) << 4));
+      p[j - 4] |= (uint8_t)((ls >> 4) << 6);
+      p[j] |= (uint8_t)((lm >> 4) << 6);
+    }
+  }
+  uint16_t d = orc_fp32_to_fp16(max_scale / 63.f);
+  uint16_t dmin = orc_fp32_to_fp16(max_min / 63.f);
+  if ((d & 0x7c00u) == 0x7c00u || (dmin & 0x7c00u) == 0x7c00u) return 2;
+  meta[0] = d & 255; meta[1] = d >> 8; meta[2] = dmin & 255; meta[3] = dmin >> 8;
+  for (int j = 0; j < 8; ++j) {
+    unsigned sc, mm;
+    orc_q4k_scale_min(meta, j, &sc, &mm);
+    float step = orc_fp16_to_fp32(d) * sc;
+    if (!step) continue;
+    float off = orc_fp16_to_fp32(dmin) * mm;
+    for (int i = 0; i < 32; ++i) {
+      int l = orc_nearest_int((x[32 * j + i] + off) / step);
+      L[32 * j + i] = (uint8_t)(l < 0 ? 0 : l > 15 ? 15 : l);
+    }
+  }
+  memcpy(codes, L, 256);
+  return 0;
+}
+
+int orc_quantize_q4k_rows(const float* x, uint64_t n, uint64_t k, uint8_t* codes,
+                          uint8_t* meta, int threads) {
+  if (k % 256) return 3;
+  int64_t blocks = (int64_t)(n * (k / 256));
+  int err = 0;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static) reduction(| : err)
+#endif
+  for (int64_t b = 0; b < blocks; ++b)
+    err |= orc_quantize_q4k_block(x + b * 256, codes + b * 256, meta + b * 16);
+  (void)threads;
+  return err;
+}
+
+void orc_q4k_logical_to_ggml(const uint8_t* codes, const uint8_t* meta,
+                             uint64_t blocks, uint8_t* ggml) {
+  for (uint64_t b = 0; b < blocks; ++b) {
+    uint8_t* y = ggml + b * 144;
+    memcpy(y, meta + b * 16, 16);
+    const uint8_t* c = codes + b * 256;
+    for (int j = 0; j < 4; ++j)
+      for (int l = 0; l < 32; ++l)
+        y[16 + 32 * j + l] = (uint8_t)(c[64 * j + l] | (c[64 * j + 32 + l] << 4));
+  }
+}
+
+void orc_q4k_ggml_to_logical(const uint8_t* ggml, uint64_t blocks, uint8_t* codes,
+                             uint8_t* meta) {
+  for (uint64_t b = 0; b < blocks; ++b) {
+    const uint8_t* y = ggml + b * 144;
+    memcpy(meta + b * 16, y, 16);
+    uint8_t* c = codes + b * 256;
+    for (int j = 0; j < 4; ++j)
+      for (int l = 0; l < 32; ++l) {
+        c[64 * j + l] = y[16 + 32 * j + l] & 15;
+        c[64 * j + 32 + l] = y[16 + 32 * j + l] >> 4;
+      }
+  }
+}
+
+/* ---- layouts ------------------------------------------------------------ */
+static inline uint64_t tile_row(uint32_t row, uint32_t kb, uint32_t kbs) {
+  return ((uint64_t)(row / 8) * kbs + kb) * 8 + row % 8;
+}
+static inline uint32_t pad8(uint32_t n) { return (n + 7u) & ~7u; }
+
+/* Byte j (0..15) of K32 group chunk -> the two logical code offsets it holds.
+ * 0x020D: sequential pairs. 0x0240: word t holds codes 8t..8t+3 in its low
+ * nibbles and 8t+4..8t+7 in its high nibbles. */
+static inline void nib_map(uint16_t layout, int j, int* lo, int* hi) {
+  if (layout == 0x020D) { *lo = 2 * j; *hi = 2 * j + 1; }
+  else { int t = j / 4, i = j % 4; *lo = 8 * t + i; *hi = 8 * t + 4 + i; }
+}
+
+int orc_pack_q4k_layout(uint16_t layout, const uint8_t* codes, const uint8_t* meta,
+                        uint32_t n, uint32_t pk, uint8_t* co, uint8_t* mo) {
+  if ((layout != 0x020D && layout != 0x0240) || pk % 256) return 1;
+  uint32_t kbs = pk / 256, pn = pad8(n);
+  memset(co, 0, (size_t)pn * pk / 2);
+  memset(mo, 0, (size_t)pn * kbs * 16);
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint32_t kb = 0; kb < kbs; ++kb) {
+      uint64_t tr = tile_row(r, kb, kbs);
+      memcpy(mo + tr * 16, meta + ((size_t)r * kbs + kb) * 16, 16);
+      const uint8_t* c = codes + (size_t)r * pk + kb * 256;
+      for (int g = 0; g < 8; ++g)
+        for (int j = 0; j < 16; ++j) {
+          int lo, hi;
+          nib_map(layout, j, &lo, &hi);
+          co[tr * 128 + g * 16 + j] = (uint8_t)(c[32 * g + lo] | (c[32 * g + hi] << 4));
+        }
+    }
+  return 0;
+}
+
+int orc_unpack_q4k_layout(uint16_t layout, const uint8_t* ci, const uint8_t* mi,
+                          uint32_t n, uint32_t pk, uint8_t* codes, uint8_t* meta) {
+  if ((layout != 0x020D && layout != 0x0240) || pk % 256) return 1;
+  uint32_t kbs = pk / 256;
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint32_t kb = 0; kb < kbs; ++kb) {
+      uint64_t tr = tile_row(r, kb, kbs);
+      memcpy(meta + ((size_t)r * kbs + kb) * 16, mi + tr * 16, 16);
+      uint8_t* c = codes + (size_t)r * pk + kb * 256;
+      for (int g = 0; g < 8; ++g)
+        for (int j = 0; j < 16; ++j) {
+          int lo, hi;
+          nib_map(layout, j, &lo, &hi);
+          uint8_t b = ci[tr * 128 + g * 16 + j];
+          c[32 * g + lo] = b & 15;
+          c[32 * g + hi] = b >> 4;
+        }
+    }
+  return 0;
+}
+
+/* ---- Q6_K quantizer (GGML published algorithm; parity unpinned) --------- */
+#define Q6_GROUP_MAX_EPS 1e-15f
+static float fit_qx(int n, int nmax, const float* x, uint8_t* L) {
+  float max = 0, amax = 0;
+  for (int i = 0; i < n; ++i) {
+    float ax = fabsf(x[i]);
+    if (ax > amax) { amax = ax; max = x[i]; }
+  }
+  if (amax < Q6_GROUP_MAX_EPS) {
+    for (int i = 0; i < n; ++i) L[i] = 0;
+    return 0.f;
+  }
+  float iscale = -nmax / max;
+  float sumlx = 0, suml2 = 0;
+  for (int i = 0; i < n; ++i) {
+    int l = orc_nearest_int(iscale * x[i]);
+    l = l < -nmax ? -nmax : l > nmax - 1 ? nmax - 1 : l;
+    L[i] = (uint8_t)(l + nmax);
+    float w = x[i] * x[i];
+    sumlx += w * x[i] * l;
+    suml2 += w * l * l;
+  }
+  float scale = suml2 ? sumlx / suml2 : 0.0f;
+  float best = scale * sumlx;
+  for (int is = -9; is <= 9; ++is) {
+    if (is == 0) continue;
+    iscale = -(nmax + 0.1f * is) / max;
+    sumlx = suml2 = 0;
+    for (int i = 0; i < n; ++i) {
+      int l = orc_nearest_int(iscale * x[i]);
+      l = l < -nmax ? -nmax : l > nmax - 1 ? nmax - 1 : l;
+      float w = x[i] * x[i];
+      sumlx += w * x[i] * l;
+      suml2 += w * l * l;
+    }
+    if (suml2 > 0 && sumlx * sumlx > best * suml2) {
+      for (int i = 0; i < n; ++i) {
+        int l = orc_nearest_int(iscale * x[i]);
+        l = l < -nmax ? -nmax : l > nmax - 1 ? nmax - 1 : l;
+        L[i] = (uint8_t)(nmax + l);
+      }
+      scale = sumlx / suml2;
+      best = scale * sumlx;
+    }
+  }
+  return scale;
+}
+
+void orc_quantize_q6k_block(const float* x, uint8_t* q, int8_t* sc, uint16_t* d) {
+  uint8_t L[256];
+  float scales[16];
+  float max_scale = 0, max_abs = 0;
+  for (int ib = 0; ib < 16; ++ib) {
+    float s = fit_qx(16, 32, x + 16 * ib, L + 16 * ib);
+    scales[ib] = s;
+    float as = fabsf(s);
+    if (as > max_abs) { max_abs = as; max_scale = s; }
+  }
+  if (max_abs < Q6_GROUP_MAX_EPS) {
+    memset(q, 0, 256);
+    memset(sc, 0, 16);
+    *d = 0;
+    return;
+  }
+  float iscale = -128.f / max_scale;
+  *d = orc_fp32_to_fp16(1 / iscale);
+  for (int ib = 0; ib < 16; ++ib) {
+    int l = orc_nearest_int(iscale * scales[ib]);
+    sc[ib] = (int8_t)(l < 127 ? l : 127);
+  }
+  for (int j = 0; j < 16; ++j) {
+    float dd = orc_fp16_to_fp32(*d) * sc[j];
+    if (!dd) continue;
+    for (int i = 0; i < 16; ++i) {
+      int l = orc_nearest_int(x[16 * j + i] / dd);
+      l = l < -32 ? -32 : l > 31 ? 31 : l;
+      L[16 * j + i] = (uint8_t)(l + 32);
+    }
+  }
+  memcpy(q, L, 256);
+}
+
+int orc_quantize_q6k_rows(const float* x, uint64_t n, uint64_t k, uint8_t* q,
+                          int8_t* sc, uint16_t* d, int threads) {
+  if (k % 256) return 3;
+  int64_t blocks = (int64_t)(n * (k / 256));
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+#endif
+  for (int64_t b = 0; b < blocks; ++b)
+    orc_quantize_q6k_block(x + b * 256, q + b * 256, sc + b * 16, d + b);
+  (void)threads;
+  return 0;
+}
+
+void orc_q6k_logical_to_ggml(const uint8_t* q, const int8_t* sc, const uint16_t* d,
+                             uint64_t blocks, uint8_t* ggml) {
+  for (uint64_t b = 0; b < blocks; ++b) {
+    uint8_t* y = ggml + b * 210;
+    const uint8_t* L = q + b * 256;
+    uint8_t* ql = y;
+    uint8_t* qh = y + 128;
+    for (int half = 0; half < 2; ++half) {
+      const uint8_t* Lh = L + 128 * half;
+      uint8_t* qlh = ql + 64 * half;
+      uint8_t* qhh = qh + 32 * half;
+      for (int l = 0; l < 32; ++l) {
+        qlh[l] = (uint8_t)((Lh[l] & 15) | ((Lh[l + 64] & 15) << 4));
+        qlh[l + 32] = (uint8_t)((Lh[l + 32] & 15) | ((Lh[l + 96] & 15) << 4));
+        qhh[l] = (uint8_t)((Lh[l] >> 4) | ((Lh[l + 32] >> 4) << 2) |
+                           ((Lh[l + 64] >> 4) << 4) | ((Lh[l + 96] >> 4) << 6));
+      }
+    }
+    memcpy(y + 192, sc + b * 16, 16);
+    y[208] = d[b] & 255;
+    y[209] = d[b] >> 8;
+  }
+}
+
+void orc_q6k_ggml_to_logical(const uint8_t* ggml, uint64_t blocks, uint8_t* q,
+                             int8_t* sc, uint16_t* d) {
+  for (uint64_t b = 0; b < blocks; ++b) {
+    const uint8_t* y = ggml + b * 210;
+    uint8_t* L = q + b * 256;
+    for (int half = 0; half < 2; ++half) {
+      const uint8_t* qlh = y + 64 * half;
+      const uint8_t* qhh = y + 128 + 32 * half;
+      uint8_t* Lh = L + 128 * half;
+      for (int l = 0; l < 32; ++l) {
+        Lh[l] = (uint8_t)((qlh[l] & 15) | (((qhh[l] >> 0) & 3) << 4));
+        Lh[l + 32] = (uint8_t)((qlh[l + 32] & 15) | (((qhh[l] >> 2) & 3) << 4));
+        Lh[l + 64] = (uint8_t)((qlh[l] >> 4) | (((qhh[l] >> 4) & 3) << 4));
+        Lh[l + 96] = (uint8_t)((qlh[l + 32] >> 4) | (((qhh[l] >> 6) & 3) << 4));
+      }
+    }
+    memcpy(sc + b * 16, y + 192, 16);
+    d[b] = (uint16_t)(y[208] | (y[209] << 8));
+  }
+}
+
+/* Q6_K wave64 layout 0x0241. Per tile row (row, kb): 128 B of low nibbles
+ * (per K32 group 16 B, nibble order as 0x0240) then 64 B of high bit pairs
+ * (per group 8 B: word u, byte i, bits 2s..2s+1 hold code 16u+4s+i).
+ * Metadata: 16 int8 scales at tile_row*16, then the fp16 d array at
+ * padded_n*kbs*16 + tile_row*2. */
+int orc_pack_q6k_layout(const uint8_t* q, const int8_t* sc, const uint16_t* d,
+                        uint32_t n, uint32_t pk, uint8_t* co, uint8_t* mo) {
+  if (pk % 256) return 1;
+  uint32_t kbs = pk / 256, pn = pad8(n);
+  uint64_t rows = (uint64_t)pn * kbs;
+  memset(co, 0, rows * 192);
+  memset(mo, 0, rows * 18);
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint32_t kb = 0; kb < kbs; ++kb) {
+      uint64_t tr = tile_row(r, kb, kbs);
+      size_t blk = (size_t)r * kbs + kb;
+      memcpy(mo + tr * 16, sc + blk * 16, 16);
+      mo[rows * 16 + tr * 2] = d[blk] & 255;
+      mo[rows * 16 + tr * 2 + 1] = d[blk] >> 8;
+      const uint8_t* c = q + (size_t)r * pk + kb * 256;
+      uint8_t* lo = co + tr * 192;
+      uint8_t* hi = lo + 128;
+      for (int g = 0; g < 8; ++g) {
+        const uint8_t* cg = c + 32 * g;
+        for (int j = 0; j < 16; ++j) {
+          int t = j / 4, i = j % 4;
+          lo[16 * g + j] = (uint8_t)((cg[8 * t + i] & 15) | ((cg[8 * t + 4 + i] & 15) << 4));
+        }
+        for (int u = 0; u < 2; ++u)
+          for (int i = 0; i < 4; ++i) {
+            uint8_t b = 0;
+            for (int s = 0; s < 4; ++s) b |= (uint8_t)(((cg[16 * u + 4 * s + i] >> 4) & 3) << (2 * s));
+            hi[8 * g + 4 * u + i] = b;
+          }
+      }
+    }
+  return 0;
+}
+
+int orc_unpack_q6k_layout(const uint8_t* ci, const uint8_t* mi, uint32_t n, uint32_t pk,
+                          uint8_t* q, int8_t* sc, uint16_t* d) {
+  if (pk % 256) return 1;
+  uint32_t kbs = pk / 256, pn = pad8(n);
+  uint64_t rows = (uint64_t)pn * kbs;
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint32_t kb = 0; kb < kbs; ++kb) {
+      uint64_t tr = tile_row(r, kb, kbs);
+      size_t blk = (size_t)r * kbs + kb;
+      memcpy(sc + blk * 16, mi + tr * 16, 16);
+      d[blk] = (uint16_t)(mi[rows * 16 + tr * 2] | (mi[rows * 16 + tr * 2 + 1] << 8));
+      uint8_t* c = q + (size_t)r * pk + kb * 256;
+      const uint8_t* lo = ci + tr * 192;
+      const uint8_t* hi = lo + 128;
+      for (int g = 0; g < 8; ++g) {
+        uint8_t* cg = c + 32 * g;
+        for (int j = 0; j < 16; ++j) {
+          int t = j / 4, i = j % 4;
+          cg[8 * t + i] = lo[16 * g + j] & 15;
+          cg[8 * t + 4 + i] = lo[16 * g + j] >> 4;
+        }
+        for (int u = 0; u < 2; ++u)
+          for (int i = 0; i < 4; ++i)
+            for (int s = 0; s < 4; ++s)
+              cg[16 * u + 4 * s + i] |= (uint8_t)(((hi[8 * g + 4 * u + i] >> (2 * s)) & 3) << 4);
+      }
+    }
+  return 0;
+}
+
+/* ---- contractions ------------------------------------------------------- */
+void orc_q4k_q8_contract(const uint8_t* codes, const uint8_t* meta, uint32_t n,
+                         uint32_t pk, const int8_t* z, const float* a,
+                         const int32_t* sums, uint32_t m, double* out64,
+                         float* out32, int32_t* dots, int threads) {
+  uint32_t groups = pk / 32, kbs = pk / 256;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 16)
+#endif
+  for (int64_t r = 0; r < (int64_t)n; ++r) {
+    for (uint32_t t = 0; t < m; ++t) {
+      double acc64 = 0;
+      float acc32 = 0;
+      for (uint32_t g = 0; g < groups; ++g) {
+        const uint8_t* mb = meta + ((size_t)r * kbs + g / 8) * 16;
+        unsigned s, mm;
+        orc_q4k_scale_min(mb, g % 8, &s, &mm);
+        float d = orc_fp16_to_fp32((uint16_t)(mb[0] | (mb[1] << 8)));
+        float dmin = orc_fp16_to_fp32((uint16_t)(mb[2] | (mb[3] << 8)));
+        const uint8_t* c = codes + (size_t)r * pk + g * 32;
+        const int8_t* zz = z + (size_t)t * pk + g * 32;
+        int32_t dot = 0;
+        for (int j = 0; j < 32; ++j) dot += (int32_t)c[j] * zz[j];
+        if (dots) dots[((size_t)t * n + r) * groups + g] = dot;
+        float ds = d * (float)s, dm = dmin * (float)mm;
+        size_t gi = (size_t)t * groups + g;
+        float term = a[gi] * (ds * (float)dot - dm * (float)sums[gi]);
+        acc64 += term;
+        acc32 += term;
+      }
+      if (out64) out64[(size_t)t * n + r] = acc64;
+      if (out32) out32[(size_t)t * n + r] = acc32;
+    }
+  }
+  (void)threads;
+}
+
+void orc_q6k_q8_contract(const uint8_t* q, const int8_t* sc, const uint16_t* d,
+                         uint32_t n, uint32_t pk, const int8_t* z, const float* a,
+                         const int32_t* sums, uint32_t m, double* out64,
+                         float* out32, int32_t* dots, int threads) {
+  uint32_t groups = pk / 32, kbs = pk / 256;
+  (void)sums;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 16)
+#endif
+  for (int64_t r = 0; r < (int64_t)n; ++r) {
+    for (uint32_t t = 0; t < m; ++t) {
+      double acc64 = 0;
+      float acc32 = 0;
+      for (uint32_t g = 0; g < groups; ++g) {
+        size_t blk = (size_t)r * kbs + g / 8;
+        float dd = orc_fp16_to_fp32(d[blk]);
+        const int8_t* s = sc + (size_t)r * (pk / 16) + 2 * g;
+        const uint8_t* c = q + (size_t)r * pk + g * 32;
+        const int8_t* zz = z + (size_t)t * pk + g * 32;
+        int32_t d0 = 0, d1 = 0;
+        for (int j = 0; j < 16; ++j) d0 += ((int32_t)c[j] - 32) * zz[j];
+        for (int j = 16; j < 32; ++j) d1 += ((int32_t)c[j] - 32) * zz[j];
+        int32_t I = s[0] * d0 + s[1] * d1;
+        if (dots) dots[((size_t)t * n + r) * groups + g] = I;
+        size_t gi = (size_t)t * groups + g;
+        float term = a[gi] * (dd * (float)I);
+        acc64 += term;
+        acc32 += term;
+      }
+      if (out64) out64[(size_t)t * n + r] = acc64;
+      if (out32) out32[(size_t)t * n + r] = acc32;
+    }
+  }
+  (void)threads;
+}
+
+/* ---- BF16-activation decode reference ----------------------------------- */
+float orc_q4k_bf16_weight(const uint8_t* mb, unsigned code, unsigned g) {
+  unsigned s, m;
+  orc_q4k_scale_min(mb, g, &s, &m);
+  float d = orc_fp16_to_fp32((uint16_t)(mb[0] | (mb[1] << 8))) * (float)s;
+  float mm = orc_fp16_to_fp32((uint16_t)(mb[2] | (mb[3] << 8))) * (float)m;
+  float v = d * (float)code - mm;
+  return orc_bf16_to_fp32(orc_fp32_to_bf16_rne(v));
+}
+
+void orc_q4k_bf16_gemv(const uint8_t* codes, const uint8_t* meta, uint32_t n,
+                       uint32_t pk, uint32_t k, const uint16_t* x, double* out64,
+                       int threads) {
+  uint32_t kbs = pk / 256;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 16)
+#endif
+  for (int64_t r = 0; r < (int64_t)n; ++r) {
+    double acc = 0;
+    for (uint32_t c = 0; c < k; ++c) {
+      const uint8_t* mb = meta + ((size_t)r * kbs + c / 256) * 16;
+      float w = orc_q4k_bf16_weight(mb, codes[(size_t)r * pk + c], (c % 256) / 32);
+      acc += (double)w * (double)orc_bf16_to_fp32(x[c]);
+    }
+    out64[r] = acc;
+  }
+  (void)threads;
+}

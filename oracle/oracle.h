@@ -1,0 +1,109 @@
+/*
+ * CPU oracle for the Q4_K / Q6_K x Q8 projection path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or the timed CPU baseline). The product path in qw38_amd/ never links,
+ * loads or falls back to it.
+ *
+ * Every function restates the reference algorithm it names (file:line in the
+ * reference tree) in plain C; the header of oracle.c lists how each one is
+ * pinned (golden vectors, the compiled pinned llama.cpp header, closed forms).
+ */
+#ifndef QW38_ORACLE_H
+#define QW38_ORACLE_H
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar conversions ------------------------------------------------ */
+float orc_fp16_to_fp32(uint16_t h);
+uint16_t orc_fp32_to_fp16(float f);
+float orc_bf16_to_fp32(uint16_t h);
+uint16_t orc_fp32_to_bf16_rne(float x);
+int orc_nearest_int(float x);
+float orc_expf(float x);
+
+/* ---- Q8 activation producers ------------------------------------------- */
+/* BF16 [m][k] -> codes int8 [m][pk], scales f32 [m][pk/32], sums i32.
+ * Returns 1 when any group was nonfinite (the device failure flag). */
+int orc_pack_q8(const uint16_t* bf16, uint32_t m, uint32_t k, uint32_t pk,
+                int8_t* codes, float* scales, int32_t* sums);
+/* Same producer over FP32 values already rounded by the caller. */
+int orc_pack_q8_f32(const float* x, uint32_t m, uint32_t k, uint32_t pk,
+                    int8_t* codes, float* scales, int32_t* sums);
+/* Zero-centred RMS (1+gamma)*x/rms -> BF16 -> Q8, hidden width 5120. */
+int orc_rms_q8(const float* residual, const uint16_t* gamma, float eps,
+               uint32_t m, int8_t* codes, float* scales, int32_t* sums,
+               uint16_t* bf16_out /* may be NULL */);
+/* BF16(SiLU(g)*u) -> Q8 over [m][n]; n % 256 == 0. */
+int orc_swiglu_q8(const float* gate, const float* up, uint32_t m, uint32_t n,
+                  int8_t* codes, float* scales, int32_t* sums,
+                  uint16_t* bf16_out /* may be NULL */);
+
+/* ---- Q4_K quantizer and layouts ----------------------------------------- */
+/* 256 floats -> codes[256] in 0..15 and meta[16] (d, dmin, 12 packed bytes).
+ * Returns 0, or 1 (nonfinite) / 2 (unrepresentable) as the reference does. */
+int orc_quantize_q4k_block(const float* x, uint8_t* codes, uint8_t* meta);
+/* Row-major [n][k] (k % 256 == 0) -> logical codes [n][k], meta [n][k/256][16]. */
+int orc_quantize_q4k_rows(const float* x, uint64_t n, uint64_t k,
+                          uint8_t* codes, uint8_t* meta, int threads);
+void orc_q4k_logical_to_ggml(const uint8_t* codes, const uint8_t* meta,
+                             uint64_t blocks, uint8_t* ggml /* 144 B each */);
+void orc_q4k_ggml_to_logical(const uint8_t* ggml, uint64_t blocks,
+                             uint8_t* codes, uint8_t* meta);
+void orc_q4k_scale_min(const uint8_t* meta, unsigned g, unsigned* s, unsigned* m);
+/* Logical [n][pk] -> physical tiles. layout 0x020D: sequential nibbles;
+ * layout 0x0240: wave64 nibble order. codes_out: padded_n*pk/2 bytes,
+ * meta_out: padded_n*(pk/256)*16 bytes. */
+int orc_pack_q4k_layout(uint16_t layout, const uint8_t* codes, const uint8_t* meta,
+                        uint32_t n, uint32_t pk, uint8_t* codes_out, uint8_t* meta_out);
+int orc_unpack_q4k_layout(uint16_t layout, const uint8_t* codes_in, const uint8_t* meta_in,
+                          uint32_t n, uint32_t pk, uint8_t* codes, uint8_t* meta);
+
+/* ---- Q6_K quantizer and layouts ----------------------------------------- */
+/* 256 floats -> q[256] in 0..63, sc[16] int8, d fp16 bits. */
+void orc_quantize_q6k_block(const float* x, uint8_t* q, int8_t* sc, uint16_t* d);
+int orc_quantize_q6k_rows(const float* x, uint64_t n, uint64_t k, uint8_t* q,
+                          int8_t* sc, uint16_t* d, int threads);
+void orc_q6k_logical_to_ggml(const uint8_t* q, const int8_t* sc, const uint16_t* d,
+                             uint64_t blocks, uint8_t* ggml /* 210 B each */);
+void orc_q6k_ggml_to_logical(const uint8_t* ggml, uint64_t blocks, uint8_t* q,
+                             int8_t* sc, uint16_t* d);
+/* layout 0x0241: codes = padded_n*kbs*192 B, scales = padded_n*kbs*18 B. */
+int orc_pack_q6k_layout(const uint8_t* q, const int8_t* sc, const uint16_t* d,
+                        uint32_t n, uint32_t pk, uint8_t* codes_out, uint8_t* meta_out);
+int orc_unpack_q6k_layout(const uint8_t* codes_in, const uint8_t* meta_in,
+                          uint32_t n, uint32_t pk, uint8_t* q, int8_t* sc, uint16_t* d);
+
+/* ---- contractions ------------------------------------------------------- */
+/* out64[t][r] = sum_g a*(ds*dot - dm*sum) in double (closed form);
+ * out32[t][r] = the same expression in FP32, ascending-K order (reference
+ * K32 order); dots[t][r][g] = exact per-group int32 dots (any may be NULL). */
+void orc_q4k_q8_contract(const uint8_t* codes, const uint8_t* meta, uint32_t n,
+                         uint32_t pk, const int8_t* z, const float* a,
+                         const int32_t* sums, uint32_t m, double* out64,
+                         float* out32, int32_t* dots, int threads);
+/* Q6_K: per K32 group I = sc0*sum16((q-32)z) + sc1*sum16((q-32)z);
+ * out += a * (d * I). dots[t][r][g] = I. */
+void orc_q6k_q8_contract(const uint8_t* q, const int8_t* sc, const uint16_t* d,
+                         uint32_t n, uint32_t pk, const int8_t* z, const float* a,
+                         const int32_t* sums, uint32_t m, double* out64,
+                         float* out32, int32_t* dots, int threads);
+
+/* ---- BF16-activation decode (decode_mmv Q4_K branch) -------------------- */
+/* Reconstructed BF16 weight operand for one logical element. */
+float orc_q4k_bf16_weight(const uint8_t* meta_block, unsigned code, unsigned g);
+/* y[r] = sum_k W[r][k]*x[k] with W reconstructed as the BF16 operand;
+ * out64 in double. */
+void orc_q4k_bf16_gemv(const uint8_t* codes, const uint8_t* meta, uint32_t n,
+                       uint32_t pk, uint32_t k, const uint16_t* x, double* out64,
+                       int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

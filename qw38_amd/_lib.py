@@ -1,0 +1,108 @@
+"""ctypes binding of the C-ABI in ``include/qw38_hip.h``.
+
+Loads ``qw38_amd/libqw38_hip.so`` built in-tree. There is no fallback: a
+missing library raises immediately, naming the build step.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+LIB_PATH = os.path.join(PKG, "libqw38_hip.so")
+HEADER = os.path.join(ROOT, "include", "qw38_hip.h")
+
+QW38_OK, QW38_STATUS, QW38_INVALID_ARGUMENT, QW38_OVERFLOW = 0, 1, 2, 3
+LAYOUT_Q4K_SEQ = 0x020D
+LAYOUT_Q4K_W64 = 0x0240
+LAYOUT_Q6K_W64 = 0x0241
+QUANTIZER_Q4K = 0x0105
+QUANTIZER_Q6K = 0x0140
+CODE_NAMES = {1: "Status", 2: "InvalidArgument", 3: "Overflow"}
+
+
+class Weight(C.Structure):
+    """qw38_weight == cuda::PrefillWeight (cuda/prefill.hpp:33-44)."""
+    _fields_ = [("codes", C.c_void_p), ("scales", C.c_void_p), ("layout", C.c_uint16),
+                ("quantizer", C.c_uint16), ("n", C.c_uint32), ("k", C.c_uint32),
+                ("padded_n", C.c_uint32), ("padded_k", C.c_uint32),
+                ("codes_bytes", C.c_uint64), ("scales_bytes", C.c_uint64)]
+
+
+class Q8Input(C.Structure):
+    """qw38_q8_input == cuda::Q8Input (cuda/q4k_q8.hpp:16-21)."""
+    _fields_ = [("codes", C.c_void_p), ("codes_len", C.c_uint64), ("scales", C.c_void_p),
+                ("scales_len", C.c_uint64), ("sums", C.c_void_p), ("sums_len", C.c_uint64),
+                ("m", C.c_uint32), ("k", C.c_uint32), ("padded_k", C.c_uint32)]
+
+
+class Qw38Error(RuntimeError):
+    def __init__(self, status, hip_status, operation, detail):
+        self.status, self.hip_status = status, hip_status
+        self.operation, self.detail = operation, detail
+        super().__init__(f"{CODE_NAMES.get(status, status)} in {operation}: {detail}"
+                         + (f" (hip {hip_status})" if hip_status else ""))
+
+
+_lib = None
+
+_V, _U16, _U32, _U64, _I, _F = C.c_void_p, C.c_uint16, C.c_uint32, C.c_uint64, C.c_int, C.c_float
+_P = C.POINTER
+SIGNATURES = {
+    "qw38_last_error": (_I, [_P(_I), C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t]),
+    "qw38_pack_q8": (_I, [_V, _U64, _P(Q8Input), _V, _U64, _V]),
+    "qw38_q4k_q8_project": (_I, [_P(Weight), _P(Q8Input), _V, _U64, _V, _U64, _V]),
+    "qw38_q8_mlp_workspace_bytes": (_U64, [_U32]),
+    "qw38_q4k_q8_mlp": (_I, [_P(Weight), _P(Weight), _P(Weight), _V, _V, _F, _V, _U32, _V, _U64,
+                             _V, _P(_I), _V]),
+    "qw38_hidden_rms_q8": (_I, [_V, _V, _F, _U32, _V, _V, _V, _V, _V]),
+    "qw38_swiglu_q8": (_I, [_V, _V, _U32, _U32, _V, _V, _V, _V, _V]),
+    "qw38_q8_group_dots": (_I, [_P(Weight), _P(Q8Input), _V, _U64, _V]),
+    "qw38_repack_q4k_blocks": (_I, [_V, _U64, _U32, _U32, _U16, _V, _U64, _V, _U64, _V]),
+    "qw38_repack_q6k_blocks": (_I, [_V, _U64, _U32, _U32, _V, _U64, _V, _U64, _V]),
+    "qw38_quantize_q4k_blocks": (_I, [_V, _U64, _U32, _U32, _V, _U64, _V, _V]),
+    "qw38_quantize_q6k_blocks": (_I, [_V, _U64, _U32, _U32, _V, _U64, _V]),
+    "qw38_code_bytes": (_U64, [_U16, _U32, _U32]),
+    "qw38_scale_bytes": (_U64, [_U16, _U32, _U32]),
+    "qw38_device_malloc": (_I, [_P(_V), _U64]),
+    "qw38_device_free": (_I, [_V, _U64]),
+    "qw38_malloc_count": (_U64, []),
+    "qw38_free_count": (_U64, []),
+    "qw38_live_bytes": (_U64, []),
+    "qw38_peak_live_bytes": (_U64, []),
+}
+
+
+def header_symbols() -> list[str]:
+    """Every function the C header declares."""
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|uint64_t|void)\s+(qw38_\w+)\s*\(", text, re.M)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() "
+                               "(hipcc for gfx950) first; there is no CPU fallback")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype, f.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+def last_error() -> Qw38Error:
+    hip = C.c_int(0)
+    op = C.create_string_buffer(96)
+    detail = C.create_string_buffer(256)
+    st = lib().qw38_last_error(C.byref(hip), op, 96, detail, 256)
+    return Qw38Error(st, hip.value, op.value.decode(), detail.value.decode())
+
+
+def check(status: int) -> None:
+    if status != QW38_OK:
+        raise last_error()

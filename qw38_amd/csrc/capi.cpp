@@ -1,0 +1,502 @@
+// C-ABI entry points: operand validation (all before any launch), dispatch to
+// the gfx950 kernels, thread-local error reporting and allocation counters.
+// Validation mirrors the reference's prelaunch contract: cuda/q4k_q8.cu:269-298
+// (geometry, device residency, non-aliasing), cuda/prefill.cu:273-325.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <initializer_list>
+#include <limits>
+
+#include "common.hpp"
+
+namespace {
+using namespace qw38hip;
+
+struct LastError {
+  int status = QW38_OK;
+  int hip_status = 0;
+  char operation[96] = {0};
+  char detail[256] = {0};
+};
+thread_local LastError g_err;
+
+int fail(int status, const char* op, const char* detail, int hip_status = 0) {
+  g_err.status = status;
+  g_err.hip_status = hip_status;
+  std::snprintf(g_err.operation, sizeof g_err.operation, "%s", op);
+  std::snprintf(g_err.detail, sizeof g_err.detail, "%s", detail);
+  return status;
+}
+int ok() {
+  g_err = LastError{};
+  return QW38_OK;
+}
+int hip_fail(hipError_t e, const char* op) {
+  (void)hipGetLastError();  // consume the sticky error
+  return fail(QW38_STATUS, op, hipGetErrorString(e), int(e));
+}
+
+std::atomic<uint64_t> g_mallocs{0}, g_frees{0}, g_live{0}, g_peak{0};
+
+constexpr uint32_t pad_k(uint32_t k) { return k == 0 ? 0 : (k + 255u) / 256u * 256u; }
+constexpr uint64_t pad_n(uint32_t n) { return n == 0 ? 0 : (uint64_t(n) + 7u) / 8u * 8u; }
+
+// Activates the stream's device for the duration of a call (cuda/device.hpp:12-50).
+struct DeviceScope {
+  int previous = -1;
+  bool restore = false;
+  hipError_t status = hipSuccess;
+  explicit DeviceScope(int device) {
+    status = hipGetDevice(&previous);
+    if (status == hipSuccess && previous != device) {
+      status = hipSetDevice(device);
+      restore = status == hipSuccess;
+    }
+  }
+  ~DeviceScope() {
+    if (restore) (void)hipSetDevice(previous);
+  }
+};
+
+int stream_device(void* stream, int* device, const char* op) {
+  hipError_t e = stream ? hipStreamGetDevice(static_cast<hipStream_t>(stream), device)
+                        : hipGetDevice(device);
+  if (e != hipSuccess) return hip_fail(e, op);
+  return QW38_OK;
+}
+
+struct Region {
+  const void* p;
+  uint64_t n;
+  uint32_t alignment;
+};
+
+// Device-resident, aligned, inside one allocation (cuda/prefill.cu:273-309).
+int validate_span(const Region& r, int device, const char* op) {
+  if (r.n == 0) return QW38_OK;
+  if (r.p == nullptr) return fail(QW38_INVALID_ARGUMENT, op, "null operand");
+  const uintptr_t b = reinterpret_cast<uintptr_t>(r.p);
+  if (r.alignment && b % r.alignment)
+    return fail(QW38_INVALID_ARGUMENT, op, "misaligned operand");
+  if (r.n > std::numeric_limits<uintptr_t>::max() - b)
+    return fail(QW38_OVERFLOW, op, "address overflow");
+  hipPointerAttribute_t attr{};
+  hipError_t e = hipPointerGetAttributes(&attr, r.p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(QW38_INVALID_ARGUMENT, op, "operand is not device memory");
+  }
+  if (attr.type != hipMemoryTypeDevice || attr.device != device)
+    return fail(QW38_INVALID_ARGUMENT, op, "operand is not memory of the stream's device");
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  e = hipMemGetAddressRange(&base, &size, const_cast<void*>(r.p));
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(QW38_INVALID_ARGUMENT, op, "operand allocation range unknown");
+  }
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(base);
+  if (b < lo || b + r.n > lo + size)
+    return fail(QW38_INVALID_ARGUMENT, op, "operand span exceeds its allocation");
+  return QW38_OK;
+}
+
+int distinct(std::initializer_list<Region> regions, int device, const char* op) {
+  const Region* rs = regions.begin();
+  const size_t count = regions.size();
+  for (size_t i = 0; i < count; ++i) {
+    if (int st = validate_span(rs[i], device, op)) return st;
+    if (rs[i].n == 0) continue;
+    const uintptr_t b = reinterpret_cast<uintptr_t>(rs[i].p);
+    for (size_t j = 0; j < i; ++j) {
+      if (rs[j].n == 0) continue;
+      const uintptr_t c = reinterpret_cast<uintptr_t>(rs[j].p);
+      if (b < c + rs[j].n && c < b + rs[i].n)
+        return fail(QW38_INVALID_ARGUMENT, "q8.alias", "live operands overlap");
+    }
+  }
+  return QW38_OK;
+}
+
+bool valid_q8(const qw38_q8_input& x, uint32_t max_m) {
+  return x.m && x.m <= max_m && x.k && x.k <= QW38_PROJECT_MAX_K && x.padded_k == pad_k(x.k) &&
+         x.codes_len == uint64_t(x.m) * x.padded_k && x.scales_len == x.codes_len / 32 &&
+         x.sums_len == x.scales_len;
+}
+
+bool layout_ok(uint16_t layout, uint16_t quantizer) {
+  if (layout == QW38_LAYOUT_Q4K_CANDIDATE_V2 || layout == QW38_LAYOUT_Q4K_WAVE64)
+    return quantizer == QW38_QUANTIZER_Q4K;
+  if (layout == QW38_LAYOUT_Q6K_WAVE64) return quantizer == QW38_QUANTIZER_Q6K;
+  return false;
+}
+
+int valid_weight(const qw38_weight& w, const char* op) {
+  if (!w.n || w.n > QW38_PROJECT_MAX_N || !w.k || w.k > QW38_PROJECT_MAX_K ||
+      !layout_ok(w.layout, w.quantizer) || w.padded_n != pad_n(w.n) ||
+      w.padded_k != pad_k(w.k) ||
+      w.codes_bytes != qw38_code_bytes(w.layout, w.padded_n, w.padded_k) ||
+      w.scales_bytes != qw38_scale_bytes(w.layout, w.padded_n, w.padded_k))
+    return fail(QW38_INVALID_ARGUMENT, op, "Q4_K/Q6_K geometry required");
+  return QW38_OK;
+}
+
+uint32_t codes_alignment(const qw38_weight& w) {
+  return w.layout == QW38_LAYOUT_Q4K_CANDIDATE_V2 ? 4u : 16u;
+}
+
+WeightView view(const qw38_weight& w) {
+  return WeightView{static_cast<const uint8_t*>(w.codes), static_cast<const uint8_t*>(w.scales),
+                    w.layout, w.n, w.k, w.padded_n, w.padded_k};
+}
+
+hipError_t project(const qw38_weight& w, const Q8View& x, float* out, const float* residual,
+                   hipStream_t s) {
+  if (x.m <= 8) return launch_gemv(view(w), x, out, residual, s);
+  return launch_mmq(view(w), x, out, residual, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int qw38_last_error(int* hip_status, char* operation, size_t operation_cap, char* detail,
+                    size_t detail_cap) {
+  if (hip_status) *hip_status = g_err.hip_status;
+  if (operation && operation_cap) std::snprintf(operation, operation_cap, "%s", g_err.operation);
+  if (detail && detail_cap) std::snprintf(detail, detail_cap, "%s", g_err.detail);
+  return g_err.status;
+}
+
+uint64_t qw38_code_bytes(uint16_t layout, uint32_t padded_n, uint32_t padded_k) {
+  const uint64_t nk = uint64_t(padded_n) * padded_k;
+  switch (layout) {
+    case QW38_LAYOUT_Q4K_CANDIDATE_V2:
+    case QW38_LAYOUT_Q4K_WAVE64: return nk / 2;
+    case QW38_LAYOUT_Q6K_WAVE64: return nk / 256 * 192;
+    default: return 0;
+  }
+}
+
+uint64_t qw38_scale_bytes(uint16_t layout, uint32_t padded_n, uint32_t padded_k) {
+  const uint64_t blocks = uint64_t(padded_n) * (padded_k / 256);
+  switch (layout) {
+    case QW38_LAYOUT_Q4K_CANDIDATE_V2:
+    case QW38_LAYOUT_Q4K_WAVE64: return blocks * 16;
+    case QW38_LAYOUT_Q6K_WAVE64: return blocks * 18;
+    default: return 0;
+  }
+}
+
+int qw38_pack_q8(const uint16_t* input, uint64_t input_len, const qw38_q8_input* output,
+                 int* failure, uint64_t failure_len, void* stream) {
+  constexpr const char* op = "q8.pack";
+  if (!output || !valid_q8(*output, QW38_PROJECT_MAX_TOKENS) ||
+      input_len != uint64_t(output->m) * output->k || failure_len != 1)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid geometry");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  const qw38_q8_input& x = *output;
+  if (int st = distinct({{input, input_len * 2, 2}, {x.codes, x.codes_len, 4},
+                         {x.scales, x.scales_len * 4, 4}, {x.sums, x.sums_len * 4, 4},
+                         {failure, 4, 4}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  hipError_t e = launch_pack_q8(input, x.m, x.k, x.padded_k, x.codes, x.scales, x.sums, failure,
+                                static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_q4k_q8_project(const qw38_weight* weight, const qw38_q8_input* input, float* output,
+                        uint64_t output_len, const float* residual, uint64_t residual_len,
+                        void* stream) {
+  constexpr const char* op = "q8.project";
+  if (!weight || !input) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
+  const qw38_weight& w = *weight;
+  const qw38_q8_input& x = *input;
+  if (int st = valid_weight(w, "q8.weight")) return st;
+  if (!valid_q8(x, QW38_PROJECT_MAX_TOKENS) || x.k != w.k ||
+      output_len != uint64_t(x.m) * w.n || (residual_len && residual_len != output_len) ||
+      (residual_len == 0) != (residual == nullptr))
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid geometry");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{w.codes, w.codes_bytes, codes_alignment(w)},
+                         {w.scales, w.scales_bytes, 2},
+                         {x.codes, x.codes_len, 4},
+                         {x.scales, x.scales_len * 4, 4},
+                         {x.sums, x.sums_len * 4, 4},
+                         {output, output_len * 4, 4},
+                         {residual, residual_len * 4, 4}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  const Q8View xv{x.codes, x.scales, x.sums, x.m, x.k, x.padded_k};
+  hipError_t e = project(w, xv, output, residual, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "q4k_q8.project");
+}
+
+uint64_t qw38_q8_mlp_workspace_bytes(uint32_t m) {
+  return uint64_t(m) * (17408 + 17408 / 32 * 8 + 2 * 17408 * 4) + 4;
+}
+
+int qw38_q4k_q8_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
+                    const float* residual, const uint16_t* gamma, float eps, float* output,
+                    uint32_t m, void* workspace, uint64_t workspace_bytes, void* stream,
+                    int* submitted, int* pending_failure) {
+  constexpr const char* op = "q8.mlp";
+  if (submitted) *submitted = 0;
+  if (!gate || !up || !down || !submitted) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!pending_failure) {
+    // Public completion API rejects stream capture (cuda/graph.cpp:21-31).
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s, &cs);
+    if (e != hipSuccess) return hip_fail(e, "graph.require_uncaptured");
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(QW38_INVALID_ARGUMENT, "graph.require_uncaptured", "stream is capturing");
+  }
+  if (!m || m > QW38_Q8_MLP_MAX_TOKENS || workspace_bytes < qw38_q8_mlp_workspace_bytes(m) ||
+      !std::isfinite(eps) || eps <= 0 || gate->n != 17408 || gate->k != 5120 ||
+      up->n != gate->n || up->k != gate->k || down->n != 5120 || down->k != 17408)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid geometry");
+  for (const qw38_weight* w : {gate, up, down})
+    if (int st = valid_weight(*w, "q8.weight")) return st;
+  if (gate->layout == QW38_LAYOUT_Q6K_WAVE64 || up->layout == QW38_LAYOUT_Q6K_WAVE64)
+    return fail(QW38_INVALID_ARGUMENT, "q8.weight", "gate/up must be Q4_K");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{gate->codes, gate->codes_bytes, codes_alignment(*gate)},
+                         {gate->scales, gate->scales_bytes, 2},
+                         {up->codes, up->codes_bytes, codes_alignment(*up)},
+                         {up->scales, up->scales_bytes, 2},
+                         {down->codes, down->codes_bytes, codes_alignment(*down)},
+                         {down->scales, down->scales_bytes, 2},
+                         {residual, uint64_t(m) * 5120 * 4, 4},
+                         {gamma, 5120 * 2, 2},
+                         {output, uint64_t(m) * 5120 * 4, 4},
+                         {workspace, workspace_bytes, 4},
+                         {pending_failure, pending_failure ? 4u : 0u, 4}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  auto* codes = static_cast<int8_t*>(workspace);
+  auto* scales = reinterpret_cast<float*>(codes + size_t(m) * 17408);
+  auto* sums = reinterpret_cast<int32_t*>(scales + size_t(m) * 544);
+  auto* g = reinterpret_cast<float*>(sums + size_t(m) * 544);
+  auto* u = g + size_t(m) * 17408;
+  int* flag = pending_failure ? pending_failure : reinterpret_cast<int*>(u + size_t(m) * 17408);
+  *submitted = 1;
+  auto bail = [&](hipError_t e, const char* what) {
+    if (!pending_failure) (void)hipStreamSynchronize(s);
+    return hip_fail(e, what);
+  };
+  hipError_t e = hipSuccess;
+  if (!pending_failure && (e = launch_fill_zero_i32(flag, 1, s)) != hipSuccess)
+    return bail(e, "q8.clear_failure");
+  if ((e = launch_rms_q8(residual, gamma, eps, m, codes, scales, sums, flag, s)) != hipSuccess)
+    return bail(e, "q8.rms_pack");
+  Q8View x{codes, scales, sums, m, 5120, 5120};
+  if ((e = project(*gate, x, g, nullptr, s)) != hipSuccess) return bail(e, "q4k_q8.project");
+  if ((e = project(*up, x, u, nullptr, s)) != hipSuccess) return bail(e, "q4k_q8.project");
+  if ((e = launch_swiglu_q8(g, u, m, 17408, codes, scales, sums, flag, s)) != hipSuccess)
+    return bail(e, "q8.swiglu_pack");
+  x = Q8View{codes, scales, sums, m, 17408, 17408};
+  if ((e = project(*down, x, output, residual, s)) != hipSuccess) return bail(e, "q4k_q8.project");
+  if (pending_failure) return ok();
+  int bad = 0;
+  if ((e = hipMemcpyAsync(&bad, flag, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return bail(e, "q8.failure");
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream.sync");
+  if (bad)
+    return fail(QW38_INVALID_ARGUMENT, "q8.producer", "nonfinite producer or invalid Q8 scale");
+  return ok();
+}
+
+int qw38_hidden_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                       int8_t* codes, float* scales, int32_t* sums, int* failure,
+                       void* stream) {
+  constexpr const char* op = "q8.rms";
+  if (!m || m > QW38_PROJECT_MAX_TOKENS || !std::isfinite(eps) || eps <= 0)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid operands");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{residual, uint64_t(m) * 5120 * 4, 4}, {gamma, 5120 * 2, 2},
+                         {codes, uint64_t(m) * 5120, 4}, {scales, uint64_t(m) * 160 * 4, 4},
+                         {sums, uint64_t(m) * 160 * 4, 4}, {failure, 4, 4}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  hipError_t e = launch_rms_q8(residual, gamma, eps, m, codes, scales, sums, failure,
+                               static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "q8.rms_pack");
+}
+
+int qw38_swiglu_q8(const float* gate, const float* up, uint32_t m, uint32_t n, int8_t* codes,
+                   float* scales, int32_t* sums, int* failure, void* stream) {
+  constexpr const char* op = "q8.swiglu";
+  if (!m || !n || n % 256 || m > QW38_PROJECT_MAX_TOKENS || n > QW38_PROJECT_MAX_K)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid geometry");
+  const uint64_t e_count = uint64_t(m) * n;
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{gate, e_count * 4, 4}, {up, e_count * 4, 4}, {codes, e_count, 4},
+                         {scales, e_count / 32 * 4, 4}, {sums, e_count / 32 * 4, 4},
+                         {failure, 4, 4}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  hipError_t e = launch_swiglu_q8(gate, up, m, n, codes, scales, sums, failure,
+                                  static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "q8.swiglu_pack");
+}
+
+int qw38_q8_group_dots(const qw38_weight* weight, const qw38_q8_input* input, int32_t* dots,
+                       uint64_t dots_len, void* stream) {
+  constexpr const char* op = "q8.group_dots";
+  if (!weight || !input) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
+  const qw38_weight& w = *weight;
+  const qw38_q8_input& x = *input;
+  if (int st = valid_weight(w, "q8.weight")) return st;
+  if (!valid_q8(x, QW38_PROJECT_MAX_TOKENS) || x.k != w.k ||
+      dots_len != uint64_t(x.m) * w.n * (w.padded_k / 32))
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid geometry");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{w.codes, w.codes_bytes, codes_alignment(w)},
+                         {w.scales, w.scales_bytes, 2}, {x.codes, x.codes_len, 4},
+                         {dots, dots_len * 4, 4}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  const Q8View xv{x.codes, x.scales, x.sums, x.m, x.k, x.padded_k};
+  hipError_t e = launch_group_dots(view(w), xv, dots, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+static int repack_common(const void* blocks, uint64_t blocks_bytes, uint64_t block_size,
+                         uint32_t n, uint32_t k, uint16_t layout, void* codes,
+                         uint64_t codes_bytes, void* scales, uint64_t scales_bytes,
+                         void* stream, const char* op, int device) {
+  if (!n || !k || k % 256 || k > QW38_PROJECT_MAX_K || n > QW38_PROJECT_MAX_N ||
+      blocks_bytes != uint64_t(n) * (k / 256) * block_size ||
+      codes_bytes != qw38_code_bytes(layout, uint32_t(pad_n(n)), k) ||
+      scales_bytes != qw38_scale_bytes(layout, uint32_t(pad_n(n)), k))
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid geometry");
+  return distinct({{blocks, blocks_bytes, 1}, {codes, codes_bytes, 16}, {scales, scales_bytes, 4}},
+                  device, op);
+}
+
+int qw38_repack_q4k_blocks(const void* blocks, uint64_t blocks_bytes, uint32_t n, uint32_t k,
+                           uint16_t layout, void* codes, uint64_t codes_bytes, void* scales,
+                           uint64_t scales_bytes, void* stream) {
+  constexpr const char* op = "upload.q4k";
+  if (layout != QW38_LAYOUT_Q4K_CANDIDATE_V2 && layout != QW38_LAYOUT_Q4K_WAVE64)
+    return fail(QW38_INVALID_ARGUMENT, op, "Q4_K layout required");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = repack_common(blocks, blocks_bytes, 144, n, k, layout, codes, codes_bytes, scales,
+                             scales_bytes, stream, op, device))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_fill_zero_i32(static_cast<int*>(codes), uint32_t(codes_bytes / 4), s);
+  if (e == hipSuccess) e = launch_fill_zero_i32(static_cast<int*>(scales), uint32_t(scales_bytes / 4), s);
+  if (e == hipSuccess)
+    e = launch_repack_q4k(static_cast<const uint8_t*>(blocks), n, k, layout,
+                          static_cast<uint8_t*>(codes), static_cast<uint8_t*>(scales), s);
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_repack_q6k_blocks(const void* blocks, uint64_t blocks_bytes, uint32_t n, uint32_t k,
+                           void* codes, uint64_t codes_bytes, void* scales,
+                           uint64_t scales_bytes, void* stream) {
+  constexpr const char* op = "upload.q6k";
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = repack_common(blocks, blocks_bytes, 210, n, k, QW38_LAYOUT_Q6K_WAVE64, codes,
+                             codes_bytes, scales, scales_bytes, stream, op, device))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_fill_zero_i32(static_cast<int*>(codes), uint32_t(codes_bytes / 4), s);
+  if (e == hipSuccess) e = launch_fill_zero_i32(static_cast<int*>(scales), uint32_t(scales_bytes / 4), s);
+  if (e == hipSuccess)
+    e = launch_repack_q6k(static_cast<const uint8_t*>(blocks), n, k, static_cast<uint8_t*>(codes),
+                          static_cast<uint8_t*>(scales), s);
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_quantize_q4k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_t k,
+                             void* blocks, uint64_t blocks_bytes, int* failure, void* stream) {
+  constexpr const char* op = "quantize.q4k";
+  if (!n || !k || k % 256 || x_len != uint64_t(n) * k ||
+      blocks_bytes != uint64_t(n) * (k / 256) * 144)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid geometry");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{x, x_len * 4, 4}, {blocks, blocks_bytes, 4}, {failure, 4, 4}}, device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  hipError_t e = launch_quantize_q4k(x, uint64_t(n) * (k / 256), static_cast<uint8_t*>(blocks),
+                                     failure, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_quantize_q6k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_t k,
+                             void* blocks, uint64_t blocks_bytes, void* stream) {
+  constexpr const char* op = "quantize.q6k";
+  if (!n || !k || k % 256 || x_len != uint64_t(n) * k ||
+      blocks_bytes != uint64_t(n) * (k / 256) * 210)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid geometry");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{x, x_len * 4, 4}, {blocks, blocks_bytes, 2}}, device, op)) return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  hipError_t e = launch_quantize_q6k(x, uint64_t(n) * (k / 256), static_cast<uint8_t*>(blocks),
+                                     static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_device_malloc(void** pointer, uint64_t bytes) {
+  if (!pointer || !bytes) return fail(QW38_INVALID_ARGUMENT, "device.malloc", "empty allocation");
+  hipError_t e = hipMalloc(pointer, bytes);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  g_mallocs.fetch_add(1);
+  const uint64_t live = g_live.fetch_add(bytes) + bytes;
+  uint64_t peak = g_peak.load();
+  while (live > peak && !g_peak.compare_exchange_weak(peak, live)) {
+  }
+  return ok();
+}
+
+int qw38_device_free(void* pointer, uint64_t bytes) {
+  if (!pointer) return ok();
+  hipError_t e = hipFree(pointer);
+  g_frees.fetch_add(1);
+  g_live.fetch_sub(std::min<uint64_t>(bytes, g_live.load()));
+  return e == hipSuccess ? ok() : hip_fail(e, "hipFree");
+}
+
+uint64_t qw38_malloc_count(void) { return g_mallocs.load(); }
+uint64_t qw38_free_count(void) { return g_frees.load(); }
+uint64_t qw38_live_bytes(void) { return g_live.load(); }
+uint64_t qw38_peak_live_bytes(void) { return g_peak.load(); }
+
+}  // extern "C"

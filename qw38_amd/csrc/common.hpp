@@ -1,0 +1,102 @@
+// Shared device helpers and internal launch interfaces of the gfx950 kernels.
+// Host code (capi.cpp) includes this header for the launcher declarations.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+#include "qw38_hip.h"
+
+namespace qw38hip {
+
+// 8-row x K256 tiles (src/format/pack.cpp:216-262): tile row index of
+// (row, kb) and the per-tile-row byte counts of each layout.
+constexpr uint32_t kTileRows = 8;
+constexpr uint32_t kTileK = 256;
+constexpr uint32_t kQ4CodeBytes = 128;  // per tile row
+constexpr uint32_t kQ4MetaBytes = 16;
+constexpr uint32_t kQ6CodeBytes = 192;  // 128 low-nibble + 64 high-pair bytes
+constexpr uint32_t kQ6ScaleBytes = 16;  // + 2 B fp16 d in a trailing array
+
+struct Q8View {
+  const int8_t* codes;
+  const float* scales;
+  const int32_t* sums;
+  uint32_t m, k, pk;
+};
+
+struct WeightView {
+  const uint8_t* codes;
+  const uint8_t* scales;
+  uint16_t layout;
+  uint32_t n, k, pn, pk;
+};
+
+// ---- device scalar helpers -------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(uint32_t(h) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
+  uint32_t b = __float_as_uint(x);
+  if (((b >> 23) & 0xffu) == 0xffu) {
+    uint16_t h = uint16_t(b >> 16);
+    if (b & 0x7fffffu) h |= 0x40u;
+    return h;
+  }
+  return uint16_t((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+// Exact FP16 -> FP32 (v_cvt_f32_f16; FP16 denormals are preserved by the
+// default gfx9 float mode).
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+  return float(__builtin_bit_cast(_Float16, uint16_t(h)));
+}
+
+// v_perm_b32: bytes of {hi:lo} selected by sel (0-3 from lo, 4-7 from hi).
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4(int(a), int(b), c, false);
+}
+
+// Q4_K 6-bit scale/min of K32 group g from the three packed metadata words
+// p0 = bytes 4..7, p1 = 8..11, p2 = 12..15 of the 16-byte tile-row metadata
+// (reference get_scale_min_k4, third_party/llama.cpp-q4k/reference.hpp:174-181).
+__device__ __forceinline__ void q4k_scale_min(uint32_t p0, uint32_t p1, uint32_t p2,
+                                              uint32_t g, uint32_t& s, uint32_t& m) {
+  if (g < 4) {
+    s = (p0 >> (8 * g)) & 63u;
+    m = (p1 >> (8 * g)) & 63u;
+  } else {
+    uint32_t j = 8 * (g - 4);
+    s = ((p2 >> j) & 15u) | (((p0 >> (j + 6)) & 3u) << 4);
+    m = ((p2 >> (j + 4)) & 15u) | (((p1 >> (j + 6)) & 3u) << 4);
+  }
+}
+
+// ---- launchers (defined in the .hip files) ---------------------------------
+hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t pk,
+                          int8_t* codes, float* scales, int32_t* sums, int* failure,
+                          hipStream_t s);
+hipError_t launch_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                         int8_t* codes, float* scales, int32_t* sums, int* failure,
+                         hipStream_t s);
+hipError_t launch_swiglu_q8(const float* gate, const float* up, uint32_t m, uint32_t n,
+                            int8_t* codes, float* scales, int32_t* sums, int* failure,
+                            hipStream_t s);
+hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out,
+                       const float* residual, hipStream_t s);
+hipError_t launch_mmq(const WeightView& w, const Q8View& x, float* out,
+                      const float* residual, hipStream_t s);
+hipError_t launch_group_dots(const WeightView& w, const Q8View& x, int32_t* dots,
+                             hipStream_t s);
+hipError_t launch_repack_q4k(const uint8_t* blocks, uint32_t n, uint32_t k, uint16_t layout,
+                             uint8_t* codes, uint8_t* scales, hipStream_t s);
+hipError_t launch_repack_q6k(const uint8_t* blocks, uint32_t n, uint32_t k, uint8_t* codes,
+                             uint8_t* scales, hipStream_t s);
+hipError_t launch_fill_zero_i32(int* p, uint32_t count, hipStream_t s);
+hipError_t launch_quantize_q4k(const float* x, uint64_t blocks, uint8_t* out, int* failure,
+                               hipStream_t s);
+hipError_t launch_quantize_q6k(const float* x, uint64_t blocks, uint8_t* out, hipStream_t s);
+
+}  // namespace qw38hip

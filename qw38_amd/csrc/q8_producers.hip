@@ -1,0 +1,182 @@
+// Q8 activation producers for gfx950: standalone BF16 pack, fused RMS->Q8 and
+// fused SwiGLU->Q8. One K32 group is one 32-lane half of a wave64; the group
+// reductions stay inside that half (width-32 shuffles, one ballot).
+//
+// Semantics (bit-exact): cuda/q8_device.cuh:6-25 -- peak = max finite |x|,
+// a = peak == 0 ? 1 : RN(peak / 127), z = clamp(rint(RN(x / a)), -127, 127),
+// sum = sum z; a nonfinite group stores a = NaN, z = 0 and raises the flag.
+#include "common.hpp"
+
+namespace qw38hip {
+namespace {
+
+__device__ __forceinline__ void q8_group32(float x, int8_t* codes, float* scales,
+                                           int32_t* sums, size_t group, int* failure) {
+  const unsigned lane = threadIdx.x & 31u;
+  const bool finite = isfinite(x);
+  float peak = finite ? fabsf(x) : 0.f;
+#pragma unroll
+  for (int off = 16; off; off >>= 1) peak = fmaxf(peak, __shfl_xor(peak, off, 32));
+  const uint64_t ballot = __ballot(finite);
+  const uint32_t half = uint32_t(ballot >> (threadIdx.x & 32u));
+  const float a = peak == 0.f ? 1.f : peak / 127.f;
+  const bool valid = half == 0xffffffffu && isfinite(a) && a > 0.f;
+  int z = 0;
+  if (valid) z = max(-127, min(127, int(rintf(x / a))));
+  codes[group * 32 + lane] = int8_t(z);
+  int sum = z;
+#pragma unroll
+  for (int off = 16; off; off >>= 1) sum += __shfl_xor(sum, off, 32);
+  if (lane == 0) {
+    scales[group] = valid ? a : __uint_as_float(0x7fc00000u);
+    sums[group] = sum;
+    if (!valid) *failure = 1;  // sticky flag, plain vector store
+  }
+}
+
+// cuda/q4k_q8.cu:44-50: grid (pk/256, m); padding columns pack as zeros.
+__global__ __launch_bounds__(256) void pack_q8_kernel(const uint16_t* __restrict__ in,
+                                                      uint32_t k, uint32_t pk,
+                                                      int8_t* codes, float* scales,
+                                                      int32_t* sums, int* failure) {
+  const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+  const uint32_t row = blockIdx.y;
+  const float x = c < k ? bf16_to_f32(in[size_t(row) * k + c]) : 0.f;
+  q8_group32(x, codes, scales, sums, (size_t(row) * pk + c) / 32, failure);
+}
+
+// 32-lane shuffle-down tree (lane i += lane i+off), result valid in lane 0 of
+// each half: the warp-32 order of cuda/activation.cu:36-50.
+__device__ __forceinline__ float tree32_sum(float v) {
+#pragma unroll
+  for (int off = 16; off; off >>= 1) v += __shfl_down(v, off, 32);
+  return v;
+}
+__device__ __forceinline__ float tree32_max(float v) {
+#pragma unroll
+  for (int off = 16; off; off >>= 1) v = fmaxf(v, __shfl_down(v, off, 32));
+  return v;
+}
+// 256-thread block reduction in the reference's order (cuda/activation.cu:
+// 52-96): eight 32-lane trees, then one tree over the 8 partials + 24 zeros.
+template <bool Max>
+__device__ float block256(float v, float* sm) {
+  v = Max ? tree32_max(v) : tree32_sum(v);
+  const unsigned w32 = threadIdx.x >> 5, lane = threadIdx.x & 31u;
+  if (lane == 0) sm[w32] = v;
+  __syncthreads();
+  if (threadIdx.x < 32) {
+    float t = lane < 8 ? sm[lane] : 0.f;
+    t = Max ? tree32_max(t) : tree32_sum(t);
+    if (lane == 0) sm[8] = t;
+  }
+  __syncthreads();
+  float r = sm[8];
+  __syncthreads();
+  return r;
+}
+
+constexpr uint32_t kHidden = 5120;
+
+// cuda/activation.cu:134-190 (Pack == 3): absmax prescale, sum of squares,
+// (1+gamma)*x/rms -> BF16 RNE -> Q8. FMAs where nvcc contracts mul+add.
+__global__ __launch_bounds__(256) void rms_q8_kernel(const float* __restrict__ residual,
+                                                     const uint16_t* __restrict__ gamma,
+                                                     float eps, int8_t* codes, float* scales,
+                                                     int32_t* sums, int* failure) {
+  __shared__ uint16_t rounded[kHidden];
+  __shared__ float sm[9];
+  const float* x = residual + size_t(blockIdx.x) * kHidden;
+  float s = 0.f;
+  for (uint32_t i = threadIdx.x; i < kHidden; i += 256) s = fmaxf(s, fabsf(x[i]));
+  const float scale = block256<true>(s, sm);
+  const float safe = scale == 0.f ? 1.f : scale;
+  float sq = 0.f;
+  for (uint32_t i = threadIdx.x; i < kHidden; i += 256) {
+    const float q = x[i] / safe;
+    sq = fmaf(q, q, sq);
+  }
+  const float sumsq = block256<false>(sq, sm);
+  const float se = sqrtf(eps) / safe;
+  const float inv = 1.0f / sqrtf(fmaf(se, se, sumsq / float(kHidden)));
+  for (uint32_t i = threadIdx.x; i < kHidden; i += 256) {
+    const float g = bf16_to_f32(gamma[i]);
+    rounded[i] = f32_to_bf16_rne((1.0f + g) * ((x[i] / safe) * inv));
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < kHidden; i += 256)
+    q8_group32(bf16_to_f32(rounded[i]), codes, scales, sums,
+               (size_t(blockIdx.x) * kHidden + i) / 32, failure);
+}
+
+// exp(x) by Cody-Waite reduction and a degree-7 Taylor polynomial with explicit
+// FMAs (Cephes two-part ln2). Within 1 ulp of the correctly rounded result.
+__device__ __forceinline__ float exp_cw(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -103.972084045410f) return 0.0f;
+  const float n = rintf(x * 1.44269502162933349609375f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.98412698412698412698e-4f;
+  p = fmaf(p, r, 1.38888888888888888889e-3f);
+  p = fmaf(p, r, 8.33333333333333333333e-3f);
+  p = fmaf(p, r, 4.16666666666666666667e-2f);
+  p = fmaf(p, r, 1.66666666666666666667e-1f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, int(n));
+}
+
+// cuda/q4k_q8.cu:52-61: v = BF16(SiLU(g) * u); nonfinite g/u -> NaN -> flag.
+__global__ __launch_bounds__(256) void swiglu_q8_kernel(const float* __restrict__ gate,
+                                                        const float* __restrict__ up,
+                                                        int8_t* codes, float* scales,
+                                                        int32_t* sums, int* failure) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  const float g = gate[i], u = up[i];
+  float v = (g / (1.f + exp_cw(-g))) * u;
+  if (!isfinite(g) || !isfinite(u)) v = __uint_as_float(0x7fc00000u);
+  q8_group32(bf16_to_f32(f32_to_bf16_rne(v)), codes, scales, sums, i / 32, failure);
+}
+
+__global__ void fill_zero_i32_kernel(int* p, uint32_t count) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i < count) p[i] = 0;
+}
+
+}  // namespace
+
+hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t pk,
+                          int8_t* codes, float* scales, int32_t* sums, int* failure,
+                          hipStream_t s) {
+  hipLaunchKernelGGL(pack_q8_kernel, dim3(pk / 256, m), dim3(256), 0, s, in, k, pk, codes,
+                     scales, sums, failure);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                         int8_t* codes, float* scales, int32_t* sums, int* failure,
+                         hipStream_t s) {
+  hipLaunchKernelGGL(rms_q8_kernel, dim3(m), dim3(256), 0, s, residual, gamma, eps, codes,
+                     scales, sums, failure);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_q8(const float* gate, const float* up, uint32_t m, uint32_t n,
+                            int8_t* codes, float* scales, int32_t* sums, int* failure,
+                            hipStream_t s) {
+  const uint64_t total = uint64_t(m) * n;
+  hipLaunchKernelGGL(swiglu_q8_kernel, dim3(uint32_t(total / 256)), dim3(256), 0, s, gate, up,
+                     codes, scales, sums, failure);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_zero_i32(int* p, uint32_t count, hipStream_t s) {
+  hipLaunchKernelGGL(fill_zero_i32_kernel, dim3((count + 255) / 256), dim3(256), 0, s, p,
+                     count);
+  return hipGetLastError();
+}
+
+}  // namespace qw38hip

@@ -1,0 +1,206 @@
+"""Python mirror of the reference operator interface for the Q4_K_M x Q8 path.
+
+Names, argument meaning and error behaviour follow ``cuda/q4k_q8.hpp`` (pack_q8,
+q4k_q8_project, q4k_q8_mlp) and ``cuda/activation.hpp`` (launch_hidden_rms_q8)
+of the reference; device memory and streams come from torch (plumbing only).
+Every call goes through the C-ABI of ``libqw38_hip.so``; errors raise
+``Qw38Error`` carrying the reference's error code names.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from ._lib import (LAYOUT_Q4K_SEQ, LAYOUT_Q4K_W64, LAYOUT_Q6K_W64, QUANTIZER_Q4K, QUANTIZER_Q6K,
+                   Q8Input as _Q8, Weight as _W, check, lib)
+
+__all__ = ["PrefillWeight", "Q8Input", "pack_q8", "q4k_q8_project", "q4k_q8_mlp",
+           "hidden_rms_q8", "swiglu_q8", "group_dots", "quantize_q4k_blocks", "quantize_q6k_blocks", "upload_q4k_blocks", "upload_q6k_blocks",
+           "q8_mlp_workspace_bytes", "code_bytes", "scale_bytes", "pad_k", "pad_n"]
+
+
+def pad_k(k: int) -> int:
+    return (k + 255) // 256 * 256
+
+
+def pad_n(n: int) -> int:
+    return (n + 7) // 8 * 8
+
+
+def code_bytes(layout: int, padded_n: int, padded_k: int) -> int:
+    return int(lib().qw38_code_bytes(layout, padded_n, padded_k))
+
+
+def scale_bytes(layout: int, padded_n: int, padded_k: int) -> int:
+    return int(lib().qw38_scale_bytes(layout, padded_n, padded_k))
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.cuda_stream
+    return int(stream)
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+@dataclass
+class PrefillWeight:
+    """Device-resident tiled weight: cuda::PrefillWeight (cuda/prefill.hpp:33-44)."""
+    codes: torch.Tensor
+    scales: torch.Tensor
+    layout: int
+    quantizer: int
+    n: int
+    k: int
+    padded_n: int
+    padded_k: int
+    codes_bytes: int = -1
+    scales_bytes: int = -1
+    codes_ptr: int | None = None  # explicit (possibly offset) pointer override
+
+    def __post_init__(self):
+        if self.codes_bytes < 0:
+            self.codes_bytes = self.codes.numel() * self.codes.element_size()
+        if self.scales_bytes < 0:
+            self.scales_bytes = self.scales.numel() * self.scales.element_size()
+
+    @staticmethod
+    def from_bytes(codes, scales, layout, n, k, device="cuda"):
+        """From host byte arrays (numpy uint8) of an already tiled layout."""
+        q = QUANTIZER_Q6K if layout == LAYOUT_Q6K_W64 else QUANTIZER_Q4K
+        c = torch.from_numpy(codes).to(device)
+        s = torch.from_numpy(scales).to(device)
+        return PrefillWeight(c, s, layout, q, n, k, pad_n(n), pad_k(k))
+
+    def struct(self) -> _W:
+        return _W(self.codes_ptr if self.codes_ptr is not None else self.codes.data_ptr(),
+                  self.scales.data_ptr(), self.layout, self.quantizer, self.n, self.k,
+                  self.padded_n, self.padded_k, self.codes_bytes, self.scales_bytes)
+
+
+@dataclass
+class Q8Input:
+    """Q8 K32 activation pack: cuda::Q8Input (cuda/q4k_q8.hpp:16-21)."""
+    codes: torch.Tensor   # int8 [m][padded_k]
+    scales: torch.Tensor  # float32 [m][padded_k/32]
+    sums: torch.Tensor    # int32 [m][padded_k/32]
+    m: int
+    k: int
+    padded_k: int
+    codes_ptr: int | None = None
+    codes_len: int | None = None
+
+    @staticmethod
+    def empty(m: int, k: int, device="cuda") -> "Q8Input":
+        pk = pad_k(k)
+        return Q8Input(torch.zeros(m, pk, dtype=torch.int8, device=device),
+                       torch.zeros(m, pk // 32, dtype=torch.float32, device=device),
+                       torch.zeros(m, pk // 32, dtype=torch.int32, device=device), m, k, pk)
+
+    def struct(self) -> _Q8:
+        n = self.codes_len if self.codes_len is not None else self.codes.numel()
+        return _Q8(self.codes_ptr if self.codes_ptr is not None else self.codes.data_ptr(), n,
+                   self.scales.data_ptr(), self.scales.numel(), self.sums.data_ptr(),
+                   self.sums.numel(), self.m, self.k, self.padded_k)
+
+
+def pack_q8(input_bf16: torch.Tensor, output: Q8Input, failure: torch.Tensor, stream=None):
+    """cuda::pack_q8 (cuda/q4k_q8.cu:318-330). input_bf16: int16/uint16 bits [m][k]."""
+    q = output.struct()
+    check(lib().qw38_pack_q8(_ptr(input_bf16), input_bf16.numel(), C.byref(q), _ptr(failure),
+                             failure.numel(), _stream(stream)))
+
+
+def q4k_q8_project(weight: PrefillWeight, x: Q8Input, output: torch.Tensor, stream=None,
+                   residual: torch.Tensor | None = None, output_ptr=None, output_len=None):
+    """cuda::q4k_q8_project (cuda/q4k_q8.cu:332-345)."""
+    w, q = weight.struct(), x.struct()
+    optr = output_ptr if output_ptr is not None else output.data_ptr()
+    olen = output_len if output_len is not None else output.numel()
+    check(lib().qw38_q4k_q8_project(C.byref(w), C.byref(q), optr, olen, _ptr(residual),
+                                    0 if residual is None else residual.numel(), _stream(stream)))
+
+
+def q8_mlp_workspace_bytes(m: int) -> int:
+    return int(lib().qw38_q8_mlp_workspace_bytes(m))
+
+
+def q4k_q8_mlp(gate: PrefillWeight, up: PrefillWeight, down: PrefillWeight,
+               residual: torch.Tensor, gamma: torch.Tensor, eps: float, output: torch.Tensor,
+               m: int, workspace: torch.Tensor, stream=None, pending_failure=None) -> bool:
+    """cuda::q4k_q8_mlp (cuda/q4k_q8.cu:347-398). Returns ``submitted``."""
+    g, u, d = gate.struct(), up.struct(), down.struct()
+    submitted = C.c_int(0)
+    st = lib().qw38_q4k_q8_mlp(C.byref(g), C.byref(u), C.byref(d), _ptr(residual), _ptr(gamma),
+                               eps, _ptr(output), m, _ptr(workspace), workspace.numel(),
+                               _stream(stream), C.byref(submitted), _ptr(pending_failure))
+    if st:
+        err = __import__("qw38_amd._lib", fromlist=["last_error"]).last_error()
+        err.submitted = bool(submitted.value)
+        raise err
+    return bool(submitted.value)
+
+
+def hidden_rms_q8(residual, gamma, eps, m, out: Q8Input, failure, stream=None):
+    """launch_hidden_rms_q8 (cuda/activation.cu:536-548)."""
+    check(lib().qw38_hidden_rms_q8(_ptr(residual), _ptr(gamma), eps, m, _ptr(out.codes),
+                                   _ptr(out.scales), _ptr(out.sums), _ptr(failure),
+                                   _stream(stream)))
+
+
+def swiglu_q8(gate, up, m, n, out: Q8Input, failure, stream=None):
+    """The SwiGLU->Q8 producer of q4k_q8_mlp (cuda/q4k_q8.cu:52-61)."""
+    check(lib().qw38_swiglu_q8(_ptr(gate), _ptr(up), m, n, _ptr(out.codes), _ptr(out.scales),
+                               _ptr(out.sums), _ptr(failure), _stream(stream)))
+
+
+def group_dots(weight: PrefillWeight, x: Q8Input, dots: torch.Tensor, stream=None):
+    w, q = weight.struct(), x.struct()
+    check(lib().qw38_q8_group_dots(C.byref(w), C.byref(q), _ptr(dots), dots.numel(),
+                                   _stream(stream)))
+
+
+def upload_q4k_blocks(blocks: torch.Tensor, n: int, k: int, layout=LAYOUT_Q4K_W64,
+                      stream=None) -> PrefillWeight:
+    """Load-time repack of GGML Q4_K super-blocks (uint8 device tensor)."""
+    pn, pk = pad_n(n), pad_k(k)
+    codes = torch.empty(code_bytes(layout, pn, pk), dtype=torch.uint8, device=blocks.device)
+    scales = torch.empty(scale_bytes(layout, pn, pk), dtype=torch.uint8, device=blocks.device)
+    check(lib().qw38_repack_q4k_blocks(_ptr(blocks), blocks.numel(), n, k, layout, _ptr(codes),
+                                       codes.numel(), _ptr(scales), scales.numel(),
+                                       _stream(stream)))
+    return PrefillWeight(codes, scales, layout, QUANTIZER_Q4K, n, k, pn, pk)
+
+
+def quantize_q4k_blocks(x: torch.Tensor, n: int, k: int, failure: torch.Tensor,
+                        stream=None) -> torch.Tensor:
+    """FP32 rows [n][k] on the device -> GGML Q4_K super-blocks (uint8)."""
+    blocks = torch.empty(n * (k // 256) * 144, dtype=torch.uint8, device=x.device)
+    check(lib().qw38_quantize_q4k_blocks(_ptr(x), x.numel(), n, k, _ptr(blocks), blocks.numel(),
+                                         _ptr(failure), _stream(stream)))
+    return blocks
+
+
+def quantize_q6k_blocks(x: torch.Tensor, n: int, k: int, stream=None) -> torch.Tensor:
+    """FP32 rows [n][k] on the device -> GGML Q6_K super-blocks (uint8)."""
+    blocks = torch.empty(n * (k // 256) * 210, dtype=torch.uint8, device=x.device)
+    check(lib().qw38_quantize_q6k_blocks(_ptr(x), x.numel(), n, k, _ptr(blocks), blocks.numel(),
+                                         _stream(stream)))
+    return blocks
+
+
+def upload_q6k_blocks(blocks: torch.Tensor, n: int, k: int, stream=None) -> PrefillWeight:
+    """Load-time repack of GGML Q6_K super-blocks (uint8 device tensor)."""
+    pn, pk = pad_n(n), pad_k(k)
+    codes = torch.empty(code_bytes(LAYOUT_Q6K_W64, pn, pk), dtype=torch.uint8, device=blocks.device)
+    scales = torch.empty(scale_bytes(LAYOUT_Q6K_W64, pn, pk), dtype=torch.uint8, device=blocks.device)
+    check(lib().qw38_repack_q6k_blocks(_ptr(blocks), blocks.numel(), n, k, _ptr(codes),
+                                       codes.numel(), _ptr(scales), scales.numel(),
+                                       _stream(stream)))
+    return PrefillWeight(codes, scales, LAYOUT_Q6K_W64, QUANTIZER_Q6K, n, k, pn, pk)
