@@ -180,6 +180,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-mmq", action="store_true")
+    ap.add_argument("--decode-m", default="1,2,4,8", help="decode token counts to time")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy (counter scale for rocprof --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -191,9 +194,20 @@ def main():
 
     import qw38_amd.ops as ops
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 5 x 1 GiB device-to-device copies done")
+        return
     layout = int(args.layout, 16)
     n, k = 34816, 5120
-    dec, base = bench_decode(torch, ops, n, k, [1, 2, 4, 8], args.steps, args.warmup, layout)
+    ms_list = [int(v) for v in args.decode_m.split(",")]
+    if 1 not in ms_list:
+        ms_list = [1] + ms_list
+    dec, base = bench_decode(torch, ops, n, k, ms_list, args.steps, args.warmup, layout)
     head = dec[1]
     mmq = None if args.no_mmq else bench_mmq(torch, ops, n, k, 512, max(20, args.steps // 8),
                                               max(3, args.warmup // 4), layout)

@@ -36,7 +36,8 @@
  *                         55-59. Pinned: round trip + _ref dequantize equality.
  *   orc_pack_q4k_layout   src/format/pack.cpp:216-262 (0x020D). Pinned: golden
  *                         tile coordinates of tests/pack_layout_test.cpp:197-245
- *                         and lossless round trip.
+ *                         and lossless round trip. 0x0240 (this build's plane
+ *                         order) pinned by round trip + explicit coordinates.
  *   orc_quantize_q6k_*    llama.cpp quantize_row_q6_K_ref / make_qx_quants
  *                         (ggml-quants.c at e6ab7c1a4, not vendored in the
  *                         reference). PARITY UNPINNED: no reference code or
@@ -475,6 +476,30 @@ static inline void nib_map(uint16_t layout, int j, int* lo, int* hi) {
   else { int t = j / 4, i = j % 4; *lo = 8 * t + i; *hi = 8 * t + 4 + i; }
 }
 
+/* Byte offsets of the 16-byte code word of (row, super-block kb, K32 group g)
+ * and of the 16-byte metadata row of (row, kb), for `strips` 8-row strips.
+ * 0x020D: tile row ((row/8)*kbs + kb)*8 + row%8: 128 code bytes (group g at
+ *   g*16) and 16 metadata bytes per tile row.
+ * 0x0240: chunk-major. Super-blocks form chunks of nk <= 8 (only the last is
+ *   short); chunk c of every strip is contiguous, strip after strip. Within
+ *   (chunk, strip) the codes are eight planes of nk*128 B, one per group, with
+ *   16-byte entries ordered (kb%8)*8 + row%8; the metadata is one such plane. */
+static inline uint64_t code_word(uint16_t layout, uint32_t row, uint32_t kb, uint32_t g,
+                                 uint32_t kbs, uint32_t strips) {
+  if (layout == 0x020D) return tile_row(row, kb, kbs) * 128 + g * 16;
+  uint32_t c = kb / 8, kq = kb % 8;
+  uint32_t nk = kbs - 8 * c < 8 ? kbs - 8 * c : 8;
+  return (uint64_t)strips * 8192 * c + (uint64_t)(row / 8) * nk * 1024 +
+         (uint64_t)g * nk * 128 + (kq * 8 + row % 8) * 16;
+}
+static inline uint64_t meta_row(uint16_t layout, uint32_t row, uint32_t kb, uint32_t kbs,
+                                uint32_t strips) {
+  if (layout == 0x020D) return tile_row(row, kb, kbs) * 16;
+  uint32_t c = kb / 8, kq = kb % 8;
+  uint32_t nk = kbs - 8 * c < 8 ? kbs - 8 * c : 8;
+  return (uint64_t)strips * 1024 * c + (uint64_t)(row / 8) * nk * 128 + (kq * 8 + row % 8) * 16;
+}
+
 int orc_pack_q4k_layout(uint16_t layout, const uint8_t* codes, const uint8_t* meta,
                         uint32_t n, uint32_t pk, uint8_t* co, uint8_t* mo) {
   if ((layout != 0x020D && layout != 0x0240) || pk % 256) return 1;
@@ -483,14 +508,14 @@ int orc_pack_q4k_layout(uint16_t layout, const uint8_t* codes, const uint8_t* me
   memset(mo, 0, (size_t)pn * kbs * 16);
   for (uint32_t r = 0; r < n; ++r)
     for (uint32_t kb = 0; kb < kbs; ++kb) {
-      uint64_t tr = tile_row(r, kb, kbs);
-      memcpy(mo + tr * 16, meta + ((size_t)r * kbs + kb) * 16, 16);
+      memcpy(mo + meta_row(layout, r, kb, kbs, pn / 8), meta + ((size_t)r * kbs + kb) * 16, 16);
       const uint8_t* c = codes + (size_t)r * pk + kb * 256;
       for (int g = 0; g < 8; ++g)
         for (int j = 0; j < 16; ++j) {
           int lo, hi;
           nib_map(layout, j, &lo, &hi);
-          co[tr * 128 + g * 16 + j] = (uint8_t)(c[32 * g + lo] | (c[32 * g + hi] << 4));
+          co[code_word(layout, r, kb, g, kbs, pn / 8) + j] =
+              (uint8_t)(c[32 * g + lo] | (c[32 * g + hi] << 4));
         }
     }
   return 0;
@@ -502,14 +527,13 @@ int orc_unpack_q4k_layout(uint16_t layout, const uint8_t* ci, const uint8_t* mi,
   uint32_t kbs = pk / 256;
   for (uint32_t r = 0; r < n; ++r)
     for (uint32_t kb = 0; kb < kbs; ++kb) {
-      uint64_t tr = tile_row(r, kb, kbs);
-      memcpy(meta + ((size_t)r * kbs + kb) * 16, mi + tr * 16, 16);
+      memcpy(meta + ((size_t)r * kbs + kb) * 16, mi + meta_row(layout, r, kb, kbs, pad8(n) / 8), 16);
       uint8_t* c = codes + (size_t)r * pk + kb * 256;
       for (int g = 0; g < 8; ++g)
         for (int j = 0; j < 16; ++j) {
           int lo, hi;
           nib_map(layout, j, &lo, &hi);
-          uint8_t b = ci[tr * 128 + g * 16 + j];
+          uint8_t b = ci[code_word(layout, r, kb, g, kbs, pad8(n) / 8) + j];
           c[32 * g + lo] = b & 15;
           c[32 * g + hi] = b >> 4;
         }

@@ -149,6 +149,11 @@ int valid_weight(const qw38_weight& w, const char* op) {
 uint32_t codes_alignment(const qw38_weight& w) {
   return w.layout == QW38_LAYOUT_Q4K_CANDIDATE_V2 ? 4u : 16u;
 }
+// 0x020D metadata may be only 2-byte aligned (the reference's fp16-backed span);
+// the 0x0240 kernels load 16-byte metadata rows.
+uint32_t scales_alignment(const qw38_weight& w) {
+  return w.layout == QW38_LAYOUT_Q4K_WAVE64 ? 16u : 2u;
+}
 
 WeightView view(const qw38_weight& w) {
   return WeightView{static_cast<const uint8_t*>(w.codes), static_cast<const uint8_t*>(w.scales),
@@ -229,7 +234,7 @@ int qw38_q4k_q8_project(const qw38_weight* weight, const qw38_q8_input* input, f
   int device = 0;
   if (int st = stream_device(stream, &device, op)) return st;
   if (int st = distinct({{w.codes, w.codes_bytes, codes_alignment(w)},
-                         {w.scales, w.scales_bytes, 2},
+                         {w.scales, w.scales_bytes, scales_alignment(w)},
                          {x.codes, x.codes_len, 4},
                          {x.scales, x.scales_len * 4, 4},
                          {x.sums, x.sums_len * 4, 4},
@@ -275,11 +280,11 @@ int qw38_q4k_q8_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_w
   int device = 0;
   if (int st = stream_device(stream, &device, op)) return st;
   if (int st = distinct({{gate->codes, gate->codes_bytes, codes_alignment(*gate)},
-                         {gate->scales, gate->scales_bytes, 2},
+                         {gate->scales, gate->scales_bytes, scales_alignment(*gate)},
                          {up->codes, up->codes_bytes, codes_alignment(*up)},
-                         {up->scales, up->scales_bytes, 2},
+                         {up->scales, up->scales_bytes, scales_alignment(*up)},
                          {down->codes, down->codes_bytes, codes_alignment(*down)},
-                         {down->scales, down->scales_bytes, 2},
+                         {down->scales, down->scales_bytes, scales_alignment(*down)},
                          {residual, uint64_t(m) * 5120 * 4, 4},
                          {gamma, 5120 * 2, 2},
                          {output, uint64_t(m) * 5120 * 4, 4},
@@ -375,7 +380,7 @@ int qw38_q8_group_dots(const qw38_weight* weight, const qw38_q8_input* input, in
   int device = 0;
   if (int st = stream_device(stream, &device, op)) return st;
   if (int st = distinct({{w.codes, w.codes_bytes, codes_alignment(w)},
-                         {w.scales, w.scales_bytes, 2}, {x.codes, x.codes_len, 4},
+                         {w.scales, w.scales_bytes, scales_alignment(w)}, {x.codes, x.codes_len, 4},
                          {dots, dots_len * 4, 4}},
                         device, op))
     return st;

@@ -74,6 +74,52 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t p0, uint32_t p1, uint32_t
   }
 }
 
+// Branch-free (v_bfe + selects) 6-bit scale/min extraction for a lane-varying group g.
+__device__ __forceinline__ void q4_scale_min_lane(uint32_t p0, uint32_t p1, uint32_t p2,
+                                                  uint32_t g, float& s, float& m) {
+  const bool hi = g >= 4;
+  const uint32_t sh = 8u * (g & 3u);
+  const uint32_t width = hi ? 4u : 6u;
+  const uint32_t hmask = hi ? 0x30u : 0u;
+  const uint32_t sl = __builtin_amdgcn_ubfe(hi ? p2 : p0, sh, width);
+  const uint32_t ml = __builtin_amdgcn_ubfe(hi ? p2 : p1, hi ? sh + 4u : sh, width);
+  const uint32_t sh2 = (__builtin_amdgcn_ubfe(p0, sh + 6u, 2u) << 4) & hmask;
+  const uint32_t mh2 = (__builtin_amdgcn_ubfe(p1, sh + 6u, 2u) << 4) & hmask;
+  s = float(sl | sh2);
+  m = float(ml | mh2);
+}
+
+// Byte offsets of the 16-byte code word of (row, super-block kb, K32 group g)
+// and of the 16-byte metadata row of (row, kb).
+// 0x020D: tile row ((row/8)*kbs + kb)*8 + row%8; codes 128 B per tile row
+//   (group g at g*16), metadata 16 B per tile row.
+// 0x0240: chunk-major. Super-blocks are grouped in chunks of nk <= 8 (only the
+//   last chunk is short); chunk c of all strips is contiguous, strip after
+//   strip. Within (chunk, strip) the codes form eight planes of nk*128 B, one
+//   per group, whose 16-byte entries are ordered (kb%8)*8 + row%8, and the
+//   metadata is one such plane. One wave64 load instruction thus reads a whole
+//   plane contiguously, and neighbouring waves (strips) read neighbouring
+//   memory at the same time.
+__host__ __device__ __forceinline__ uint64_t q4k_code_word(uint16_t layout, uint32_t row,
+                                                          uint32_t kb, uint32_t g,
+                                                          uint32_t kbs, uint32_t strips) {
+  if (layout == QW38_LAYOUT_Q4K_CANDIDATE_V2)
+    return ((uint64_t(row / 8) * kbs + kb) * 8 + row % 8) * 128 + g * 16;
+  const uint32_t c = kb / 8, kq = kb % 8;
+  const uint32_t nk = kbs - 8 * c < 8 ? kbs - 8 * c : 8;
+  return uint64_t(strips) * 8192 * c + uint64_t(row / 8) * nk * 1024 + uint64_t(g) * nk * 128 +
+         (kq * 8 + row % 8) * 16;
+}
+__host__ __device__ __forceinline__ uint64_t q4k_meta_row(uint16_t layout, uint32_t row,
+                                                         uint32_t kb, uint32_t kbs,
+                                                         uint32_t strips) {
+  if (layout == QW38_LAYOUT_Q4K_CANDIDATE_V2)
+    return ((uint64_t(row / 8) * kbs + kb) * 8 + row % 8) * 16;
+  const uint32_t c = kb / 8, kq = kb % 8;
+  const uint32_t nk = kbs - 8 * c < 8 ? kbs - 8 * c : 8;
+  return uint64_t(strips) * 1024 * c + uint64_t(row / 8) * nk * 128 + (kq * 8 + row % 8) * 16;
+}
+
 // ---- launchers (defined in the .hip files) ---------------------------------
 hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t pk,
                           int8_t* codes, float* scales, int32_t* sums, int* failure,
@@ -86,6 +132,11 @@ hipError_t launch_swiglu_q8(const float* gate, const float* up, uint32_t m, uint
                             hipStream_t s);
 hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out,
                        const float* residual, hipStream_t s);
+hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,
+                              const float* residual, hipStream_t s, int ws_override,
+                              uint32_t max_blocks);
+hipError_t launch_gemv_w64(const WeightView& w, const Q8View& x, float* out,
+                           const float* residual, hipStream_t s);
 hipError_t launch_mmq(const WeightView& w, const Q8View& x, float* out,
                       const float* residual, hipStream_t s);
 hipError_t launch_group_dots(const WeightView& w, const Q8View& x, int32_t* dots,

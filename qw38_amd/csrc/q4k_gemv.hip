@@ -11,6 +11,8 @@
 //   (|dot| <= 60960); the FP32 affine a*(ds*dot - dm*sum) per (row, token,
 //   group) follows cuda/q4k_q8.cu:97. Per-lane partials are reduced with a
 //   transpose-reduce butterfly, then across the waves that split K.
+#include <cstdlib>
+
 #include "common.hpp"
 
 namespace qw38hip {
@@ -52,21 +54,6 @@ __device__ __forceinline__ void q6_unpack(const uint32_t w[4], const uint32_t h[
     const uint32_t hh = (h[j >> 2] >> (2 * (j & 3))) & 0x03030303u;
     v[j] = nib | (hh << 4);
   }
-}
-
-// Branch-free 6-bit scale/min extraction for a lane-varying group g.
-__device__ __forceinline__ void q4_scale_min_lane(uint32_t p0, uint32_t p1, uint32_t p2,
-                                                  uint32_t g, float& s, float& m) {
-  const bool hi = g >= 4;
-  const uint32_t sh = 8u * (g & 3u);
-  const uint32_t width = hi ? 4u : 6u;
-  const uint32_t hmask = hi ? 0x30u : 0u;
-  const uint32_t sl = __builtin_amdgcn_ubfe(hi ? p2 : p0, sh, width);
-  const uint32_t ml = __builtin_amdgcn_ubfe(hi ? p2 : p1, hi ? sh + 4u : sh, width);
-  const uint32_t sh2 = (__builtin_amdgcn_ubfe(p0, sh + 6u, 2u) << 4) & hmask;
-  const uint32_t mh2 = (__builtin_amdgcn_ubfe(p1, sh + 6u, 2u) << 4) & hmask;
-  s = float(sl | sh2);
-  m = float(ml | mh2);
 }
 
 template <bool Fast>
@@ -273,7 +260,7 @@ __global__ void group_dots_kernel(const uint8_t* __restrict__ codes,
   load_act<false>(xc + size_t(t) * pk + size_t(g_all) * 32, z);
   if constexpr (Layout != QW38_LAYOUT_Q6K_WAVE64) {
     uint32_t w[4];
-    load16<false>(codes + tr * 128 + g * 16, w);
+    load16<false>(codes + q4k_code_word(Layout, r, kb, g, kbs, strips), w);
     q4_unpack<Layout>(w, v);
     dots[idx] = dot32(v, z);
   } else {
@@ -308,6 +295,12 @@ hipError_t gemv_ws(const WeightView& w, const Q8View& x, float* out, const float
   int ws = 1;
   if (strips < 4096 && chunks >= 2) ws = 2;
   if (strips < 2048 && chunks >= 4) ws = 4;
+  // Tuning override for measurement sweeps (1, 2 or 4 waves per strip).
+  static const int ws_env = [] {
+    const char* e = std::getenv("QW38_GEMV_WS");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (ws_env == 1 || ws_env == 2 || ws_env == 4) ws = ws_env;
 #define QW38_GEMV_LAUNCH(WSV)                                                               \
   hipLaunchKernelGGL((gemv_kernel<Layout, MT, Fast, WSV>),                                 \
                      dim3((strips + (4 / WSV) - 1) / (4 / WSV)), dim3(256), 0, s, w.codes, \
@@ -340,6 +333,24 @@ hipError_t gemv_m(const WeightView& w, const Q8View& x, float* out, const float*
 
 hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out, const float* residual,
                        hipStream_t s) {
+  // Tuning knobs for measurement sweeps: QW38_GEMV_STREAM=0 disables the
+  // linear-streaming kernel; QW38_GEMV_STREAM_WS / _BLOCKS override its shape.
+  static const int env_stream = [] {
+    const char* e = std::getenv("QW38_GEMV_STREAM");
+    return e ? std::atoi(e) : 1;
+  }();
+  static const int env_ws = [] {
+    const char* e = std::getenv("QW38_GEMV_STREAM_WS");
+    return e ? std::atoi(e) : 0;
+  }();
+  static const int env_blocks = [] {
+    const char* e = std::getenv("QW38_GEMV_STREAM_BLOCKS");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (env_stream) {
+    const hipError_t e = launch_gemv_stream(w, x, out, residual, s, env_ws, uint32_t(env_blocks));
+    if (e != hipErrorNotSupported) return e;
+  }
   const bool fast = (reinterpret_cast<uintptr_t>(w.codes) % 16 == 0) &&
                     (reinterpret_cast<uintptr_t>(w.scales) % 16 == 0) &&
                     (reinterpret_cast<uintptr_t>(x.codes) % 16 == 0);
@@ -348,8 +359,7 @@ hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out, const f
       return fast ? gemv_m<QW38_LAYOUT_Q4K_CANDIDATE_V2, true>(w, x, out, residual, s)
                   : gemv_m<QW38_LAYOUT_Q4K_CANDIDATE_V2, false>(w, x, out, residual, s);
     case QW38_LAYOUT_Q4K_WAVE64:
-      return fast ? gemv_m<QW38_LAYOUT_Q4K_WAVE64, true>(w, x, out, residual, s)
-                  : gemv_m<QW38_LAYOUT_Q4K_WAVE64, false>(w, x, out, residual, s);
+      return launch_gemv_w64(w, x, out, residual, s);
     case QW38_LAYOUT_Q6K_WAVE64:
       // Q6_K layout requires 16-byte aligned codes (validated by the caller).
       return (reinterpret_cast<uintptr_t>(x.codes) % 16 == 0)

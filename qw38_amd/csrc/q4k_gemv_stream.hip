@@ -1,0 +1,312 @@
+// Linear-streaming Q4_K GEMV for M = 1..2 tokens (the decode hot path).
+//
+// In the 8-row x K256 tiling an 8-row strip's codes are contiguous (kbs x
+// 1 KB) and so is its metadata (kbs x 128 B in the scales span). One wave
+// streams one strip two tiles at a time: lane l owns 32 contiguous code bytes
+// at l*32 of the tile pair -- tile h = l/32, row r = (l%32)/4, K32 groups
+// 2j, 2j+1 with j = l%4 -- so the wave's two 16 B loads read 2 KB with no
+// gaps. One 4 B/lane load reads the pair's 256 B of metadata; the four dwords
+// of (row r, tile h) land exactly in lane l's quad, so DPP quad broadcasts
+// hand them over without LDS traffic. Loads run two tile pairs ahead.
+//
+// The Q8 activations are staged once per block in LDS as codes plus
+// (a, a*sum) pairs. Per (row, token, super-block) the affine is factored as
+//   acc += d * sum_g (a_g s_g) dot_g - dmin * sum_g (a_g sum_g) m_g,
+// the reference's sum_g a_g (d s_g dot_g - dmin m_g sum_g)
+// (cuda/q4k_q8.cu:97) reassociated, with exact int32 K32 dots from
+// v_dot4_i32_i8. Row partials are summed over the row's 8 lanes (xor 1, 2, 32)
+// and, when WS waves split K, across those waves in LDS in a fixed order.
+// Unaligned (4-byte) code / activation spans and 2-byte metadata spans use
+// narrower loads with identical arithmetic, so results are bitwise equal.
+#include "common.hpp"
+
+namespace qw38hip {
+namespace {
+
+template <uint16_t Layout>
+__device__ __forceinline__ void unpack8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                        uint32_t v[8]) {
+  const uint32_t ws[4] = {w0, w1, w2, w3};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t lo = ws[t] & 0x0f0f0f0fu;
+    const uint32_t hi = (ws[t] >> 4) & 0x0f0f0f0fu;
+    if constexpr (Layout == QW38_LAYOUT_Q4K_WAVE64) {
+      v[2 * t] = lo;
+      v[2 * t + 1] = hi;
+    } else {
+      v[2 * t] = perm(hi, lo, 0x05010400u);
+      v[2 * t + 1] = perm(hi, lo, 0x07030602u);
+    }
+  }
+}
+
+// DPP quad broadcast of lane (quad base + J).
+template <int J>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+  constexpr int ctrl = J | (J << 2) | (J << 4) | (J << 6);  // quad_perm:[J,J,J,J]
+  return uint32_t(__builtin_amdgcn_mov_dpp(int(v), ctrl, 0xf, 0xf, false));
+}
+
+struct Tile {
+  uint32_t c[8];  // 32 code bytes of this lane
+  uint32_t m;     // one metadata dword of the tile pair
+};
+
+template <bool Fast>
+__device__ __forceinline__ void load_tile(const uint8_t* cbase, const uint8_t* mbase,
+                                          uint32_t coff, uint32_t moff, Tile& t) {
+  if constexpr (Fast) {
+    const uint4 a = *reinterpret_cast<const uint4*>(cbase + coff);
+    const uint4 b = *reinterpret_cast<const uint4*>(cbase + coff + 16);
+    t.c[0] = a.x; t.c[1] = a.y; t.c[2] = a.z; t.c[3] = a.w;
+    t.c[4] = b.x; t.c[5] = b.y; t.c[6] = b.z; t.c[7] = b.w;
+    t.m = *reinterpret_cast<const uint32_t*>(mbase + moff);
+  } else {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(cbase + coff);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t.c[i] = q[i];
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(mbase + moff);
+    t.m = uint32_t(h[0]) | (uint32_t(h[1]) << 16);
+  }
+}
+
+// 6-bit scale s and min m of groups g0 = 2j and g0 + 1 (j = lane % 4) from
+// packed words p0 = bytes 4..7, p1 = 8..11, p2 = 12..15 (get_scale_min_k4,
+// third_party/llama.cpp-q4k/reference.hpp:174-181), branch-free in j.
+__device__ __forceinline__ void scale_min_pair(uint32_t p0, uint32_t p1, uint32_t p2, bool hi,
+                                               uint32_t sh, float s[2], float m[2]) {
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const uint32_t o = sh + 8u * e;  // byte offset of group g0+e (mod 4) in bits
+    const uint32_t sl = __builtin_amdgcn_ubfe(hi ? p2 : p0, o, hi ? 4u : 6u);
+    const uint32_t ml = __builtin_amdgcn_ubfe(hi ? p2 : p1, hi ? o + 4u : o, hi ? 4u : 6u);
+    const uint32_t sh2 = hi ? __builtin_amdgcn_ubfe(p0, o + 6u, 2u) << 4 : 0u;
+    const uint32_t mh2 = hi ? __builtin_amdgcn_ubfe(p1, o + 6u, 2u) << 4 : 0u;
+    s[e] = float(sl | sh2);
+    m[e] = float(ml | mh2);
+  }
+}
+
+template <uint16_t Layout, int MT, bool Fast>
+__device__ __forceinline__ void consume(const Tile& t, uint32_t kb, uint32_t g0, bool hi,
+                                        uint32_t sh, const int8_t* sz, const float2* sau,
+                                        uint32_t groups, float acc[MT]) {
+  const uint32_t dd = quad_bcast<0>(t.m), p0 = quad_bcast<1>(t.m), p1 = quad_bcast<2>(t.m),
+                 p2 = quad_bcast<3>(t.m);
+  float s[2], m[2];
+  scale_min_pair(p0, p1, p2, hi, sh, s, m);
+  const float d = f16_to_f32(dd & 0xffffu), dmin = f16_to_f32(dd >> 16);
+  uint32_t v[2][8];
+  unpack8<Layout>(t.c[0], t.c[1], t.c[2], t.c[3], v[0]);
+  unpack8<Layout>(t.c[4], t.c[5], t.c[6], t.c[7], v[1]);
+#pragma unroll
+  for (int tk = 0; tk < MT; ++tk) {
+    const uint32_t gi = tk * groups + kb * 8 + g0;
+    const uint4* zp = reinterpret_cast<const uint4*>(sz + size_t(gi) * 32);
+    const float4 au = *reinterpret_cast<const float4*>(sau + gi);  // (a0, u0, a1, u1)
+    float X = 0.f, Y = 0.f;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint4 za = zp[2 * e], zb = zp[2 * e + 1];
+      int dot = 0;
+      dot = dot4(v[e][0], za.x, dot);
+      dot = dot4(v[e][1], za.y, dot);
+      dot = dot4(v[e][2], za.z, dot);
+      dot = dot4(v[e][3], za.w, dot);
+      dot = dot4(v[e][4], zb.x, dot);
+      dot = dot4(v[e][5], zb.y, dot);
+      dot = dot4(v[e][6], zb.z, dot);
+      dot = dot4(v[e][7], zb.w, dot);
+      const float a = e ? au.z : au.x, u = e ? au.w : au.y;
+      X = fmaf(a * s[e], float(dot), X);
+      Y = fmaf(u, m[e], Y);
+    }
+    acc[tk] = fmaf(-dmin, Y, fmaf(d, X, acc[tk]));
+  }
+}
+
+template <uint16_t Layout, int MT, bool Fast, int WS>
+__global__ __launch_bounds__(256) void gemv_stream_kernel(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n,
+    uint32_t strips, uint32_t kbs, const int8_t* __restrict__ xc,
+    const float* __restrict__ xa, const int32_t* __restrict__ xs, uint32_t pk,
+    float* __restrict__ out, const float* __restrict__ residual, uint32_t persistent) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int SPB = 4 / WS;
+  const uint32_t groups = pk / 32;
+  int8_t* sz = reinterpret_cast<int8_t*>(smem);
+  float2* sau = reinterpret_cast<float2*>(smem + MT * pk);
+  float* red = reinterpret_cast<float*>(smem + MT * pk + MT * groups * 8);
+
+  // ---- stage the Q8 activations once per block: codes and (a, a*sum) ----
+  if constexpr (Fast) {
+    const uint4* src = reinterpret_cast<const uint4*>(xc);
+    uint4* dst = reinterpret_cast<uint4*>(sz);
+    for (uint32_t i = threadIdx.x; i < MT * pk / 16; i += 256) dst[i] = src[i];
+  } else {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(xc);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(sz);
+    for (uint32_t i = threadIdx.x; i < MT * pk / 4; i += 256) dst[i] = src[i];
+  }
+  for (uint32_t i = threadIdx.x; i < MT * groups; i += 256) {
+    const float a = xa[i];
+    sau[i] = make_float2(a, a * float(xs[i]));
+  }
+  __syncthreads();
+
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t h = lane >> 5;              // tile of the pair
+  const uint32_t r = (lane >> 2) & 7u;       // row in the strip
+  const uint32_t j = lane & 3u;              // group pair 2j, 2j+1
+  const uint32_t g0 = 2 * j;
+  const bool hi = j >= 2;
+  const uint32_t sh = 16u * (j & 1u);        // bit offset of group g0 % 4
+  const uint32_t ks = wave % WS;
+  const uint32_t pairs = kbs / 2;            // full tile pairs; an odd tail tile follows
+  const uint32_t q0 = uint32_t(uint64_t(pairs) * ks / WS);
+  const uint32_t q1 = uint32_t(uint64_t(pairs) * (ks + 1) / WS);
+  const bool tail = (kbs & 1u) && ks == WS - 1;
+  const uint32_t coff = lane * 32, moff = lane * 4;
+
+  const uint32_t stride = persistent ? gridDim.x * SPB : SPB * gridDim.x + strips;
+  // WS > 1 blocks run exactly one strip group and synchronise after it.
+  for (uint32_t strip = blockIdx.x * SPB + wave / WS; WS > 1 || strip < strips; strip += stride) {
+    const bool live = strip < strips;
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = 0.f;
+    if (live) {
+      const uint8_t* cstrip = codes + size_t(strip) * kbs * 1024;
+      const uint8_t* mstrip = meta + size_t(strip) * kbs * 128;
+      // Batches of kBatch tile pairs: every load of a batch is issued before the
+      // first is consumed, so up to kBatch * 2 KB per wave is in flight.
+      constexpr uint32_t kBatch = 4;
+      uint32_t q = q0;
+      for (; q + kBatch <= q1; q += kBatch) {
+        Tile T[kBatch];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u)
+          load_tile<Fast>(cstrip + size_t(q + u) * 2048, mstrip + size_t(q + u) * 256, coff,
+                          moff, T[u]);
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u)
+          consume<Layout, MT, Fast>(T[u], 2 * (q + u) + h, g0, hi, sh, sz, sau, groups, acc);
+      }
+      for (; q < q1; ++q) {
+        Tile T;
+        load_tile<Fast>(cstrip + size_t(q) * 2048, mstrip + size_t(q) * 256, coff, moff, T);
+        consume<Layout, MT, Fast>(T, 2 * q + h, g0, hi, sh, sz, sau, groups, acc);
+      }
+      if (tail) {  // odd last tile: only lanes of tile 0 hold data
+        const uint32_t kb = kbs - 1;
+        Tile T;
+        if (h == 0) {
+          load_tile<Fast>(cstrip + size_t(kb) * 1024, mstrip + size_t(kb) * 128, coff, moff, T);
+        } else {
+          for (int i = 0; i < 8; ++i) T.c[i] = 0;
+          T.m = 0;
+        }
+        float part[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) part[t] = 0.f;
+        consume<Layout, MT, Fast>(T, h == 0 ? kb : 0, g0, hi, sh, sz, sau, groups, part);
+        if (h == 0) {
+#pragma unroll
+          for (int t = 0; t < MT; ++t) acc[t] += part[t];
+        }
+      }
+    }
+    // a row's partials live in lanes {4r..4r+3} and {32+4r..32+4r+3}
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      acc[t] += __shfl_xor(acc[t], 1);
+      acc[t] += __shfl_xor(acc[t], 2);
+      acc[t] += __shfl_xor(acc[t], 32);
+    }
+    const uint32_t row = strip * 8 + r;
+    const bool writer = (lane & 35u) == 0;
+    if constexpr (WS == 1) {
+      if (writer && row < n) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const size_t i = size_t(t) * n + row;
+          out[i] = acc[t] + (residual ? residual[i] : 0.f);
+        }
+      }
+    } else {
+      if (writer) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) red[(wave * MT + t) * 8 + r] = acc[t];
+      }
+      __syncthreads();
+      if (live && ks == 0 && writer && row < n) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          float total = 0.f;
+#pragma unroll
+          for (int q = 0; q < WS; ++q) total += red[((wave + q) * MT + t) * 8 + r];
+          const size_t i = size_t(t) * n + row;
+          out[i] = total + (residual ? residual[i] : 0.f);
+        }
+      }
+      break;
+    }
+  }
+}
+
+template <uint16_t Layout, int MT, bool Fast>
+hipError_t stream_ws(const WeightView& w, const Q8View& x, float* out, const float* residual,
+                     hipStream_t s, int ws, uint32_t max_blocks) {
+  const uint32_t strips = w.pn / 8, kbs = w.pk / 256;
+  const uint32_t groups = w.pk / 32;
+  const size_t lds = size_t(MT) * w.pk + size_t(MT) * groups * 8 + 4 * MT * 8 * 4;
+#define QW38_STREAM_LAUNCH(WSV)                                                          \
+  do {                                                                                   \
+    const uint32_t need = (strips + (4 / WSV) - 1) / (4 / WSV);                          \
+    const uint32_t persistent = (WSV == 1 && need > max_blocks) ? 1u : 0u;               \
+    const uint32_t grid = persistent ? max_blocks : need;                                \
+    hipLaunchKernelGGL((gemv_stream_kernel<Layout, MT, Fast, WSV>), dim3(grid), dim3(256), \
+                       lds, s, w.codes, w.scales, w.n, strips, kbs, x.codes, x.scales,   \
+                       x.sums, x.pk, out, residual, persistent);                         \
+  } while (0)
+  if (ws == 4) QW38_STREAM_LAUNCH(4);
+  else if (ws == 2) QW38_STREAM_LAUNCH(2);
+  else QW38_STREAM_LAUNCH(1);
+#undef QW38_STREAM_LAUNCH
+  return hipGetLastError();
+}
+
+template <uint16_t Layout, bool Fast>
+hipError_t stream_m(const WeightView& w, const Q8View& x, float* out, const float* residual,
+                    hipStream_t s, int ws, uint32_t max_blocks) {
+  return x.m == 1 ? stream_ws<Layout, 1, Fast>(w, x, out, residual, s, ws, max_blocks)
+                  : stream_ws<Layout, 2, Fast>(w, x, out, residual, s, ws, max_blocks);
+}
+
+}  // namespace
+
+// Returns hipErrorNotSupported when this path does not apply (caller falls back).
+hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,
+                              const float* residual, hipStream_t s, int ws_override,
+                              uint32_t max_blocks) {
+  if (x.m > 2 || w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2) return hipErrorNotSupported;
+  const size_t lds = size_t(x.m) * w.pk * 5 / 4 + 4 * x.m * 8 * 4;
+  if (lds > 56 * 1024) return hipErrorNotSupported;
+  const bool fast = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(x.codes)) %
+                         16 == 0) &&
+                    reinterpret_cast<uintptr_t>(w.scales) % 4 == 0;
+  const uint32_t strips = w.pn / 8, kbs = w.pk / 256;
+  int ws = 1;
+  if (strips < 3072 && kbs >= 8) ws = 2;
+  if (strips < 1536 && kbs >= 16) ws = 4;
+  if (ws_override == 1 || ws_override == 2 || ws_override == 4) ws = ws_override;
+  if (max_blocks == 0) max_blocks = 2048;
+  if (w.layout == QW38_LAYOUT_Q4K_CANDIDATE_V2)
+    return fast ? stream_m<QW38_LAYOUT_Q4K_CANDIDATE_V2, true>(w, x, out, residual, s, ws, max_blocks)
+                : stream_m<QW38_LAYOUT_Q4K_CANDIDATE_V2, false>(w, x, out, residual, s, ws, max_blocks);
+  return fast ? stream_m<QW38_LAYOUT_Q4K_WAVE64, true>(w, x, out, residual, s, ws, max_blocks)
+              : stream_m<QW38_LAYOUT_Q4K_WAVE64, false>(w, x, out, residual, s, ws, max_blocks);
+}
+
+}  // namespace qw38hip

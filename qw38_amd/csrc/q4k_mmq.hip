@@ -104,10 +104,12 @@ __global__ __launch_bounds__(256) void mmq_kernel(
         const uint64_t tr = (uint64_t(row / 8) * kbs + kb) * 8 + row % 8;
         uint32_t v[8];
         if constexpr (!kQ6) {
-          const uint32_t* cp = reinterpret_cast<const uint32_t*>(codes + tr * 128 + g * 16);
+          const uint32_t* cp =
+              reinterpret_cast<const uint32_t*>(codes + q4k_code_word(Layout, row, kb, g, kbs, pn / 8));
           uint32_t w[4] = {cp[0], cp[1], cp[2], cp[3]};
           unpack32<Layout>(w, v);
-          const uint16_t* mp = reinterpret_cast<const uint16_t*>(meta + tr * 16);
+          const uint16_t* mp =
+              reinterpret_cast<const uint16_t*>(meta + q4k_meta_row(Layout, row, kb, kbs, pn / 8));
           uint32_t mw[8];
 #pragma unroll
           for (int i = 0; i < 8; ++i) mw[i] = mp[i];

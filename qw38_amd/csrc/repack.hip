@@ -35,9 +35,10 @@ __global__ void repack_q4k_kernel(const uint8_t* __restrict__ blocks, uint32_t n
       lo = 8 * (j / 4) + (j % 4);
       hi = lo + 4;
     }
-    codes[tr * 128 + byte] = uint8_t(q4_code(blk, 32 * g + lo) | (q4_code(blk, 32 * g + hi) << 4));
+    codes[q4k_code_word(layout, row, kb, g, kbs, (n + 7) / 8) + j] =
+        uint8_t(q4_code(blk, 32 * g + lo) | (q4_code(blk, 32 * g + hi) << 4));
   }
-  if (lane < 16) meta[tr * 16 + lane] = blk[lane];
+  if (lane < 16) meta[q4k_meta_row(layout, row, kb, kbs, (n + 7) / 8) + lane] = blk[lane];
 }
 
 // GGML block_q6_K: ql[128], qh[64], scales[16], d (fp16 at byte 208).

@@ -1,0 +1,90 @@
+"""Summarise a rocprofv3 SQLite output (``*_results.db``) as short text.
+
+    python -m qw38_amd.rocprof_summary <results.db> [--match SUBSTR] [--top N]
+
+Prints, per kernel: dispatch count and average / min / max duration (us), and,
+when the run collected ``--pmc`` counters, the per-dispatch average of every
+counter. Used to turn rocprofv3 runs into the text summaries under profiles/.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import re
+import sqlite3
+import sys
+
+
+def _short(name: str) -> str:
+    name = re.sub(r"\s+", " ", name)
+    m = re.search(r"(\w+)<", name)
+    base = name
+    if "qw38hip" in name:
+        m2 = re.search(r"qw38hip::(?:\(anonymous namespace\)::)?(\w+)(<[^()]*>)?", name)
+        if m2:
+            base = m2.group(1) + (m2.group(2) or "")
+    elif m:
+        base = name[:120]
+    return base[:140]
+
+
+def summarize(path: str, match: str | None = None, top: int = 12) -> str:
+    db = sqlite3.connect(path)
+    names = [r[0] for r in db.execute("select name from sqlite_master where type in ('table','view')")]
+    out = []
+    # kernel durations
+    rows = db.execute("select id, name, start, end from kernels").fetchall()
+    by = collections.defaultdict(list)
+    ids = {}
+    for kid, name, s, e in rows:
+        if match and match not in name:
+            continue
+        by[name].append((e - s) / 1e3)
+        ids.setdefault(name, []).append(kid)
+    tot = sum(sum(v) for v in by.values()) or 1.0
+    out.append(f"{'kernel':<72} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'time%':>6}")
+    for name, v in sorted(by.items(), key=lambda kv: -sum(kv[1]))[:top]:
+        out.append(f"{_short(name):<72} {len(v):>6} {sum(v)/len(v):>9.3f} {min(v):>9.3f} "
+                   f"{max(v):>9.3f} {100*sum(v)/tot:>6.1f}")
+    # counters, when present
+    if "counters_collection" in names:
+        cols = [r[1] for r in db.execute("pragma table_info(counters_collection)")]
+        kcol = "kernel_name" if "kernel_name" in cols else None
+        vcol = "value" if "value" in cols else "counter_value"
+        ncol = "counter_name" if "counter_name" in cols else "name"
+        if kcol:
+            q = f"select {kcol}, {ncol}, avg({vcol}), count(*) from (select {kcol}, {ncol}, dispatch_id, sum({vcol}) as {vcol} from counters_collection group by {kcol}, {ncol}, dispatch_id) group by {kcol}, {ncol}"
+            agg = collections.defaultdict(dict)
+            for kname, cname, avg, cnt in db.execute(q):
+                if match and match not in kname:
+                    continue
+                agg[kname][cname] = (avg, cnt)
+            if agg:
+                out.append("")
+                out.append("per-dispatch counter averages:")
+                for kname, cs in sorted(agg.items(), key=lambda kv: kv[0]):
+                    vals = "  ".join(f"{c}={a:.6g}" for c, (a, _) in sorted(cs.items()))
+                    n = max(c for _, c in cs.values())
+                    out.append(f"  {_short(kname)} (dispatches={n}): {vals}")
+    return "\n".join(out)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("db")
+    ap.add_argument("--match")
+    ap.add_argument("--top", type=int, default=12)
+    ap.add_argument("--schema", action="store_true")
+    a = ap.parse_args(argv)
+    if a.schema:
+        db = sqlite3.connect(a.db)
+        for (t,) in db.execute("select name from sqlite_master where type in ('table','view')"):
+            cols = [r[1] for r in db.execute(f"pragma table_info('{t}')")]
+            print(t, cols)
+        return 0
+    print(summarize(a.db, a.match, a.top))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
