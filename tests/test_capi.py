@@ -1,0 +1,94 @@
+"""C-ABI surface on the CPU: the library loads, exports every symbol the header
+declares, sizes agree with the layout definitions, and contract violations are
+rejected before any device work (no GPU needed for those paths)."""
+import ctypes as C
+import re
+
+import pytest
+
+import qw38_amd
+from qw38_amd import _lib
+
+
+def test_library_exports_every_header_symbol():
+    L = qw38_amd.lib()
+    syms = _lib.header_symbols()
+    assert len(syms) >= 18
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+    # and the ctypes binding covers exactly the header
+    assert set(_lib.SIGNATURES) == set(syms)
+
+
+def test_header_is_plain_c():
+    text = open(_lib.HEADER).read()
+    assert 'extern "C"' in text
+    code = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    code = re.sub(r"//[^\n]*", "", code)
+    for bad in ("torch", "std::", "hip_runtime", "namespace", "template", "class "):
+        assert bad not in code
+
+
+def test_layout_sizes():
+    L = qw38_amd.lib()
+    assert L.qw38_code_bytes(0x020D, 5120, 5120) == 5120 * 5120 // 2
+    assert L.qw38_scale_bytes(0x020D, 5120, 5120) == 5120 * 20 * 16
+    assert L.qw38_code_bytes(0x0240, 34816, 5120) == 34816 * 5120 // 2
+    assert L.qw38_code_bytes(0x0241, 5120, 17408) == 5120 * 68 * 192
+    assert L.qw38_scale_bytes(0x0241, 5120, 17408) == 5120 * 68 * 18
+    assert L.qw38_code_bytes(0x0123, 8, 256) == 0
+    # Q4_K: 144 B per 256 weights; Q6_K: 210 B per 256 weights
+    assert (L.qw38_code_bytes(0x0240, 8, 256) + L.qw38_scale_bytes(0x0240, 8, 256)) == 8 * 144
+    assert (L.qw38_code_bytes(0x0241, 8, 256) + L.qw38_scale_bytes(0x0241, 8, 256)) == 8 * 210
+    # workspace formula of cuda/q4k_q8.hpp:28-30
+    for m in (1, 7, 512):
+        assert L.qw38_q8_mlp_workspace_bytes(m) == m * (17408 + 17408 // 32 * 8 + 2 * 17408 * 4) + 4
+
+
+def _q8(m, k, pk, n_codes=None):
+    return _lib.Q8Input(0x1000, m * pk if n_codes is None else n_codes, 0x2000, m * pk // 32,
+                        0x3000, m * pk // 32, m, k, pk)
+
+
+def test_prelaunch_rejections_without_device():
+    L = qw38_amd.lib()
+    q = _q8(3, 259, 512)
+    bad_pk = _q8(3, 259, 256)
+    flag = C.c_int(0)
+    assert L.qw38_pack_q8(None, 3 * 259, C.byref(bad_pk), C.addressof(flag), 1, None) == 2
+    assert L.qw38_pack_q8(None, 3 * 258, C.byref(q), C.addressof(flag), 1, None) == 2
+    assert L.qw38_pack_q8(None, 3 * 259, C.byref(q), C.addressof(flag), 2, None) == 2
+    err = _lib.last_error()
+    assert err.status == 2 and err.operation == "q8.pack" and "geometry" in err.detail
+    w = _lib.Weight(0x4000, 0x5000, 0x020D, 0x0105, 137, 259, 144, 512, 144 * 256, 144 * 2 * 16 - 1)
+    assert L.qw38_q4k_q8_project(C.byref(w), C.byref(q), 0x6000, 3 * 137, None, 0, None) == 2
+    assert _lib.last_error().operation == "q8.weight"
+    w.scales_bytes += 1
+    w.quantizer = 0x0140  # Q6_K quantizer with a Q4_K layout
+    assert L.qw38_q4k_q8_project(C.byref(w), C.byref(q), 0x6000, 3 * 137, None, 0, None) == 2
+    w.quantizer = 0x0105
+    assert L.qw38_q4k_q8_project(C.byref(w), C.byref(q), 0x6000, 3 * 138, None, 0, None) == 2
+    assert L.qw38_q4k_q8_project(C.byref(w), C.byref(q), 0x6000, 3 * 137, 0x7000, 1, None) == 2
+    too_many = _q8(4097, 256, 256)
+    w2 = _lib.Weight(0x4000, 0x5000, 0x020D, 0x0105, 8, 256, 8, 256, 8 * 128, 8 * 16)
+    assert L.qw38_q4k_q8_project(C.byref(w2), C.byref(too_many), 0x6000, 4097 * 8, None, 0, None) == 2
+    sub = C.c_int(7)
+    g = _lib.Weight(0x4000, 0x5000, 0x020D, 0x0105, 17408, 5120, 17408, 5120, 0, 0)
+    # pending_failure supplied: internal submission skips the capture query
+    assert L.qw38_q4k_q8_mlp(C.byref(g), C.byref(g), C.byref(g), None, None, 1e-6, None, 0,
+                             None, 0, None, C.byref(sub), C.addressof(flag)) == 2
+    assert sub.value == 0, "submitted stays false on prelaunch rejection"
+    assert L.qw38_hidden_rms_q8(None, None, float("nan"), 1, None, None, None, None, None) == 2
+    assert L.qw38_swiglu_q8(None, None, 1, 300, None, None, None, None, None) == 2
+
+
+def test_no_cpu_fallback_symbols():
+    """The product library has no host compute path: no exported symbol names a
+    CPU/host implementation of the contraction."""
+    L = qw38_amd.lib()
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True).stdout
+    exported = re.findall(r" T (qw38_\w+)", out)
+    assert exported and all(not re.search(r"cpu|host|oracle", s) for s in exported)
+    assert "orc_" not in out

@@ -1,0 +1,147 @@
+"""GPU parity at the BASELINE.json configurations (configs 1-4) plus the Q6_K
+path, against the oracle on the same inputs. Weights are fitted on the GPU by
+the library (bit-exactness of that fitter is tested separately) and handed to
+the oracle as the same GGML bytes. Tolerance (north star): max|y-ref| <=
+1e-3*rms(ref) and mean|y-ref|/mean|ref| <= 1e-5, ref in float64."""
+import numpy as np
+import pytest
+
+import oracle
+from _fix import normal, outlier_rows, random_q6k, silu_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _fit_q4k(torch, ops, n, k, seed, layout):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn(n, k, generator=g, device="cuda") * 0.02
+    fail = torch.zeros(1, dtype=torch.int32, device="cuda")
+    blocks = ops.quantize_q4k_blocks(x, n, k, fail)
+    w = ops.upload_q4k_blocks(blocks, n, k, layout=layout)
+    torch.cuda.synchronize()
+    assert int(fail.item()) == 0
+    return w, oracle.Q4K.from_ggml(blocks.cpu().numpy(), n, k)
+
+
+def _fit_q6k(torch, ops, n, k, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn(n, k, generator=g, device="cuda") * 0.02
+    blocks = ops.quantize_q6k_blocks(x, n, k)
+    w = ops.upload_q6k_blocks(blocks, n, k)
+    torch.cuda.synchronize()
+    return w, oracle.Q6K.from_ggml(blocks.cpu().numpy(), n, k)
+
+
+def _q8(torch, ops, x_f32):
+    m, k = x_f32.shape
+    bf = oracle.fp32_to_bf16(x_f32)
+    q = ops.Q8Input.empty(m, k)
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ops.pack_q8(_dev(torch, bf.view(np.int16)), q, flag)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 0
+    ob = oracle.pack_q8(bf, m, k)
+    assert np.array_equal(q.codes.cpu().numpy(), ob.codes)
+    return q, ob
+
+
+def _project(torch, ops, w, q, m, n):
+    out = torch.full((m, n), float("nan"), device="cuda")
+    ops.q4k_q8_project(w, q, out)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _check(y, ref, label):
+    ok, ma, mr = oracle.parity_ok(y, ref)
+    print(f"{label}: max_abs/rms={ma:.3g} mean_rel={mr:.3g}", flush=True)
+    assert ok, f"{label}: max_abs/rms={ma:.3g} mean_rel={mr:.3g}"
+
+
+@pytest.mark.parametrize("layout", [oracle.LAYOUT_Q4K_SEQ, oracle.LAYOUT_Q4K_W64], ids=["020D", "0240"])
+def test_config1_gemv_5120(torch_gpu, layout):
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n = k = 5120
+    w, wl = _fit_q4k(torch, ops, n, k, 101, layout)
+    q, ob = _q8(torch, ops, normal((1, k), 102))
+    y = _project(torch, ops, w, q, 1, n)
+    ref, _, _ = oracle.q4k_q8_contract(wl, ob)
+    _check(y, ref, f"config1 layout={layout:#x}")
+
+
+@pytest.mark.parametrize("layout", [oracle.LAYOUT_Q4K_SEQ, oracle.LAYOUT_Q4K_W64], ids=["020D", "0240"])
+def test_config2_fused_gate_up(torch_gpu, layout):
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 34816, 5120
+    w, wl = _fit_q4k(torch, ops, n, k, 201, layout)
+    for m in (1, 2, 4, 8):
+        q, ob = _q8(torch, ops, outlier_rows(m, k, 202 + m))
+        y = _project(torch, ops, w, q, m, n)
+        ref, _, _ = oracle.q4k_q8_contract(wl, ob)
+        _check(y, ref, f"config2 layout={layout:#x} M={m}")
+
+
+def test_config3_q6k_down(torch_gpu):
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 5120, 17408
+    w, wl = _fit_q6k(torch, ops, n, k, 301)
+    for m in (1, 8, 40):
+        q, ob = _q8(torch, ops, silu_rows(m, k, 302 + m))
+        y = _project(torch, ops, w, q, m, n)
+        ref, _, _ = oracle.q6k_q8_contract(wl, ob)
+        _check(y, ref, f"config3 Q6_K M={m}")
+
+
+def test_q6k_small_shapes_and_dots(torch_gpu):
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    for (n, k) in [(37, 512), (64, 1024), (8, 256)]:
+        wl = random_q6k(n, k, n + k)
+        co, mo = wl.physical()
+        w = ops.PrefillWeight.from_bytes(co, mo, oracle.LAYOUT_Q6K_W64, n, k)
+        for m in (1, 3, 8, 9, 33, 130):
+            q, ob = _q8(torch, ops, normal((m, k), m + 7))
+            y = _project(torch, ops, w, q, m, n)
+            ref, _, dots = oracle.q6k_q8_contract(wl, ob, want_dots=True)
+            _check(y, ref, f"Q6_K n={n} k={k} M={m}")
+            if m in (3, 33):
+                d = torch.zeros(m * n * (k // 32), dtype=torch.int32, device="cuda")
+                ops.group_dots(w, q, d)
+                torch.cuda.synchronize()
+                assert np.array_equal(d.cpu().numpy().reshape(dots.shape), dots)
+
+
+@pytest.mark.parametrize("n,k,m", [(12288, 5120, 128), (34816, 5120, 512), (12288, 5120, 2048)])
+def test_config4_mmq_row_sample(torch_gpu, n, k, m):
+    """MMQ at the config-4 shapes; the oracle checks a seeded sample of 512 rows."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    w, wl = _fit_q4k(torch, ops, n, k, 401 + m, oracle.LAYOUT_Q4K_W64)
+    q, ob = _q8(torch, ops, normal((m, k), 402 + m))
+    y = _project(torch, ops, w, q, m, n)
+    rows = np.sort(np.random.Generator(np.random.PCG64(m)).choice(n, 512, replace=False))
+    sub = oracle.Q4K(wl.codes[rows], wl.meta[rows], len(rows), k)
+    ref, _, _ = oracle.q4k_q8_contract(sub, ob)
+    _check(y[:, rows], ref, f"config4 N={n} M={m}")
+
+
+def test_config4_q6k_mmq_row_sample(torch_gpu):
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k, m = 5120, 17408, 512
+    w, wl = _fit_q6k(torch, ops, n, k, 501)
+    q, ob = _q8(torch, ops, silu_rows(m, k, 502))
+    y = _project(torch, ops, w, q, m, n)
+    rows = np.sort(np.random.Generator(np.random.PCG64(5)).choice(n, 256, replace=False))
+    sub = oracle.Q6K(wl.q[rows], wl.sc[rows], wl.d[rows], len(rows), k)
+    ref, _, _ = oracle.q6k_q8_contract(sub, ob)
+    _check(y[:, rows], ref, "config4 Q6_K M=512")

@@ -1,0 +1,167 @@
+"""Fused producers and the whole Q8 MLP (cuda/q4k_q8.cu:347-398) on the GPU:
+RMS->Q8 and SwiGLU->Q8 are bit-exact against the oracle; the MLP output is
+checked against the oracle chain; failure semantics follow the reference
+(typed error on a nonfinite producer, submitted flag, deferred pending flag,
+no device allocation inside the call)."""
+import numpy as np
+import pytest
+
+import oracle
+from _fix import normal, random_q4k, random_q6k
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def test_rms_q8_bit_exact(torch_gpu):
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    for m in (1, 3, 17):
+        res = (normal((m, 5120), 10 + m) * 3).astype(np.float32)
+        res[0, :7] = 0
+        if m > 2:
+            res[2] = 0.0  # all-zero row: scale 1 path
+        gamma = oracle.fp32_to_bf16(normal(5120, 20, 0.1))
+        q = ops.Q8Input.empty(m, 5120)
+        flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+        ops.hidden_rms_q8(_dev(torch, res), _dev(torch, gamma.view(np.int16)), 1e-6, m, q, flag)
+        torch.cuda.synchronize()
+        ref, _ = oracle.rms_q8(res, gamma, 1e-6)
+        assert int(flag.item()) == 0
+        assert np.array_equal(q.codes.cpu().numpy(), ref.codes)
+        assert np.array_equal(q.scales.cpu().numpy().view(np.uint32), ref.scales.view(np.uint32))
+        assert np.array_equal(q.sums.cpu().numpy(), ref.sums)
+    res[1, 100] = np.nan
+    ops.hidden_rms_q8(_dev(torch, res), _dev(torch, gamma.view(np.int16)), 1e-6, m, q, flag)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 1
+
+
+def test_swiglu_q8_bit_exact(torch_gpu):
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    m, n = 5, 17408
+    g = (normal((m, n), 30) * 5).astype(np.float32)
+    u = normal((m, n), 31)
+    g[0, :4] = [0.0, -120.0, 95.0, 1e-30]  # exp overflow / underflow / tiny
+    q = ops.Q8Input.empty(m, n)
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ops.swiglu_q8(_dev(torch, g), _dev(torch, u), m, n, q, flag)
+    torch.cuda.synchronize()
+    ref, _ = oracle.swiglu_q8(g, u)
+    assert int(flag.item()) == 0
+    assert np.array_equal(q.codes.cpu().numpy(), ref.codes)
+    assert np.array_equal(q.scales.cpu().numpy().view(np.uint32), ref.scales.view(np.uint32))
+    assert np.array_equal(q.sums.cpu().numpy(), ref.sums)
+    g[3, 5000] = np.inf
+    ops.swiglu_q8(_dev(torch, g), _dev(torch, u), m, n, q, flag)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 1
+
+
+@pytest.fixture(scope="module")
+def mlp_weights(torch_gpu):
+    import qw38_amd.ops as ops
+    out = {}
+    gl = random_q4k(17408, 5120, 41)
+    ul = random_q4k(17408, 5120, 42)
+    dl4 = random_q4k(5120, 17408, 43)
+    dl6 = random_q6k(5120, 17408, 44)
+    for name, wl, layout in (("gate", gl, oracle.LAYOUT_Q4K_W64), ("up", ul, oracle.LAYOUT_Q4K_W64),
+                             ("down4", dl4, oracle.LAYOUT_Q4K_SEQ)):
+        co, mo = wl.physical(layout)
+        out[name] = (ops.PrefillWeight.from_bytes(co, mo, layout, wl.n, wl.k), wl)
+    co, mo = dl6.physical()
+    out["down6"] = (ops.PrefillWeight.from_bytes(co, mo, oracle.LAYOUT_Q6K_W64, 5120, 17408), dl6)
+    return out
+
+
+def _workspace_views(ws, m):
+    """The reference workspace layout (cuda/q4k_q8.cu:367-372): Q8 codes
+    [m][17408], scales/sums [m][544], gate and up fp32 [m][17408]."""
+    b = ws.cpu().numpy()
+    o = 0
+    codes = b[o:o + m * 17408].view(np.int8).reshape(m, 17408); o += m * 17408
+    scales = b[o:o + m * 544 * 4].view(np.float32).reshape(m, 544); o += m * 544 * 4
+    sums = b[o:o + m * 544 * 4].view(np.int32).reshape(m, 544); o += m * 544 * 4
+    g = b[o:o + m * 17408 * 4].view(np.float32).reshape(m, 17408); o += m * 17408 * 4
+    u = b[o:o + m * 17408 * 4].view(np.float32).reshape(m, 17408)
+    return codes, scales, sums, g, u
+
+
+@pytest.mark.parametrize("down", ["down4", "down6"])
+def test_q8_mlp_end_to_end(torch_gpu, mlp_weights, down):
+    """Stage by stage on the same inputs: RMS->Q8 pack (bit-exact, checked in
+    test_rms_q8_bit_exact), gate/up projections (tolerance), the SwiGLU->Q8
+    pack of the device's own gate/up values (bit-exact), down + residual
+    (tolerance)."""
+    torch = torch_gpu
+    import qw38_amd
+    import qw38_amd.ops as ops
+    gate, gl = mlp_weights["gate"]
+    up, ul = mlp_weights["up"]
+    dn, dl = mlp_weights[down]
+    gamma = oracle.fp32_to_bf16(normal(5120, 50, 0.1))
+    for m in (1, 3, 129):
+        print(f"mlp {down} m={m}", flush=True)
+        res = normal((m, 5120), 60 + m)
+        ws = torch.zeros(ops.q8_mlp_workspace_bytes(m), dtype=torch.uint8, device="cuda")
+        out = torch.full((m, 5120), float("nan"), device="cuda")
+        dres, dgam = _dev(torch, res), _dev(torch, gamma.view(np.int16))
+        before = qw38_amd.lib().qw38_malloc_count()
+        assert ops.q4k_q8_mlp(gate, up, dn, dres, dgam, 1e-6, out, m, ws)
+        assert qw38_amd.lib().qw38_malloc_count() == before, "no allocation on the hot path"
+        y = out.cpu().numpy()
+        codes, scales, sums, g, u = _workspace_views(ws, m)
+        q1, _ = oracle.rms_q8(res, gamma, 1e-6)
+        g64, _, _ = oracle.q4k_q8_contract(gl, q1)
+        u64, _, _ = oracle.q4k_q8_contract(ul, q1)
+        for name, dev, ref in (("gate", g, g64), ("up", u, u64)):
+            ok, ma, mr = oracle.parity_ok(dev, ref)
+            print(f"  {name}: max_abs/rms={ma:.3g} mean_rel={mr:.3g}", flush=True)
+            assert ok
+        q2, _ = oracle.swiglu_q8(g, u)
+        assert np.array_equal(codes, q2.codes), "SwiGLU->Q8 pack of the device gate/up"
+        assert np.array_equal(scales.view(np.uint32), q2.scales.view(np.uint32))
+        assert np.array_equal(sums, q2.sums)
+        if isinstance(dl, oracle.Q6K):
+            d64, _, _ = oracle.q6k_q8_contract(dl, q2)
+        else:
+            d64, _, _ = oracle.q4k_q8_contract(dl, q2)
+        ok, ma, mr = oracle.parity_ok(y - res, d64)
+        print(f"  down: max_abs/rms={ma:.3g} mean_rel={mr:.3g}", flush=True)
+        assert ok
+
+
+def test_q8_mlp_failure_semantics(torch_gpu, mlp_weights):
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    from qw38_amd import Qw38Error
+    gate, _ = mlp_weights["gate"]
+    up, _ = mlp_weights["up"]
+    dn, _ = mlp_weights["down4"]
+    m = 2
+    gamma = oracle.fp32_to_bf16(normal(5120, 50, 0.1))
+    res = normal((m, 5120), 70)
+    res[1, 9] = np.nan
+    ws = torch.zeros(ops.q8_mlp_workspace_bytes(m), dtype=torch.uint8, device="cuda")
+    out = torch.zeros(m, 5120, device="cuda")
+    dres, dgam = _dev(torch, res), _dev(torch, gamma.view(np.int16))
+    with pytest.raises(Qw38Error) as e:
+        ops.q4k_q8_mlp(gate, up, dn, dres, dgam, 1e-6, out, m, ws)
+    assert e.value.operation == "q8.producer" and e.value.status == 2
+    assert e.value.submitted
+    # internal submission: enqueue only, sticky flag read by the owner
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    assert ops.q4k_q8_mlp(gate, up, dn, dres, dgam, 1e-6, out, m, ws, pending_failure=flag)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 1
+    # prelaunch rejection: bad eps, short workspace
+    with pytest.raises(Qw38Error) as e:
+        ops.q4k_q8_mlp(gate, up, dn, dres, dgam, -1.0, out, m, ws)
+    assert not e.value.submitted
+    with pytest.raises(Qw38Error):
+        ops.q4k_q8_mlp(gate, up, dn, dres, dgam, 1e-6, out, m, ws[:-8])

