@@ -1,36 +1,54 @@
-// Prefill MMQ (M > 8) on gfx950 matrix cores.
+// Prefill MMQ (M > 8) on gfx950 matrix cores (v_mfma_f32_16x16x32_f16).
 //
-// Exactness argument. For a Q4_K weight row r and K32 group g the reference
-// contraction (cuda/q4k_q8.cu:140,245) is a_tg * (d_r s_rg dot_rtg -
-// dmin_r m_rg sum_tg) with an exact int32 dot. Here the A operand holds the
-// integers s_rg * w_rk (<= 63 * 15 = 945) and the B operand the int8 codes
-// z_tk, both exact in FP16; one v_mfma_f32_16x16x32_f16 covers exactly one
-// K32 group, and every partial sum of its products is an integer below 2^24,
-// so the FP32 result P = s_rg * dot_rtg is exact regardless of the hardware's
-// accumulation order. The FP32 affine is then, per super-block kb,
-//   X_rt = sum_{g in kb} a_tg * P_rtg            (one FMA per output-group)
-//   acc_rt += d_r * X_rt - dmin_r * sum_g m_rg (a_tg sum_tg)
-// -- the same value as the reference's per-group expression, reassociated.
-// Every tiling below runs the same per-(row, token) operation sequence, so all
-// M-tile shapes give bitwise-identical outputs (the reference's J32 == J128
-// property, tests/q4k_q8_test.cpp:118-120).
+// Exactness. For Q4_K row r and K32 group g the reference contraction
+// (cuda/q4k_q8.cu:140,245) is a_tg (d_r s_rg dot_rtg - dmin_r m_rg sum_tg)
+// with an exact int32 dot. The A tile holds the integers s_rg * w_rk (<= 945)
+// and the B tile the int8 codes z_tk, both exact in FP16; one MFMA covers
+// exactly one K32 group and every partial sum of its products is an integer
+// below 2^24, so its FP32 result P = s_rg * dot_rtg is exact whatever the
+// accumulation order inside the matrix core. Per super-block kb:
+//   X_rt  = sum_{g in kb} a_tg P_rtg                 (one VALU FMA per output)
+//   Y_rt  = sum_{g in kb} m_rg (a_tg sum_tg)          (two 16x16x16 MFMAs with
+//           the FP32 products a*sum, scaled per token by a power of two,
+//           split into FP16 hi + lo; K zero-padded from 8 to 16)
+//   acc  += d_r X_rt - dmin_r Y_rt
+// which is the reference's per-group expression reassociated. Every M-tiling
+// runs the same per-(row, token) operation sequence, so all tile shapes give
+// bitwise-identical outputs (the reference's J32 == J128 property,
+// tests/q4k_q8_test.cpp:118-120).
 //
-// Q6_K (layout 0x0241): A holds q - 32 (exact), two v_mfma_f32_16x16x16_f16
-// per group give the sub-block dots, combined as a_tg * d * (sc0 P0 + sc1 P1).
+// Q6_K (layout 0x0241): the A tile holds v = sc_sub (q - 32) (|v| <= 4096),
+// split exactly into FP16 hi = RN(v) and lo = v - hi; two MFMAs per group give
+// P_hi + P_lo = the exact integer I_rtg, and acc += d_r sum_g a_tg I_rtg.
+//
+// Tiles are converted to FP16 while staging: bytes become FP16 1024 + b by a
+// v_perm with 0x64 high bytes, then one packed FP16 FMA/add recovers the exact
+// integer value (scaled by s for Q4_K weights). Rows of the LDS tiles are
+// 64 halfs + 8 pad; all stores are 16 B.
+#include <cstdlib>
+
 #include "common.hpp"
 
 namespace qw38hip {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-typedef float float4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kStepK = 64;       // two K32 groups per LDS stage
-constexpr int kLdsStride = 72;   // halfs per LDS row (64 + 8 pad: 144 B)
+constexpr int kStride = 72;  // halfs per LDS tile row: 2 groups x 32 + 8 pad
 
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// bytes b0, b1 of v -> half2(1024 + b0, 1024 + b1); bytes b2, b3 likewise
+__device__ __forceinline__ h2 lo_pair(uint32_t v) { return as_h2(perm(0x64646464u, v, 0x04010400u)); }
+__device__ __forceinline__ h2 hi_pair(uint32_t v) { return as_h2(perm(0x64646464u, v, 0x04030402u)); }
+
+// Logical-order code vectors (vector j = codes 4j..4j+3) of one Q4_K group.
 template <uint16_t Layout>
-__device__ __forceinline__ void unpack32(const uint32_t w[4], uint32_t v[8]) {
+__device__ __forceinline__ void q4_vectors(const uint32_t w[4], uint32_t v[8]) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const uint32_t lo = w[t] & 0x0f0f0f0fu;
@@ -45,43 +63,257 @@ __device__ __forceinline__ void unpack32(const uint32_t w[4], uint32_t v[8]) {
   }
 }
 
-// Tile config: 4 waves as WR x WT, each wave NI x NJ 16x16 output tiles.
 template <int WR, int WT, int NI, int NJ>
 struct Cfg {
   static constexpr int BR = WR * NI * 16;  // weight rows per block
   static constexpr int BT = WT * NJ * 16;  // tokens per block
 };
 
+// Block-to-tile order: hardware places block b on XCD b % 8; each XCD gets a
+// contiguous range of tiles so the token blocks of one weight-row block share
+// that XCD's L2 (a bijection when the tile count is a multiple of 8).
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t nblk) {
+  return (nblk % 8 == 0) ? (b % 8) * (nblk / 8) + b / 8 : b;
+}
+
+// Global operands of one K step (two K32 groups), loaded into registers one
+// step ahead of their LDS store so the loads overlap the matrix-core work.
+// Loads of rows past the padded weight and of tokens past m read a clamped
+// (valid) row or token instead: every output element depends only on its own
+// row and token, and those rows and tokens are never stored.
+template <int ZW, int GPT>
+struct Fetch {
+  uint32_t w[4];     // A: 16 B of codes of (row, group)
+  uint32_t x[4];     // A: Q4_K metadata row | Q6_K: qh words 0-1, scale pair, d
+  uint32_t z[ZW];    // B: this thread's share of a (token, group) code row
+  float a[GPT];      // super-block token data (first step of a super-block
+  int32_t su[GPT];   // only): this thread's GPT groups of token kt
+};
+
 template <uint16_t Layout, int WR, int WT, int NI, int NJ>
-__global__ __launch_bounds__(256) void mmq_kernel(
+__global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) void mmq_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n,
     uint32_t pn, uint32_t kbs, const int8_t* __restrict__ xc, const float* __restrict__ xa,
     const int32_t* __restrict__ xs, uint32_t m, uint32_t pk, float* __restrict__ out,
     const float* __restrict__ residual, uint32_t row_blocks, uint32_t tok_blocks) {
-  using C = Cfg<WR, WT, NI, NJ>;
   constexpr bool kQ6 = Layout == QW38_LAYOUT_Q6K_WAVE64;
-  __shared__ _Float16 As[C::BR * kLdsStride];
-  __shared__ _Float16 Bs[C::BT * kLdsStride];
-  __shared__ float Mm[C::BR * 8];   // Q4: m per group (float); Q6: sc0, sc1 per group pair
-  __shared__ float Mq6[kQ6 ? C::BR * 8 : 1];
-  __shared__ float Dd[C::BR * 2];   // d, dmin
-  __shared__ float Aa[C::BT * 8];   // a per group
-  __shared__ float Uu[C::BT * 8];   // a * sum per group
+  using C = Cfg<WR, WT, NI, NJ>;
+  constexpr int BR = C::BR, BT = C::BT, NT = WR * WT * 64;
+  static_assert(2 * BR == NT, "A staging: one (row, group) per thread");
+  constexpr int BB = BT * 64 / NT;  // B bytes staged per thread per step
+  static_assert(BB == 8 || BB == 16 || BB == 32, "B staging share");
+  constexpr int ZW = BB / 4, PARTS = 32 / BB;
+  constexpr int TPT = NT / BT, GPT = 8 / TPT;  // super-block token data: threads per token
+  static_assert(TPT >= 1 && TPT <= 8 && GPT * TPT == 8, "token-data share");
+  constexpr int kPlanes = kQ6 ? 2 : 1;  // Q6_K stages hi and lo FP16 planes
+  constexpr int kMinR = kQ6 ? 1 : BR * 16, kMinT = kQ6 ? 1 : BT * 16;
+  __shared__ __align__(16) _Float16 As[2][kPlanes][BR * kStride];
+  __shared__ __align__(16) _Float16 Bs[2][BT * kStride];
+  __shared__ __align__(16) _Float16 Mq[2][kMinR];  // m of groups 0..7, zeros 8..15
+  __shared__ __align__(16) _Float16 Uh[2][kMinT];  // scaled a*sum hi, zero padded
+  __shared__ __align__(16) _Float16 Ul[2][kMinT];  // scaled a*sum lo, zero padded
+  __shared__ float Ue[2][BT];                      // inverse of the per-token scale
+  __shared__ float Aa[2][BT * 8];
+  __shared__ float2 Dd[2][BR];                     // (d, dmin) | (d, 0)
 
-  // XCD-aware tile order: hardware places block b on XCD b % 8; give each XCD
-  // a contiguous range of logical tiles so the token blocks of one weight-row
-  // block share that XCD's L2.
-  const uint32_t nblk = row_blocks * tok_blocks;
-  const uint32_t b = blockIdx.x;
-  // (a bijection only when the block count is a multiple of 8; else identity)
-  const uint32_t tile = (nblk % 8 == 0) ? (b % 8) * (nblk / 8) + b / 8 : b;
-  const uint32_t rb = tile / tok_blocks, tb = tile % tok_blocks;
-  const uint32_t row0 = rb * C::BR, tok0 = tb * C::BT;
-
+  const uint32_t tile = xcd_tile(blockIdx.x, row_blocks * tok_blocks);
+  const uint32_t row0 = (tile / tok_blocks) * BR, tok0 = (tile % tok_blocks) * BT;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wr = wave / WT, wt = wave % WT;
   const uint32_t lr = lane & 15u, lk = lane >> 4;
-  const uint32_t groups = pk / 32;
+  const uint32_t groups = pk / 32, strips = pn / 8;
+  const uint64_t tiles = uint64_t(pn) * kbs;
+  const uint32_t steps = kbs * 4;
+
+  // A staging role: row ar, group-in-step asel (clamped row for the loads)
+  const uint32_t ar = tid >> 1, asel = tid & 1u;
+  const uint32_t arow = min(row0 + ar, pn - 1);
+  // B staging role: token bt, group-in-step bsel, byte part bpart of BB bytes
+  const uint32_t bpart = tid % PARTS, bsel = (tid / PARTS) & 1u, bt = tid / (2 * PARTS);
+  const uint32_t btok = min(tok0 + bt, m - 1);
+  const uint32_t kt = tid / TPT, kg = (tid % TPT) * GPT;  // token kt, groups kg..kg+GPT-1
+  const uint32_t ktok = min(tok0 + kt, m - 1);
+  const bool xc_vec = (reinterpret_cast<uintptr_t>(xc) % BB) == 0;
+
+  // Per-thread address parts (the per-step parts are wave-uniform).
+  const int8_t* const zrow = xc + (size_t(btok) * groups + bsel) * 32 + bpart * BB;
+  const size_t krow = size_t(ktok) * groups + kg;
+  uint64_t a_base = 0, m_base = 0;
+  uint32_t a_r1 = 0, a_r2 = 0, m_r1 = 0;
+  if constexpr (Layout == QW38_LAYOUT_Q4K_WAVE64) {
+    a_r1 = (arow / 8) * 1024 + asel * 128;  // scaled by the chunk's super-block count
+    a_r2 = (arow % 8) * 16;
+    m_r1 = (arow / 8) * 128;
+  } else {  // 0x020D and Q6_K: tile row ((row/8)*kbs + kb)*8 + row%8
+    const uint64_t tr0 = uint64_t(arow / 8) * kbs * 8 + arow % 8;
+    a_base = kQ6 ? tr0 : tr0 * 128 + asel * 16;
+    m_base = tr0 * 16;
+  }
+
+  if constexpr (!kQ6) {
+    for (uint32_t i = tid; i < 2 * BR * 8; i += NT)
+      Mq[i / (BR * 8)][(i % (BR * 8)) / 8 * 16 + 8 + i % 8] = _Float16(0.f);
+    for (uint32_t i = tid; i < 2 * BT * 8; i += NT) {
+      Uh[i / (BT * 8)][(i % (BT * 8)) / 8 * 16 + 8 + i % 8] = _Float16(0.f);
+      Ul[i / (BT * 8)][(i % (BT * 8)) / 8 * 16 + 8 + i % 8] = _Float16(0.f);
+    }
+  }
+
+  auto fetch = [&](uint32_t s, Fetch<ZW, GPT>& F) {
+    const uint32_t kb = s >> 2, q = s & 3u;
+    if constexpr (Layout == QW38_LAYOUT_Q4K_WAVE64) {
+      const uint32_t c = kb / 8, kq = kb % 8;
+      const uint32_t nk = min(kbs - 8 * c, 8u);
+      const uint8_t* cp = codes + uint64_t(strips) * 8192 * c +
+                          (nk * a_r1 + a_r2 + (2 * q * nk + kq) * 128);
+      const uint8_t* mp = meta + uint64_t(strips) * 1024 * c + (nk * m_r1 + a_r2 + kq * 128);
+      const uint4 cw = *reinterpret_cast<const uint4*>(cp);
+      const uint4 mw = *reinterpret_cast<const uint4*>(mp);
+      F.w[0] = cw.x; F.w[1] = cw.y; F.w[2] = cw.z; F.w[3] = cw.w;
+      F.x[0] = mw.x; F.x[1] = mw.y; F.x[2] = mw.z; F.x[3] = mw.w;
+    } else if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2) {  // 4 B / 2 B aligned
+      const uint32_t* c4 = reinterpret_cast<const uint32_t*>(codes + a_base + kb * 1024 + q * 32);
+      const uint16_t* m2 = reinterpret_cast<const uint16_t*>(meta + m_base + kb * 128);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        F.w[i] = c4[i];
+        F.x[i] = uint32_t(m2[2 * i]) | (uint32_t(m2[2 * i + 1]) << 16);
+      }
+    } else {
+      const uint32_t g = 2 * q + asel;
+      const uint64_t tr = a_base + kb * 8;
+      const uint8_t* rowp = codes + tr * 192;
+      const uint4 cw = *reinterpret_cast<const uint4*>(rowp + g * 16);
+      const uint2 hw = *reinterpret_cast<const uint2*>(rowp + 128 + g * 8);
+      F.w[0] = cw.x; F.w[1] = cw.y; F.w[2] = cw.z; F.w[3] = cw.w;
+      F.x[0] = hw.x; F.x[1] = hw.y;
+      F.x[2] = *reinterpret_cast<const uint16_t*>(meta + tr * 16 + g * 2);
+      F.x[3] = *reinterpret_cast<const uint16_t*>(meta + tiles * 16 + tr * 2);
+    }
+    const int8_t* zp = zrow + (kb * 8 + 2 * q) * 32;
+    if (xc_vec) {
+      if constexpr (BB == 8) {
+        const uint2 v = *reinterpret_cast<const uint2*>(zp);
+        F.z[0] = v.x; F.z[1] = v.y;
+      } else {
+#pragma unroll
+        for (int i = 0; i < BB / 16; ++i) {
+          const uint4 v = reinterpret_cast<const uint4*>(zp)[i];
+          F.z[4 * i] = v.x; F.z[4 * i + 1] = v.y; F.z[4 * i + 2] = v.z; F.z[4 * i + 3] = v.w;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < ZW; ++i) F.z[i] = reinterpret_cast<const uint32_t*>(zp)[i];
+    }
+    if (q == 0) {
+#pragma unroll
+      for (int i = 0; i < GPT; ++i) {
+        F.a[i] = xa[krow + kb * 8 + i];
+        if constexpr (!kQ6) F.su[i] = xs[krow + kb * 8 + i];
+      }
+    }
+  };
+
+  auto store = [&](uint32_t s, const Fetch<ZW, GPT>& F) {
+    const uint32_t buf = s & 1u, kp = (s >> 2) & 1u, q = s & 3u, g = 2 * q + asel;
+    // ---- A: 32 FP16 values of (row ar, group g) ----
+    if constexpr (!kQ6) {
+      float sf, mf;
+      q4_scale_min_lane(F.x[1], F.x[2], F.x[3], g, sf, mf);
+      Mq[kp][ar * 16 + g] = _Float16(mf);
+      if (q == 0 && asel == 0)
+        Dd[kp][ar] = make_float2(f16_to_f32(F.x[0] & 0xffffu), f16_to_f32(F.x[0] >> 16));
+      uint32_t v[8];
+      q4_vectors<Layout>(F.w, v);
+      const _Float16 sh = _Float16(sf), bh = _Float16(-1024.f * sf);
+      const h2 s2 = {sh, sh}, b2 = {bh, bh};
+      uint32_t o[16];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {  // (1024 + c) s - 1024 s = c s exactly (c s <= 945)
+        o[2 * j] = as_u32(__builtin_elementwise_fma(lo_pair(v[j]), s2, b2));
+        o[2 * j + 1] = as_u32(__builtin_elementwise_fma(hi_pair(v[j]), s2, b2));
+      }
+      uint4* dst = reinterpret_cast<uint4*>(&As[buf][0][ar * kStride + asel * 32]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    } else {
+      if (q == 0 && asel == 0) Dd[kp][ar] = make_float2(f16_to_f32(F.x[3]), 0.f);
+      const h2 off = {_Float16(-1056.f), _Float16(-1056.f)};  // 1024 + q -> q - 32
+      uint32_t oh[16], ol[16];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t nib = (j & 1) ? (F.w[j >> 1] >> 4) & 0x0f0f0f0fu : F.w[j >> 1] & 0x0f0f0f0fu;
+        const uint32_t hh = (F.x[j >> 2] >> (2 * (j & 3))) & 0x03030303u;
+        const uint32_t qv = nib | (hh << 4);
+        const _Float16 sc = _Float16(float(int8_t(j < 4 ? F.x[2] & 0xffu : F.x[2] >> 8)));
+        const h2 s2 = {sc, sc};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const h2 c = (e ? hi_pair(qv) : lo_pair(qv)) + off;   // q - 32, exact
+          const h2 hi = c * s2;                                  // RN(sc (q - 32))
+          const h2 lo = __builtin_elementwise_fma(c, s2, -hi);  // exact remainder
+          oh[2 * j + e] = as_u32(hi);
+          ol[2 * j + e] = as_u32(lo);
+        }
+      }
+      uint4* dh = reinterpret_cast<uint4*>(&As[buf][0][ar * kStride + asel * 32]);
+      uint4* dl = reinterpret_cast<uint4*>(&As[buf][kPlanes - 1][ar * kStride + asel * 32]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dh[i] = make_uint4(oh[4 * i], oh[4 * i + 1], oh[4 * i + 2], oh[4 * i + 3]);
+        dl[i] = make_uint4(ol[4 * i], ol[4 * i + 1], ol[4 * i + 2], ol[4 * i + 3]);
+      }
+    }
+    // ---- B: this thread's BB codes z of (token bt, group) as FP16 ----
+    {
+      const h2 off = {_Float16(-1152.f), _Float16(-1152.f)};
+      uint32_t o[2 * ZW];
+#pragma unroll
+      for (int j = 0; j < ZW; ++j) {
+        const uint32_t u = F.z[j] ^ 0x80808080u;  // z + 128 as unsigned bytes
+        o[2 * j] = as_u32(lo_pair(u) + off);
+        o[2 * j + 1] = as_u32(hi_pair(u) + off);
+      }
+      _Float16* dst = &Bs[buf][bt * kStride + bsel * 32 + bpart * BB];
+      if constexpr (BB == 8) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < ZW / 2; ++i)
+          reinterpret_cast<uint4*>(dst)[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+      }
+    }
+    // ---- super-block token data: a per group; for Q4_K the min-term
+    // operand u = a * sum scaled per token by a power of two so the largest
+    // |u| lies in [2^13, 2^14), split into FP16 hi + lo (FP16 range and 22-bit
+    // relative precision whatever the activation magnitude) ----
+    if (q == 0) {
+#pragma unroll
+      for (int i = 0; i < GPT; ++i) Aa[kp][kt * 8 + kg + i] = F.a[i];
+      if constexpr (!kQ6) {
+        float u[GPT], mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < GPT; ++i) {
+          u[i] = F.a[i] * float(F.su[i]);
+          mx = fmaxf(mx, fabsf(u[i]));
+        }
+#pragma unroll
+        for (int w = 1; w < TPT; w *= 2) mx = fmaxf(mx, __shfl_xor(mx, w));  // the token's lanes
+        const int ex = int(__float_as_uint(mx) >> 23);  // NaN and inf give 255
+        const int se = min(max(267 - ex, 1), 253);
+        const float scale = __uint_as_float(uint32_t(se) << 23);
+        if (kg == 0) Ue[kp][kt] = __uint_as_float(uint32_t(254 - se) << 23);
+#pragma unroll
+        for (int i = 0; i < GPT; ++i) {
+          const float v = u[i] * scale;
+          const _Float16 h = _Float16(v);
+          Uh[kp][kt * 16 + kg + i] = h;
+          Ul[kp][kt * 16 + kg + i] = _Float16(v - float(h));
+        }
+      }
+    }
+  };
 
   float acc[NI][NJ][4], X[NI][NJ][4];
 #pragma unroll
@@ -91,226 +323,192 @@ __global__ __launch_bounds__(256) void mmq_kernel(
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[i][j][v] = X[i][j][v] = 0.f;
 
-  const uint32_t steps = kbs * 4;
-  for (uint32_t st = 0; st < steps; ++st) {
-    const uint32_t kb = st / 4, q = st % 4;
-    __syncthreads();
-    // ---- stage A: BR rows x 2 groups (one row-group of 32 codes per thread) ----
-    for (uint32_t idx = tid; idx < C::BR * 2; idx += 256) {
-      const uint32_t r = idx / 2, gs = idx % 2, g = 2 * q + gs;
-      const uint32_t row = row0 + r;
-      _Float16* dst = As + r * kLdsStride + gs * 32;
-      if (row < pn) {
-        const uint64_t tr = (uint64_t(row / 8) * kbs + kb) * 8 + row % 8;
-        uint32_t v[8];
-        if constexpr (!kQ6) {
-          const uint32_t* cp =
-              reinterpret_cast<const uint32_t*>(codes + q4k_code_word(Layout, row, kb, g, kbs, pn / 8));
-          uint32_t w[4] = {cp[0], cp[1], cp[2], cp[3]};
-          unpack32<Layout>(w, v);
-          const uint16_t* mp =
-              reinterpret_cast<const uint16_t*>(meta + q4k_meta_row(Layout, row, kb, kbs, pn / 8));
-          uint32_t mw[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) mw[i] = mp[i];
-          const uint32_t p0 = mw[2] | (mw[3] << 16), p1 = mw[4] | (mw[5] << 16),
-                         p2 = mw[6] | (mw[7] << 16);
-          uint32_t s, mm;
-          q4k_scale_min(p0, p1, p2, g, s, mm);
-          Mm[r * 8 + g] = float(mm);
-          if (q == 0 && gs == 0) {
-            Dd[r * 2] = f16_to_f32(mw[0]);
-            Dd[r * 2 + 1] = f16_to_f32(mw[1]);
-          }
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              dst[4 * i + e] = _Float16(float(((v[i] >> (8 * e)) & 0xffu) * s));
-        } else {
-          const uint8_t* rowp = codes + tr * 192;
-          const uint32_t* cp = reinterpret_cast<const uint32_t*>(rowp + g * 16);
-          const uint32_t* hp = reinterpret_cast<const uint32_t*>(rowp + 128 + g * 8);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const uint32_t w = cp[j >> 1];
-            const uint32_t nib = (j & 1) ? (w >> 4) & 0x0f0f0f0fu : w & 0x0f0f0f0fu;
-            const uint32_t hh = (hp[j >> 2] >> (2 * (j & 3))) & 0x03030303u;
-            v[j] = nib | (hh << 4);
-          }
-          const uint16_t scw = *reinterpret_cast<const uint16_t*>(meta + tr * 16 + g * 2);
-          Mm[r * 8 + g] = float(int8_t(scw & 0xffu));
-          Mq6[r * 8 + g] = float(int8_t(scw >> 8));
-          if (q == 0 && gs == 0) {
-            const uint64_t rows = uint64_t(pn) * kbs;
-            Dd[r * 2] = f16_to_f32(*reinterpret_cast<const uint16_t*>(meta + rows * 16 + tr * 2));
-            Dd[r * 2 + 1] = 0.f;
-          }
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              dst[4 * i + e] = _Float16(float(int((v[i] >> (8 * e)) & 0xffu) - 32));
-        }
-      } else {
-        for (int i = 0; i < 32; ++i) dst[i] = _Float16(0.f);
-        Mm[r * 8 + g] = 0.f;
-        if constexpr (kQ6) Mq6[r * 8 + g] = 0.f;
-        if (q == 0 && gs == 0) { Dd[r * 2] = 0.f; Dd[r * 2 + 1] = 0.f; }
-      }
-    }
-    // ---- stage B: BT tokens x 2 groups -----------------------------------------
-    for (uint32_t idx = tid; idx < C::BT * 2; idx += 256) {
-      const uint32_t t = idx / 2, gs = idx % 2, g = 2 * q + gs;
-      const uint32_t tok = tok0 + t;
-      _Float16* dst = Bs + t * kLdsStride + gs * 32;
-      if (tok < m) {
-        const size_t gi = size_t(tok) * groups + kb * 8 + g;
-        const uint32_t* zp = reinterpret_cast<const uint32_t*>(xc + gi * 32);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t zw = zp[i];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) dst[4 * i + e] = _Float16(float(int8_t(zw >> (8 * e))));
-        }
-        const float a = xa[gi];
-        Aa[t * 8 + g] = a;
-        Uu[t * 8 + g] = a * float(xs[gi]);
-      } else {
-        for (int i = 0; i < 32; ++i) dst[i] = _Float16(0.f);
-        Aa[t * 8 + g] = 0.f;
-        Uu[t * 8 + g] = 0.f;
-      }
-    }
-    __syncthreads();
+  Fetch<ZW, GPT> F;
+  fetch(0, F);
+  store(0, F);
+  if (steps > 1) fetch(1, F);
+  for (uint32_t s = 0; s < steps; ++s) {
+    __syncthreads();  // step s staged; step s-1 fully consumed
+    if (s + 1 < steps) store(s + 1, F);
+    if (s + 2 < steps) fetch(s + 2, F);
+    const uint32_t buf = s & 1u, kp = (s >> 2) & 1u, q = s & 3u;
 
-    // ---- MFMA over the two groups of this stage -------------------------------
+    // ---- one 16x16x32 MFMA per (row tile, token tile, group). Small wave
+    // tiles issue the MFMAs of both groups of the step before any result is
+    // scaled, so the matrix core pipelines them while the VALU applies a_tg;
+    // large wave tiles scale row tile i while the MFMAs of row tile i+1 run. ----
+    if constexpr (NI * NJ <= 8) {
+      f4 P[2][NI][NJ];
+      float at[2][NJ];
 #pragma unroll
-    for (uint32_t gs = 0; gs < 2; ++gs) {
-      const uint32_t g = 2 * q + gs;
-      float at[NJ];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) at[j] = Aa[(wt * NJ * 16 + j * 16 + lr) * 8 + g];
-      if constexpr (!kQ6) {
+      for (uint32_t gsel = 0; gsel < 2; ++gsel) {
+        const uint32_t g = 2 * q + gsel;
         half8 af[NI], bf[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const uint32_t t = wt * NJ * 16 + j * 16 + lr;
+          at[gsel][j] = Aa[kp][t * 8 + g];
+          bf[j] = *reinterpret_cast<const half8*>(&Bs[buf][t * kStride + gsel * 32 + lk * 8]);
+        }
 #pragma unroll
         for (int i = 0; i < NI; ++i)
           af[i] = *reinterpret_cast<const half8*>(
-              As + (wr * NI * 16 + i * 16 + lr) * kLdsStride + gs * 32 + lk * 8);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          bf[j] = *reinterpret_cast<const half8*>(
-              Bs + (wt * NJ * 16 + j * 16 + lr) * kLdsStride + gs * 32 + lk * 8);
+              &As[buf][0][(wr * NI * 16 + i * 16 + lr) * kStride + gsel * 32 + lk * 8]);
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            const float4v zero = {0.f, 0.f, 0.f, 0.f};
-            const float4v P = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], zero, 0, 0, 0);
+          for (int j = 0; j < NJ; ++j)
+            P[gsel][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], f4{0, 0, 0, 0}, 0, 0, 0);
+        if constexpr (kQ6) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) X[i][j][v] = fmaf(at[j], P[v], X[i][j][v]);
+          for (int i = 0; i < NI; ++i) {
+            af[i] = *reinterpret_cast<const half8*>(
+                &As[buf][kPlanes - 1][(wr * NI * 16 + i * 16 + lr) * kStride + gsel * 32 + lk * 8]);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)  // hi + lo partial sums stay exact integers below 2^24
+              P[gsel][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], P[gsel][i][j], 0, 0, 0);
           }
-      } else {
-        // Two K16 sub-blocks: lanes hold k = 4*lk .. 4*lk+3 of each half.
-        half4 af0[NI], af1[NI], bf0[NJ], bf1[NJ];
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          const _Float16* p = As + (wr * NI * 16 + i * 16 + lr) * kLdsStride + gs * 32 + lk * 4;
-          af0[i] = *reinterpret_cast<const half4*>(p);
-          af1[i] = *reinterpret_cast<const half4*>(p + 16);
         }
+      }
+#pragma unroll
+      for (uint32_t gsel = 0; gsel < 2; ++gsel)
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) X[i][j][v] = fmaf(at[gsel][j], P[gsel][i][j][v], X[i][j][v]);
+    } else {
+#pragma unroll
+      for (uint32_t gsel = 0; gsel < 2; ++gsel) {
+        const uint32_t g = 2 * q + gsel;
+        float at[NJ];
+        half8 bf[NJ];
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          const _Float16* p = Bs + (wt * NJ * 16 + j * 16 + lr) * kLdsStride + gs * 32 + lk * 4;
-          bf0[j] = *reinterpret_cast<const half4*>(p);
-          bf1[j] = *reinterpret_cast<const half4*>(p + 16);
+          const uint32_t t = wt * NJ * 16 + j * 16 + lr;
+          at[j] = Aa[kp][t * 8 + g];
+          bf[j] = *reinterpret_cast<const half8*>(&Bs[buf][t * kStride + gsel * 32 + lk * 8]);
         }
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-          float s0[4], s1[4];
+          const uint32_t ro = (wr * NI * 16 + i * 16 + lr) * kStride + gsel * 32 + lk * 8;
+          const half8 af = *reinterpret_cast<const half8*>(&As[buf][0][ro]);
+          f4 P[NJ];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const uint32_t r = wr * NI * 16 + i * 16 + lk * 4 + v;
-            s0[v] = Mm[r * 8 + g];
-            s1[v] = Mq6[r * 8 + g];
+          for (int j = 0; j < NJ; ++j)
+            P[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], f4{0, 0, 0, 0}, 0, 0, 0);
+          if constexpr (kQ6) {
+            const half8 al = *reinterpret_cast<const half8*>(&As[buf][kPlanes - 1][ro]);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)  // hi + lo partial sums stay exact integers below 2^24
+              P[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[j], P[j], 0, 0, 0);
           }
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            const float4v zero = {0.f, 0.f, 0.f, 0.f};
-            const float4v P0 = __builtin_amdgcn_mfma_f32_16x16x16f16(af0[i], bf0[j], zero, 0, 0, 0);
-            const float4v P1 = __builtin_amdgcn_mfma_f32_16x16x16f16(af1[i], bf1[j], zero, 0, 0, 0);
+          for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-              X[i][j][v] = fmaf(at[j], fmaf(s1[v], P1[v], s0[v] * P0[v]), X[i][j][v]);
-          }
+            for (int v = 0; v < 4; ++v) X[i][j][v] = fmaf(at[j], P[j][v], X[i][j][v]);
         }
       }
     }
 
-    // ---- super-block epilogue: acc += d*X - dmin * sum_g m*(a*sum) -------------
+    // ---- end of super-block: fold X (and the Q4_K min term) into acc ----
     if (q == 3) {
+      half4 mf[NI], uh[NJ], ul[NJ];
+      float ue[NJ];
+      if constexpr (!kQ6) {
 #pragma unroll
-      for (int i = 0; i < NI; ++i)
+        for (int i = 0; i < NI; ++i)
+          mf[i] = *reinterpret_cast<const half4*>(&Mq[kp][(wr * NI * 16 + i * 16 + lr) * 16 + lk * 4]);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const uint32_t r = wr * NI * 16 + i * 16 + lk * 4 + v;
-          const float d = Dd[r * 2], dmin = Dd[r * 2 + 1];
-          float mg[8];
-#pragma unroll
-          for (int g = 0; g < 8; ++g) mg[g] = kQ6 ? 0.f : Mm[r * 8 + g];
-#pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            if constexpr (!kQ6) {
-              const uint32_t t = wt * NJ * 16 + j * 16 + lr;
-              float mt = 0.f;
-#pragma unroll
-              for (int g = 0; g < 8; ++g) mt = fmaf(mg[g], Uu[t * 8 + g], mt);
-              acc[i][j][v] = fmaf(-dmin, mt, fmaf(d, X[i][j][v], acc[i][j][v]));
-            } else {
-              acc[i][j][v] = fmaf(d, X[i][j][v], acc[i][j][v]);
-            }
-            X[i][j][v] = 0.f;
-          }
+        for (int j = 0; j < NJ; ++j) {
+          const uint32_t t = wt * NJ * 16 + j * 16 + lr;
+          ue[j] = Ue[kp][t];
+          uh[j] = *reinterpret_cast<const half4*>(&Uh[kp][t * 16 + lk * 4]);
+          ul[j] = *reinterpret_cast<const half4*>(&Ul[kp][t * 16 + lk * 4]);
         }
+      }
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        float2 dd[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) dd[v] = Dd[kp][wr * NI * 16 + i * 16 + lk * 4 + v];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          if constexpr (!kQ6) {
+            f4 Y = __builtin_amdgcn_mfma_f32_16x16x16f16(mf[i], uh[j], f4{0, 0, 0, 0}, 0, 0, 0);
+            Y = __builtin_amdgcn_mfma_f32_16x16x16f16(mf[i], ul[j], Y, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              acc[i][j][v] = fmaf(-dd[v].y, Y[v] * ue[j], fmaf(dd[v].x, X[i][j][v], acc[i][j][v]));
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[i][j][v] = fmaf(dd[v].x, X[i][j][v], acc[i][j][v]);
+          }
+#pragma unroll
+          for (int v = 0; v < 4; ++v) X[i][j][v] = 0.f;
+        }
+      }
     }
   }
 
-  // ---- store: lane holds rows 4*lk..4*lk+3 of token lr in each tile ------------
+  // ---- store: lane holds rows 4*lk..4*lk+3 of token lr in each tile ----
+  const bool vec = (n % 4 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0;
 #pragma unroll
   for (int i = 0; i < NI; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const uint32_t tok = tok0 + wt * NJ * 16 + j * 16 + lr;
-      if (tok >= m) continue;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const uint32_t row = row0 + wr * NI * 16 + i * 16 + lk * 4 + v;
-        if (row < n) {
-          const size_t o = size_t(tok) * n + row;
-          out[o] = acc[i][j][v] + (residual ? residual[o] : 0.f);
+      const uint32_t r4 = row0 + wr * NI * 16 + i * 16 + lk * 4;
+      if (tok >= m || r4 >= n) continue;
+      const size_t o = size_t(tok) * n + r4;
+      if (vec) {  // n % 4 == 0, so all four rows are in range
+        float4 y = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        if (residual) {
+          const float4 rv = *reinterpret_cast<const float4*>(residual + o);
+          y.x += rv.x; y.y += rv.y; y.z += rv.z; y.w += rv.w;
         }
+        *reinterpret_cast<float4*>(out + o) = y;
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (r4 + v < n) out[o + v] = acc[i][j][v] + (residual ? residual[o + v] : 0.f);
       }
     }
 }
 
 template <uint16_t Layout, int WR, int WT, int NI, int NJ>
-hipError_t mmq_launch(const WeightView& w, const Q8View& x, float* out, const float* residual,
+hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const float* residual,
                       hipStream_t s) {
   using C = Cfg<WR, WT, NI, NJ>;
   const uint32_t row_blocks = (w.pn + C::BR - 1) / C::BR;
   const uint32_t tok_blocks = (x.m + C::BT - 1) / C::BT;
-  hipLaunchKernelGGL((mmq_kernel<Layout, WR, WT, NI, NJ>), dim3(row_blocks * tok_blocks),
-                     dim3(256), 0, s, w.codes, w.scales, w.n, w.pn, w.pk / 256, x.codes,
-                     x.scales, x.sums, x.m, x.pk, out, residual, row_blocks, tok_blocks);
+  const dim3 grid(row_blocks * tok_blocks);
+  hipLaunchKernelGGL((mmq_kernel<Layout, WR, WT, NI, NJ>), grid, dim3(WR * WT * 64), 0, s, w.codes, w.scales,
+                     w.n, w.pn, w.pk / 256, x.codes, x.scales, x.sums, x.m, x.pk, out, residual,
+                     row_blocks, tok_blocks);
   return hipGetLastError();
 }
 
 template <uint16_t Layout>
 hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const float* residual,
                         hipStream_t s) {
-  if (x.m <= 32) return mmq_launch<Layout, 4, 1, 2, 2>(w, x, out, residual, s);   // 128 x 32
-  if (x.m <= 64) return mmq_launch<Layout, 2, 2, 4, 2>(w, x, out, residual, s);   // 128 x 64
-  return mmq_launch<Layout, 2, 2, 4, 4>(w, x, out, residual, s);                  // 128 x 128
+  // QW38_MMQ_TILE=32|64|128 pins the token tile (256: 256 rows x 128 tokens) (tuning aid; all tiles give
+  // bitwise-identical results).
+  static const int forced = [] {
+    const char* e = std::getenv("QW38_MMQ_TILE");
+    return e ? std::atoi(e) : 0;
+  }();
+  const int bt = forced ? forced : (x.m <= 32 ? 32 : x.m <= 64 ? 64 : 256);
+  if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2>(w, x, out, residual, s);  // 128 x 32
+  if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4>(w, x, out, residual, s);  // 128 x 64
+  if constexpr (Layout == QW38_LAYOUT_Q6K_WAVE64) {  // Q6_K's two A planes: 128 x 128 at most
+    return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s);
+  } else {
+    if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s);  // 128 x 128
+    return launch_cfg<Layout, 4, 2, 4, 4>(w, x, out, residual, s);                 // 256 x 128
+  }
 }
 
 }  // namespace
