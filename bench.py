@@ -32,6 +32,30 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA (AMD published)
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA (AMD published)
 METRIC = "Q4_K×Q8 GEMV GB/s (% of 8 TB/s) at M=1; MMQ int8 TOPS (% peak) at M=512"
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "gemv_w64_config2_m1_traffic.txt")
+
+
+def measured_traffic(path=TRAFFIC_PROFILE):
+    """HBM bytes per launch of the config-2 M=1 GEMV (layout 0x0240) from the
+    committed rocprofv3 --pmc summary: FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch), each scaled by what the same counter reads for a device copy
+    of exactly 1 GiB read + 1 GiB written. None when the summary is absent."""
+    import re
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    vals = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        g = re.search(r"gemv_w64_kernel<1[^\n]*\(dispatches=\d+\): " + counter + r"=([\d.e+]+)", text)
+        c = re.search(r"__amd_rocclr_copyBuffer \(dispatches=\d+\): " + counter + r"=([\d.e+]+)", text)
+        if not g or not c:
+            return None
+        scale = (1 << 20) / float(c.group(1))  # KiB the counter should read for 1 GiB
+        vals[counter] = float(g.group(1)) * scale * 1024
+    return {"bytes": vals["FETCH_SIZE"] + vals["WRITE_SIZE"], "read": vals["FETCH_SIZE"],
+            "written": vals["WRITE_SIZE"], "source": "profiles/gemv_w64_config2_m1_traffic.txt"}
 
 
 def log(*a):
@@ -215,6 +239,7 @@ def main():
     if not args.no_cpu:
         _, blocks = make_weight(torch, ops, n, k, 11, layout)
         cpu = cpu_baseline(torch, blocks, n, k, 1, args.cpu_seconds)
+    traffic = measured_traffic() if layout == 0x0240 else None
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 2),
@@ -235,7 +260,10 @@ def main():
                    "timing": head["mode"]},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                     "copy-calibrated)",
+                     "algorithmic_bytes": q4k_bytes(n, k) + k * 5 // 4 + n * 4},
         "decode_m": {str(m): {"gbs": round(v["gbs"], 1), "us": round(v["ms"] * 1e3, 3),
                               "frac_hbm": round(v["gbs"] / HBM_PEAK_GBS, 4)}
                      for m, v in dec.items()},
