@@ -157,6 +157,27 @@ def bench_decode(torch, ops, n, k, ms, steps, warmup, layout, seed=11):
     return res, base
 
 
+def bench_decode_bf16(torch, ops, n, k, steps, warmup, seed=31):
+    """BF16-activation decode_mmv (Q4_K 0x020D, M=1, StoreFp32) on the config-2
+    shape, rotating weight copies like the Q8 decode."""
+    wbytes = q4k_bytes(n, k)
+    copies = max(2, math.ceil(1.2e9 / wbytes))
+    base, _ = make_weight(torch, ops, n, k, seed, 0x020D)
+    ws = [base] + [clone_weight(ops, base) for _ in range(copies - 1)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1)
+    x = torch.randn(k, generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
+    outs = [torch.empty(n, device="cuda") for _ in range(copies)]
+    descs = [ops.decode_desc(ws[i], x, outs[i], ops.DECODE_STORE_FP32) for i in range(copies)]
+    ms_step, nsteps, mode = time_launches(torch, lambda i: ops.decode_mmv(descs[i]), copies,
+                                          steps, warmup)
+    algo = wbytes + k * 2 + n * 4
+    gbs = algo / (ms_step * 1e-3) / 1e9
+    log(f"decode_bf16 N={n} K={k}: {ms_step*1e3:.2f} us/launch, {gbs:.0f} GB/s ({mode})")
+    return {"us": round(ms_step * 1e3, 3), "gbs": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "layout": "0x020d", "steps": nsteps}
+
+
 def bench_mmq(torch, ops, n, k, m, steps, warmup, layout, seed=21):
     w, _ = make_weight(torch, ops, n, k, seed, layout)
     q, _ = make_q8(torch, ops, m, k, seed + 1)
@@ -204,6 +225,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-mmq", action="store_true")
+    ap.add_argument("--no-bf16", action="store_true", help="skip the BF16-activation decode_mmv")
     ap.add_argument("--decode-m", default="1,2,4,8", help="decode token counts to time")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (counter scale for rocprof --pmc)")
@@ -235,6 +257,7 @@ def main():
     head = dec[1]
     mmq = None if args.no_mmq else bench_mmq(torch, ops, n, k, 512, max(20, args.steps // 8),
                                               max(3, args.warmup // 4), layout)
+    dbf16 = None if args.no_bf16 else bench_decode_bf16(torch, ops, n, k, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu:
         _, blocks = make_weight(torch, ops, n, k, 11, layout)
@@ -268,6 +291,7 @@ def main():
                               "frac_hbm": round(v["gbs"] / HBM_PEAK_GBS, 4)}
                      for m, v in dec.items()},
         "mmq_m512": mmq,
+        "decode_bf16_m1": dbf16,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -149,6 +149,93 @@ int qw38_quantize_q4k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_
 int qw38_quantize_q6k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_t k,
                              void* blocks, uint64_t blocks_bytes, void* stream);
 
+/* ---- BF16-activation decode GEMV (cuda/decode_mmv.hpp) -------------------
+ * Field-for-field mirrors of DecodeOperandView, DecodeMmvDesc and the enums
+ * (cuda/decode_mmv.hpp:25-134). Validation follows the reference's contract
+ * (cuda/decode_mmv.cu:245-560): typed views, padded geometry, exact byte
+ * counts, alignment, writability and non-overlap, all before any launch.
+ * This build implements the Q4_K layout 0x020D (quantizer 0x0105); the other
+ * reference layouts are recognised and rejected with QW38_INVALID_ARGUMENT
+ * ("not implemented on this build"). */
+#define QW38_DECODE_LAYOUT_Q4G64_V0 0x0201
+#define QW38_DECODE_LAYOUT_Q8G32_V0 0x0202
+#define QW38_DECODE_LAYOUT_BF16_DENSE_TILE_V0 0x0203
+#define QW38_DECODE_LAYOUT_BF16_VECTOR_V0 0x0205
+#define QW38_DECODE_LAYOUT_FP32_VECTOR_V0 0x020A
+#define QW38_DECODE_LAYOUT_Q4G64_CANDIDATE_V1 0x020B
+#define QW38_DECODE_LAYOUT_Q8G32_CANDIDATE_V1 0x020C
+#define QW38_DECODE_LAYOUT_NVFP4_V1 0x020E
+#define QW38_DECODE_LAYOUT_FP8_V1 0x020F
+#define QW38_DECODE_QUANTIZER_NONE 0x0100
+#define QW38_DECODE_QUANTIZER_Q4G64_V0 0x0101
+#define QW38_DECODE_QUANTIZER_Q8G32_V0 0x0102
+#define QW38_DECODE_QUANTIZER_Q4G64_CANDIDATE_V1 0x0103
+#define QW38_DECODE_QUANTIZER_Q8G32_CANDIDATE_V1 0x0104
+#define QW38_DECODE_QUANTIZER_NVFP4_V1 0x0106
+#define QW38_DECODE_QUANTIZER_FP8_V1 0x0107
+#define QW38_DECODE_MAX_K 17408u
+
+/* DecodeEpilogue */
+#define QW38_DECODE_STORE_BF16 1
+#define QW38_DECODE_STORE_FP32 2
+#define QW38_DECODE_RESIDUAL_ADD_FP32 3
+#define QW38_DECODE_SWIGLU_BF16 4
+/* DecodeMemorySpace */
+#define QW38_DECODE_SPACE_DEVICE 1
+#define QW38_DECODE_SPACE_HOST 2
+/* DecodeDtype */
+#define QW38_DECODE_DTYPE_Q4 1
+#define QW38_DECODE_DTYPE_Q8 2
+#define QW38_DECODE_DTYPE_BF16 3
+#define QW38_DECODE_DTYPE_FP16 4
+#define QW38_DECODE_DTYPE_FP32 5
+#define QW38_DECODE_DTYPE_NVFP4 6
+#define QW38_DECODE_DTYPE_FP8 7
+/* DecodeActivationPolicy */
+#define QW38_DECODE_ACTIVATION_BF16 1
+
+typedef struct qw38_decode_view {
+  void* pointer;
+  uint8_t space;
+  uint8_t dtype;
+  uint16_t layout;
+  uint32_t logical_n;
+  uint32_t logical_k;
+  uint32_t padded_n;
+  uint32_t padded_k;
+  uint64_t bytes;
+  uint32_t alignment;
+  uint8_t writable;
+} qw38_decode_view;
+
+typedef struct qw38_decode_desc {
+  uint16_t layout;
+  uint16_t quantizer;
+  uint8_t activation_policy;
+  uint32_t n;
+  uint32_t k;
+  uint32_t padded_n;
+  uint32_t padded_k;
+  qw38_decode_view codes;
+  qw38_decode_view scales;
+  qw38_decode_view input;
+  qw38_decode_view output;
+  qw38_decode_view residual;
+  uint8_t epilogue;
+} qw38_decode_desc;
+
+/* Replaces qw38::cuda::launch_decode_mmv (cuda/decode_mmv.hpp:205-206,
+ * cuda/decode_mmv.cu:755-766). y[n] = W x, x BF16 [k], FP32 accumulation of
+ * the rebuilt BF16 weights, then the epilogue. */
+int qw38_decode_mmv(const qw38_decode_desc* desc, void* stream);
+/* Replaces launch_decode_mmv_paired (cuda/decode_mmv.hpp:208-209,
+ * cuda/decode_mmv.cu:768-779): gate/up sharing K and input, separate outputs
+ * or SwiGLU -> BF16 into a's output. */
+int qw38_decode_mmv_paired(const qw38_decode_desc* a, const qw38_decode_desc* b, void* stream);
+/* Replaces launch_decode_mmv_ranges (cuda/decode_mmv.hpp:216-217,
+ * cuda/decode_mmv.cu:781-853): two or three BF16-store projections sharing
+ * layout, K and input. */
+int qw38_decode_mmv_ranges(const qw38_decode_desc* ranges, uint32_t count, void* stream);
 /* Byte sizes of a tiled weight (cuda/decode_mmv.hpp:330-369 for 0x020D,
  * extended with this build's layouts). 0 for an unknown layout. */
 uint64_t qw38_code_bytes(uint16_t layout, uint32_t padded_n, uint32_t padded_k);

@@ -38,6 +38,23 @@ class Q8Input(C.Structure):
                 ("m", C.c_uint32), ("k", C.c_uint32), ("padded_k", C.c_uint32)]
 
 
+class DecodeView(C.Structure):
+    """qw38_decode_view == cuda::DecodeOperandView (cuda/decode_mmv.hpp:80-93)."""
+    _fields_ = [("pointer", C.c_void_p), ("space", C.c_uint8), ("dtype", C.c_uint8),
+                ("layout", C.c_uint16), ("logical_n", C.c_uint32), ("logical_k", C.c_uint32),
+                ("padded_n", C.c_uint32), ("padded_k", C.c_uint32), ("bytes", C.c_uint64),
+                ("alignment", C.c_uint32), ("writable", C.c_uint8)]
+
+
+class DecodeDesc(C.Structure):
+    """qw38_decode_desc == cuda::DecodeMmvDesc (cuda/decode_mmv.hpp:117-134)."""
+    _fields_ = [("layout", C.c_uint16), ("quantizer", C.c_uint16),
+                ("activation_policy", C.c_uint8), ("n", C.c_uint32), ("k", C.c_uint32),
+                ("padded_n", C.c_uint32), ("padded_k", C.c_uint32), ("codes", DecodeView),
+                ("scales", DecodeView), ("input", DecodeView), ("output", DecodeView),
+                ("residual", DecodeView), ("epilogue", C.c_uint8)]
+
+
 class Qw38Error(RuntimeError):
     def __init__(self, status, hip_status, operation, detail):
         self.status, self.hip_status = status, hip_status
@@ -64,6 +81,9 @@ SIGNATURES = {
     "qw38_repack_q6k_blocks": (_I, [_V, _U64, _U32, _U32, _V, _U64, _V, _U64, _V]),
     "qw38_quantize_q4k_blocks": (_I, [_V, _U64, _U32, _U32, _V, _U64, _V, _V]),
     "qw38_quantize_q6k_blocks": (_I, [_V, _U64, _U32, _U32, _V, _U64, _V]),
+    "qw38_decode_mmv": (_I, [_P(DecodeDesc), _V]),
+    "qw38_decode_mmv_paired": (_I, [_P(DecodeDesc), _P(DecodeDesc), _V]),
+    "qw38_decode_mmv_ranges": (_I, [_P(DecodeDesc), _U32, _V]),
     "qw38_code_bytes": (_U64, [_U16, _U32, _U32]),
     "qw38_scale_bytes": (_U64, [_U16, _U32, _U32]),
     "qw38_device_malloc": (_I, [_P(_V), _U64]),

@@ -160,6 +160,244 @@ WeightView view(const qw38_weight& w) {
                     w.layout, w.n, w.k, w.padded_n, w.padded_k};
 }
 
+// ---- decode_mmv contract (cuda/decode_mmv.cu:245-560, restated) ----------
+using DView = qw38_decode_view;
+using DDesc = qw38_decode_desc;
+
+bool reference_layout_quantizer(uint16_t layout, uint16_t quantizer) {
+  switch (layout) {
+    case QW38_DECODE_LAYOUT_FP8_V1: return quantizer == QW38_DECODE_QUANTIZER_FP8_V1;
+    case QW38_DECODE_LAYOUT_NVFP4_V1: return quantizer == QW38_DECODE_QUANTIZER_NVFP4_V1;
+    case QW38_LAYOUT_Q4K_CANDIDATE_V2: return quantizer == QW38_QUANTIZER_Q4K;
+    case QW38_DECODE_LAYOUT_Q4G64_V0: return quantizer == QW38_DECODE_QUANTIZER_Q4G64_V0;
+    case QW38_DECODE_LAYOUT_Q4G64_CANDIDATE_V1:
+      return quantizer == QW38_DECODE_QUANTIZER_Q4G64_CANDIDATE_V1;
+    case QW38_DECODE_LAYOUT_Q8G32_V0: return quantizer == QW38_DECODE_QUANTIZER_Q8G32_V0;
+    case QW38_DECODE_LAYOUT_Q8G32_CANDIDATE_V1:
+      return quantizer == QW38_DECODE_QUANTIZER_Q8G32_CANDIDATE_V1;
+    case QW38_DECODE_LAYOUT_BF16_DENSE_TILE_V0: return quantizer == QW38_DECODE_QUANTIZER_NONE;
+    default: return false;
+  }
+}
+
+bool view_empty(const DView& v) {
+  return v.pointer == nullptr && v.space == 0 && v.dtype == 0 && v.layout == 0 &&
+         v.logical_n == 0 && v.logical_k == 0 && v.padded_n == 0 && v.padded_k == 0 &&
+         v.bytes == 0 && v.alignment == 0 && v.writable == 0;
+}
+
+bool view_equal(const DView& a, const DView& b) {
+  return a.pointer == b.pointer && a.space == b.space && a.dtype == b.dtype &&
+         a.layout == b.layout && a.logical_n == b.logical_n && a.logical_k == b.logical_k &&
+         a.padded_n == b.padded_n && a.padded_k == b.padded_k && a.bytes == b.bytes &&
+         a.alignment == b.alignment && a.writable == b.writable;
+}
+
+int check_view(const DView& v, uint8_t dtype, uint16_t layout, uint32_t ln, uint32_t lk,
+               uint32_t pn, uint32_t pk, uint64_t bytes, uint32_t min_align, bool writable,
+               const char* op, const char* name) {
+  const bool bad = v.pointer == nullptr || v.space != QW38_DECODE_SPACE_DEVICE ||
+                   v.dtype != dtype || v.layout != layout || v.logical_n != ln ||
+                   v.logical_k != lk || v.padded_n != pn || v.padded_k != pk ||
+                   v.bytes != bytes || v.alignment < min_align ||
+                   (v.alignment & (v.alignment - 1u)) != 0u ||
+                   reinterpret_cast<uintptr_t>(v.pointer) % v.alignment != 0u ||
+                   (v.writable != 0) != writable;
+  if (!bad) return QW38_OK;
+  char detail[128];
+  std::snprintf(detail, sizeof detail, "%s typed view does not match the required contract", name);
+  return fail(QW38_INVALID_ARGUMENT, op, detail);
+}
+
+bool views_overlap(const DView& a, const DView& b) {
+  if (!a.pointer || !b.pointer || !a.bytes || !b.bytes) return false;
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a.pointer), y = reinterpret_cast<uintptr_t>(b.pointer);
+  if (a.bytes > std::numeric_limits<uintptr_t>::max() - x ||
+      b.bytes > std::numeric_limits<uintptr_t>::max() - y)
+    return true;
+  return x < y + b.bytes && y < x + a.bytes;
+}
+
+uint64_t decode_code_bytes_ref(uint16_t layout, uint32_t pn, uint32_t pk) {
+  const uint64_t nk = uint64_t(pn) * pk;
+  switch (layout) {
+    case QW38_DECODE_LAYOUT_NVFP4_V1:
+    case QW38_DECODE_LAYOUT_Q4G64_V0:
+    case QW38_DECODE_LAYOUT_Q4G64_CANDIDATE_V1:
+    case QW38_LAYOUT_Q4K_CANDIDATE_V2: return nk / 2;
+    case QW38_DECODE_LAYOUT_FP8_V1:
+    case QW38_DECODE_LAYOUT_Q8G32_V0:
+    case QW38_DECODE_LAYOUT_Q8G32_CANDIDATE_V1: return nk;
+    case QW38_DECODE_LAYOUT_BF16_DENSE_TILE_V0: return nk * 2;
+    default: return 0;
+  }
+}
+
+uint64_t decode_scale_bytes_ref(uint16_t layout, uint32_t pn, uint32_t pk) {
+  const uint64_t rows = pn;
+  switch (layout) {
+    case QW38_DECODE_LAYOUT_NVFP4_V1: return 256 + (rows + 127) / 128 * 128 * (pk / 16u);
+    case QW38_LAYOUT_Q4K_CANDIDATE_V2: return rows * (pk / 256u) * 16u;
+    case QW38_DECODE_LAYOUT_Q4G64_V0:
+    case QW38_DECODE_LAYOUT_Q4G64_CANDIDATE_V1: return rows * (pk / 64u) * 2u;
+    case QW38_DECODE_LAYOUT_FP8_V1: return (rows / 128) * (pk / 128) * 4;
+    case QW38_DECODE_LAYOUT_Q8G32_V0:
+    case QW38_DECODE_LAYOUT_Q8G32_CANDIDATE_V1: return rows * (pk / 32u) * 2u;
+    default: return 0;
+  }
+}
+
+uint8_t decode_weight_dtype(uint16_t layout) {
+  switch (layout) {
+    case QW38_DECODE_LAYOUT_FP8_V1: return QW38_DECODE_DTYPE_FP8;
+    case QW38_DECODE_LAYOUT_NVFP4_V1: return QW38_DECODE_DTYPE_NVFP4;
+    case QW38_LAYOUT_Q4K_CANDIDATE_V2:
+    case QW38_DECODE_LAYOUT_Q4G64_V0:
+    case QW38_DECODE_LAYOUT_Q4G64_CANDIDATE_V1: return QW38_DECODE_DTYPE_Q4;
+    case QW38_DECODE_LAYOUT_Q8G32_V0:
+    case QW38_DECODE_LAYOUT_Q8G32_CANDIDATE_V1: return QW38_DECODE_DTYPE_Q8;
+    default: return QW38_DECODE_DTYPE_BF16;
+  }
+}
+
+uint32_t decode_group(uint16_t layout) {
+  switch (layout) {
+    case QW38_DECODE_LAYOUT_FP8_V1: return 128;
+    case QW38_LAYOUT_Q4K_CANDIDATE_V2: return 256;
+    case QW38_DECODE_LAYOUT_Q4G64_V0:
+    case QW38_DECODE_LAYOUT_Q4G64_CANDIDATE_V1: return 64;
+    case QW38_DECODE_LAYOUT_Q8G32_V0:
+    case QW38_DECODE_LAYOUT_Q8G32_CANDIDATE_V1: return 32;
+    default: return 1;
+  }
+}
+
+// Geometry and typed views of one projection; paired_b allows the SwiGLU epilogue.
+int decode_geometry(const DDesc& d, const char* op, bool paired_b) {
+  if (!reference_layout_quantizer(d.layout, d.quantizer))
+    return fail(QW38_INVALID_ARGUMENT, op, "layout/quantizer version mismatch");
+  if (d.activation_policy != QW38_DECODE_ACTIVATION_BF16)
+    return fail(QW38_INVALID_ARGUMENT, op, "unsupported decode activation policy");
+  if (d.n == 0 || d.k == 0) return fail(QW38_INVALID_ARGUMENT, op, "N and K must be nonzero");
+  if (d.n > std::numeric_limits<uint32_t>::max() - 7u)
+    return fail(QW38_OVERFLOW, op, "N exceeds the largest supported row-tile-padded value");
+  if (d.k > QW38_DECODE_MAX_K || d.padded_k > QW38_DECODE_MAX_K)
+    return fail(QW38_INVALID_ARGUMENT, op, "K exceeds decode staging limit 17408");
+  if (d.padded_n != pad_n(d.n) || d.padded_k != pad_k(d.k))
+    return fail(QW38_INVALID_ARGUMENT, op, "padded N/K metadata does not match layout tiles");
+  if (d.layout == QW38_DECODE_LAYOUT_BF16_DENSE_TILE_V0) {
+    if (d.n % 8 || d.k % 256)
+      return fail(QW38_INVALID_ARGUMENT, op, "BF16 dense tile requires N%8==0 and K%256==0");
+  } else if (d.k % decode_group(d.layout)) {
+    return fail(QW38_INVALID_ARGUMENT, op, "logical K must divide the quantizer group");
+  }
+  const uint64_t want_codes = decode_code_bytes_ref(d.layout, d.padded_n, d.padded_k);
+  const uint64_t want_scales = decode_scale_bytes_ref(d.layout, d.padded_n, d.padded_k);
+  if (int st = check_view(d.codes, decode_weight_dtype(d.layout), d.layout, d.n, d.k, d.padded_n,
+                          d.padded_k, want_codes, 16, false, op, "codes"))
+    return st;
+  if (want_scales == 0) {
+    if (!view_empty(d.scales))
+      return fail(QW38_INVALID_ARGUMENT, op, "BF16 dense tile must not supply scales");
+  } else {
+    const bool fp8 = d.layout == QW38_DECODE_LAYOUT_FP8_V1;
+    const bool one_row = fp8 || d.layout == QW38_DECODE_LAYOUT_NVFP4_V1;
+    const uint32_t rows = one_row ? 1u : d.padded_n;
+    const uint32_t units = uint32_t(want_scales / rows / (fp8 ? 4u : 2u));
+    if (int st = check_view(d.scales, fp8 ? QW38_DECODE_DTYPE_FP32 : QW38_DECODE_DTYPE_FP16,
+                            d.layout, rows, units, rows, units, want_scales, one_row ? 16u : 2u,
+                            false, op, "scales"))
+      return st;
+  }
+  if (int st = check_view(d.input, QW38_DECODE_DTYPE_BF16, QW38_DECODE_LAYOUT_BF16_VECTOR_V0, d.k,
+                          1, d.k, 1, uint64_t(d.k) * 2, 2, false, op, "input"))
+    return st;
+  if (d.epilogue < QW38_DECODE_STORE_BF16 || d.epilogue > QW38_DECODE_SWIGLU_BF16)
+    return fail(QW38_INVALID_ARGUMENT, op, "unknown epilogue");
+  if (d.epilogue == QW38_DECODE_SWIGLU_BF16 && !paired_b)
+    return fail(QW38_INVALID_ARGUMENT, op, "SwiGLU epilogue requires paired gate/up launch");
+  if (d.epilogue == QW38_DECODE_RESIDUAL_ADD_FP32) {
+    const bool separate = !view_empty(d.output);
+    if (int st = check_view(d.residual, QW38_DECODE_DTYPE_FP32, QW38_DECODE_LAYOUT_FP32_VECTOR_V0,
+                            d.n, 1, d.n, 1, uint64_t(d.n) * 4, 4, !separate, op, "residual"))
+      return st;
+    if (separate) {
+      if (int st = check_view(d.output, QW38_DECODE_DTYPE_FP32, QW38_DECODE_LAYOUT_FP32_VECTOR_V0,
+                              d.n, 1, d.n, 1, uint64_t(d.n) * 4, 4, true, op, "output"))
+        return st;
+    }
+  } else {
+    if (!view_empty(d.residual))
+      return fail(QW38_INVALID_ARGUMENT, op, "store epilogue must not supply residual");
+    const bool f32 = d.epilogue == QW38_DECODE_STORE_FP32;
+    if (int st = check_view(d.output, f32 ? QW38_DECODE_DTYPE_FP32 : QW38_DECODE_DTYPE_BF16,
+                            f32 ? QW38_DECODE_LAYOUT_FP32_VECTOR_V0 : QW38_DECODE_LAYOUT_BF16_VECTOR_V0,
+                            d.n, 1, d.n, 1, uint64_t(d.n) * (f32 ? 4 : 2), f32 ? 4u : 2u, true, op,
+                            "output"))
+      return st;
+  }
+  const DView* vs[] = {&d.codes, &d.scales, &d.input, &d.output, &d.residual};
+  for (int i = 0; i < 5; ++i)
+    for (int j = i + 1; j < 5; ++j)
+      if (views_overlap(*vs[i], *vs[j]))
+        return fail(QW38_INVALID_ARGUMENT, op, "operand views must not overlap");
+  return QW38_OK;
+}
+
+// Layouts the reference knows but this build does not implement for decode.
+int decode_supported(const DDesc& d, const char* op) {
+  if (d.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2)
+    return fail(QW38_INVALID_ARGUMENT, op, "decode layout not implemented on this build");
+  return QW38_OK;
+}
+
+int decode_paired_contract(const DDesc& a, const DDesc& b, const char* op) {
+  if (int st = decode_geometry(a, op, true)) return st;
+  DDesc bv = b;
+  if (a.epilogue == QW38_DECODE_SWIGLU_BF16) {
+    if (!view_empty(b.output) || !view_empty(b.residual))
+      return fail(QW38_INVALID_ARGUMENT, op,
+                  "SwiGLU paired B must not declare a separately materialized output");
+    bv.output = a.output;
+  }
+  if (int st = decode_geometry(bv, op, true)) return st;
+  if (b.layout != a.layout || b.quantizer != a.quantizer ||
+      b.activation_policy != a.activation_policy || b.n != a.n || b.k != a.k ||
+      b.padded_n != a.padded_n || b.padded_k != a.padded_k || b.epilogue != a.epilogue ||
+      !view_equal(b.input, a.input))
+    return fail(QW38_INVALID_ARGUMENT, op,
+                "paired B must match A shape, layout, input, and epilogue contract");
+  const DView* av[] = {&a.codes, &a.scales, &a.output, &a.residual};
+  const DView* bw[] = {&b.codes, &b.scales, &b.output, &b.residual};
+  for (const DView* x : av)
+    for (const DView* y : bw)
+      if (views_overlap(*x, *y))
+        return fail(QW38_INVALID_ARGUMENT, op, "paired A/B operands must not overlap");
+  return QW38_OK;
+}
+
+WeightView decode_weight(const DDesc& d) {
+  return WeightView{static_cast<const uint8_t*>(d.codes.pointer),
+                    static_cast<const uint8_t*>(d.scales.pointer), d.layout, d.n, d.k,
+                    d.padded_n, d.padded_k};
+}
+
+int decode_launch(const DDesc& a, const DDesc* b, void* stream, const char* op) {
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  const WeightView wa = decode_weight(a);
+  WeightView wb{};
+  if (b) wb = decode_weight(*b);
+  hipError_t e = launch_decode_bf16(
+      wa, b ? &wb : nullptr, static_cast<const uint16_t*>(a.input.pointer), a.output.pointer,
+      b ? b->output.pointer : nullptr, static_cast<const float*>(a.residual.pointer),
+      b ? static_cast<const float*>(b->residual.pointer) : nullptr, a.epilogue,
+      static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
 hipError_t project(const qw38_weight& w, const Q8View& x, float* out, const float* residual,
                    hipStream_t s) {
   if (x.m <= 8) return launch_gemv(view(w), x, out, residual, s);
@@ -444,6 +682,62 @@ int qw38_repack_q6k_blocks(const void* blocks, uint64_t blocks_bytes, uint32_t n
     e = launch_repack_q6k(static_cast<const uint8_t*>(blocks), n, k, static_cast<uint8_t*>(codes),
                           static_cast<uint8_t*>(scales), s);
   return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_decode_mmv(const qw38_decode_desc* desc, void* stream) {
+  constexpr const char* op = "decode_mmv";
+  if (!desc) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
+  if (int st = decode_geometry(*desc, op, false)) return st;
+  if (int st = decode_supported(*desc, op)) return st;
+  return decode_launch(*desc, nullptr, stream, op);
+}
+
+int qw38_decode_mmv_paired(const qw38_decode_desc* a, const qw38_decode_desc* b, void* stream) {
+  constexpr const char* op = "decode_mmv_paired";
+  if (!a || !b) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
+  if (int st = decode_paired_contract(*a, *b, op)) return st;
+  if (int st = decode_supported(*a, op)) return st;
+  return decode_launch(*a, b, stream, op);
+}
+
+int qw38_decode_mmv_ranges(const qw38_decode_desc* ranges, uint32_t count, void* stream) {
+  constexpr const char* op = "decode_mmv_ranges";
+  if (!ranges || count < 2 || count > 3)
+    return fail(QW38_INVALID_ARGUMENT, op, "ranged launch requires two or three projections");
+  const DDesc& first = ranges[0];
+  if (first.layout == QW38_DECODE_LAYOUT_NVFP4_V1)
+    return fail(QW38_INVALID_ARGUMENT, op,
+                "NVFP4 supports single or paired gate/up launches only");
+  if (first.epilogue != QW38_DECODE_STORE_BF16)
+    return fail(QW38_INVALID_ARGUMENT, op, "ranged projections store BF16");
+  if (int st = decode_geometry(first, "decode_mmv_ranges[0]", false)) return st;
+  for (uint32_t i = 1; i < count; ++i) {
+    const DDesc& d = ranges[i];
+    if (d.layout != first.layout || d.quantizer != first.quantizer ||
+        d.activation_policy != first.activation_policy)
+      return fail(QW38_INVALID_ARGUMENT, op, "ranged projections must share one layout family");
+    if (d.k != first.k || d.padded_k != first.padded_k)
+      return fail(QW38_INVALID_ARGUMENT, op, "ranged projections must share K");
+    if (!view_equal(d.input, first.input))
+      return fail(QW38_INVALID_ARGUMENT, op, "ranged projections must share the input");
+    if (d.epilogue != QW38_DECODE_STORE_BF16)
+      return fail(QW38_INVALID_ARGUMENT, op, "ranged projections store BF16");
+    if (int st = decode_geometry(d, op, false)) return st;
+  }
+  for (uint32_t i = 0; i < count; ++i)
+    for (uint32_t j = i + 1; j < count; ++j) {
+      const DView* l[] = {&ranges[i].codes, &ranges[i].scales, &ranges[i].output};
+      const DView* r[] = {&ranges[j].codes, &ranges[j].scales, &ranges[j].output};
+      for (const DView* x : l)
+        for (const DView* y : r)
+          if (views_overlap(*x, *y))
+            return fail(QW38_INVALID_ARGUMENT, op, "ranged projection operand spans must not overlap");
+    }
+  if (int st = decode_supported(first, op)) return st;
+  // One launch per range on the same stream: same results as one fused grid.
+  for (uint32_t i = 0; i < count; ++i)
+    if (int st = decode_launch(ranges[i], nullptr, stream, op)) return st;
+  return ok();
 }
 
 int qw38_quantize_q4k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_t k,

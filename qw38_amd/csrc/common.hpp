@@ -89,6 +89,26 @@ __device__ __forceinline__ void q4_scale_min_lane(uint32_t p0, uint32_t p1, uint
   m = float(ml | mh2);
 }
 
+// exp(x) by Cody-Waite reduction and a degree-7 Taylor polynomial with explicit
+// FMAs (Cephes two-part ln2). Within 1 ulp of the correctly rounded result.
+__device__ __forceinline__ float exp_cw(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -103.972084045410f) return 0.0f;
+  const float n = rintf(x * 1.44269502162933349609375f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.98412698412698412698e-4f;
+  p = fmaf(p, r, 1.38888888888888888889e-3f);
+  p = fmaf(p, r, 8.33333333333333333333e-3f);
+  p = fmaf(p, r, 4.16666666666666666667e-2f);
+  p = fmaf(p, r, 1.66666666666666666667e-1f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, int(n));
+}
+
 // Byte offsets of the 16-byte code word of (row, super-block kb, K32 group g)
 // and of the 16-byte metadata row of (row, kb).
 // 0x020D: tile row ((row/8)*kbs + kb)*8 + row%8; codes 128 B per tile row
@@ -139,6 +159,9 @@ hipError_t launch_gemv_w64(const WeightView& w, const Q8View& x, float* out,
                            const float* residual, hipStream_t s);
 hipError_t launch_mmq(const WeightView& w, const Q8View& x, float* out,
                       const float* residual, hipStream_t s);
+hipError_t launch_decode_bf16(const WeightView& a, const WeightView* b, const uint16_t* x,
+                              void* out_a, void* out_b, const float* res_a, const float* res_b,
+                              int epilogue, hipStream_t s);
 hipError_t launch_group_dots(const WeightView& w, const Q8View& x, int32_t* dots,
                              hipStream_t s);
 hipError_t launch_repack_q4k(const uint8_t* blocks, uint32_t n, uint32_t k, uint16_t layout,

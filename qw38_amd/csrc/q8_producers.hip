@@ -109,26 +109,6 @@ __global__ __launch_bounds__(256) void rms_q8_kernel(const float* __restrict__ r
                (size_t(blockIdx.x) * kHidden + i) / 32, failure);
 }
 
-// exp(x) by Cody-Waite reduction and a degree-7 Taylor polynomial with explicit
-// FMAs (Cephes two-part ln2). Within 1 ulp of the correctly rounded result.
-__device__ __forceinline__ float exp_cw(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return __builtin_inff();
-  if (x < -103.972084045410f) return 0.0f;
-  const float n = rintf(x * 1.44269502162933349609375f);
-  float r = fmaf(n, -0.693145751953125f, x);
-  r = fmaf(n, -1.428606765330187045e-06f, r);
-  float p = 1.98412698412698412698e-4f;
-  p = fmaf(p, r, 1.38888888888888888889e-3f);
-  p = fmaf(p, r, 8.33333333333333333333e-3f);
-  p = fmaf(p, r, 4.16666666666666666667e-2f);
-  p = fmaf(p, r, 1.66666666666666666667e-1f);
-  p = fmaf(p, r, 0.5f);
-  p = fmaf(p, r, 1.0f);
-  p = fmaf(p, r, 1.0f);
-  return ldexpf(p, int(n));
-}
-
 // cuda/q4k_q8.cu:52-61: v = BF16(SiLU(g) * u); nonfinite g/u -> NaN -> flag.
 __global__ __launch_bounds__(256) void swiglu_q8_kernel(const float* __restrict__ gate,
                                                         const float* __restrict__ up,

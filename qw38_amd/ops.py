@@ -18,7 +18,8 @@ from ._lib import (LAYOUT_Q4K_SEQ, LAYOUT_Q4K_W64, LAYOUT_Q6K_W64, QUANTIZER_Q4K
 
 __all__ = ["PrefillWeight", "Q8Input", "pack_q8", "q4k_q8_project", "q4k_q8_mlp",
            "hidden_rms_q8", "swiglu_q8", "group_dots", "quantize_q4k_blocks", "quantize_q6k_blocks", "upload_q4k_blocks", "upload_q6k_blocks",
-           "q8_mlp_workspace_bytes", "code_bytes", "scale_bytes", "pad_k", "pad_n"]
+           "q8_mlp_workspace_bytes", "code_bytes", "scale_bytes", "pad_k", "pad_n",
+           "decode_view", "decode_desc", "decode_mmv", "decode_mmv_paired", "decode_mmv_ranges"]
 
 
 def pad_k(k: int) -> int:
@@ -204,3 +205,64 @@ def upload_q6k_blocks(blocks: torch.Tensor, n: int, k: int, stream=None) -> Pref
                                        codes.numel(), _ptr(scales), scales.numel(),
                                        _stream(stream)))
     return PrefillWeight(codes, scales, LAYOUT_Q6K_W64, QUANTIZER_Q6K, n, k, pn, pk)
+
+
+# ---- BF16-activation decode GEMV (cuda/decode_mmv.hpp) ----------------------
+DECODE_STORE_BF16, DECODE_STORE_FP32, DECODE_RESIDUAL_ADD_FP32, DECODE_SWIGLU_BF16 = 1, 2, 3, 4
+DTYPE_Q4, DTYPE_Q8, DTYPE_BF16, DTYPE_FP16, DTYPE_FP32 = 1, 2, 3, 4, 5
+LAYOUT_BF16_VECTOR, LAYOUT_FP32_VECTOR = 0x0205, 0x020A
+
+
+def decode_view(t, dtype, layout, logical_n, logical_k, padded_n, padded_k, alignment,
+                writable, nbytes=None):
+    """cuda::decode_matrix_view / decode_vector_view (cuda/decode_mmv.hpp:95-112)."""
+    from ._lib import DecodeView
+    if t is None:
+        return DecodeView()
+    b = t.numel() * t.element_size() if nbytes is None else nbytes
+    return DecodeView(t.data_ptr(), 1, dtype, layout, logical_n, logical_k, padded_n, padded_k,
+                      b, alignment, 1 if writable else 0)
+
+
+def decode_desc(w: PrefillWeight, x, output, epilogue=DECODE_STORE_FP32, residual=None,
+                output_view=True):
+    """A DecodeMmvDesc for a Q4_K (0x020D) weight, BF16 input x [k] (int16
+    tensor of BF16 bits), output [n] (FP32, or BF16 bits for the BF16
+    epilogues) and residual [n] FP32 for the residual epilogue. With
+    output=None and the residual epilogue the update is in place."""
+    from ._lib import DecodeDesc
+    d = DecodeDesc()
+    d.layout, d.quantizer, d.activation_policy = w.layout, w.quantizer, 1
+    d.n, d.k, d.padded_n, d.padded_k = w.n, w.k, w.padded_n, w.padded_k
+    d.codes = decode_view(w.codes, DTYPE_Q4, w.layout, w.n, w.k, w.padded_n, w.padded_k, 16, False)
+    units = w.scales.numel() * w.scales.element_size() // w.padded_n // 2
+    d.scales = decode_view(w.scales, DTYPE_FP16, w.layout, w.padded_n, units, w.padded_n, units, 2,
+                           False)
+    d.input = decode_view(x, DTYPE_BF16, LAYOUT_BF16_VECTOR, w.k, 1, w.k, 1, 2, False)
+    bf16_out = epilogue in (DECODE_STORE_BF16, DECODE_SWIGLU_BF16)
+    if output is not None and output_view:
+        d.output = decode_view(output, DTYPE_BF16 if bf16_out else DTYPE_FP32,
+                               LAYOUT_BF16_VECTOR if bf16_out else LAYOUT_FP32_VECTOR, w.n, 1, w.n,
+                               1, 2 if bf16_out else 4, True)
+    if residual is not None:
+        d.residual = decode_view(residual, DTYPE_FP32, LAYOUT_FP32_VECTOR, w.n, 1, w.n, 1, 4,
+                                 output is None)
+    d.epilogue = epilogue
+    return d
+
+
+def decode_mmv(desc, stream=None) -> None:
+    """cuda::launch_decode_mmv (cuda/decode_mmv.hpp:205-206)."""
+    check(lib().qw38_decode_mmv(C.byref(desc), _stream(stream)))
+
+
+def decode_mmv_paired(a, b, stream=None) -> None:
+    """cuda::launch_decode_mmv_paired (cuda/decode_mmv.hpp:208-209)."""
+    check(lib().qw38_decode_mmv_paired(C.byref(a), C.byref(b), _stream(stream)))
+
+
+def decode_mmv_ranges(descs, stream=None) -> None:
+    """cuda::launch_decode_mmv_ranges (cuda/decode_mmv.hpp:216-217)."""
+    from ._lib import DecodeDesc
+    arr = (DecodeDesc * len(descs))(*descs)
+    check(lib().qw38_decode_mmv_ranges(arr, len(descs), _stream(stream)))

@@ -92,3 +92,67 @@ def test_no_cpu_fallback_symbols():
     exported = re.findall(r" T (qw38_\w+)", out)
     assert exported and all(not re.search(r"cpu|host|oracle", s) for s in exported)
     assert "orc_" not in out
+
+
+def _decode_desc(n=40, k=512, epi=2):
+    """A decode_mmv descriptor over fake (never dereferenced) addresses; only
+    ever passed with one field broken, so validation rejects it before any
+    device call."""
+    pn, pk = (n + 7) // 8 * 8, (k + 255) // 256 * 256
+    V = _lib.DecodeView
+    d = _lib.DecodeDesc()
+    d.layout, d.quantizer, d.activation_policy = 0x020D, 0x0105, 1
+    d.n, d.k, d.padded_n, d.padded_k = n, k, pn, pk
+    d.codes = V(0x100000, 1, 1, 0x020D, n, k, pn, pk, pn * pk // 2, 16, 0)
+    units = pk // 256 * 8
+    d.scales = V(0x200000, 1, 4, 0x020D, pn, units, pn, units, pn * pk // 256 * 16, 2, 0)
+    d.input = V(0x300000, 1, 3, 0x0205, k, 1, k, 1, 2 * k, 2, 0)
+    d.output = V(0x400000, 1, 5 if epi == 2 else 3, 0x020A if epi == 2 else 0x0205, n, 1, n, 1,
+                 n * (4 if epi == 2 else 2), 4 if epi == 2 else 2, 1)
+    d.epilogue = epi
+    return d
+
+
+def test_decode_rejections_without_device():
+    L = qw38_amd.lib()
+    cases = []
+    d = _decode_desc(); d.quantizer = 0x0101; cases.append((d, "layout/quantizer"))
+    d = _decode_desc(); d.scales.bytes //= 2; cases.append((d, "scales typed view"))
+    d = _decode_desc(); d.padded_k = 768; cases.append((d, "padded N/K"))
+    d = _decode_desc(k=300); cases.append((d, "quantizer group"))
+    d = _decode_desc(k=17664); cases.append((d, "staging limit"))
+    d = _decode_desc(); d.codes.alignment = 8; cases.append((d, "codes typed view"))
+    d = _decode_desc(); d.output.writable = 0; cases.append((d, "output typed view"))
+    d = _decode_desc(); d.input.pointer = 0x100010; cases.append((d, "overlap"))
+    d = _decode_desc(); d.epilogue = 4; cases.append((d, "paired gate/up"))
+    d = _decode_desc(); d.epilogue = 9; cases.append((d, "unknown epilogue"))
+    d = _decode_desc(); d.activation_policy = 2; cases.append((d, "activation policy"))
+    d = _decode_desc(); d.residual = d.output; cases.append((d, "must not supply residual"))
+    for desc, needle in cases:
+        assert L.qw38_decode_mmv(C.byref(desc), None) == 2, needle
+        err = _lib.last_error()
+        assert err.operation.startswith("decode_mmv") and needle in err.detail, (needle, err.detail)
+    # a reference layout this build does not implement (Q8G32 V0, 1 B codes)
+    d = _decode_desc()
+    d.layout, d.quantizer = 0x0202, 0x0102
+    d.codes.layout = d.scales.layout = 0x0202
+    d.codes.dtype, d.codes.bytes = 2, d.padded_n * d.padded_k
+    d.scales.logical_k = d.scales.padded_k = d.padded_k // 32
+    d.scales.bytes = d.padded_n * d.padded_k // 32 * 2
+    assert L.qw38_decode_mmv(C.byref(d), None) == 2
+    assert "not implemented" in _lib.last_error().detail
+    # paired: B must match A; SwiGLU B declares no output
+    a, b = _decode_desc(), _decode_desc()
+    b.codes.pointer, b.scales.pointer, b.output.pointer = 0x500000, 0x600000, 0x700000
+    b.k = 256
+    assert L.qw38_decode_mmv_paired(C.byref(a), C.byref(b), None) == 2
+    a, b = _decode_desc(epi=4), _decode_desc(epi=4)
+    b.codes.pointer, b.scales.pointer = 0x500000, 0x600000
+    assert L.qw38_decode_mmv_paired(C.byref(a), C.byref(b), None) == 2
+    assert "separately materialized" in _lib.last_error().detail
+    # ranges: count and BF16 store contract
+    arr = (_lib.DecodeDesc * 1)(_decode_desc(epi=1))
+    assert L.qw38_decode_mmv_ranges(arr, 1, None) == 2
+    arr = (_lib.DecodeDesc * 2)(_decode_desc(epi=2), _decode_desc(epi=2))
+    assert L.qw38_decode_mmv_ranges(arr, 2, None) == 2
+    assert "store BF16" in _lib.last_error().detail
