@@ -178,6 +178,22 @@ def bench_decode_bf16(torch, ops, n, k, steps, warmup, seed=31):
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "layout": "0x020d", "steps": nsteps}
 
 
+def bench_prefill_bf16(torch, ops, n, k, m, steps, warmup, seed=41):
+    """BF16 PrefillEngine::project (Q4_K 0x020D operands rebuilt as BF16,
+    BF16 MFMA) on the config-4 shape."""
+    w, _ = make_weight(torch, ops, n, k, seed, 0x020D)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1)
+    x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
+    out = torch.empty(m, n, device="cuda")
+    ms_step, nsteps, mode = time_launches(
+        torch, lambda i: ops.prefill_project(w, x, m, out, ops.DECODE_STORE_FP32), 1, steps, warmup)
+    tf = 2.0 * m * n * k / (ms_step * 1e-3) / 1e12
+    log(f"prefill_bf16 N={n} K={k} M={m}: {ms_step*1e3:.1f} us/launch, {tf:.1f} TFLOP/s ({mode})")
+    return {"us": round(ms_step * 1e3, 2), "tflops": round(tf, 1),
+            "frac_bf16_mfma_peak": round(tf / FP16_PEAK_TFLOPS, 4), "m": m, "n": n, "k": k}
+
+
 def bench_mmq(torch, ops, n, k, m, steps, warmup, layout, seed=21):
     w, _ = make_weight(torch, ops, n, k, seed, layout)
     q, _ = make_q8(torch, ops, m, k, seed + 1)
@@ -258,6 +274,8 @@ def main():
     mmq = None if args.no_mmq else bench_mmq(torch, ops, n, k, 512, max(20, args.steps // 8),
                                               max(3, args.warmup // 4), layout)
     dbf16 = None if args.no_bf16 else bench_decode_bf16(torch, ops, n, k, args.steps, args.warmup)
+    pbf16 = None if (args.no_bf16 or args.no_mmq) else bench_prefill_bf16(
+        torch, ops, n, k, 512, max(20, args.steps // 8), max(3, args.warmup // 4))
     cpu = None
     if not args.no_cpu:
         _, blocks = make_weight(torch, ops, n, k, 11, layout)
@@ -292,6 +310,7 @@ def main():
                      for m, v in dec.items()},
         "mmq_m512": mmq,
         "decode_bf16_m1": dbf16,
+        "prefill_bf16_m512": pbf16,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -236,6 +236,39 @@ int qw38_decode_mmv_paired(const qw38_decode_desc* a, const qw38_decode_desc* b,
  * cuda/decode_mmv.cu:781-853): two or three BF16-store projections sharing
  * layout, K and input. */
 int qw38_decode_mmv_ranges(const qw38_decode_desc* ranges, uint32_t count, void* stream);
+/* ---- BF16 prefill projections (cuda/prefill.hpp) -------------------------
+ * Stateless C-ABI under qw38::cuda::PrefillEngine (cuda/prefill.hpp:72-160):
+ * BF16 token-major activations [tokens][k] times a Q4_K 0x020D weight whose
+ * operands are rebuilt as BF16 exactly as decode_mmv does, FP32 accumulation
+ * on the matrix cores. Epilogue IDs are PrefillEpilogue's (cuda/prefill.hpp:
+ * 46-50): QW38_DECODE_STORE_BF16 / _STORE_FP32 / _RESIDUAL_ADD_FP32. Weights
+ * with other layouts are rejected as not implemented on this build. */
+#define QW38_PREFILL_MAX_K 17408u
+
+/* Replaces PrefillEngine::project (cuda/prefill.cu:510-628) for Q4_K. output
+ * [tokens][n] BF16 or FP32; residual [tokens][n] FP32 only with the residual
+ * epilogue. */
+int qw38_prefill_project(const qw38_weight* weight, const uint16_t* input, uint32_t tokens,
+                         void* output, const float* residual, int epilogue, void* stream);
+/* Replaces PrefillEngine::paired_swiglu (cuda/prefill.cu:630-715): swiglu
+ * [tokens][n] BF16 = BF16(SiLU(X gate^T) * (X up^T)). */
+int qw38_prefill_paired_swiglu(const qw38_weight* gate, const qw38_weight* up,
+                               const uint16_t* normalized, uint16_t* swiglu, uint32_t tokens,
+                               void* stream);
+/* Replaces launch_hidden_rms (cuda/activation.hpp, cuda/activation.cu:477-
+ * 500): the zero-centred RMS of hidden 5120 written as BF16 [m][5120]. */
+int qw38_hidden_rms_bf16(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                         uint16_t* output, void* stream);
+/* Workspace of qw38_prefill_mlp: BF16 normalized [tokens][5120] and SwiGLU
+ * [tokens][17408] (the PrefillEngine's normalized_/swiglu_ buffers,
+ * cuda/prefill.cu:388-397). */
+uint64_t qw38_prefill_mlp_workspace_bytes(uint32_t tokens);
+/* Replaces PrefillEngine::mlp (cuda/prefill.cu:717-779): RMS -> BF16, paired
+ * gate/up SwiGLU, down projection + residual into next_h [tokens][5120]. */
+int qw38_prefill_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
+                     const float* h_mid, const uint16_t* gamma, float eps, float* next_h,
+                     uint32_t tokens, void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Byte sizes of a tiled weight (cuda/decode_mmv.hpp:330-369 for 0x020D,
  * extended with this build's layouts). 0 for an unknown layout. */
 uint64_t qw38_code_bytes(uint16_t layout, uint32_t padded_n, uint32_t padded_k);

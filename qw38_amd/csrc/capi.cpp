@@ -398,6 +398,20 @@ int decode_launch(const DDesc& a, const DDesc* b, void* stream, const char* op) 
   return e == hipSuccess ? ok() : hip_fail(e, op);
 }
 
+// ---- BF16 prefill contract (cuda/prefill.cu:434-466, 510-560, restated) ----
+int prefill_weight(const qw38_weight& w, uint32_t tokens, const char* op) {
+  if (!tokens || tokens > QW38_PROJECT_MAX_TOKENS || !w.codes || !w.n || !w.k ||
+      w.k > QW38_PREFILL_MAX_K || w.padded_n != pad_n(w.n) || w.padded_k != pad_k(w.k) ||
+      w.k % 256 || w.quantizer != QW38_QUANTIZER_Q4K ||
+      (w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2 && w.layout != QW38_LAYOUT_Q4K_WAVE64) ||
+      w.codes_bytes != qw38_code_bytes(w.layout, w.padded_n, w.padded_k) ||
+      w.scales_bytes != qw38_scale_bytes(w.layout, w.padded_n, w.padded_k) || !w.scales)
+    return fail(QW38_INVALID_ARGUMENT, op, "weight, layout or token contract mismatch");
+  if (w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2)
+    return fail(QW38_INVALID_ARGUMENT, op, "prefill layout not implemented on this build");
+  return QW38_OK;
+}
+
 hipError_t project(const qw38_weight& w, const Q8View& x, float* out, const float* residual,
                    hipStream_t s) {
   if (x.m <= 8) return launch_gemv(view(w), x, out, residual, s);
@@ -738,6 +752,121 @@ int qw38_decode_mmv_ranges(const qw38_decode_desc* ranges, uint32_t count, void*
   for (uint32_t i = 0; i < count; ++i)
     if (int st = decode_launch(ranges[i], nullptr, stream, op)) return st;
   return ok();
+}
+
+int qw38_prefill_project(const qw38_weight* weight, const uint16_t* input, uint32_t tokens,
+                         void* output, const float* residual, int epilogue, void* stream) {
+  constexpr const char* op = "prefill.project";
+  if (!weight) return fail(QW38_INVALID_ARGUMENT, op, "null weight");
+  const qw38_weight& w = *weight;
+  if (int st = prefill_weight(w, tokens, "prefill.weight")) return st;
+  const bool res = epilogue == QW38_DECODE_RESIDUAL_ADD_FP32;
+  if (!input || !output || res != (residual != nullptr) ||
+      (epilogue != QW38_DECODE_STORE_BF16 && epilogue != QW38_DECODE_STORE_FP32 && !res))
+    return fail(QW38_INVALID_ARGUMENT, op, "input, output, position or epilogue contract mismatch");
+  const uint32_t ob = epilogue == QW38_DECODE_STORE_BF16 ? 2u : 4u;
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{w.codes, w.codes_bytes, 2},
+                         {w.scales, w.scales_bytes, 2},
+                         {input, uint64_t(tokens) * w.k * 2, 2},
+                         {output, uint64_t(tokens) * w.n * ob, ob},
+                         {residual, res ? uint64_t(tokens) * w.n * 4 : 0, 4}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  hipError_t e = launch_prefill_bf16(view(w), nullptr, input, tokens, output, residual, epilogue,
+                                     static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_prefill_paired_swiglu(const qw38_weight* gate, const qw38_weight* up,
+                               const uint16_t* normalized, uint16_t* swiglu, uint32_t tokens,
+                               void* stream) {
+  constexpr const char* op = "prefill.swiglu";
+  if (!gate || !up) return fail(QW38_INVALID_ARGUMENT, op, "null weight");
+  if (int st = prefill_weight(*gate, tokens, "prefill.weight")) return st;
+  if (int st = prefill_weight(*up, tokens, "prefill.weight")) return st;
+  if (!normalized || !swiglu || gate->n != up->n || gate->k != up->k ||
+      gate->layout != up->layout || gate->quantizer != up->quantizer)
+    return fail(QW38_INVALID_ARGUMENT, op, "paired weight or activation contract mismatch");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{gate->codes, gate->codes_bytes, 2},
+                         {gate->scales, gate->scales_bytes, 2},
+                         {up->codes, up->codes_bytes, 2},
+                         {up->scales, up->scales_bytes, 2},
+                         {normalized, uint64_t(tokens) * gate->k * 2, 2},
+                         {swiglu, uint64_t(tokens) * gate->n * 2, 2}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  const WeightView u = view(*up);
+  hipError_t e = launch_prefill_bf16(view(*gate), &u, normalized, tokens, swiglu, nullptr,
+                                     QW38_DECODE_STORE_BF16, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_hidden_rms_bf16(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                         uint16_t* output, void* stream) {
+  constexpr const char* op = "hidden_rms";
+  if (!residual || !gamma || !output) return fail(QW38_INVALID_ARGUMENT, op, "null residual, gamma, or out");
+  if (!m || m > QW38_PROJECT_MAX_TOKENS || !std::isfinite(eps) || eps <= 0.f)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid token count or epsilon");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{residual, uint64_t(m) * 5120 * 4, 4}, {gamma, 5120 * 2, 2},
+                         {output, uint64_t(m) * 5120 * 2, 2}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  hipError_t e = launch_rms_bf16(residual, gamma, eps, m, output, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+uint64_t qw38_prefill_mlp_workspace_bytes(uint32_t tokens) {
+  return uint64_t(tokens) * (5120u * 2u + 17408u * 2u);
+}
+
+int qw38_prefill_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
+                     const float* h_mid, const uint16_t* gamma, float eps, float* next_h,
+                     uint32_t tokens, void* workspace, uint64_t workspace_bytes, void* stream) {
+  constexpr const char* op = "prefill.mlp";
+  if (!gate || !up || !down || !h_mid || !gamma || !next_h || !workspace ||
+      !std::isfinite(eps) || eps <= 0.f || gate->n != 17408 || gate->k != 5120 ||
+      down->n != 5120 || down->k != 17408 || up->n != gate->n || up->k != gate->k ||
+      up->layout != gate->layout || up->quantizer != gate->quantizer ||
+      workspace_bytes < qw38_prefill_mlp_workspace_bytes(tokens))
+    return fail(QW38_INVALID_ARGUMENT, op, "MLP shape or pointer contract mismatch");
+  for (const qw38_weight* w : {gate, up, down})
+    if (int st = prefill_weight(*w, tokens, "prefill.weight")) return st;
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  const uint64_t act = uint64_t(tokens) * 5120;
+  if (int st = distinct({{h_mid, act * 4, 4}, {next_h, act * 4, 4}, {gamma, 5120 * 2, 2},
+                         {workspace, qw38_prefill_mlp_workspace_bytes(tokens), 2},
+                         {gate->codes, gate->codes_bytes, 2}, {gate->scales, gate->scales_bytes, 2},
+                         {up->codes, up->codes_bytes, 2}, {up->scales, up->scales_bytes, 2},
+                         {down->codes, down->codes_bytes, 2}, {down->scales, down->scales_bytes, 2}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* normalized = static_cast<uint16_t*>(workspace);
+  uint16_t* sw = normalized + act;
+  hipError_t e = launch_rms_bf16(h_mid, gamma, eps, tokens, normalized, s);
+  const WeightView u = view(*up);
+  if (e == hipSuccess)
+    e = launch_prefill_bf16(view(*gate), &u, normalized, tokens, sw, nullptr,
+                            QW38_DECODE_STORE_BF16, s);
+  if (e == hipSuccess)
+    e = launch_prefill_bf16(view(*down), nullptr, sw, tokens, next_h, h_mid,
+                            QW38_DECODE_RESIDUAL_ADD_FP32, s);
+  return e == hipSuccess ? ok() : hip_fail(e, op);
 }
 
 int qw38_quantize_q4k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_t k,

@@ -147,6 +147,8 @@ hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t p
 hipError_t launch_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
                          int8_t* codes, float* scales, int32_t* sums, int* failure,
                          hipStream_t s);
+hipError_t launch_rms_bf16(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                           uint16_t* out, hipStream_t s);
 hipError_t launch_swiglu_q8(const float* gate, const float* up, uint32_t m, uint32_t n,
                             int8_t* codes, float* scales, int32_t* sums, int* failure,
                             hipStream_t s);
@@ -159,6 +161,9 @@ hipError_t launch_gemv_w64(const WeightView& w, const Q8View& x, float* out,
                            const float* residual, hipStream_t s);
 hipError_t launch_mmq(const WeightView& w, const Q8View& x, float* out,
                       const float* residual, hipStream_t s);
+hipError_t launch_prefill_bf16(const WeightView& a, const WeightView* b, const uint16_t* x,
+                               uint32_t m, void* out, const float* residual, int epilogue,
+                               hipStream_t s);
 hipError_t launch_decode_bf16(const WeightView& a, const WeightView* b, const uint16_t* x,
                               void* out_a, void* out_b, const float* res_a, const float* res_b,
                               int epilogue, hipStream_t s);

@@ -1,0 +1,224 @@
+// BF16 prefill projection over Q4_K weights (layout 0x020D) on gfx950 matrix
+// cores: Y[m][n] = X[m][k] (BF16) * W^T, W rebuilt as BF16 operands.
+//
+// Semantics (cuda/prefill.cu:62-77, 116-142, 510-715): every weight is the
+// BF16 operand BF16_RNE(fl(fl(d * s_g) * c) - fl(dmin * m_g)) -- the same
+// operand as the BF16 decode GEMV, built here with fma(ds, c, -dm), which is
+// bit-identical because fl(d * s) * c is exact -- and the products with the
+// BF16 activations are summed in FP32 (v_mfma_f32_16x16x32_bf16, the matrix
+// core accumulating over all of K). Epilogues: StoreBf16, StoreFp32,
+// ResidualAddFp32; the paired gate/up launch writes BF16(SiLU(g) * u).
+//
+// Block: 128 weight rows x 64 tokens, four waves as 2 x 2, each a 64 x 32
+// wave tile of 16x16 outputs. Per 64-wide K step every thread rebuilds one
+// (row, K32 group) of the weight tile (v_cvt_pk_bf16_f32 on pairs) and copies
+// a quarter of a (token, K32 group) activation row; operands for step s+1
+// are loaded into registers while step s runs on the matrix cores.
+#include "common.hpp"
+
+namespace qw38hip {
+namespace {
+
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef float fl2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRows = 128, kToks = 64, kStride = 72;  // LDS row: 64 BF16 + 8 pad
+
+// Loads of one K step.
+struct WFetch {
+  uint32_t c[4];  // 16 code bytes of (row, group): sequential nibbles
+  uint32_t m[4];  // the super-block's metadata row
+};
+
+template <bool Fast>
+__device__ __forceinline__ void fetch_w(const uint8_t* codes, const uint8_t* meta, uint64_t tr,
+                                        uint32_t g, WFetch& f) {
+  const uint8_t* cp = codes + tr * 128 + g * 16;
+  const uint8_t* mp = meta + tr * 16;
+  if constexpr (Fast) {
+    const uint4 cv = *reinterpret_cast<const uint4*>(cp);
+    const uint4 mv = *reinterpret_cast<const uint4*>(mp);
+    f.c[0] = cv.x; f.c[1] = cv.y; f.c[2] = cv.z; f.c[3] = cv.w;
+    f.m[0] = mv.x; f.m[1] = mv.y; f.m[2] = mv.z; f.m[3] = mv.w;
+  } else {  // 2-byte aligned spans (the reference's minimum)
+    const uint16_t* c2 = reinterpret_cast<const uint16_t*>(cp);
+    const uint16_t* m2 = reinterpret_cast<const uint16_t*>(mp);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f.c[i] = uint32_t(c2[2 * i]) | (uint32_t(c2[2 * i + 1]) << 16);
+      f.m[i] = uint32_t(m2[2 * i]) | (uint32_t(m2[2 * i + 1]) << 16);
+    }
+  }
+}
+
+// 32 BF16 operands of (row, group g) into LDS (64 B).
+__device__ __forceinline__ void store_w(const WFetch& f, uint32_t g, _Float16* dst_h) {
+  float s, m;
+  q4_scale_min_lane(f.m[1], f.m[2], f.m[3], g, s, m);
+  const float ds = f16_to_f32(f.m[0] & 0xffffu) * s;            // exact
+  const float ndm = -(f16_to_f32(f.m[0] >> 16) * m);           // exact
+  uint32_t o[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // code word i = codes 8i..8i+7 (byte b: codes 2b, 2b+1)
+    const uint32_t lo = f.c[i] & 0x0f0f0f0fu, hv = (f.c[i] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const fl2 wv = {fmaf(ds, float((lo >> (8 * q)) & 0xffu), ndm),
+                      fmaf(ds, float((hv >> (8 * q)) & 0xffu), ndm)};
+      o[4 * i + q] = __builtin_bit_cast(uint32_t, __builtin_convertvector(wv, bf2));
+    }
+  }
+  uint4* dst = reinterpret_cast<uint4*>(dst_h);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+}
+
+__device__ __forceinline__ float silu(float z) {
+  float sg;
+  if (z >= 0.f) {
+    sg = 1.f / (1.f + exp_cw(-z));
+  } else {
+    const float e = exp_cw(z);
+    sg = e / (1.f + e);
+  }
+  return z * sg;
+}
+
+template <bool Paired, bool Fast>
+__global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(
+    const uint8_t* __restrict__ codes_a, const uint8_t* __restrict__ meta_a,
+    const uint8_t* __restrict__ codes_b, const uint8_t* __restrict__ meta_b, uint32_t n,
+    uint32_t k, const uint16_t* __restrict__ x, uint32_t m, void* out,
+    const float* __restrict__ residual, int epi, uint32_t row_blocks, uint32_t tok_blocks) {
+  constexpr int NW = Paired ? 2 : 1;
+  __shared__ __align__(16) _Float16 As[NW][kRows * kStride];
+  __shared__ __align__(16) _Float16 Bs[kToks * kStride];
+
+  const uint32_t nblk = row_blocks * tok_blocks;
+  const uint32_t b = blockIdx.x;
+  const uint32_t tile = (nblk % 8 == 0) ? (b % 8) * (nblk / 8) + b / 8 : b;  // XCD-contiguous
+  const uint32_t row0 = (tile / tok_blocks) * kRows, tok0 = (tile % tok_blocks) * kToks;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t wr = wave >> 1, wt = wave & 1u, lr = lane & 15u, lk = lane >> 4;
+  const uint32_t kbs = k / 256, steps = k / 64;
+  const uint32_t pn8 = (n + 7) / 8 * 8;
+
+  // A role: row ar (clamped), group-in-step asel. B role: token bt, 16 B part bp.
+  const uint32_t ar = tid >> 1, asel = tid & 1u;
+  const uint32_t arow = min(row0 + ar, pn8 - 1);
+  const uint64_t trow0 = uint64_t(arow / 8) * kbs * 8 + arow % 8;
+  const uint32_t bt = tid >> 2, bp = tid & 3u;
+  const uint16_t* xrow = x + size_t(min(tok0 + bt, m - 1)) * k + bp * 16;
+
+  f4 acc[NW][4][2];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[w][i][j] = f4{0, 0, 0, 0};
+
+  WFetch fa, fb;
+  uint32_t xv[8];
+  auto fetch = [&](uint32_t s) {
+    const uint32_t kb = s >> 2, g = 2 * (s & 3u) + asel;
+    fetch_w<Fast>(codes_a, meta_a, trow0 + kb * 8, g, fa);
+    if constexpr (Paired) fetch_w<Fast>(codes_b, meta_b, trow0 + kb * 8, g, fb);
+    const uint16_t* xp = xrow + s * 64;
+    if constexpr (Fast) {
+      const uint4 v0 = reinterpret_cast<const uint4*>(xp)[0];
+      const uint4 v1 = reinterpret_cast<const uint4*>(xp)[1];
+      xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
+      xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[i] = uint32_t(xp[2 * i]) | (uint32_t(xp[2 * i + 1]) << 16);
+    }
+  };
+
+  fetch(0);
+  for (uint32_t s = 0; s < steps; ++s) {
+    __syncthreads();  // previous step's tiles fully read
+    const uint32_t g = 2 * (s & 3u) + asel;
+    store_w(fa, g, &As[0][ar * kStride + asel * 32]);
+    if constexpr (Paired) store_w(fb, g, &As[NW - 1][ar * kStride + asel * 32]);
+    {
+      uint4* dst = reinterpret_cast<uint4*>(&Bs[bt * kStride + bp * 16]);
+      dst[0] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+      dst[1] = make_uint4(xv[4], xv[5], xv[6], xv[7]);
+    }
+    __syncthreads();
+    if (s + 1 < steps) fetch(s + 1);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf8 bfr[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bfr[j] = *reinterpret_cast<const bf8*>(&Bs[(wt * 32 + j * 16 + lr) * kStride + ks * 32 + lk * 8]);
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bf8 afr = *reinterpret_cast<const bf8*>(
+              &As[w][(wr * 64 + i * 16 + lr) * kStride + ks * 32 + lk * 8]);
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[w][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr, bfr[j], acc[w][i][j], 0, 0, 0);
+        }
+    }
+  }
+
+  // ---- epilogue: lane holds rows 4 lk .. 4 lk + 3 of token lr in each tile ----
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t tok = tok0 + wt * 32 + j * 16 + lr;
+      if (tok >= m) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const uint32_t row = row0 + wr * 64 + i * 16 + lk * 4 + v;
+        if (row >= n) continue;
+        const size_t o = size_t(tok) * n + row;
+        const float y = acc[0][i][j][v];
+        if constexpr (Paired) {
+          static_cast<uint16_t*>(out)[o] = f32_to_bf16_rne(silu(y) * acc[NW - 1][i][j][v]);
+        } else if (epi == QW38_DECODE_STORE_BF16) {
+          static_cast<uint16_t*>(out)[o] = f32_to_bf16_rne(y);
+        } else if (epi == QW38_DECODE_STORE_FP32) {
+          static_cast<float*>(out)[o] = y;
+        } else {
+          static_cast<float*>(out)[o] = residual[o] + y;
+        }
+      }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_prefill_bf16(const WeightView& a, const WeightView* b, const uint16_t* x,
+                               uint32_t m, void* out, const float* residual, int epilogue,
+                               hipStream_t s) {
+  if (a.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2 || a.pk != a.k) return hipErrorInvalidValue;
+  auto al = [](const void* p, uintptr_t q) { return reinterpret_cast<uintptr_t>(p) % q == 0; };
+  const bool fast = al(a.codes, 16) && al(a.scales, 16) && al(x, 16) && a.k % 8 == 0 &&
+                    (!b || (al(b->codes, 16) && al(b->scales, 16)));
+  const uint32_t row_blocks = (a.n + kRows - 1) / kRows, tok_blocks = (m + kToks - 1) / kToks;
+  const dim3 grid(row_blocks * tok_blocks);
+  const uint8_t* cb = b ? b->codes : nullptr;
+  const uint8_t* mb = b ? b->scales : nullptr;
+#define QW38_PF_LAUNCH(P, F)                                                                   \
+  hipLaunchKernelGGL((prefill_bf16_kernel<P, F>), grid, dim3(256), 0, s, a.codes, a.scales, cb, mb, \
+                     a.n, a.k, x, m, out, residual, epilogue, row_blocks, tok_blocks)
+  if (b) {
+    if (fast) QW38_PF_LAUNCH(true, true); else QW38_PF_LAUNCH(true, false);
+  } else {
+    if (fast) QW38_PF_LAUNCH(false, true); else QW38_PF_LAUNCH(false, false);
+  }
+#undef QW38_PF_LAUNCH
+  return hipGetLastError();
+}
+
+}  // namespace qw38hip

@@ -80,13 +80,17 @@ constexpr uint32_t kHidden = 5120;
 
 // cuda/activation.cu:134-190 (Pack == 3): absmax prescale, sum of squares,
 // (1+gamma)*x/rms -> BF16 RNE -> Q8. FMAs where nvcc contracts mul+add.
-__global__ __launch_bounds__(256) void rms_q8_kernel(const float* __restrict__ residual,
-                                                     const uint16_t* __restrict__ gamma,
-                                                     float eps, int8_t* codes, float* scales,
-                                                     int32_t* sums, int* failure) {
-  __shared__ uint16_t rounded[kHidden];
+// Pack: BF16 -> Q8 pack (hidden_rms_kernel<3>); otherwise the BF16 values are
+// the output (hidden_rms_kernel<0>, cuda/activation.cu:134-190).
+template <bool Pack>
+__global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ residual,
+                                                  const uint16_t* __restrict__ gamma, float eps,
+                                                  uint16_t* out_bf16, int8_t* codes, float* scales,
+                                                  int32_t* sums, int* failure) {
+  __shared__ uint16_t rounded[Pack ? kHidden : 1];
   __shared__ float sm[9];
   const float* x = residual + size_t(blockIdx.x) * kHidden;
+  uint16_t* y = Pack ? rounded : out_bf16 + size_t(blockIdx.x) * kHidden;
   float s = 0.f;
   for (uint32_t i = threadIdx.x; i < kHidden; i += 256) s = fmaxf(s, fabsf(x[i]));
   const float scale = block256<true>(s, sm);
@@ -101,12 +105,14 @@ __global__ __launch_bounds__(256) void rms_q8_kernel(const float* __restrict__ r
   const float inv = 1.0f / sqrtf(fmaf(se, se, sumsq / float(kHidden)));
   for (uint32_t i = threadIdx.x; i < kHidden; i += 256) {
     const float g = bf16_to_f32(gamma[i]);
-    rounded[i] = f32_to_bf16_rne((1.0f + g) * ((x[i] / safe) * inv));
+    y[i] = f32_to_bf16_rne((1.0f + g) * ((x[i] / safe) * inv));
   }
-  __syncthreads();
-  for (uint32_t i = threadIdx.x; i < kHidden; i += 256)
-    q8_group32(bf16_to_f32(rounded[i]), codes, scales, sums,
-               (size_t(blockIdx.x) * kHidden + i) / 32, failure);
+  if constexpr (Pack) {
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < kHidden; i += 256)
+      q8_group32(bf16_to_f32(rounded[i]), codes, scales, sums,
+                 (size_t(blockIdx.x) * kHidden + i) / 32, failure);
+  }
 }
 
 // cuda/q4k_q8.cu:52-61: v = BF16(SiLU(g) * u); nonfinite g/u -> NaN -> flag.
@@ -139,8 +145,15 @@ hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t p
 hipError_t launch_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
                          int8_t* codes, float* scales, int32_t* sums, int* failure,
                          hipStream_t s) {
-  hipLaunchKernelGGL(rms_q8_kernel, dim3(m), dim3(256), 0, s, residual, gamma, eps, codes,
-                     scales, sums, failure);
+  hipLaunchKernelGGL(rms_kernel<true>, dim3(m), dim3(256), 0, s, residual, gamma, eps, nullptr,
+                     codes, scales, sums, failure);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_bf16(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                           uint16_t* out, hipStream_t s) {
+  hipLaunchKernelGGL(rms_kernel<false>, dim3(m), dim3(256), 0, s, residual, gamma, eps, out,
+                     nullptr, nullptr, nullptr, nullptr);
   return hipGetLastError();
 }
 

@@ -19,7 +19,9 @@ from ._lib import (LAYOUT_Q4K_SEQ, LAYOUT_Q4K_W64, LAYOUT_Q6K_W64, QUANTIZER_Q4K
 __all__ = ["PrefillWeight", "Q8Input", "pack_q8", "q4k_q8_project", "q4k_q8_mlp",
            "hidden_rms_q8", "swiglu_q8", "group_dots", "quantize_q4k_blocks", "quantize_q6k_blocks", "upload_q4k_blocks", "upload_q6k_blocks",
            "q8_mlp_workspace_bytes", "code_bytes", "scale_bytes", "pad_k", "pad_n",
-           "decode_view", "decode_desc", "decode_mmv", "decode_mmv_paired", "decode_mmv_ranges"]
+           "decode_view", "decode_desc", "decode_mmv", "decode_mmv_paired", "decode_mmv_ranges",
+           "prefill_project", "prefill_paired_swiglu", "hidden_rms_bf16", "prefill_mlp",
+           "prefill_mlp_workspace_bytes"]
 
 
 def pad_k(k: int) -> int:
@@ -266,3 +268,36 @@ def decode_mmv_ranges(descs, stream=None) -> None:
     from ._lib import DecodeDesc
     arr = (DecodeDesc * len(descs))(*descs)
     check(lib().qw38_decode_mmv_ranges(arr, len(descs), _stream(stream)))
+
+
+# ---- BF16 prefill projections (cuda/prefill.hpp) ----------------------------
+def prefill_project(w: PrefillWeight, x, tokens: int, output, epilogue=DECODE_STORE_FP32,
+                    residual=None, stream=None) -> None:
+    """PrefillEngine::project for Q4_K: x BF16 bits [tokens][k] -> output."""
+    check(lib().qw38_prefill_project(C.byref(w.struct()), x.data_ptr(), tokens, output.data_ptr(),
+                                     _ptr(residual), epilogue, _stream(stream)))
+
+
+def prefill_paired_swiglu(gate: PrefillWeight, up: PrefillWeight, normalized, swiglu, tokens,
+                          stream=None) -> None:
+    """PrefillEngine::paired_swiglu: BF16(SiLU(X gate^T) * (X up^T))."""
+    check(lib().qw38_prefill_paired_swiglu(C.byref(gate.struct()), C.byref(up.struct()),
+                                           normalized.data_ptr(), swiglu.data_ptr(), tokens,
+                                           _stream(stream)))
+
+
+def hidden_rms_bf16(residual, gamma, eps, m, output, stream=None) -> None:
+    """launch_hidden_rms: RMS over hidden 5120 -> BF16 [m][5120]."""
+    check(lib().qw38_hidden_rms_bf16(residual.data_ptr(), gamma.data_ptr(), float(eps), m,
+                                     output.data_ptr(), _stream(stream)))
+
+
+def prefill_mlp_workspace_bytes(tokens: int) -> int:
+    return int(lib().qw38_prefill_mlp_workspace_bytes(tokens))
+
+
+def prefill_mlp(gate, up, down, h_mid, gamma, eps, next_h, tokens, workspace, stream=None):
+    """PrefillEngine::mlp: RMS -> BF16 -> paired SwiGLU -> down + residual."""
+    check(lib().qw38_prefill_mlp(C.byref(gate.struct()), C.byref(up.struct()), C.byref(down.struct()),
+                                 h_mid.data_ptr(), gamma.data_ptr(), float(eps), next_h.data_ptr(),
+                                 tokens, workspace.data_ptr(), workspace.numel(), _stream(stream)))
