@@ -7,8 +7,8 @@
  *
  * Each declaration names the reference interface it replaces (paths are in the
  * Enucatl/qw38 tree). The C++ mirror of those interfaces (namespace
- * qw38::cuda, headers under qw38_amd/cpp/cuda/) is implemented on top of this
- * ABI.
+ * qw38::cuda, headers under qw38_amd/cpp/cuda/, sources under
+ * qw38_amd/cpp/src/) is implemented on top of this ABI.
  */
 #ifndef QW38_HIP_H
 #define QW38_HIP_H
@@ -282,6 +282,10 @@ uint64_t qw38_malloc_count(void);
 uint64_t qw38_free_count(void);
 uint64_t qw38_live_bytes(void);
 uint64_t qw38_peak_live_bytes(void);
+/* Accounting of allocations made outside qw38_device_malloc
+ * (cuda::record_malloc / record_free, cuda/alloc.hpp:15-16). */
+void qw38_record_malloc(uint64_t bytes);
+void qw38_record_free(uint64_t bytes);
 
 #ifdef __cplusplus
 }

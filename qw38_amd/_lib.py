@@ -98,6 +98,8 @@ SIGNATURES = {
     "qw38_free_count": (_U64, []),
     "qw38_live_bytes": (_U64, []),
     "qw38_peak_live_bytes": (_U64, []),
+    "qw38_record_malloc": (None, [_U64]),
+    "qw38_record_free": (None, [_U64]),
 }
 
 

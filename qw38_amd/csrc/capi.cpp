@@ -927,4 +927,17 @@ uint64_t qw38_free_count(void) { return g_frees.load(); }
 uint64_t qw38_live_bytes(void) { return g_live.load(); }
 uint64_t qw38_peak_live_bytes(void) { return g_peak.load(); }
 
+void qw38_record_malloc(uint64_t bytes) {
+  g_mallocs.fetch_add(1);
+  const uint64_t live = g_live.fetch_add(bytes) + bytes;
+  uint64_t peak = g_peak.load();
+  while (live > peak && !g_peak.compare_exchange_weak(peak, live)) {
+  }
+}
+
+void qw38_record_free(uint64_t bytes) {
+  g_frees.fetch_add(1);
+  g_live.fetch_sub(std::min<uint64_t>(bytes, g_live.load()));
+}
+
 }  // extern "C"
