@@ -14,6 +14,8 @@
 // (row, K32 group) of the weight tile (v_cvt_pk_bf16_f32 on pairs) and copies
 // a quarter of a (token, K32 group) activation row; operands for step s+1
 // are loaded into registers while step s runs on the matrix cores.
+#include <cstdlib>
+
 #include "common.hpp"
 
 namespace qw38hip {
@@ -24,7 +26,11 @@ typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float fl2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kRows = 128, kToks = 64, kStride = 72;  // LDS row: 64 BF16 + 8 pad
+constexpr int kRows = 128, kToks = 64;
+// LDS row stride in halfs: 64 BF16 + 16 pad. A stride of 40 dwords (an odd
+// multiple of 8) keeps the wave's b128 fragment reads free of bank conflicts on
+// the 64-bank LDS; 36 dwords (64 + 8 halfs) halves the read rate.
+constexpr int kStride = 80;
 
 // Loads of one K step.
 struct WFetch {
@@ -196,6 +202,128 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(
     }
 }
 
+// Large-M variant: 256 weight rows x 128 tokens per block, eight waves as
+// 4 x 2 with 64 x 64 wave tiles (sixteen independent accumulators each, so
+// the matrix core never waits on its own results). LDS is double-buffered:
+// one barrier per 64-wide K step separates the staging of step s+1 from the
+// last reads of that buffer at step s-1, and step s+2's operands are loaded
+// into registers while step s runs.
+template <bool Fast>
+__global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n, uint32_t k,
+    const uint16_t* __restrict__ x, uint32_t m, void* out, const float* __restrict__ residual,
+    int epi, uint32_t row_blocks, uint32_t tok_blocks) {
+  constexpr int BR = 256, BT = 128;
+  __shared__ __align__(16) _Float16 As[2][BR * kStride];
+  __shared__ __align__(16) _Float16 Bs[2][BT * kStride];
+
+  const uint32_t nblk = row_blocks * tok_blocks, b = blockIdx.x;
+  const uint32_t tile = (nblk % 8 == 0) ? (b % 8) * (nblk / 8) + b / 8 : b;
+  const uint32_t row0 = (tile / tok_blocks) * BR, tok0 = (tile % tok_blocks) * BT;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t wr = wave >> 1, wt = wave & 1u, lr = lane & 15u, lk = lane >> 4;
+  const uint32_t kbs = k / 256, steps = k / 64;
+  const uint32_t pn8 = (n + 7) / 8 * 8;
+
+  const uint32_t ar = tid >> 1, asel = tid & 1u;
+  const uint32_t arow = min(row0 + ar, pn8 - 1);
+  const uint64_t trow0 = uint64_t(arow / 8) * kbs * 8 + arow % 8;
+  const uint32_t bt = tid >> 2, bp = tid & 3u;
+  const uint16_t* xrow = x + size_t(min(tok0 + bt, m - 1)) * k + bp * 16;
+
+  f4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0, 0, 0, 0};
+
+  WFetch fa;
+  uint32_t xv[8];
+  auto fetch = [&](uint32_t s) {
+    fetch_w<Fast>(codes, meta, trow0 + (s >> 2) * 8, 2 * (s & 3u) + asel, fa);
+    const uint16_t* xp = xrow + s * 64;
+    if constexpr (Fast) {
+      const uint4 v0 = reinterpret_cast<const uint4*>(xp)[0];
+      const uint4 v1 = reinterpret_cast<const uint4*>(xp)[1];
+      xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
+      xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[i] = uint32_t(xp[2 * i]) | (uint32_t(xp[2 * i + 1]) << 16);
+    }
+  };
+  auto store = [&](uint32_t s) {
+    const uint32_t buf = s & 1u;
+    store_w(fa, 2 * (s & 3u) + asel, &As[buf][ar * kStride + asel * 32]);
+    uint4* dst = reinterpret_cast<uint4*>(&Bs[buf][bt * kStride + bp * 16]);
+    dst[0] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+    dst[1] = make_uint4(xv[4], xv[5], xv[6], xv[7]);
+  };
+
+  // Fragment reads of a K step are issued before the staging work that
+  // follows the barrier (and those of its second half before the first
+  // half's MFMAs), so LDS latency hides behind VALU and matrix-core work.
+  bf8 af[2][4], bf[2][4];
+  auto read_frags = [&](uint32_t buf, int ks) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      bf[ks][j] = *reinterpret_cast<const bf8*>(&Bs[buf][(wt * 64 + j * 16 + lr) * kStride + ks * 32 + lk * 8]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      af[ks][i] = *reinterpret_cast<const bf8*>(&As[buf][(wr * 64 + i * 16 + lr) * kStride + ks * 32 + lk * 8]);
+  };
+  auto mma = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
+  };
+
+  fetch(0);
+  store(0);
+  if (steps > 1) fetch(1);
+  for (uint32_t s = 0; s < steps; ++s) {
+    __syncthreads();
+    const uint32_t buf = s & 1u;
+    read_frags(buf, 0);
+    if (s + 1 < steps) store(s + 1);
+    if (s + 2 < steps) fetch(s + 2);
+    read_frags(buf, 1);
+    mma(0);
+    mma(1);
+  }
+
+  const bool vec = (n % 4 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t tok = tok0 + wt * 64 + j * 16 + lr;
+      const uint32_t r4 = row0 + wr * 64 + i * 16 + lk * 4;
+      if (tok >= m || r4 >= n) continue;
+      const size_t o = size_t(tok) * n + r4;
+      if (epi == QW38_DECODE_STORE_FP32 && vec) {
+        *reinterpret_cast<float4*>(static_cast<float*>(out) + o) =
+            make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        continue;
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (r4 + v >= n) continue;
+        const float y = acc[i][j][v];
+        if (epi == QW38_DECODE_STORE_BF16) {
+          static_cast<uint16_t*>(out)[o + v] = f32_to_bf16_rne(y);
+        } else if (epi == QW38_DECODE_STORE_FP32) {
+          static_cast<float*>(out)[o + v] = y;
+        } else {
+          static_cast<float*>(out)[o + v] = residual[o + v] + y;
+        }
+      }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_prefill_bf16(const WeightView& a, const WeightView* b, const uint16_t* x,
@@ -205,6 +333,22 @@ hipError_t launch_prefill_bf16(const WeightView& a, const WeightView* b, const u
   auto al = [](const void* p, uintptr_t q) { return reinterpret_cast<uintptr_t>(p) % q == 0; };
   const bool fast = al(a.codes, 16) && al(a.scales, 16) && al(x, 16) && a.k % 8 == 0 &&
                     (!b || (al(b->codes, 16) && al(b->scales, 16)));
+  // QW38_PREFILL_TILE=64|128 pins the token tile (tuning aid).
+  static const int forced = [] {
+    const char* e = std::getenv("QW38_PREFILL_TILE");
+    return e ? std::atoi(e) : 0;
+  }();
+  const bool big = !b && (forced ? forced == 128 : m > 64);
+  if (big) {
+    const uint32_t rb = (a.n + 255) / 256, tb = (m + 127) / 128;
+    if (fast)
+      hipLaunchKernelGGL((prefill_bf16_big_kernel<true>), dim3(rb * tb), dim3(512), 0, s, a.codes,
+                         a.scales, a.n, a.k, x, m, out, residual, epilogue, rb, tb);
+    else
+      hipLaunchKernelGGL((prefill_bf16_big_kernel<false>), dim3(rb * tb), dim3(512), 0, s, a.codes,
+                         a.scales, a.n, a.k, x, m, out, residual, epilogue, rb, tb);
+    return hipGetLastError();
+  }
   const uint32_t row_blocks = (a.n + kRows - 1) / kRows, tok_blocks = (m + kToks - 1) / kToks;
   const dim3 grid(row_blocks * tok_blocks);
   const uint8_t* cb = b ? b->codes : nullptr;

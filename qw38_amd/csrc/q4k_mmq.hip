@@ -37,7 +37,10 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kStride = 72;  // halfs per LDS tile row: 2 groups x 32 + 8 pad
+// Halfs per LDS tile row: 2 groups x 32 + 16 pad. A 40-dword stride (an odd
+// multiple of 8) keeps the b128 fragment reads free of bank conflicts on the
+// 64-bank LDS; a 36-dword stride (+8 pad) halves the read rate.
+constexpr int kStride = 80;
 
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -106,12 +109,12 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   constexpr int TPT = NT / BT, GPT = 8 / TPT;  // super-block token data: threads per token
   static_assert(TPT >= 1 && TPT <= 8 && GPT * TPT == 8, "token-data share");
   constexpr int kPlanes = kQ6 ? 2 : 1;  // Q6_K stages hi and lo FP16 planes
-  constexpr int kMinR = kQ6 ? 1 : BR * 16, kMinT = kQ6 ? 1 : BT * 16;
+  constexpr int kMinR = kQ6 ? 1 : BR * 8, kMinT = kQ6 ? 1 : BT * 8;
   __shared__ __align__(16) _Float16 As[2][kPlanes][BR * kStride];
   __shared__ __align__(16) _Float16 Bs[2][BT * kStride];
-  __shared__ __align__(16) _Float16 Mq[2][kMinR];  // m of groups 0..7, zeros 8..15
-  __shared__ __align__(16) _Float16 Uh[2][kMinT];  // scaled a*sum hi, zero padded
-  __shared__ __align__(16) _Float16 Ul[2][kMinT];  // scaled a*sum lo, zero padded
+  __shared__ __align__(16) _Float16 Mq[2][kMinR];  // m of groups 0..7 per row
+  __shared__ __align__(16) _Float16 Uh[2][kMinT];  // scaled a*sum hi per token
+  __shared__ __align__(16) _Float16 Ul[2][kMinT];  // scaled a*sum lo per token
   __shared__ float Ue[2][BT];                      // inverse of the per-token scale
   __shared__ float Aa[2][BT * 8];
   __shared__ float2 Dd[2][BR];                     // (d, dmin) | (d, 0)
@@ -148,15 +151,6 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     const uint64_t tr0 = uint64_t(arow / 8) * kbs * 8 + arow % 8;
     a_base = kQ6 ? tr0 : tr0 * 128 + asel * 16;
     m_base = tr0 * 16;
-  }
-
-  if constexpr (!kQ6) {
-    for (uint32_t i = tid; i < 2 * BR * 8; i += NT)
-      Mq[i / (BR * 8)][(i % (BR * 8)) / 8 * 16 + 8 + i % 8] = _Float16(0.f);
-    for (uint32_t i = tid; i < 2 * BT * 8; i += NT) {
-      Uh[i / (BT * 8)][(i % (BT * 8)) / 8 * 16 + 8 + i % 8] = _Float16(0.f);
-      Ul[i / (BT * 8)][(i % (BT * 8)) / 8 * 16 + 8 + i % 8] = _Float16(0.f);
-    }
   }
 
   auto fetch = [&](uint32_t s, Fetch<ZW, GPT>& F) {
@@ -221,7 +215,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     if constexpr (!kQ6) {
       float sf, mf;
       q4_scale_min_lane(F.x[1], F.x[2], F.x[3], g, sf, mf);
-      Mq[kp][ar * 16 + g] = _Float16(mf);
+      Mq[kp][ar * 8 + g] = _Float16(mf);
       if (q == 0 && asel == 0)
         Dd[kp][ar] = make_float2(f16_to_f32(F.x[0] & 0xffffu), f16_to_f32(F.x[0] >> 16));
       uint32_t v[8];
@@ -308,8 +302,8 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
         for (int i = 0; i < GPT; ++i) {
           const float v = u[i] * scale;
           const _Float16 h = _Float16(v);
-          Uh[kp][kt * 16 + kg + i] = h;
-          Ul[kp][kt * 16 + kg + i] = _Float16(v - float(h));
+          Uh[kp][kt * 8 + kg + i] = h;
+          Ul[kp][kt * 8 + kg + i] = _Float16(v - float(h));
         }
       }
     }
@@ -419,13 +413,14 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
       if constexpr (!kQ6) {
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-          mf[i] = *reinterpret_cast<const half4*>(&Mq[kp][(wr * NI * 16 + i * 16 + lr) * 16 + lk * 4]);
+          mf[i] = lk < 2 ? *reinterpret_cast<const half4*>(&Mq[kp][(wr * NI * 16 + i * 16 + lr) * 8 + lk * 4])
+                         : half4{0, 0, 0, 0};  // K = 8..15 of the MFMA: zero padding
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           const uint32_t t = wt * NJ * 16 + j * 16 + lr;
           ue[j] = Ue[kp][t];
-          uh[j] = *reinterpret_cast<const half4*>(&Uh[kp][t * 16 + lk * 4]);
-          ul[j] = *reinterpret_cast<const half4*>(&Ul[kp][t * 16 + lk * 4]);
+          uh[j] = lk < 2 ? *reinterpret_cast<const half4*>(&Uh[kp][t * 8 + lk * 4]) : half4{0, 0, 0, 0};
+          ul[j] = lk < 2 ? *reinterpret_cast<const half4*>(&Ul[kp][t * 8 + lk * 4]) : half4{0, 0, 0, 0};
         }
       }
 #pragma unroll
