@@ -26,6 +26,7 @@
 // integer value (scaled by s for Q4_K weights). Rows of the LDS tiles are
 // 64 halfs + 8 pad; all stores are 16 B.
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n,
     uint32_t pn, uint32_t kbs, const int8_t* __restrict__ xc, const float* __restrict__ xa,
     const int32_t* __restrict__ xs, uint32_t m, uint32_t pk, float* __restrict__ out,
-    const float* __restrict__ residual, uint32_t row_blocks, uint32_t tok_blocks) {
+    const float* __restrict__ residual, uint32_t row_begin, uint32_t row_blocks, uint32_t tok_blocks) {
   constexpr bool kQ6 = Layout == QW38_LAYOUT_Q6K_WAVE64;
   using C = Cfg<WR, WT, NI, NJ>;
   constexpr int BR = C::BR, BT = C::BT, NT = WR * WT * 64;
@@ -115,12 +116,12 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   __shared__ __align__(16) _Float16 Mq[2][kMinR];  // m of groups 0..7 per row
   __shared__ __align__(16) _Float16 Uh[2][kMinT];  // scaled a*sum hi per token
   __shared__ __align__(16) _Float16 Ul[2][kMinT];  // scaled a*sum lo per token
-  __shared__ float Ue[2][BT];                      // inverse of the per-token scale
+  __shared__ float Ti[BT];                         // inverse of the per-token scale
   __shared__ float Aa[2][BT * 8];
-  __shared__ float2 Dd[2][BR];                     // (d, dmin) | (d, 0)
+  __shared__ float2 Dd[2][BR];                     // (d, -dmin) | (d, 0)
 
   const uint32_t tile = xcd_tile(blockIdx.x, row_blocks * tok_blocks);
-  const uint32_t row0 = (tile / tok_blocks) * BR, tok0 = (tile % tok_blocks) * BT;
+  const uint32_t row0 = row_begin + (tile / tok_blocks) * BR, tok0 = (tile % tok_blocks) * BT;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wr = wave / WT, wt = wave % WT;
   const uint32_t lr = lane & 15u, lk = lane >> 4;
@@ -153,8 +154,31 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     m_base = tr0 * 16;
   }
 
-  auto fetch = [&](uint32_t s, Fetch<ZW, GPT>& F) {
-    const uint32_t kb = s >> 2, q = s & 3u;
+  // ---- Q4_K per-token scale: ts_t = 2^e with max_g |a_tg| * 2^12 * ts_t in
+  // [2^13, 2^14). |sum_tg| <= 32 * 127 < 2^12, so every min-term operand
+  // u = a * sum * ts fits FP16 with 22-bit hi + lo precision, and a * ts stays
+  // small. ts is fixed over all of K, so the accumulator is kept scaled by ts
+  // (acc' = ts * acc, exact: a power of two) and unscaled once at the store. ----
+  float ts = 1.f;
+  if constexpr (!kQ6) {
+    float mx = 0.f;
+    const float* ap = xa + size_t(ktok) * groups;
+#pragma unroll 4
+    for (uint32_t g = tid % TPT; g < kbs * 8; g += TPT) mx = fmaxf(mx, fabsf(ap[g]));
+#pragma unroll
+    for (int w = 1; w < TPT; w *= 2) mx = fmaxf(mx, __shfl_xor(mx, w));  // the token's lanes
+    const int ex = int(__float_as_uint(mx) >> 23);  // 0 for zero/subnormal, 255 for NaN/inf
+    const int se = min(max(255 - ex, 1), 253);
+    ts = __uint_as_float(uint32_t(se) << 23);
+    if (tid % TPT == 0) Ti[kt] = __uint_as_float(uint32_t(254 - se) << 23);
+  }
+
+  // Step s = 4 kb + q stages K groups 2q, 2q+1 of super-block kb. q is a
+  // compile-time constant everywhere below, so a super-block is one branch-free
+  // block the scheduler can interleave (staging VALU beside the MFMAs).
+  auto fetch = [&](auto qc, uint32_t kb_in, Fetch<ZW, GPT>& F) {
+    constexpr uint32_t q = decltype(qc)::value;
+    const uint32_t kb = min(kb_in, kbs - 1);  // past the end: a harmless re-read
     if constexpr (Layout == QW38_LAYOUT_Q4K_WAVE64) {
       const uint32_t c = kb / 8, kq = kb % 8;
       const uint32_t nk = min(kbs - 8 * c, 8u);
@@ -200,7 +224,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
 #pragma unroll
       for (int i = 0; i < ZW; ++i) F.z[i] = reinterpret_cast<const uint32_t*>(zp)[i];
     }
-    if (q == 0) {
+    if constexpr (q == 0) {
 #pragma unroll
       for (int i = 0; i < GPT; ++i) {
         F.a[i] = xa[krow + kb * 8 + i];
@@ -209,15 +233,17 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     }
   };
 
-  auto store = [&](uint32_t s, const Fetch<ZW, GPT>& F) {
-    const uint32_t buf = s & 1u, kp = (s >> 2) & 1u, q = s & 3u, g = 2 * q + asel;
+  // Stores step (kb, q) into LDS buffer q & 1 and super-block slot kb & 1.
+  auto store = [&](auto qc, uint32_t kb, const Fetch<ZW, GPT>& F) {
+    constexpr uint32_t q = decltype(qc)::value, buf = q & 1u;
+    const uint32_t kp = kb & 1u, g = 2 * q + asel;
     // ---- A: 32 FP16 values of (row ar, group g) ----
     if constexpr (!kQ6) {
       float sf, mf;
       q4_scale_min_lane(F.x[1], F.x[2], F.x[3], g, sf, mf);
       Mq[kp][ar * 8 + g] = _Float16(mf);
       if (q == 0 && asel == 0)
-        Dd[kp][ar] = make_float2(f16_to_f32(F.x[0] & 0xffffu), f16_to_f32(F.x[0] >> 16));
+        Dd[kp][ar] = make_float2(f16_to_f32(F.x[0] & 0xffffu), -f16_to_f32(F.x[0] >> 16));
       uint32_t v[8];
       q4_vectors<Layout>(F.w, v);
       const _Float16 sh = _Float16(sf), bh = _Float16(-1024.f * sf);
@@ -278,29 +304,15 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
           reinterpret_cast<uint4*>(dst)[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
       }
     }
-    // ---- super-block token data: a per group; for Q4_K the min-term
-    // operand u = a * sum scaled per token by a power of two so the largest
-    // |u| lies in [2^13, 2^14), split into FP16 hi + lo (FP16 range and 22-bit
-    // relative precision whatever the activation magnitude) ----
-    if (q == 0) {
+    // ---- super-block token data: a * ts per group; for Q4_K the min-term
+    // operand u = a * ts * sum split into FP16 hi + lo ----
+    if constexpr (q == 0) {
 #pragma unroll
-      for (int i = 0; i < GPT; ++i) Aa[kp][kt * 8 + kg + i] = F.a[i];
-      if constexpr (!kQ6) {
-        float u[GPT], mx = 0.f;
-#pragma unroll
-        for (int i = 0; i < GPT; ++i) {
-          u[i] = F.a[i] * float(F.su[i]);
-          mx = fmaxf(mx, fabsf(u[i]));
-        }
-#pragma unroll
-        for (int w = 1; w < TPT; w *= 2) mx = fmaxf(mx, __shfl_xor(mx, w));  // the token's lanes
-        const int ex = int(__float_as_uint(mx) >> 23);  // NaN and inf give 255
-        const int se = min(max(267 - ex, 1), 253);
-        const float scale = __uint_as_float(uint32_t(se) << 23);
-        if (kg == 0) Ue[kp][kt] = __uint_as_float(uint32_t(254 - se) << 23);
-#pragma unroll
-        for (int i = 0; i < GPT; ++i) {
-          const float v = u[i] * scale;
+      for (int i = 0; i < GPT; ++i) {
+        const float a = F.a[i] * ts;
+        Aa[kp][kt * 8 + kg + i] = a;
+        if constexpr (!kQ6) {
+          const float v = a * float(F.su[i]);
           const _Float16 h = _Float16(v);
           Uh[kp][kt * 8 + kg + i] = h;
           Ul[kp][kt * 8 + kg + i] = _Float16(v - float(h));
@@ -315,18 +327,17 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[i][j][v] = X[i][j][v] = 0.f;
+      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
 
-  Fetch<ZW, GPT> F;
-  fetch(0, F);
-  store(0, F);
-  if (steps > 1) fetch(1, F);
-  for (uint32_t s = 0; s < steps; ++s) {
-    __syncthreads();  // step s staged; step s-1 fully consumed
-    if (s + 1 < steps) store(s + 1, F);
-    if (s + 2 < steps) fetch(s + 2, F);
-    const uint32_t buf = s & 1u, kp = (s >> 2) & 1u, q = s & 3u;
+  // X += a P, or X = a P for the super-block's first group
+  auto scale_add = [&](bool first, float at, const f4& P, float (&x)[4]) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) x[v] = first ? at * P[v] : fmaf(at, P[v], x[v]);
+  };
 
+  auto compute = [&](auto qc, uint32_t kb) {
+    constexpr uint32_t q = decltype(qc)::value, buf = q & 1u;
+    const uint32_t kp = kb & 1u;
     // ---- one 16x16x32 MFMA per (row tile, token tile, group). Small wave
     // tiles issue the MFMAs of both groups of the step before any result is
     // scaled, so the matrix core pipelines them while the VALU applies a_tg;
@@ -369,9 +380,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
-          for (int j = 0; j < NJ; ++j)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) X[i][j][v] = fmaf(at[gsel][j], P[gsel][i][j][v], X[i][j][v]);
+          for (int j = 0; j < NJ; ++j) scale_add(q == 0 && gsel == 0, at[gsel][j], P[gsel][i][j], X[i][j]);
     } else {
 #pragma unroll
       for (uint32_t gsel = 0; gsel < 2; ++gsel) {
@@ -399,17 +408,24 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
               P[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[j], P[j], 0, 0, 0);
           }
 #pragma unroll
-          for (int j = 0; j < NJ; ++j)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) X[i][j][v] = fmaf(at[j], P[j][v], X[i][j][v]);
+          for (int j = 0; j < NJ; ++j) scale_add(q == 0 && gsel == 0, at[j], P[j], X[i][j]);
         }
       }
     }
 
-    // ---- end of super-block: fold X (and the Q4_K min term) into acc ----
-    if (q == 3) {
+    // Pin X here: otherwise the compiler defers the scaling FMAs of a
+    // super-block's first steps and keeps (spills) their MFMA results.
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(X[i][j][v]));
+
+    // ---- end of super-block: acc' += d X' - dmin Y' (Dd holds d, -dmin) ----
+    if constexpr (q == 3) {
+      __builtin_amdgcn_sched_barrier(0);  // epilogue operands load after the step's MFMAs
       half4 mf[NI], uh[NJ], ul[NJ];
-      float ue[NJ];
       if constexpr (!kQ6) {
 #pragma unroll
         for (int i = 0; i < NI; ++i)
@@ -418,7 +434,6 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           const uint32_t t = wt * NJ * 16 + j * 16 + lr;
-          ue[j] = Ue[kp][t];
           uh[j] = lk < 2 ? *reinterpret_cast<const half4*>(&Uh[kp][t * 8 + lk * 4]) : half4{0, 0, 0, 0};
           ul[j] = lk < 2 ? *reinterpret_cast<const half4*>(&Ul[kp][t * 8 + lk * 4]) : half4{0, 0, 0, 0};
         }
@@ -435,18 +450,39 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
             Y = __builtin_amdgcn_mfma_f32_16x16x16f16(mf[i], ul[j], Y, 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-              acc[i][j][v] = fmaf(-dd[v].y, Y[v] * ue[j], fmaf(dd[v].x, X[i][j][v], acc[i][j][v]));
+              acc[i][j][v] = fmaf(dd[v].y, Y[v], fmaf(dd[v].x, X[i][j][v], acc[i][j][v]));
           } else {
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[i][j][v] = fmaf(dd[v].x, X[i][j][v], acc[i][j][v]);
           }
-#pragma unroll
-          for (int v = 0; v < 4; ++v) X[i][j][v] = 0.f;
         }
       }
     }
-  }
+  };
 
+  Fetch<ZW, GPT> F;
+  // One step: wait for step (kb, q) to be staged, stage step s+1 from the
+  // registers, load step s+2 into them, then compute step s. The stores of the
+  // last step and the loads of the last two land in the buffer and
+  // super-block slot that no remaining step reads.
+  auto step = [&](auto qc, uint32_t kb) {
+    constexpr uint32_t q = decltype(qc)::value;
+    __syncthreads();  // step s staged; step s-1 fully consumed
+    store(std::integral_constant<uint32_t, (q + 1) & 3u>{}, kb + (q == 3 ? 1u : 0u), F);
+    fetch(std::integral_constant<uint32_t, (q + 2) & 3u>{}, kb + (q >= 2 ? 1u : 0u), F);
+    compute(qc, kb);
+  };
+
+  fetch(std::integral_constant<uint32_t, 0>{}, 0, F);
+  store(std::integral_constant<uint32_t, 0>{}, 0, F);
+  fetch(std::integral_constant<uint32_t, 1>{}, 0, F);
+  for (uint32_t kb = 0; kb < kbs; ++kb) {
+    step(std::integral_constant<uint32_t, 0>{}, kb);
+    step(std::integral_constant<uint32_t, 1>{}, kb);
+    step(std::integral_constant<uint32_t, 2>{}, kb);
+    step(std::integral_constant<uint32_t, 3>{}, kb);
+  }
+  __syncthreads();  // Ti visible (also when kbs is small)
   // ---- store: lane holds rows 4*lk..4*lk+3 of token lr in each tile ----
   const bool vec = (n % 4 == 0) &&
                    ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0;
@@ -458,6 +494,11 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
       const uint32_t r4 = row0 + wr * NI * 16 + i * 16 + lk * 4;
       if (tok >= m || r4 >= n) continue;
       const size_t o = size_t(tok) * n + r4;
+      if constexpr (!kQ6) {  // acc' = ts acc: unscale (exact, a power of two)
+        const float inv = Ti[wt * NJ * 16 + j * 16 + lr];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[i][j][v] *= inv;
+      }
       if (vec) {  // n % 4 == 0, so all four rows are in range
         float4 y = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
         if (residual) {
@@ -473,36 +514,75 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     }
 }
 
+// Launches one tile shape over weight rows [row_begin, row_end) (row_begin a
+// multiple of the tile height; row_end = pn or a multiple of it).
 template <uint16_t Layout, int WR, int WT, int NI, int NJ>
 hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const float* residual,
-                      hipStream_t s) {
+                      hipStream_t s, uint32_t row_begin, uint32_t row_end) {
   using C = Cfg<WR, WT, NI, NJ>;
-  const uint32_t row_blocks = (w.pn + C::BR - 1) / C::BR;
+  const uint32_t row_blocks = (row_end - row_begin + C::BR - 1) / C::BR;
   const uint32_t tok_blocks = (x.m + C::BT - 1) / C::BT;
+  if (row_blocks == 0) return hipSuccess;
   const dim3 grid(row_blocks * tok_blocks);
   hipLaunchKernelGGL((mmq_kernel<Layout, WR, WT, NI, NJ>), grid, dim3(WR * WT * 64), 0, s, w.codes, w.scales,
                      w.n, w.pn, w.pk / 256, x.codes, x.scales, x.sums, x.m, x.pk, out, residual,
-                     row_blocks, tok_blocks);
+                     row_begin, row_blocks, tok_blocks);
   return hipGetLastError();
+}
+
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cached[dev] = v;
+  }
+  return cached[dev];
 }
 
 template <uint16_t Layout>
 hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const float* residual,
                         hipStream_t s) {
-  // QW38_MMQ_TILE=32|64|128 pins the token tile (256: 256 rows x 128 tokens) (tuning aid; all tiles give
-  // bitwise-identical results).
+  // QW38_MMQ_TILE=32|64|128 pins the token tile (256: 256 rows x 128 tokens);
+  // QW38_MMQ_SPLIT=0 disables the tail split (tuning aids; every tile shape
+  // and split gives bitwise-identical results).
   static const int forced = [] {
     const char* e = std::getenv("QW38_MMQ_TILE");
     return e ? std::atoi(e) : 0;
   }();
+  static const bool split = [] {
+    const char* e = std::getenv("QW38_MMQ_SPLIT");
+    return !(e && std::atoi(e) == 0);
+  }();
   const int bt = forced ? forced : (x.m <= 32 ? 32 : x.m <= 64 ? 64 : 256);
-  if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2>(w, x, out, residual, s);  // 128 x 32
-  if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4>(w, x, out, residual, s);  // 128 x 64
+  const uint32_t pn = w.pn;
+  if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2>(w, x, out, residual, s, 0, pn);  // 128 x 32
+  if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4>(w, x, out, residual, s, 0, pn);  // 128 x 64
   if constexpr (Layout == QW38_LAYOUT_Q6K_WAVE64) {  // Q6_K's two A planes: 128 x 128 at most
-    return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s);
+    return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s, 0, pn);
   } else {
-    if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s);  // 128 x 128
-    return launch_cfg<Layout, 4, 2, 4, 4>(w, x, out, residual, s);                 // 256 x 128
+    if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s, 0, pn);  // 128 x 128
+    // 256 x 128 tiles, one block per CU. When the last round of tiles would
+    // leave most CUs idle, the big tiles cover whole rounds of row blocks and
+    // the remaining rows run as 128 x 32 tiles (two blocks per CU) when they
+    // fit one such round, which takes about half as long as a big round.
+    const uint32_t cus = uint32_t(cu_count());
+    const uint32_t rb = (pn + 255) / 256, tb = (x.m + 127) / 128;
+    uint32_t big_rows = pn;
+    if (split && !forced && uint64_t(rb) * tb > cus) {
+      const uint32_t full_rb = uint32_t(uint64_t(rb * tb / cus) * cus / tb);
+      if (full_rb > 0 && full_rb < rb) {
+        const uint64_t tail_blocks = uint64_t((pn - full_rb * 256 + 127) / 128) * ((x.m + 31) / 32);
+        const uint64_t tail_rounds = (tail_blocks + 2 * cus - 1) / (2 * cus);
+        if (tail_rounds <= 1) big_rows = full_rb * 256;
+      }
+    }
+    hipError_t e = launch_cfg<Layout, 4, 2, 4, 4>(w, x, out, residual, s, 0, big_rows);
+    if (e != hipSuccess || big_rows == pn) return e;
+    return launch_cfg<Layout, 4, 1, 2, 2>(w, x, out, residual, s, big_rows, pn);
   }
 }
 
