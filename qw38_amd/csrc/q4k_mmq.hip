@@ -51,10 +51,10 @@ __device__ __forceinline__ h2 lo_pair(uint32_t v) { return as_h2(perm(0x64646464
 __device__ __forceinline__ h2 hi_pair(uint32_t v) { return as_h2(perm(0x64646464u, v, 0x04030402u)); }
 
 // Logical-order code vectors (vector j = codes 4j..4j+3) of one Q4_K group.
-template <uint16_t Layout>
-__device__ __forceinline__ void q4_vectors(const uint32_t w[4], uint32_t v[8]) {
+template <uint16_t Layout, int NW>
+__device__ __forceinline__ void q4_vectors(const uint32_t w[NW], uint32_t v[2 * NW]) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < NW; ++t) {
     const uint32_t lo = w[t] & 0x0f0f0f0fu;
     const uint32_t hi = (w[t] >> 4) & 0x0f0f0f0fu;
     if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2) {
@@ -85,9 +85,9 @@ __device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t nblk) {
 // Loads of rows past the padded weight and of tokens past m read a clamped
 // (valid) row or token instead: every output element depends only on its own
 // row and token, and those rows and tokens are never stored.
-template <int ZW, int GPT>
+template <int ZW, int GPT, int AW>
 struct Fetch {
-  uint32_t w[4];     // A: 16 B of codes of (row, group)
+  uint32_t w[AW];    // A: this thread's share (16 B or 8 B) of the codes of (row, group)
   uint32_t x[4];     // A: Q4_K metadata row | Q6_K: qh words 0-1, scale pair, d
   uint32_t z[ZW];    // B: this thread's share of a (token, group) code row
   float a[GPT];      // super-block token data (first step of a super-block
@@ -103,7 +103,8 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   constexpr bool kQ6 = Layout == QW38_LAYOUT_Q6K_WAVE64;
   using C = Cfg<WR, WT, NI, NJ>;
   constexpr int BR = C::BR, BT = C::BT, NT = WR * WT * 64;
-  static_assert(2 * BR == NT, "A staging: one (row, group) per thread");
+  constexpr int APT = NT / (2 * BR), AW = 4 / APT;  // A staging: threads per (row, group), code words each
+  static_assert(APT * 2 * BR == NT && (APT == 1 || (APT == 2 && !kQ6)), "A staging share");
   constexpr int BB = BT * 64 / NT;  // B bytes staged per thread per step
   static_assert(BB == 8 || BB == 16 || BB == 32, "B staging share");
   constexpr int ZW = BB / 4, PARTS = 32 / BB;
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   const uint32_t steps = kbs * 4;
 
   // A staging role: row ar, group-in-step asel (clamped row for the loads)
-  const uint32_t ar = tid >> 1, asel = tid & 1u;
+  const uint32_t ar = (tid / APT) >> 1, asel = (tid / APT) & 1u, ah = tid % APT;
   const uint32_t arow = min(row0 + ar, pn - 1);
   // B staging role: token bt, group-in-step bsel, byte part bpart of BB bytes
   const uint32_t bpart = tid % PARTS, bsel = (tid / PARTS) & 1u, bt = tid / (2 * PARTS);
@@ -176,27 +177,31 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   // Step s = 4 kb + q stages K groups 2q, 2q+1 of super-block kb. q is a
   // compile-time constant everywhere below, so a super-block is one branch-free
   // block the scheduler can interleave (staging VALU beside the MFMAs).
-  auto fetch = [&](auto qc, uint32_t kb_in, Fetch<ZW, GPT>& F) {
+  auto fetch = [&](auto qc, uint32_t kb_in, Fetch<ZW, GPT, AW>& F) {
     constexpr uint32_t q = decltype(qc)::value;
     const uint32_t kb = min(kb_in, kbs - 1);  // past the end: a harmless re-read
     if constexpr (Layout == QW38_LAYOUT_Q4K_WAVE64) {
       const uint32_t c = kb / 8, kq = kb % 8;
       const uint32_t nk = min(kbs - 8 * c, 8u);
       const uint8_t* cp = codes + uint64_t(strips) * 8192 * c +
-                          (nk * a_r1 + a_r2 + (2 * q * nk + kq) * 128);
+                          (nk * a_r1 + a_r2 + (2 * q * nk + kq) * 128) + ah * 4 * AW;
       const uint8_t* mp = meta + uint64_t(strips) * 1024 * c + (nk * m_r1 + a_r2 + kq * 128);
-      const uint4 cw = *reinterpret_cast<const uint4*>(cp);
+      if constexpr (AW == 4) {
+        const uint4 cw = *reinterpret_cast<const uint4*>(cp);
+        F.w[0] = cw.x; F.w[1] = cw.y; F.w[2] = cw.z; F.w[3] = cw.w;
+      } else {
+        const uint2 cw = *reinterpret_cast<const uint2*>(cp);
+        F.w[0] = cw.x; F.w[1] = cw.y;
+      }
       const uint4 mw = *reinterpret_cast<const uint4*>(mp);
-      F.w[0] = cw.x; F.w[1] = cw.y; F.w[2] = cw.z; F.w[3] = cw.w;
       F.x[0] = mw.x; F.x[1] = mw.y; F.x[2] = mw.z; F.x[3] = mw.w;
     } else if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2) {  // 4 B / 2 B aligned
       const uint32_t* c4 = reinterpret_cast<const uint32_t*>(codes + a_base + kb * 1024 + q * 32);
       const uint16_t* m2 = reinterpret_cast<const uint16_t*>(meta + m_base + kb * 128);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        F.w[i] = c4[i];
-        F.x[i] = uint32_t(m2[2 * i]) | (uint32_t(m2[2 * i + 1]) << 16);
-      }
+      for (int i = 0; i < AW; ++i) F.w[i] = c4[ah * AW + i];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) F.x[i] = uint32_t(m2[2 * i]) | (uint32_t(m2[2 * i + 1]) << 16);
     } else {
       const uint32_t g = 2 * q + asel;
       const uint64_t tr = a_base + kb * 8;
@@ -234,29 +239,29 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   };
 
   // Stores step (kb, q) into LDS buffer q & 1 and super-block slot kb & 1.
-  auto store = [&](auto qc, uint32_t kb, const Fetch<ZW, GPT>& F) {
+  auto store = [&](auto qc, uint32_t kb, const Fetch<ZW, GPT, AW>& F) {
     constexpr uint32_t q = decltype(qc)::value, buf = q & 1u;
     const uint32_t kp = kb & 1u, g = 2 * q + asel;
     // ---- A: 32 FP16 values of (row ar, group g) ----
     if constexpr (!kQ6) {
       float sf, mf;
       q4_scale_min_lane(F.x[1], F.x[2], F.x[3], g, sf, mf);
-      Mq[kp][ar * 8 + g] = _Float16(mf);
-      if (q == 0 && asel == 0)
+      if (ah == 0) Mq[kp][ar * 8 + g] = _Float16(mf);
+      if (q == 0 && asel == 0 && ah == 0)
         Dd[kp][ar] = make_float2(f16_to_f32(F.x[0] & 0xffffu), -f16_to_f32(F.x[0] >> 16));
-      uint32_t v[8];
-      q4_vectors<Layout>(F.w, v);
+      uint32_t v[2 * AW];
+      q4_vectors<Layout, AW>(F.w, v);
       const _Float16 sh = _Float16(sf), bh = _Float16(-1024.f * sf);
       const h2 s2 = {sh, sh}, b2 = {bh, bh};
-      uint32_t o[16];
+      uint32_t o[4 * AW];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {  // (1024 + c) s - 1024 s = c s exactly (c s <= 945)
+      for (int j = 0; j < 2 * AW; ++j) {  // (1024 + c) s - 1024 s = c s exactly (c s <= 945)
         o[2 * j] = as_u32(__builtin_elementwise_fma(lo_pair(v[j]), s2, b2));
         o[2 * j + 1] = as_u32(__builtin_elementwise_fma(hi_pair(v[j]), s2, b2));
       }
-      uint4* dst = reinterpret_cast<uint4*>(&As[buf][0][ar * kStride + asel * 32]);
+      uint4* dst = reinterpret_cast<uint4*>(&As[buf][0][ar * kStride + asel * 32 + ah * 8 * AW]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+      for (int i = 0; i < AW; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
     } else {
       if (q == 0 && asel == 0) Dd[kp][ar] = make_float2(f16_to_f32(F.x[3]), 0.f);
       const h2 off = {_Float16(-1056.f), _Float16(-1056.f)};  // 1024 + q -> q - 32
@@ -342,7 +347,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     // tiles issue the MFMAs of both groups of the step before any result is
     // scaled, so the matrix core pipelines them while the VALU applies a_tg;
     // large wave tiles scale row tile i while the MFMAs of row tile i+1 run. ----
-    if constexpr (NI * NJ <= 8) {
+    if constexpr (NI * NJ <= 8 && WR * WT <= 4) {
       f4 P[2][NI][NJ];
       float at[2][NJ];
 #pragma unroll
@@ -460,7 +465,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     }
   };
 
-  Fetch<ZW, GPT> F;
+  Fetch<ZW, GPT, AW> F;
   // One step: wait for step (kb, q) to be staged, stage step s+1 from the
   // registers, load step s+2 into them, then compute step s. The stores of the
   // last step and the loads of the last two land in the buffer and
