@@ -154,9 +154,10 @@ int qw38_quantize_q6k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_
  * (cuda/decode_mmv.hpp:25-134). Validation follows the reference's contract
  * (cuda/decode_mmv.cu:245-560): typed views, padded geometry, exact byte
  * counts, alignment, writability and non-overlap, all before any launch.
- * This build implements the Q4_K layout 0x020D (quantizer 0x0105); the other
- * reference layouts are recognised and rejected with QW38_INVALID_ARGUMENT
- * ("not implemented on this build"). */
+ * This build implements the Q4_K layout 0x020D (quantizer 0x0105), Q4G64
+ * (0x0201, 0x020B), Q8G32 (0x0202, 0x020C) and BF16 dense tiles (0x0203);
+ * FP8 (0x020F) and NVFP4 (0x020E) are recognised and rejected with
+ * QW38_INVALID_ARGUMENT ("not implemented on this build"). */
 #define QW38_DECODE_LAYOUT_Q4G64_V0 0x0201
 #define QW38_DECODE_LAYOUT_Q8G32_V0 0x0202
 #define QW38_DECODE_LAYOUT_BF16_DENSE_TILE_V0 0x0203
@@ -236,6 +237,10 @@ int qw38_decode_mmv_paired(const qw38_decode_desc* a, const qw38_decode_desc* b,
  * cuda/decode_mmv.cu:781-853): two or three BF16-store projections sharing
  * layout, K and input. */
 int qw38_decode_mmv_ranges(const qw38_decode_desc* ranges, uint32_t count, void* stream);
+/* Replaces launch_decode_ab_bf16 (cuda/decode_mmv.hpp:211-213,
+ * cuda/decode_mmv.cu:781-800): two BF16 dense-tile matrices (the GDN a/b
+ * projections) sharing K and input, FP32 outputs, one launch. */
+int qw38_decode_ab_bf16(const qw38_decode_desc* a, const qw38_decode_desc* b, void* stream);
 /* ---- BF16 prefill projections (cuda/prefill.hpp) -------------------------
  * Stateless C-ABI under qw38::cuda::PrefillEngine (cuda/prefill.hpp:72-160):
  * BF16 token-major activations [tokens][k] times a Q4_K 0x020D weight whose

@@ -71,6 +71,9 @@ def lib():
             "orc_q6k_q8_contract": (None, [V, V, V, U32, U32, V, V, V, U32, V, V, V, I]),
             "orc_q4k_bf16_weight": (C.c_float, [V, C.c_uint, C.c_uint]),
             "orc_q4k_bf16_gemv": (None, [V, V, U32, U32, U32, V, V, I]),
+            "orc_pack_dense_layout": (I, [U16, V, V, U32, U32, V, V]),
+            "orc_pack_bf16_tile": (I, [V, U32, U32, V]),
+            "orc_dense_operands": (None, [U16, V, V, U32, U32, V]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -315,6 +318,53 @@ def q4k_bf16_gemv(w: Q4K, x_bf16: np.ndarray, threads=None):
     x = np.ascontiguousarray(x_bf16, np.uint16)
     lib().orc_q4k_bf16_gemv(_p(w.codes), _p(w.meta), w.n, w.pk, w.k, _p(x), _p(out), threads or _threads())
     return out
+
+
+# ---- decode_mmv dense layouts (Q4G64, Q8G32, BF16 dense tile) ---------------
+LAYOUT_Q4G64, LAYOUT_Q8G32, LAYOUT_BF16_TILE = 0x0201, 0x0202, 0x0203
+LAYOUT_Q4G64_CAND, LAYOUT_Q8G32_CAND = 0x020B, 0x020C
+
+
+def dense_group(layout: int) -> int:
+    return 64 if layout in (LAYOUT_Q4G64, LAYOUT_Q4G64_CAND) else 32
+
+
+def pack_dense(layout: int, codes: np.ndarray, scales: np.ndarray, n: int, k: int):
+    """Logical int8 codes [n][k] + FP16 scale bits [n][k/group] -> (codes, scales)
+    in the reference tile layout (src/format/pack.cpp:143-215)."""
+    pn, pk = pad8(n), pad256(k)
+    q4 = layout in (LAYOUT_Q4G64, LAYOUT_Q4G64_CAND)
+    co = np.zeros(pn * pk // (2 if q4 else 1), np.uint8)
+    so = np.zeros(pn * (pk // dense_group(layout)) * 2, np.uint8)
+    c = np.ascontiguousarray(codes, np.int8)
+    sc = np.ascontiguousarray(scales, np.uint16)
+    assert c.size == n * k and sc.size == n * (k // dense_group(layout))
+    st = lib().orc_pack_dense_layout(layout, _p(c), _p(sc), n, k, _p(co), _p(so))
+    assert st == 0, "unsupported dense layout/shape"
+    return co, so
+
+
+def pack_bf16_tile(w_bf16: np.ndarray, n: int, k: int) -> np.ndarray:
+    """Row-major BF16 bits [n][k] -> BF16 dense tiles (src/format/pack.cpp:247-290)."""
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    co = np.zeros(n * k * 2, np.uint8)
+    assert lib().orc_pack_bf16_tile(_p(w), n, k, _p(co)) == 0
+    return co
+
+
+def dense_operands(layout: int, co: np.ndarray, so, pn: int, pk: int) -> np.ndarray:
+    """BF16 operand bits [pn][pk] as decode_mmv rebuilds them (cuda/decode_mmv.cu:92-180)."""
+    out = np.zeros((pn, pk), np.uint16)
+    so = np.zeros(1, np.uint8) if so is None else np.ascontiguousarray(so, np.uint8)
+    lib().orc_dense_operands(layout, _p(np.ascontiguousarray(co, np.uint8)), _p(so), pn, pk, _p(out))
+    return out
+
+
+def bf16_gemv(w_bf16: np.ndarray, x_bf16: np.ndarray) -> np.ndarray:
+    """y = W x in double for BF16 operand bits W [n][k] and x [k]."""
+    w = bf16_to_fp32(np.ascontiguousarray(w_bf16, np.uint16)).astype(np.float64)
+    x = bf16_to_fp32(np.ascontiguousarray(x_bf16, np.uint16)).astype(np.float64)
+    return w @ x
 
 
 # ---- parity metrics -------------------------------------------------------

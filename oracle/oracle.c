@@ -54,6 +54,17 @@
  *   orc_q4k_bf16_*        cuda/decode_mmv.cu:121-140 (BF16 operand rebuild).
  *                         Pinned: one-hot operand fixture of
  *                         tests/decode_mmv_unit_test.cpp:405-478 restated.
+ *   orc_pack_dense_layout src/format/pack.cpp:143-215 (Q4G64 / Q8G32 tiles).
+ *                         Pinned: the golden bytes and coordinates of
+ *                         tests/pack_layout_test.cpp:313-460 (nibble order,
+ *                         two's complement, tile/row/group order, padding).
+ *   orc_pack_bf16_tile    src/format/pack.cpp:247-290. Pinned: explicit
+ *                         coordinates and lossless inverse via the operands.
+ *   orc_dense_operands    cuda/decode_mmv.cu:92-180 (decode8 Q4 / Q8 / BF16).
+ *                         Pinned: equals BF16_RNE(code * scale) computed from
+ *                         the logical codes (packer and decoder restated
+ *                         independently), zero and max-FP16 cases of
+ *                         tests/decode_mmv_unit_test.cpp:335-400.
  *
  * Build with -ffp-contract=off -fno-fast-math: every FMA here is explicit.
  */
@@ -854,4 +865,90 @@ void orc_q4k_bf16_gemv(const uint8_t* codes, const uint8_t* meta, uint32_t n,
     out64[r] = acc;
   }
   (void)threads;
+}
+
+/* ---- decode_mmv dense layouts: Q4G64, Q8G32, BF16 dense tile ------------- */
+static int dense_q4(uint16_t layout) { return layout == 0x0201 || layout == 0x020B; }
+static int dense_q8(uint16_t layout) { return layout == 0x0202 || layout == 0x020C; }
+
+/* src/format/pack.cpp:143-215: tile_row = ((row/8)*tiles_k + kb)*8 + row%8;
+ * Q4: 128 B per tile row, byte c/2 = nibble(code c) | nibble(code c+1) << 4;
+ * Q8: 256 B per tile row, one two's-complement byte per code; FP16 scale bits
+ * per group (Q4: 4, Q8: 8 per tile row). Padded rows / K are zero. */
+int orc_pack_dense_layout(uint16_t layout, const int8_t* codes, const uint16_t* scales,
+                          uint32_t n, uint32_t k, uint8_t* co, uint8_t* so) {
+  if (!dense_q4(layout) && !dense_q8(layout)) return 1;
+  const uint32_t group = dense_q4(layout) ? 64 : 32;
+  if (k % group) return 1;
+  const uint32_t pn = pad8(n), pk = (k + 255) / 256 * 256, tiles_k = pk / 256;
+  const uint32_t row_bytes = dense_q4(layout) ? 128 : 256, gpt = 256 / group;
+  memset(co, 0, (size_t)pn * tiles_k * row_bytes);
+  memset(so, 0, (size_t)pn * tiles_k * gpt * 2);
+  for (uint32_t row = 0; row < n; ++row)
+    for (uint32_t kb = 0; kb < tiles_k; ++kb) {
+      const size_t tr = ((size_t)(row / 8) * tiles_k + kb) * 8 + row % 8;
+      for (uint32_t g = 0; g < gpt; ++g) {
+        const uint32_t c0 = kb * 256 + g * group;
+        if (c0 < k) {
+          const uint16_t b = scales[(size_t)row * (k / group) + c0 / group];
+          so[(tr * gpt + g) * 2] = (uint8_t)(b & 0xff);
+          so[(tr * gpt + g) * 2 + 1] = (uint8_t)(b >> 8);
+        }
+      }
+      for (uint32_t c = 0; c < 256; ++c) {
+        const uint32_t col = kb * 256 + c;
+        const uint8_t v = col < k ? (uint8_t)codes[(size_t)row * k + col] : 0;
+        if (dense_q4(layout))
+          co[tr * 128 + c / 2] |= (uint8_t)((v & 0x0f) << (4 * (c & 1)));
+        else
+          co[tr * 256 + c] = v;
+      }
+    }
+  return 0;
+}
+
+/* src/format/pack.cpp:247-290: row-major BF16 [n][k] (n%8 == 0, k%256 == 0)
+ * to 512 B tile rows. */
+int orc_pack_bf16_tile(const uint16_t* w, uint32_t n, uint32_t k, uint8_t* co) {
+  if (n % 8 || k % 256) return 1;
+  const uint32_t tiles_k = k / 256;
+  for (uint32_t row = 0; row < n; ++row)
+    for (uint32_t kb = 0; kb < tiles_k; ++kb) {
+      const size_t tr = ((size_t)(row / 8) * tiles_k + kb) * 8 + row % 8;
+      memcpy(co + tr * 512, w + (size_t)row * k + kb * 256, 512);
+    }
+  return 0;
+}
+
+/* cuda/decode_mmv.cu:92-180 (decode8): the BF16 operand of every padded
+ * element, out[pn][pk]: Q4 sign-extended nibble or Q8 int8 times the group's
+ * FP16 scale (0 when the scale is 0), rounded to BF16; BF16 tiles as stored. */
+void orc_dense_operands(uint16_t layout, const uint8_t* co, const uint8_t* so, uint32_t pn,
+                        uint32_t pk, uint16_t* out) {
+  const uint32_t tiles_k = pk / 256;
+  for (uint32_t row = 0; row < pn; ++row)
+    for (uint32_t col = 0; col < pk; ++col) {
+      const size_t tr = ((size_t)(row / 8) * tiles_k + col / 256) * 8 + row % 8;
+      const uint32_t c = col % 256;
+      uint16_t w;
+      if (dense_q4(layout) || dense_q8(layout)) {
+        int code;
+        uint16_t sb;
+        if (dense_q4(layout)) {
+          const uint8_t b = co[tr * 128 + c / 2];
+          const int nib = (c & 1) ? (b >> 4) : (b & 15);
+          code = nib >= 8 ? nib - 16 : nib;
+          sb = (uint16_t)(so[(tr * 4 + c / 64) * 2] | (so[(tr * 4 + c / 64) * 2 + 1] << 8));
+        } else {
+          code = (int8_t)co[tr * 256 + c];
+          sb = (uint16_t)(so[(tr * 8 + c / 32) * 2] | (so[(tr * 8 + c / 32) * 2 + 1] << 8));
+        }
+        const float scale = orc_fp16_to_fp32(sb);
+        const float v = scale != 0.0f ? (float)code * scale : 0.0f;
+        w = orc_fp32_to_bf16_rne(v);
+      } else {
+        w = (uint16_t)(co[tr * 512 + 2 * c] | (co[tr * 512 + 2 * c + 1] << 8));
+      }
+      out[(size_t)row * pk + col] = w;
+    }
 }

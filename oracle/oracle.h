@@ -103,6 +103,17 @@ void orc_q4k_bf16_gemv(const uint8_t* codes, const uint8_t* meta, uint32_t n,
                        uint32_t pk, uint32_t k, const uint16_t* x, double* out64,
                        int threads);
 
+/* ---- decode_mmv dense layouts (Q4G64 0x0201/0x020B, Q8G32 0x0202/0x020C,
+ * BF16 dense tile 0x0203) ---------------------------------------------------- */
+/* Logical codes [n][k] and FP16 scale bits [n][k/group] -> tiled codes/scales. */
+int orc_pack_dense_layout(uint16_t layout, const int8_t* codes, const uint16_t* scales,
+                          uint32_t n, uint32_t k, uint8_t* co, uint8_t* so);
+/* Row-major BF16 [n][k] -> BF16 dense tiles. */
+int orc_pack_bf16_tile(const uint16_t* w, uint32_t n, uint32_t k, uint8_t* co);
+/* BF16 operand bits of every padded element, out[pn][pk]. */
+void orc_dense_operands(uint16_t layout, const uint8_t* co, const uint8_t* so, uint32_t pn,
+                        uint32_t pk, uint16_t* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,6 +84,7 @@ SIGNATURES = {
     "qw38_decode_mmv": (_I, [_P(DecodeDesc), _V]),
     "qw38_decode_mmv_paired": (_I, [_P(DecodeDesc), _P(DecodeDesc), _V]),
     "qw38_decode_mmv_ranges": (_I, [_P(DecodeDesc), _U32, _V]),
+    "qw38_decode_ab_bf16": (_I, [_P(DecodeDesc), _P(DecodeDesc), _V]),
     "qw38_prefill_project": (_I, [_P(Weight), _V, _U32, _V, _V, _I, _V]),
     "qw38_prefill_paired_swiglu": (_I, [_P(Weight), _P(Weight), _V, _V, _U32, _V]),
     "qw38_hidden_rms_bf16": (_I, [_V, _V, _F, _U32, _V, _V]),

@@ -1,7 +1,8 @@
 // BF16-activation decode GEMV (interface of cuda/decode_mmv.hpp in
 // Enucatl/qw38). The descriptor types, wire IDs, padding and byte-count
-// helpers are the reference's; this build implements the Q4_K layout 0x020D
-// and rejects the other layouts as not implemented.
+// helpers are the reference's; this build implements the Q4_K (0x020D), Q4G64,
+// Q8G32 and BF16 dense-tile layouts and rejects FP8 and NVFP4 as not
+// implemented.
 #pragma once
 
 #include "cuda/error.hpp"
@@ -181,7 +182,7 @@ struct DecodeMmvRangeDesc {
                                                            Stream const& stream);
 [[nodiscard]] expected<void, Error> launch_decode_mmv_paired(DecodeMmvPairedDesc const& desc,
                                                                   Stream const& stream);
-// Grouped GDN a/b over BF16 dense tiles: not implemented on this build.
+// Grouped GDN a/b: two BF16 dense-tile matrices, FP32 outputs, one launch.
 [[nodiscard]] expected<void, Error> launch_decode_ab_bf16(DecodeMmvPairedDesc const& desc,
                                                                Stream const& stream);
 [[nodiscard]] expected<void, Error> launch_decode_mmv_ranges(DecodeMmvRangeDesc const& desc,

@@ -156,9 +156,12 @@ expected<void, Error> launch_decode_mmv_paired(DecodeMmvPairedDesc const& desc, 
   return from_abi(qw38_decode_mmv_paired(&a, &b, stream.native()));
 }
 
-expected<void, Error> launch_decode_ab_bf16(DecodeMmvPairedDesc const&, Stream const& stream) {
+expected<void, Error> launch_decode_ab_bf16(DecodeMmvPairedDesc const& desc, Stream const& stream) {
   if (auto st = require_stream(stream, "decode_ab_bf16"); !st) return st;
-  return unexpected(not_implemented("decode_ab_bf16", "the BF16 dense-tile a/b decode"));
+  auto guard = stream.activate();
+  if (!guard) return unexpected(guard.error());
+  const qw38_decode_desc a = abi(desc.a), b = abi(desc.b);
+  return from_abi(qw38_decode_ab_bf16(&a, &b, stream.native()));
 }
 
 expected<void, Error> launch_decode_mmv_ranges(DecodeMmvRangeDesc const& desc, Stream const& stream) {

@@ -279,6 +279,10 @@ int decode_geometry(const DDesc& d, const char* op, bool paired_b) {
   if (d.activation_policy != QW38_DECODE_ACTIVATION_BF16)
     return fail(QW38_INVALID_ARGUMENT, op, "unsupported decode activation policy");
   if (d.n == 0 || d.k == 0) return fail(QW38_INVALID_ARGUMENT, op, "N and K must be nonzero");
+  if (d.layout == QW38_DECODE_LAYOUT_FP8_V1 && (d.n > 17408 || d.n % 128 || d.k % 256))
+    return fail(QW38_INVALID_ARGUMENT, op, "FP8 requires aligned mixer geometry");
+  if (d.layout == QW38_DECODE_LAYOUT_NVFP4_V1 && d.n > 248320)
+    return fail(QW38_INVALID_ARGUMENT, op, "NVFP4 N exceeds model geometry");
   if (d.n > std::numeric_limits<uint32_t>::max() - 7u)
     return fail(QW38_OVERFLOW, op, "N exceeds the largest supported row-tile-padded value");
   if (d.k > QW38_DECODE_MAX_K || d.padded_k > QW38_DECODE_MAX_K)
@@ -344,11 +348,20 @@ int decode_geometry(const DDesc& d, const char* op, bool paired_b) {
   return QW38_OK;
 }
 
-// Layouts the reference knows but this build does not implement for decode.
+// Layouts the reference knows but this build does not implement for decode
+// (FP8 and NVFP4).
 int decode_supported(const DDesc& d, const char* op) {
-  if (d.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2)
-    return fail(QW38_INVALID_ARGUMENT, op, "decode layout not implemented on this build");
-  return QW38_OK;
+  switch (d.layout) {
+    case QW38_LAYOUT_Q4K_CANDIDATE_V2:
+    case QW38_DECODE_LAYOUT_Q4G64_V0:
+    case QW38_DECODE_LAYOUT_Q4G64_CANDIDATE_V1:
+    case QW38_DECODE_LAYOUT_Q8G32_V0:
+    case QW38_DECODE_LAYOUT_Q8G32_CANDIDATE_V1:
+    case QW38_DECODE_LAYOUT_BF16_DENSE_TILE_V0:
+      return QW38_OK;
+    default:
+      return fail(QW38_INVALID_ARGUMENT, op, "decode layout not implemented on this build");
+  }
 }
 
 int decode_paired_contract(const DDesc& a, const DDesc& b, const char* op) {
@@ -390,7 +403,8 @@ int decode_launch(const DDesc& a, const DDesc* b, void* stream, const char* op) 
   const WeightView wa = decode_weight(a);
   WeightView wb{};
   if (b) wb = decode_weight(*b);
-  hipError_t e = launch_decode_bf16(
+  auto* launch = a.layout == QW38_LAYOUT_Q4K_CANDIDATE_V2 ? launch_decode_bf16 : launch_decode_dense;
+  hipError_t e = launch(
       wa, b ? &wb : nullptr, static_cast<const uint16_t*>(a.input.pointer), a.output.pointer,
       b ? b->output.pointer : nullptr, static_cast<const float*>(a.residual.pointer),
       b ? static_cast<const float*>(b->residual.pointer) : nullptr, a.epilogue,
@@ -711,6 +725,17 @@ int qw38_decode_mmv_paired(const qw38_decode_desc* a, const qw38_decode_desc* b,
   if (!a || !b) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
   if (int st = decode_paired_contract(*a, *b, op)) return st;
   if (int st = decode_supported(*a, op)) return st;
+  return decode_launch(*a, b, stream, op);
+}
+
+int qw38_decode_ab_bf16(const qw38_decode_desc* a, const qw38_decode_desc* b, void* stream) {
+  constexpr const char* op = "decode_ab_bf16";
+  if (!a || !b) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
+  if (a->layout != QW38_DECODE_LAYOUT_BF16_DENSE_TILE_V0 || a->quantizer != QW38_DECODE_QUANTIZER_NONE)
+    return fail(QW38_INVALID_ARGUMENT, op, "a/b contraction requires cuda_bf16_dense_tile_v0");
+  if (a->epilogue != QW38_DECODE_STORE_FP32)
+    return fail(QW38_INVALID_ARGUMENT, op, "a/b contraction requires FP32 output");
+  if (int st = decode_paired_contract(*a, *b, op)) return st;
   return decode_launch(*a, b, stream, op);
 }
 

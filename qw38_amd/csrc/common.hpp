@@ -167,6 +167,10 @@ hipError_t launch_prefill_bf16(const WeightView& a, const WeightView* b, const u
 hipError_t launch_decode_bf16(const WeightView& a, const WeightView* b, const uint16_t* x,
                               void* out_a, void* out_b, const float* res_a, const float* res_b,
                               int epilogue, hipStream_t s);
+// Q4G64 / Q8G32 / BF16 dense-tile decode_mmv layouts (same arguments).
+hipError_t launch_decode_dense(const WeightView& a, const WeightView* b, const uint16_t* x,
+                               void* out_a, void* out_b, const float* res_a, const float* res_b,
+                               int epilogue, hipStream_t s);
 hipError_t launch_group_dots(const WeightView& w, const Q8View& x, int32_t* dots,
                              hipStream_t s);
 hipError_t launch_repack_q4k(const uint8_t* blocks, uint32_t n, uint32_t k, uint16_t layout,

@@ -270,4 +270,266 @@ hipError_t launch_decode_bf16(const WeightView& a, const WeightView* b, const ui
                                         out_b, res_a, res_b, epilogue, s);
 }
 
+// ---------------------------------------------------------------------------
+// The reference's other decode_mmv weight layouts (cuda/decode_mmv.cu:92-180):
+//   Q4G64 (0x0201 / 0x020B): signed nibbles, one FP16 scale per 64 weights
+//   Q8G32 (0x0202 / 0x020C): int8 codes, one FP16 scale per 32 weights
+//   BF16 dense tile (0x0203): BF16 weights
+// all in the 8-row x K256 tile order (tile_row = ((row/8) * K/256 + kb) * 8 +
+// row % 8, so an 8-row strip is one contiguous run of tiles). Each weight is
+// the BF16 operand  w = BF16_RNE(code * scale)  (code * scale is exact in FP32:
+// an 11-bit significand times at most 8 bits), or the stored BF16 value.
+// A zero scale gives a signed zero where the reference writes +0; no sum can
+// tell them apart.
+//
+// Mapping: one wave64 streams one strip, 2 KB (Q4: a tile pair; Q8: one
+// tile) or 4 KB (BF16: one tile) per iteration, every lane reading 32 or 64
+// contiguous bytes:
+//   Q4:   lane l -> tile l/32 of the pair, row (l%32)/4, 64 weights of group l%4
+//   Q8:   lane l -> row l/8, 32 weights of group l%8
+//   BF16: lane l -> row l/8, 32 weights at K offset (l%8)*32
+// so each lane needs exactly one FP16 scale, and the lane-order scale entries
+// of one iteration are contiguous (one 2 B load per lane).
+// ---------------------------------------------------------------------------
+namespace {
+
+enum class DKind { Q4, Q8, Bf16 };
+
+template <DKind K>
+struct DUnit {
+  static constexpr int kWords = K == DKind::Bf16 ? 16 : 8;
+  uint32_t c[kWords];
+  uint32_t s;  // FP16 scale bits (Q4, Q8)
+};
+
+template <DKind K>
+struct DGeom {
+  static constexpr uint32_t kTileBytes = K == DKind::Q4 ? 1024 : K == DKind::Q8 ? 2048 : 4096;
+  static constexpr uint32_t kTileScales = K == DKind::Q4 ? 64 : 128;  // bytes per tile
+  static constexpr uint32_t kTilesPerUnit = K == DKind::Q4 ? 2 : 1;
+};
+
+// Loads unit (first tile t0) of one lane; `half` limits a Q4 tail unit to its
+// first tile (lanes of the missing second tile read nothing).
+template <DKind K>
+__device__ __forceinline__ void load_unit(const uint8_t* codes, const uint8_t* scales, size_t t0,
+                                          uint32_t lane, bool half, DUnit<K>& u) {
+  using G = DGeom<K>;
+  const bool skip = half && lane >= 32;
+  if (skip) {
+#pragma unroll
+    for (int i = 0; i < DUnit<K>::kWords; ++i) u.c[i] = 0;
+    u.s = 0;
+    return;
+  }
+  const uint4* cp = reinterpret_cast<const uint4*>(codes + t0 * G::kTileBytes +
+                                                   lane * (K == DKind::Bf16 ? 64u : 32u));
+#pragma unroll
+  for (int i = 0; i < DUnit<K>::kWords / 4; ++i) {
+    const uint4 v = cp[i];
+    u.c[4 * i] = v.x; u.c[4 * i + 1] = v.y; u.c[4 * i + 2] = v.z; u.c[4 * i + 3] = v.w;
+  }
+  if constexpr (K != DKind::Bf16)
+    u.s = *reinterpret_cast<const uint16_t*>(scales + t0 * G::kTileScales + lane * 2u);
+}
+
+// acc += sum over this lane's weights of w * x; k0 = K offset of the lane's first weight.
+template <DKind K>
+__device__ __forceinline__ void consume_unit(const DUnit<K>& u, uint32_t k0, const uint32_t* xs,
+                                             float& acc) {
+  const uint4* xp = reinterpret_cast<const uint4*>(xs + k0 / 2);
+  if constexpr (K == DKind::Bf16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 xv = xp[i];
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, u.c[4 * i + q]),
+                                              __builtin_bit_cast(bf2, xw[q]), acc, false);
+    }
+  } else if constexpr (K == DKind::Q4) {
+    const float s = f16_to_f32(u.s);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // word i: bytes 4i..4i+3 = weights 8i..8i+7 (low nibble first)
+      const uint4 xv = xp[i];
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int lo = __builtin_amdgcn_sbfe(int(u.c[i]), 8 * q, 4);
+        const int hi = __builtin_amdgcn_sbfe(int(u.c[i]), 8 * q + 4, 4);
+        const fl2 wv = {float(lo) * s, float(hi) * s};
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_convertvector(wv, bf2),
+                                              __builtin_bit_cast(bf2, xw[q]), acc, false);
+      }
+    }
+  } else {
+    const float s = f16_to_f32(u.s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // words 2i, 2i+1: weights 8i..8i+7
+      const uint4 xv = xp[i];
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t w = u.c[2 * i + (q >> 1)];
+        const int c0 = __builtin_amdgcn_sbfe(int(w), 16 * (q & 1), 8);
+        const int c1 = __builtin_amdgcn_sbfe(int(w), 16 * (q & 1) + 8, 8);
+        const fl2 wv = {float(c0) * s, float(c1) * s};
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_convertvector(wv, bf2),
+                                              __builtin_bit_cast(bf2, xw[q]), acc, false);
+      }
+    }
+  }
+}
+
+template <DKind K, bool Paired, int WS>
+__global__ __launch_bounds__(256) void decode_dense_kernel(
+    const uint8_t* __restrict__ codes_a, const uint8_t* __restrict__ scales_a,
+    const uint8_t* __restrict__ codes_b, const uint8_t* __restrict__ scales_b,
+    const uint16_t* __restrict__ x, uint32_t k, uint32_t pk, uint32_t n, uint32_t strips,
+    void* out_a, void* out_b, const float* res_a, const float* res_b, int epi) {
+  using G = DGeom<K>;
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int SPB = 4 / WS;
+  uint32_t* xs = reinterpret_cast<uint32_t*>(smem);
+  float* red = reinterpret_cast<float*>(smem + size_t(pk) * 2);
+  const uint32_t tiles_k = pk / 256;
+  {
+    uint16_t* x16 = reinterpret_cast<uint16_t*>(smem);
+    for (uint32_t i = threadIdx.x; i < pk; i += 256) x16[i] = i < k ? x[i] : uint16_t(0);
+  }
+  __syncthreads();
+
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t ks = wave % WS;
+  const uint32_t strip = blockIdx.x * SPB + wave / WS;
+  const bool live = strip < strips;
+  // this lane's row in the strip and K offset within a unit
+  const uint32_t r = K == DKind::Q4 ? (lane >> 2) & 7u : lane >> 3;
+  const uint32_t koff = K == DKind::Q4 ? (lane >> 5) * 256 + (lane & 3u) * 64 : (lane & 7u) * 32;
+  const uint32_t units = tiles_k / G::kTilesPerUnit;
+  const bool tail = K == DKind::Q4 && (tiles_k & 1u) && ks == WS - 1;
+  const uint32_t u0 = uint32_t(uint64_t(units) * ks / WS);
+  const uint32_t u1 = uint32_t(uint64_t(units) * (ks + 1) / WS);
+
+  float acc_a = 0.f, acc_b = 0.f;
+  if (live) {
+    const size_t tbase = size_t(strip) * tiles_k;
+    // double-buffered: unit u+1 is in flight while unit u is consumed
+    DUnit<K> A[2], B[Paired ? 2 : 1];
+    uint32_t u = u0;
+    if (u < u1) {
+      load_unit<K>(codes_a, scales_a, tbase + u * G::kTilesPerUnit, lane, false, A[0]);
+      if constexpr (Paired) load_unit<K>(codes_b, scales_b, tbase + u * G::kTilesPerUnit, lane, false, B[0]);
+    }
+    for (; u + 2 <= u1; u += 2) {
+      load_unit<K>(codes_a, scales_a, tbase + (u + 1) * G::kTilesPerUnit, lane, false, A[1]);
+      if constexpr (Paired) load_unit<K>(codes_b, scales_b, tbase + (u + 1) * G::kTilesPerUnit, lane, false, B[1]);
+      consume_unit<K>(A[0], u * 256 * G::kTilesPerUnit + koff, xs, acc_a);
+      if constexpr (Paired) consume_unit<K>(B[0], u * 256 * G::kTilesPerUnit + koff, xs, acc_b);
+      if (u + 2 < u1) {
+        load_unit<K>(codes_a, scales_a, tbase + (u + 2) * G::kTilesPerUnit, lane, false, A[0]);
+        if constexpr (Paired) load_unit<K>(codes_b, scales_b, tbase + (u + 2) * G::kTilesPerUnit, lane, false, B[0]);
+      }
+      consume_unit<K>(A[1], (u + 1) * 256 * G::kTilesPerUnit + koff, xs, acc_a);
+      if constexpr (Paired) consume_unit<K>(B[1], (u + 1) * 256 * G::kTilesPerUnit + koff, xs, acc_b);
+    }
+    if (u < u1) {
+      consume_unit<K>(A[0], u * 256 * G::kTilesPerUnit + koff, xs, acc_a);
+      if constexpr (Paired) consume_unit<K>(B[0], u * 256 * G::kTilesPerUnit + koff, xs, acc_b);
+    }
+    if (tail) {  // odd last Q4 tile: lanes of the first tile of the pair only
+      const uint32_t t = tiles_k - 1;
+      load_unit<K>(codes_a, scales_a, tbase + t, lane, true, A[0]);
+      if (lane < 32) consume_unit<K>(A[0], t * 256 + koff, xs, acc_a);
+      if constexpr (Paired) {
+        load_unit<K>(codes_b, scales_b, tbase + t, lane, true, B[0]);
+        if (lane < 32) consume_unit<K>(B[0], t * 256 + koff, xs, acc_b);
+      }
+    }
+  }
+  // row partials: Q4 lanes {4r..4r+3, 32+4r..32+4r+3}; Q8/BF16 lanes 8r..8r+7
+  constexpr int kX3 = K == DKind::Q4 ? 32 : 4;
+  acc_a += __shfl_xor(acc_a, 1);
+  acc_a += __shfl_xor(acc_a, 2);
+  acc_a += __shfl_xor(acc_a, kX3);
+  if constexpr (Paired) {
+    acc_b += __shfl_xor(acc_b, 1);
+    acc_b += __shfl_xor(acc_b, 2);
+    acc_b += __shfl_xor(acc_b, kX3);
+  }
+  const uint32_t row = strip * 8 + r;
+  const bool writer = K == DKind::Q4 ? (lane & 35u) == 0 : (lane & 7u) == 0;
+  if constexpr (WS > 1) {
+    if (writer) {
+      red[(wave * 2 + 0) * 8 + r] = acc_a;
+      red[(wave * 2 + 1) * 8 + r] = acc_b;
+    }
+    __syncthreads();
+    if (ks != 0) return;
+    acc_a = acc_b = 0.f;
+#pragma unroll
+    for (int qq = 0; qq < WS; ++qq) {
+      acc_a += red[((wave + qq) * 2 + 0) * 8 + r];
+      acc_b += red[((wave + qq) * 2 + 1) * 8 + r];
+    }
+  }
+  if (!live || !writer || row >= n) return;
+  if (Paired && epi == QW38_DECODE_SWIGLU_BF16) {
+    static_cast<uint16_t*>(out_a)[row] = f32_to_bf16_rne(silu(acc_a) * acc_b);
+    return;
+  }
+  epilogue(epi, out_a, res_a, row, acc_a);
+  if constexpr (Paired) epilogue(epi, out_b, res_b, row, acc_b);
+}
+
+template <DKind K, bool Paired>
+hipError_t launch_dense_ws(const WeightView& a, const WeightView* b, const uint16_t* x, void* oa,
+                           void* ob, const float* ra, const float* rb, int epi, hipStream_t s) {
+  const uint32_t strips = a.pn / 8, tiles_k = a.pk / 256;
+  const uint64_t strip_bytes = uint64_t(tiles_k) * DGeom<K>::kTileBytes;
+  // enough waves in flight: split K when there are few strips of long K
+  int ws = 1;
+  if (strips < 6144 && strip_bytes >= 8192) ws = 2;
+  if (strips < 1536 && strip_bytes >= 16384) ws = 4;
+  const size_t lds = size_t(a.pk) * 2 + 4 * 2 * 8 * 4;
+  const uint8_t* cb = b ? b->codes : nullptr;
+  const uint8_t* sb = b ? b->scales : nullptr;
+#define QW38_DENSE_LAUNCH(WSV)                                                                  \
+  hipLaunchKernelGGL((decode_dense_kernel<K, Paired, WSV>),                                     \
+                     dim3((strips + (4 / WSV) - 1) / (4 / WSV)), dim3(256), lds, s, a.codes,     \
+                     a.scales, cb, sb, x, a.k, a.pk, a.n, strips, oa, ob, ra, rb, epi)
+  if (ws == 4) QW38_DENSE_LAUNCH(4);
+  else if (ws == 2) QW38_DENSE_LAUNCH(2);
+  else QW38_DENSE_LAUNCH(1);
+#undef QW38_DENSE_LAUNCH
+  return hipGetLastError();
+}
+
+template <DKind K>
+hipError_t launch_dense_kind(const WeightView& a, const WeightView* b, const uint16_t* x, void* oa,
+                             void* ob, const float* ra, const float* rb, int epi, hipStream_t s) {
+  return b ? launch_dense_ws<K, true>(a, b, x, oa, ob, ra, rb, epi, s)
+           : launch_dense_ws<K, false>(a, b, x, oa, ob, ra, rb, epi, s);
+}
+
+}  // namespace
+
+hipError_t launch_decode_dense(const WeightView& a, const WeightView* b, const uint16_t* x,
+                               void* out_a, void* out_b, const float* res_a, const float* res_b,
+                               int epilogue, hipStream_t s) {
+  switch (a.layout) {
+    case QW38_DECODE_LAYOUT_Q4G64_V0:
+    case QW38_DECODE_LAYOUT_Q4G64_CANDIDATE_V1:
+      return launch_dense_kind<DKind::Q4>(a, b, x, out_a, out_b, res_a, res_b, epilogue, s);
+    case QW38_DECODE_LAYOUT_Q8G32_V0:
+    case QW38_DECODE_LAYOUT_Q8G32_CANDIDATE_V1:
+      return launch_dense_kind<DKind::Q8>(a, b, x, out_a, out_b, res_a, res_b, epilogue, s);
+    case QW38_DECODE_LAYOUT_BF16_DENSE_TILE_V0:
+      return launch_dense_kind<DKind::Bf16>(a, b, x, out_a, out_b, res_a, res_b, epilogue, s);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace qw38hip

@@ -7,7 +7,8 @@
 // 2j, 2j+1 with j = l%4 -- so the wave's two 16 B loads read 2 KB with no
 // gaps. One 4 B/lane load reads the pair's 256 B of metadata; the four dwords
 // of (row r, tile h) land exactly in lane l's quad, so DPP quad broadcasts
-// hand them over without LDS traffic. Loads run two tile pairs ahead.
+// hand them over without LDS traffic. Loads run one tile pair ahead of the
+// pair being consumed.
 //
 // The Q8 activations are staged once per block in LDS as codes plus
 // (a, a*sum) pairs. Per (row, token, super-block) the affine is factored as
@@ -181,17 +182,38 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
       const uint8_t* mstrip = meta + size_t(strip) * kbs * 128;
       // Batches of kBatch tile pairs: every load of a batch is issued before the
       // first is consumed, so up to kBatch * 2 KB per wave is in flight.
-      constexpr uint32_t kBatch = 4;
+      // Double-buffered batches of kB tile pairs: the loads of batch b+1 are
+      // issued before batch b is consumed, so memory stays busy while this wave
+      // computes.
+      constexpr uint32_t kB = 1;
       uint32_t q = q0;
-      for (; q + kBatch <= q1; q += kBatch) {
-        Tile T[kBatch];
+      const uint32_t nb = (q1 - q0) / kB;
+      if (nb > 0) {
+        Tile A[kB], B[kB];
+        auto ld = [&](Tile (&T)[kB], uint32_t qq) {
 #pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u)
-          load_tile<Fast>(cstrip + size_t(q + u) * 2048, mstrip + size_t(q + u) * 256, coff,
-                          moff, T[u]);
+          for (uint32_t u = 0; u < kB; ++u)
+            load_tile<Fast>(cstrip + size_t(qq + u) * 2048, mstrip + size_t(qq + u) * 256, coff, moff, T[u]);
+        };
+        auto cs = [&](const Tile (&T)[kB], uint32_t qq) {
 #pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u)
-          consume<Layout, MT, Fast>(T[u], 2 * (q + u) + h, g0, hi, sh, sz, sau, groups, acc);
+          for (uint32_t u = 0; u < kB; ++u)
+            consume<Layout, MT, Fast>(T[u], 2 * (qq + u) + h, g0, hi, sh, sz, sau, groups, acc);
+        };
+        ld(A, q);
+        uint32_t b = 0;
+        for (; b + 2 <= nb; b += 2) {
+          ld(B, q + kB);
+          cs(A, q);
+          q += kB;
+          if (b + 2 < nb) ld(A, q + kB);
+          cs(B, q);
+          q += kB;
+        }
+        if (b < nb) {
+          cs(A, q);
+          q += kB;
+        }
       }
       for (; q < q1; ++q) {
         Tile T;
@@ -298,7 +320,7 @@ hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,
                     reinterpret_cast<uintptr_t>(w.scales) % 4 == 0;
   const uint32_t strips = w.pn / 8, kbs = w.pk / 256;
   int ws = 1;
-  if (strips < 3072 && kbs >= 8) ws = 2;
+  if (strips < 6144 && kbs >= 8) ws = 2;
   if (strips < 1536 && kbs >= 16) ws = 4;
   if (ws_override == 1 || ws_override == 2 || ws_override == 4) ws = ws_override;
   if (max_blocks == 0) max_blocks = 2048;

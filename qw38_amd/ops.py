@@ -71,7 +71,8 @@ class PrefillWeight:
         if self.codes_bytes < 0:
             self.codes_bytes = self.codes.numel() * self.codes.element_size()
         if self.scales_bytes < 0:
-            self.scales_bytes = self.scales.numel() * self.scales.element_size()
+            self.scales_bytes = (0 if self.scales is None else
+                                 self.scales.numel() * self.scales.element_size())
 
     @staticmethod
     def from_bytes(codes, scales, layout, n, k, device="cuda"):
@@ -226,20 +227,42 @@ def decode_view(t, dtype, layout, logical_n, logical_k, padded_n, padded_k, alig
                       b, alignment, 1 if writable else 0)
 
 
+DECODE_LAYOUT_Q4G64, DECODE_LAYOUT_Q8G32, DECODE_LAYOUT_BF16_TILE = 0x0201, 0x0202, 0x0203
+DECODE_LAYOUT_Q4G64_CAND, DECODE_LAYOUT_Q8G32_CAND = 0x020B, 0x020C
+_DENSE_QUANTIZER = {0x0201: 0x0101, 0x0202: 0x0102, 0x0203: 0x0100, 0x020B: 0x0103, 0x020C: 0x0104}
+
+
+def dense_weight(layout: int, codes: torch.Tensor, scales, n: int, k: int) -> PrefillWeight:
+    """A decode_mmv weight in one of the reference's dense tile layouts
+    (Q4G64, Q8G32, BF16 dense tile; cuda/decode_mmv.hpp:25-35): device byte
+    tensors already in the tile order, scales None for BF16."""
+    return PrefillWeight(codes, scales, layout, _DENSE_QUANTIZER[layout], n, k, pad_n(n), pad_k(k))
+
+
+def _weight_dtype(layout: int) -> int:
+    if layout in (0x0202, 0x020C):
+        return DTYPE_Q8
+    if layout == 0x0203:
+        return DTYPE_BF16
+    return DTYPE_Q4
+
+
 def decode_desc(w: PrefillWeight, x, output, epilogue=DECODE_STORE_FP32, residual=None,
                 output_view=True):
-    """A DecodeMmvDesc for a Q4_K (0x020D) weight, BF16 input x [k] (int16
-    tensor of BF16 bits), output [n] (FP32, or BF16 bits for the BF16
-    epilogues) and residual [n] FP32 for the residual epilogue. With
-    output=None and the residual epilogue the update is in place."""
+    """A DecodeMmvDesc for a decode weight (Q4_K 0x020D or a dense layout), BF16
+    input x [k] (int16 tensor of BF16 bits), output [n] (FP32, or BF16 bits
+    for the BF16 epilogues) and residual [n] FP32 for the residual epilogue.
+    With output=None and the residual epilogue the update is in place."""
     from ._lib import DecodeDesc
     d = DecodeDesc()
     d.layout, d.quantizer, d.activation_policy = w.layout, w.quantizer, 1
     d.n, d.k, d.padded_n, d.padded_k = w.n, w.k, w.padded_n, w.padded_k
-    d.codes = decode_view(w.codes, DTYPE_Q4, w.layout, w.n, w.k, w.padded_n, w.padded_k, 16, False)
-    units = w.scales.numel() * w.scales.element_size() // w.padded_n // 2
-    d.scales = decode_view(w.scales, DTYPE_FP16, w.layout, w.padded_n, units, w.padded_n, units, 2,
-                           False)
+    d.codes = decode_view(w.codes, _weight_dtype(w.layout), w.layout, w.n, w.k, w.padded_n,
+                          w.padded_k, 16, False)
+    if w.scales is not None:
+        units = w.scales.numel() * w.scales.element_size() // w.padded_n // 2
+        d.scales = decode_view(w.scales, DTYPE_FP16, w.layout, w.padded_n, units, w.padded_n,
+                               units, 2, False)
     d.input = decode_view(x, DTYPE_BF16, LAYOUT_BF16_VECTOR, w.k, 1, w.k, 1, 2, False)
     bf16_out = epilogue in (DECODE_STORE_BF16, DECODE_SWIGLU_BF16)
     if output is not None and output_view:
@@ -261,6 +284,11 @@ def decode_mmv(desc, stream=None) -> None:
 def decode_mmv_paired(a, b, stream=None) -> None:
     """cuda::launch_decode_mmv_paired (cuda/decode_mmv.hpp:208-209)."""
     check(lib().qw38_decode_mmv_paired(C.byref(a), C.byref(b), _stream(stream)))
+
+
+def decode_ab_bf16(a, b, stream=None) -> None:
+    """cuda::launch_decode_ab_bf16 (cuda/decode_mmv.hpp:211-213)."""
+    check(lib().qw38_decode_ab_bf16(C.byref(a), C.byref(b), _stream(stream)))
 
 
 def decode_mmv_ranges(descs, stream=None) -> None:

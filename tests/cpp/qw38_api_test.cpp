@@ -379,7 +379,7 @@ void test_decode_onehot(Stream const& s) {
   bad = d;
   bad.scales.bytes /= 2;
   expect(!launch_decode_mmv(bad, s), "decode_mmv: truncated metadata rejected");
-  expect(!launch_decode_ab_bf16({d, d}, s), "decode_ab_bf16 reports not implemented");
+  expect(!launch_decode_ab_bf16({d, d}, s), "decode_ab_bf16 rejects a layout other than BF16 dense tiles");
 }
 
 void test_graph_replay(Stream const& s) {

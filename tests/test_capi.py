@@ -132,15 +132,22 @@ def test_decode_rejections_without_device():
         assert L.qw38_decode_mmv(C.byref(desc), None) == 2, needle
         err = _lib.last_error()
         assert err.operation.startswith("decode_mmv") and needle in err.detail, (needle, err.detail)
-    # a reference layout this build does not implement (Q8G32 V0, 1 B codes)
-    d = _decode_desc()
-    d.layout, d.quantizer = 0x0202, 0x0102
-    d.codes.layout = d.scales.layout = 0x0202
-    d.codes.dtype, d.codes.bytes = 2, d.padded_n * d.padded_k
-    d.scales.logical_k = d.scales.padded_k = d.padded_k // 32
-    d.scales.bytes = d.padded_n * d.padded_k // 32 * 2
+    # a reference layout this build does not implement (FP8 V1: 1 B codes, one
+    # FP32 scale per 128x128 block) passes validation and is then rejected
+    d = _decode_desc(n=128, k=256)
+    d.layout, d.quantizer = 0x020F, 0x0107
+    d.codes.layout = 0x020F
+    d.codes.dtype, d.codes.bytes = 7, 128 * 256
+    d.scales = _lib.DecodeView(0x200000, 1, 5, 0x020F, 1, 2, 1, 2, 8, 16, 0)
     assert L.qw38_decode_mmv(C.byref(d), None) == 2
     assert "not implemented" in _lib.last_error().detail
+    d.n = d.codes.logical_n = d.output.logical_n = d.output.padded_n = 120
+    assert L.qw38_decode_mmv(C.byref(d), None) == 2
+    assert "FP8 requires aligned mixer geometry" in _lib.last_error().detail
+    # a/b contraction: BF16 dense tiles with FP32 output only
+    a, b = _decode_desc(), _decode_desc()
+    assert L.qw38_decode_ab_bf16(C.byref(a), C.byref(b), None) == 2
+    assert "cuda_bf16_dense_tile_v0" in _lib.last_error().detail
     # paired: B must match A; SwiGLU B declares no output
     a, b = _decode_desc(), _decode_desc()
     b.codes.pointer, b.scales.pointer, b.output.pointer = 0x500000, 0x600000, 0x700000

@@ -296,3 +296,115 @@ def test_swiglu_q8_closed_form():
     g[0, 3] = np.inf
     qn, _ = oracle.swiglu_q8(g, u)
     assert qn.failed
+
+
+# ---- decode_mmv dense layouts (Q4G64, Q8G32, BF16 dense tile) ----------------
+def _le16(a, i):
+    return int(a[i]) | (int(a[i + 1]) << 8)
+
+
+def _dense_logical(layout, n, k):
+    g = oracle.dense_group(layout)
+    return np.zeros((n, k), np.int8), np.zeros((n, k // g), np.uint16)
+
+
+def test_dense_q4_golden_bytes():
+    """tests/pack_layout_test.cpp:329-351: nibble order, signed nibbles, scale LE."""
+    c, s = _dense_logical(0x0201, 8, 256)
+    c[0, :6] = [1, 2, 3, 4, -1, 7]
+    s[0, 0] = 0x3C00
+    co, so = oracle.pack_dense(0x0201, c, s, 8, 256)
+    assert co.size == 8 * 128 and so.size == 8 * 4 * 2
+    assert (co[0], co[1], co[2]) == (0x21, 0x43, 0x7F)
+    assert _le16(so, 0) == 0x3C00
+
+
+def test_dense_q4_tile_coordinates_and_padding():
+    """tests/pack_layout_test.cpp:353-400: (row 9, col 300) of 16x512 lands at
+    byte 3222 (tn=1, tk=1, r=1, c=44), scale index [N/8, K/256, row, group];
+    a 5x192 matrix pads to 8x256 with zero codes and zero padded-group scales."""
+    c, s = _dense_logical(0x0201, 16, 512)
+    c[9, 300] = 5
+    s[9, 300 // 64] = 0x4200
+    co, so = oracle.pack_dense(0x0201, c, s, 16, 512)
+    assert co.size == 2 * 2 * 8 * 128
+    assert co[3222] & 0x0F == 5 and np.count_nonzero(co) == 1
+    si = ((1 * 2 + 1) * 8 + 1) * 4 + (44 // 64)
+    assert _le16(so, 2 * si) == 0x4200
+    c, s = _dense_logical(0x0201, 5, 192)
+    c[0, 0], s[0, 0] = 3, 0x4000
+    co, so = oracle.pack_dense(0x0201, c, s, 5, 192)
+    assert co.size == 8 * 128 and so.size == 8 * 4 * 2
+    assert co[0] == 3 and np.count_nonzero(co) == 1
+    assert so[2] == 0 and so[3] == 0  # padded K group scale
+
+
+def test_dense_q8_golden_bytes_and_coordinates():
+    """tests/pack_layout_test.cpp:399-460: two's complement codes, eight scales
+    per tile row, four-tile 16x512 placement."""
+    c, s = _dense_logical(0x0202, 8, 256)
+    c[0, :3] = [1, -1, -127]
+    s[0, 0] = 0x3C00
+    co, so = oracle.pack_dense(0x0202, c, s, 8, 256)
+    assert co.size == 8 * 256 and so.size == 8 * 8 * 2
+    assert (co[0], co[1], co[2]) == (1, 0xFF, 0x81)
+    c, s = _dense_logical(0x0202, 16, 512)
+    c[9, 300], c[15, 511] = -127, 126
+    s[9, 300 // 32], s[15, 511 // 32] = 0x4200, 0x3555
+    co, so = oracle.pack_dense(0x0202, c, s, 16, 512)
+    tr = lambda row, col: ((row // 8) * 2 + col // 256) * 8 + row % 8
+    assert co[tr(9, 300) * 256 + 300 % 256] == 0x81
+    assert co[tr(15, 511) * 256 + 511 % 256] == 126
+    i = tr(15, 511) * 8 + (511 % 256) // 32
+    assert _le16(so, 2 * i) == 0x3555
+    assert np.count_nonzero(co) == 2
+
+
+@pytest.mark.parametrize("layout", [0x0201, 0x020B, 0x0202, 0x020C])
+def test_dense_operands_equal_scaled_codes(layout):
+    """Packer and decoder are restated independently; composing them must give
+    BF16_RNE(code * scale) in logical order (0 for a zero scale), including
+    padding (zero) and ragged shapes."""
+    rng = np.random.Generator(np.random.PCG64(layout))
+    g = oracle.dense_group(layout)
+    n, k = 21, 5 * 64 if g == 64 else 7 * 32
+    q4 = g == 64
+    c = rng.integers(-8 if q4 else -127, 8 if q4 else 128, (n, k)).astype(np.int8)
+    s = (rng.random((n, k // g)) * 2 - 1).astype(np.float16).view(np.uint16)
+    s[0, 0] = 0  # zero scale
+    s[1, 0] = 0x8000  # negative zero
+    s[2, 0] = 0x0001  # subnormal scale
+    co, so = oracle.pack_dense(layout, c, s, n, k)
+    pn, pk = oracle.pad8(n), oracle.pad256(k)
+    w = oracle.dense_operands(layout, co, so, pn, pk)
+    scale = np.repeat(s.view(np.float16).astype(np.float32), g, axis=1)
+    want = oracle.fp32_to_bf16(np.where(scale != 0, c.astype(np.float32) * scale, 0).astype(np.float32))
+    assert np.array_equal(w[:n, :k], want)
+    assert not w[n:].any() and not w[:, k:].any()
+
+
+def test_dense_extreme_and_zero_cases():
+    """tests/decode_mmv_unit_test.cpp:335-400: all-zero codes/scales give zero
+    operands; code 127 with the largest FP16 scale 0x7BFF is BF16(127 * 65504)."""
+    c, s = _dense_logical(0x0201, 8, 256)
+    co, so = oracle.pack_dense(0x0201, c, s, 8, 256)
+    assert not oracle.dense_operands(0x0201, co, so, 8, 256).any()
+    c, s = _dense_logical(0x0202, 8, 256)
+    c[:], s[:] = 127, 0x7BFF
+    co, so = oracle.pack_dense(0x0202, c, s, 8, 256)
+    w = oracle.dense_operands(0x0202, co, so, 8, 256)
+    assert np.all(w == oracle.fp32_to_bf16(np.array([127.0 * 65504.0], np.float32))[0])
+
+
+def test_bf16_tile_coordinates_roundtrip():
+    """src/format/pack.cpp:247-290: element (row, col) at tile row
+    ((row/8)*K/256 + col/256)*8 + row%8, offset 2*(col%256); the operand decoder
+    inverts it exactly."""
+    rng = np.random.Generator(np.random.PCG64(7))
+    n, k = 16, 768
+    w = rng.integers(0, 65536, (n, k)).astype(np.uint16)
+    co = oracle.pack_bf16_tile(w, n, k)
+    row, col = 11, 600
+    tr = ((row // 8) * 3 + col // 256) * 8 + row % 8
+    assert _le16(co, tr * 512 + 2 * (col % 256)) == w[row, col]
+    assert np.array_equal(oracle.dense_operands(0x0203, co, None, n, k), w)
