@@ -32,30 +32,38 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA (AMD published)
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA (AMD published)
 METRIC = "Q4_K×Q8 GEMV GB/s (% of 8 TB/s) at M=1; MMQ int8 TOPS (% peak) at M=512"
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "gemv_w64_config2_m1_traffic.txt")
+# rocprofv3 --pmc summaries of the config-2 M=1 decode kernel, per weight layout:
+# (file under profiles/, kernel-name prefix of the M=1 instantiation)
+TRAFFIC_PROFILES = {
+    0x020D: ("gemv_stream_config2_m1_traffic.txt", r"gemv_stream_kernel"),
+    0x0240: ("gemv_w64_config2_m1_traffic.txt", r"gemv_w64_kernel<1,"),
+}
 
 
-def measured_traffic(path=TRAFFIC_PROFILE):
-    """HBM bytes per launch of the config-2 M=1 GEMV (layout 0x0240) from the
-    committed rocprofv3 --pmc summary: FETCH_SIZE and WRITE_SIZE (KiB per
-    dispatch), each scaled by what the same counter reads for a device copy
-    of exactly 1 GiB read + 1 GiB written. None when the summary is absent."""
+def measured_traffic(layout):
+    """HBM bytes per launch of the config-2 M=1 GEMV from the committed
+    rocprofv3 --pmc summary for this layout: FETCH_SIZE and WRITE_SIZE (KiB
+    per dispatch), each scaled by what the same counter reads for a device
+    copy of exactly 1 GiB read + 1 GiB written. None when the summary is absent."""
     import re
+    if layout not in TRAFFIC_PROFILES:
+        return None
+    name, kernel = TRAFFIC_PROFILES[layout]
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         text = open(path).read()
     except OSError:
         return None
     vals = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        g = re.search(r"gemv_w64_kernel<1[^\n]*\(dispatches=\d+\): " + counter + r"=([\d.e+]+)", text)
+        g = re.search(kernel + r"[^\n]*\(dispatches=\d+\): " + counter + r"=([\d.e+]+)", text)
         c = re.search(r"__amd_rocclr_copyBuffer \(dispatches=\d+\): " + counter + r"=([\d.e+]+)", text)
         if not g or not c:
             return None
         scale = (1 << 20) / float(c.group(1))  # KiB the counter should read for 1 GiB
         vals[counter] = float(g.group(1)) * scale * 1024
     return {"bytes": vals["FETCH_SIZE"] + vals["WRITE_SIZE"], "read": vals["FETCH_SIZE"],
-            "written": vals["WRITE_SIZE"], "source": "profiles/gemv_w64_config2_m1_traffic.txt"}
+            "written": vals["WRITE_SIZE"], "source": "profiles/" + name}
 
 
 def log(*a):
@@ -237,7 +245,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=24)
-    ap.add_argument("--layout", default="0x0240")
+    ap.add_argument("--layout", default="0x020D", help="decode weight layout")
+    ap.add_argument("--mmq-layout", default="0x0240", help="MMQ weight layout")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-mmq", action="store_true")
@@ -271,8 +280,9 @@ def main():
         ms_list = [1] + ms_list
     dec, base = bench_decode(torch, ops, n, k, ms_list, args.steps, args.warmup, layout)
     head = dec[1]
+    mmq_layout = int(args.mmq_layout, 16)
     mmq = None if args.no_mmq else bench_mmq(torch, ops, n, k, 512, max(20, args.steps // 8),
-                                              max(3, args.warmup // 4), layout)
+                                              max(3, args.warmup // 4), mmq_layout)
     dbf16 = None if args.no_bf16 else bench_decode_bf16(torch, ops, n, k, args.steps, args.warmup)
     pbf16 = None if (args.no_bf16 or args.no_mmq) else bench_prefill_bf16(
         torch, ops, n, k, 512, max(20, args.steps // 8), max(3, args.warmup // 4))
@@ -280,7 +290,7 @@ def main():
     if not args.no_cpu:
         _, blocks = make_weight(torch, ops, n, k, 11, layout)
         cpu = cpu_baseline(torch, blocks, n, k, 1, args.cpu_seconds)
-    traffic = measured_traffic() if layout == 0x0240 else None
+    traffic = measured_traffic(layout)
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 2),
@@ -297,6 +307,7 @@ def main():
                 "~N(0,1) activations with 1% channels x20 -> BF16 -> Q8)",
         "config": {"workload": "config 2: fused gate+up Q4_K x Q8 decode GEMV, N=34816, "
                                "K=5120, M=1", "layout": f"{layout:#06x}",
+                   "mmq_layout": f"{mmq_layout:#06x}",
                    "weight_copies_rotated": max(2, math.ceil(1.2e9 / q4k_bytes(n, k))),
                    "timing": head["mode"]},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS,

@@ -152,6 +152,8 @@ hipError_t launch_rms_bf16(const float* residual, const uint16_t* gamma, float e
 hipError_t launch_swiglu_q8(const float* gate, const float* up, uint32_t m, uint32_t n,
                             int8_t* codes, float* scales, int32_t* sums, int* failure,
                             hipStream_t s);
+// Compute units of the current device (cached per device).
+int cu_count();
 hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out,
                        const float* residual, hipStream_t s);
 hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,

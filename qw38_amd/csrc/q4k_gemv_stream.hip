@@ -170,10 +170,14 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
   const bool tail = (kbs & 1u) && ks == WS - 1;
   const uint32_t coff = lane * 32, moff = lane * 4;
 
+  // Blocks walk strip groups with a block-uniform stride (a persistent grid
+  // when it is smaller than the strip groups); with WS > 1 every wave of the
+  // block runs every iteration, since the K-split reduction synchronises.
   const uint32_t stride = persistent ? gridDim.x * SPB : SPB * gridDim.x + strips;
-  // WS > 1 blocks run exactly one strip group and synchronise after it.
-  for (uint32_t strip = blockIdx.x * SPB + wave / WS; WS > 1 || strip < strips; strip += stride) {
+  for (uint32_t base = blockIdx.x * SPB; base < strips; base += stride) {
+    const uint32_t strip = base + wave / WS;
     const bool live = strip < strips;
+    if (WS == 1 && !live) break;
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = 0.f;
@@ -272,7 +276,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
           out[i] = total + (residual ? residual[i] : 0.f);
         }
       }
-      break;
+      if (base + stride < strips) __syncthreads();  // red is rewritten by the next strip group
     }
   }
 }
@@ -286,7 +290,7 @@ hipError_t stream_ws(const WeightView& w, const Q8View& x, float* out, const flo
 #define QW38_STREAM_LAUNCH(WSV)                                                          \
   do {                                                                                   \
     const uint32_t need = (strips + (4 / WSV) - 1) / (4 / WSV);                          \
-    const uint32_t persistent = (WSV == 1 && need > max_blocks) ? 1u : 0u;               \
+    const uint32_t persistent = need > max_blocks ? 1u : 0u;                             \
     const uint32_t grid = persistent ? max_blocks : need;                                \
     hipLaunchKernelGGL((gemv_stream_kernel<Layout, MT, Fast, WSV>), dim3(grid), dim3(256), \
                        lds, s, w.codes, w.scales, w.n, strips, kbs, x.codes, x.scales,   \
@@ -319,11 +323,20 @@ hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,
                          16 == 0) &&
                     reinterpret_cast<uintptr_t>(w.scales) % 4 == 0;
   const uint32_t strips = w.pn / 8, kbs = w.pk / 256;
+  // K split and grid. Long K: a persistent grid of four blocks per CU, so
+  // each block stages the activations once for several strips; at M = 1 four
+  // waves share a strip (short contiguous runs per wave read HBM best), at
+  // M = 2 (twice the consume work per byte) one wave streams a whole strip.
   int ws = 1;
   if (strips < 6144 && kbs >= 8) ws = 2;
   if (strips < 1536 && kbs >= 16) ws = 4;
+  uint32_t blocks = 0xffffffffu;
+  if (kbs >= 16) {
+    ws = x.m == 1 ? 4 : 1;
+    blocks = 4u * uint32_t(cu_count());
+  }
   if (ws_override == 1 || ws_override == 2 || ws_override == 4) ws = ws_override;
-  if (max_blocks == 0) max_blocks = 2048;
+  if (max_blocks == 0) max_blocks = blocks;
   if (w.layout == QW38_LAYOUT_Q4K_CANDIDATE_V2)
     return fast ? stream_m<QW38_LAYOUT_Q4K_CANDIDATE_V2, true>(w, x, out, residual, s, ws, max_blocks)
                 : stream_m<QW38_LAYOUT_Q4K_CANDIDATE_V2, false>(w, x, out, residual, s, ws, max_blocks);

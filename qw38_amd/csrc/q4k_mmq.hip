@@ -535,19 +535,6 @@ hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const fl
   return hipGetLastError();
 }
 
-// Compute units of the current device (cached per device).
-int cu_count() {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    cached[dev] = v;
-  }
-  return cached[dev];
-}
-
 template <uint16_t Layout>
 hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const float* residual,
                         hipStream_t s) {
@@ -592,6 +579,19 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
 }
 
 }  // namespace
+
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
 
 hipError_t launch_mmq(const WeightView& w, const Q8View& x, float* out, const float* residual,
                       hipStream_t s) {
