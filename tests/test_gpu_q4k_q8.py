@@ -11,7 +11,7 @@ from _fix import REF_K, REF_N, ref_fixture_input, ref_fixture_weight
 
 pytestmark = pytest.mark.gpu
 
-M_SWEEP = [1, 2, 3, 5, 8, 9, 31, 33, 64, 65, 127, 128, 129, 256, 257, 511, 512]
+M_SWEEP = [1, 2, 3, 5, 8, 9, 16, 17, 31, 32, 33, 64, 65, 127, 128, 129, 256, 257, 511, 512]
 LAYOUTS = [oracle.LAYOUT_Q4K_SEQ, oracle.LAYOUT_Q4K_W64]
 
 
