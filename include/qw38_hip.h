@@ -155,9 +155,9 @@ int qw38_quantize_q6k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_
  * (cuda/decode_mmv.cu:245-560): typed views, padded geometry, exact byte
  * counts, alignment, writability and non-overlap, all before any launch.
  * This build implements the Q4_K layout 0x020D (quantizer 0x0105), Q4G64
- * (0x0201, 0x020B), Q8G32 (0x0202, 0x020C) and BF16 dense tiles (0x0203);
- * FP8 (0x020F) and NVFP4 (0x020E) are recognised and rejected with
- * QW38_INVALID_ARGUMENT ("not implemented on this build"). */
+ * (0x0201, 0x020B), Q8G32 (0x0202, 0x020C), BF16 dense tiles (0x0203) and FP8
+ * (0x020F, single and ranged launches); NVFP4 (0x020E) is recognised and
+ * rejected with QW38_INVALID_ARGUMENT ("not implemented on this build"). */
 #define QW38_DECODE_LAYOUT_Q4G64_V0 0x0201
 #define QW38_DECODE_LAYOUT_Q8G32_V0 0x0202
 #define QW38_DECODE_LAYOUT_BF16_DENSE_TILE_V0 0x0203
@@ -241,6 +241,47 @@ int qw38_decode_mmv_ranges(const qw38_decode_desc* ranges, uint32_t count, void*
  * cuda/decode_mmv.cu:781-800): two BF16 dense-tile matrices (the GDN a/b
  * projections) sharing K and input, FP32 outputs, one launch. */
 int qw38_decode_ab_bf16(const qw38_decode_desc* a, const qw38_decode_desc* b, void* stream);
+/* ---- FP8 (OCP E4M3FN) projections (cuda/fp8.hpp) -------------------------
+ * Fp8Weight / Fp8Input (cuda/fp8.hpp:13-22): E4M3 codes row-major with padded
+ * extents that are multiples of 128, FP32 scales per 128-column block: weights
+ * [k/128][n/128] (128 x 128 blocks), activations [k/128][m] (1 x 128 blocks). */
+typedef struct qw38_fp8_weight {
+  const uint8_t* codes;
+  uint64_t codes_len; /* elements (bytes) */
+  const float* scales;
+  uint64_t scales_len; /* elements */
+  uint32_t n, k;
+} qw38_fp8_weight;
+typedef struct qw38_fp8_input {
+  const uint8_t* codes;
+  uint64_t codes_len;
+  const float* scales;
+  uint64_t scales_len;
+  uint32_t m, k;
+} qw38_fp8_input;
+/* Replaces cuda::pack_fp8 (cuda/fp8.hpp:29-31, cuda/fp8.cu:172-183): BF16
+ * [m][k] (m <= 1024, k <= 17408) -> codes [pm][pk], scales [pk/128][pm],
+ * absmax/448 per (row, 128 block), NaN scale for a nonfinite block. */
+int qw38_pack_fp8(const uint16_t* input, uint64_t input_len, uint32_t m, uint32_t k,
+                  uint8_t* codes, uint64_t codes_len, float* scales, uint64_t scales_len,
+                  void* stream);
+/* Replaces cuda::fp8_gemv (cuda/fp8.hpp:35-37, cuda/fp8.cu:195-203): y[n] FP32
+ * from BF16 x[k]. */
+int qw38_fp8_gemv(const qw38_fp8_weight* weight, const uint16_t* x, uint64_t x_len, float* y,
+                  uint64_t y_len, void* stream);
+/* Replaces cuda::fp8_gemm (cuda/fp8.hpp:32-34, cuda/fp8.cu:137-160): y[m][n]
+ * FP32, m a multiple of 128 up to 1024. The workspace and SM count are
+ * accepted for interface parity and must be non-empty / positive; the kernel
+ * needs no workspace. */
+int qw38_fp8_gemm(const qw38_fp8_weight* weight, const qw38_fp8_input* input, float* y,
+                  uint64_t y_len, void* workspace, uint64_t workspace_bytes, int sm_count,
+                  void* stream);
+/* Replaces cuda::fp8_store_bf16 (cuda/fp8.hpp:27-28, cuda/fp8.cu:161-171). */
+int qw38_fp8_store_bf16(const float* x, uint16_t* y, uint64_t count, void* stream);
+/* Replaces cuda::prepare_fp8_gemm (cuda/fp8.hpp:26, cuda/fp8.cu:113-123):
+ * compute units of the stream's device. */
+int qw38_fp8_prepare(void* stream, int* sm_count);
+
 /* ---- BF16 prefill projections (cuda/prefill.hpp) -------------------------
  * Stateless C-ABI under qw38::cuda::PrefillEngine (cuda/prefill.hpp:72-160):
  * BF16 token-major activations [tokens][k] times a Q4_K 0x020D weight whose

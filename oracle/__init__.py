@@ -74,6 +74,11 @@ def lib():
             "orc_pack_dense_layout": (I, [U16, V, V, U32, U32, V, V]),
             "orc_pack_bf16_tile": (I, [V, U32, U32, V]),
             "orc_dense_operands": (None, [U16, V, V, U32, U32, V]),
+            "orc_e4m3_to_fp32": (C.c_float, [C.c_uint8]),
+            "orc_fp32_to_e4m3": (C.c_uint8, [C.c_float]),
+            "orc_pack_fp8": (None, [V, U32, U32, V, V]),
+            "orc_fp8_gemv": (None, [V, V, U32, U32, V, V, V]),
+            "orc_fp8_gemm": (None, [V, V, U32, U32, V, V, U32, V, V]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -365,6 +370,53 @@ def bf16_gemv(w_bf16: np.ndarray, x_bf16: np.ndarray) -> np.ndarray:
     w = bf16_to_fp32(np.ascontiguousarray(w_bf16, np.uint16)).astype(np.float64)
     x = bf16_to_fp32(np.ascontiguousarray(x_bf16, np.uint16)).astype(np.float64)
     return w @ x
+
+
+# ---- FP8 (OCP E4M3FN) path (cuda/fp8.cu) ------------------------------------
+def pad128(v: int) -> int:
+    return (v + 127) // 128 * 128
+
+
+def e4m3_to_fp32(codes) -> np.ndarray:
+    """Values of E4M3FN codes (NaN for 0x7F / 0xFF)."""
+    table = np.array([lib().orc_e4m3_to_fp32(c) for c in range(256)], np.float32)
+    return table[np.asarray(codes, np.uint8)]
+
+
+def fp32_to_e4m3(x) -> np.ndarray:
+    """Round to nearest even E4M3FN, saturating finite values at +-448."""
+    f = lib().orc_fp32_to_e4m3
+    a = np.asarray(x, np.float32)
+    return np.array([f(float(v)) for v in a.ravel()], np.uint8).reshape(a.shape)
+
+
+def pack_fp8(x_bf16: np.ndarray, m: int, k: int):
+    """pack_fp8 (cuda/fp8.cu:64-81): codes [pm][pk], scales [pk/128][pm]."""
+    pm, pk = pad128(m), pad128(k)
+    codes = np.zeros((pm, pk), np.uint8)
+    scales = np.zeros((pk // 128, pm), np.float32)
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    lib().orc_pack_fp8(_p(x), m, k, _p(codes), _p(scales))
+    return codes, scales
+
+
+def fp8_gemv(codes, wscales, n: int, k: int, x_bf16):
+    """(y, l1) in double: y[r] = sum_c value(code) * scale * x."""
+    y = np.zeros(n, np.float64)
+    l1 = np.zeros(n, np.float64)
+    lib().orc_fp8_gemv(_p(np.ascontiguousarray(codes, np.uint8)), _p(np.ascontiguousarray(wscales, np.float32)),
+                       n, k, _p(np.ascontiguousarray(x_bf16, np.uint16)), _p(y), _p(l1))
+    return y, l1
+
+
+def fp8_gemm(wc, ws, n: int, k: int, xc, xs, m: int):
+    """(y [m][n], l1) in double for packed FP8 operands (xs is [k/128][m])."""
+    y = np.zeros((m, n), np.float64)
+    l1 = np.zeros((m, n), np.float64)
+    lib().orc_fp8_gemm(_p(np.ascontiguousarray(wc, np.uint8)), _p(np.ascontiguousarray(ws, np.float32)), n, k,
+                       _p(np.ascontiguousarray(xc, np.uint8)), _p(np.ascontiguousarray(xs, np.float32)), m,
+                       _p(y), _p(l1))
+    return y, l1
 
 
 # ---- parity metrics -------------------------------------------------------

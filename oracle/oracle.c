@@ -65,6 +65,17 @@
  *                         the logical codes (packer and decoder restated
  *                         independently), zero and max-FP16 cases of
  *                         tests/decode_mmv_unit_test.cpp:335-400.
+ *   orc_e4m3_*            OCP E4M3FN (cutlass::float_e4m3_t, cuda/fp8.cu:79).
+ *                         Pinned: decode of all 256 codes and encode (RNE,
+ *                         ties to the even code, saturation at 448) against
+ *                         the independent value()/nearest() search of
+ *                         tests/fp8_test.cpp:34-43 and torch.float8_e4m3fn.
+ *   orc_pack_fp8          cuda/fp8.cu:64-81. Pinned: per-block absmax/448
+ *                         closed form, zero tails, row independence and the
+ *                         nonfinite rule, as tests/fp8_test.cpp:55-92 checks.
+ *   orc_fp8_gemv/_gemm    cuda/fp8.cu:82-160 contraction in double; pinned as
+ *                         the reference test's own closed form
+ *                         (tests/fp8_test.cpp:105-116).
  *
  * Build with -ffp-contract=off -fno-fast-math: every FMA here is explicit.
  */
@@ -950,5 +961,97 @@ void orc_dense_operands(uint16_t layout, const uint8_t* co, const uint8_t* so, u
         w = (uint16_t)(co[tr * 512 + 2 * c] | (co[tr * 512 + 2 * c + 1] << 8));
       }
       out[(size_t)row * pk + col] = w;
+    }
+}
+
+/* ---- FP8 (OCP E4M3FN) path: cuda/fp8.cu -------------------------------- */
+/* E4M3FN value of a code: 1.mmm * 2^(e-7), subnormal m * 2^-9, 0x7F/0xFF NaN. */
+float orc_e4m3_to_fp32(uint8_t c) {
+  const unsigned mag = c & 0x7Fu, e = mag >> 3, m = mag & 7u;
+  float v;
+  if (mag == 0x7Fu) v = NAN;
+  else if (e == 0) v = ldexpf((float)m, -9);
+  else v = ldexpf(1.0f + (float)m / 8.0f, (int)e - 7);
+  return (c & 0x80u) ? -v : v;
+}
+
+/* Round to nearest even E4M3FN, finite values saturating at +-448, NaN to
+ * 0x7F (the conversion cutlass::float_e4m3_t performs in cuda/fp8.cu:79). */
+uint8_t orc_fp32_to_e4m3(float x) {
+  if (x != x) return 0x7F;
+  const uint8_t s = signbit(x) ? 0x80 : 0x00;
+  const float a = fabsf(x);
+  if (a >= 448.0f) return s | 0x7E;
+  if (a < 0.015625f) {  /* below the smallest normal 2^-6: multiples of 2^-9 */
+    const float q = rintf(a * 512.0f);  /* exact scaling; rintf rounds half to even */
+    return s | (uint8_t)q;              /* q == 8 is the smallest normal, code 0x08 */
+  }
+  int e;
+  const float f = frexpf(a, &e);        /* a = f * 2^e, f in [0.5, 1) */
+  const float q = rintf((f * 2.0f - 1.0f) * 8.0f);  /* 3-bit mantissa, half to even */
+  int ee = e - 1, mm = (int)q;
+  if (mm == 8) { mm = 0; ++ee; }
+  if (ee > 8 || (ee == 8 && mm == 7)) return s | 0x7E;
+  return s | (uint8_t)(((ee + 7) << 3) | mm);
+}
+
+/* pack_fp8 (cuda/fp8.cu:64-81): BF16 [m][k] -> E4M3 codes [pm][pk] and FP32
+ * scales [pk/128][pm], pm, pk padded to 128. Scale per (row, 128-column block):
+ * absmax/448 floored at 2^-126, 1 for an all-zero block, NaN when the block holds
+ * a nonfinite value; padding is zero. */
+void orc_pack_fp8(const uint16_t* x, uint32_t m, uint32_t k, uint8_t* codes, float* scales) {
+  const uint32_t pm = (m + 127) / 128 * 128, pk = (k + 127) / 128 * 128;
+  for (uint32_t r = 0; r < pm; ++r)
+    for (uint32_t b = 0; b < pk / 128; ++b) {
+      float peak = 0.0f;
+      int finite = 1;
+      for (uint32_t c = b * 128; c < b * 128 + 128; ++c) {
+        const float v = (r < m && c < k) ? orc_bf16_to_fp32(x[(size_t)r * k + c]) : 0.0f;
+        if (!isfinite(v)) finite = 0;
+        else if (fabsf(v) > peak) peak = fabsf(v);
+      }
+      const float scale = !finite ? NAN : (peak == 0.0f ? 1.0f : fmaxf(peak / 448.0f, 0x1p-126f));
+      scales[(size_t)b * pm + r] = scale;
+      for (uint32_t c = b * 128; c < b * 128 + 128; ++c) {
+        const float v = (r < m && c < k) ? orc_bf16_to_fp32(x[(size_t)r * k + c]) : 0.0f;
+        codes[(size_t)r * pk + c] = orc_fp32_to_e4m3(v / scale);
+      }
+    }
+}
+
+/* y[r] = sum_c value(code[r][c]) * wscale[(c/128)*(n/128) + r/128] * x[c] in
+ * double (cuda/fp8.cu:82-112); l1 = sum of the absolute products. */
+void orc_fp8_gemv(const uint8_t* codes, const float* wscales, uint32_t n, uint32_t k,
+                  const uint16_t* x, double* out, double* l1) {
+  for (uint32_t r = 0; r < n; ++r) {
+    double acc = 0, s1 = 0;
+    for (uint32_t c = 0; c < k; ++c) {
+      const double z = (double)orc_e4m3_to_fp32(codes[(size_t)r * k + c]) *
+                       (double)wscales[(size_t)(c / 128) * (n / 128) + r / 128] *
+                       (double)orc_bf16_to_fp32(x[c]);
+      acc += z;
+      s1 += fabs(z);
+    }
+    out[r] = acc;
+    if (l1) l1[r] = s1;
+  }
+}
+
+/* y[t][r] = sum_c (value(xc[t][c]) xs[c/128][t]) (value(wc[r][c]) ws[(c/128)*(n/128) + r/128])
+ * in double (the contraction fp8_gemm performs, cuda/fp8.cu:137-160). */
+void orc_fp8_gemm(const uint8_t* wc, const float* ws, uint32_t n, uint32_t k, const uint8_t* xc,
+                  const float* xs, uint32_t m, double* out, double* l1) {
+  for (uint32_t t = 0; t < m; ++t)
+    for (uint32_t r = 0; r < n; ++r) {
+      double acc = 0, s1 = 0;
+      for (uint32_t c = 0; c < k; ++c) {
+        const double a = (double)orc_e4m3_to_fp32(xc[(size_t)t * k + c]) * (double)xs[(size_t)(c / 128) * m + t];
+        const double b = (double)orc_e4m3_to_fp32(wc[(size_t)r * k + c]) *
+                         (double)ws[(size_t)(c / 128) * (n / 128) + r / 128];
+        acc += a * b;
+        s1 += fabs(a * b);
+      }
+      out[(size_t)t * n + r] = acc;
+      if (l1) l1[(size_t)t * n + r] = s1;
     }
 }

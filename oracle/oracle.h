@@ -114,6 +114,18 @@ int orc_pack_bf16_tile(const uint16_t* w, uint32_t n, uint32_t k, uint8_t* co);
 void orc_dense_operands(uint16_t layout, const uint8_t* co, const uint8_t* so, uint32_t pn,
                         uint32_t pk, uint16_t* out);
 
+/* ---- FP8 (OCP E4M3FN) path (cuda/fp8.cu) ---------------------------------- */
+float orc_e4m3_to_fp32(uint8_t c);
+uint8_t orc_fp32_to_e4m3(float x);
+/* BF16 [m][k] -> codes [pm][pk], scales [pk/128][pm] (pm, pk padded to 128). */
+void orc_pack_fp8(const uint16_t* x, uint32_t m, uint32_t k, uint8_t* codes, float* scales);
+/* y[n] and per-row sum of |products| (l1, may be NULL) in double. */
+void orc_fp8_gemv(const uint8_t* codes, const float* wscales, uint32_t n, uint32_t k,
+                  const uint16_t* x, double* out, double* l1);
+/* y[m][n] and l1 [m][n] (may be NULL) in double; xs is [k/128][m]. */
+void orc_fp8_gemm(const uint8_t* wc, const float* ws, uint32_t n, uint32_t k, const uint8_t* xc,
+                  const float* xs, uint32_t m, double* out, double* l1);
+
 #ifdef __cplusplus
 }
 #endif

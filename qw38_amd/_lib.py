@@ -55,6 +55,18 @@ class DecodeDesc(C.Structure):
                 ("residual", DecodeView), ("epilogue", C.c_uint8)]
 
 
+class Fp8Weight(C.Structure):
+    """qw38_fp8_weight == cuda::Fp8Weight (cuda/fp8.hpp:18-22)."""
+    _fields_ = [("codes", C.c_void_p), ("codes_len", C.c_uint64), ("scales", C.c_void_p),
+                ("scales_len", C.c_uint64), ("n", C.c_uint32), ("k", C.c_uint32)]
+
+
+class Fp8Input(C.Structure):
+    """qw38_fp8_input == cuda::Fp8Input (cuda/fp8.hpp:13-17)."""
+    _fields_ = [("codes", C.c_void_p), ("codes_len", C.c_uint64), ("scales", C.c_void_p),
+                ("scales_len", C.c_uint64), ("m", C.c_uint32), ("k", C.c_uint32)]
+
+
 class Qw38Error(RuntimeError):
     def __init__(self, status, hip_status, operation, detail):
         self.status, self.hip_status = status, hip_status
@@ -85,6 +97,11 @@ SIGNATURES = {
     "qw38_decode_mmv_paired": (_I, [_P(DecodeDesc), _P(DecodeDesc), _V]),
     "qw38_decode_mmv_ranges": (_I, [_P(DecodeDesc), _U32, _V]),
     "qw38_decode_ab_bf16": (_I, [_P(DecodeDesc), _P(DecodeDesc), _V]),
+    "qw38_pack_fp8": (_I, [_V, _U64, _U32, _U32, _V, _U64, _V, _U64, _V]),
+    "qw38_fp8_gemv": (_I, [_P(Fp8Weight), _V, _U64, _V, _U64, _V]),
+    "qw38_fp8_gemm": (_I, [_P(Fp8Weight), _P(Fp8Input), _V, _U64, _V, _U64, _I, _V]),
+    "qw38_fp8_store_bf16": (_I, [_V, _V, _U64, _V]),
+    "qw38_fp8_prepare": (_I, [_V, _P(_I)]),
     "qw38_prefill_project": (_I, [_P(Weight), _V, _U32, _V, _V, _I, _V]),
     "qw38_prefill_paired_swiglu": (_I, [_P(Weight), _P(Weight), _V, _V, _U32, _V]),
     "qw38_hidden_rms_bf16": (_I, [_V, _V, _F, _U32, _V, _V]),

@@ -349,9 +349,10 @@ int decode_geometry(const DDesc& d, const char* op, bool paired_b) {
 }
 
 // Layouts the reference knows but this build does not implement for decode
-// (FP8 and NVFP4).
+// (NVFP4).
 int decode_supported(const DDesc& d, const char* op) {
   switch (d.layout) {
+    case QW38_DECODE_LAYOUT_FP8_V1:
     case QW38_LAYOUT_Q4K_CANDIDATE_V2:
     case QW38_DECODE_LAYOUT_Q4G64_V0:
     case QW38_DECODE_LAYOUT_Q4G64_CANDIDATE_V1:
@@ -400,6 +401,14 @@ int decode_launch(const DDesc& a, const DDesc* b, void* stream, const char* op) 
   if (int st = stream_device(stream, &device, op)) return st;
   DeviceScope scope(device);
   if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  if (a.layout == QW38_DECODE_LAYOUT_FP8_V1) {  // cuda/fp8.cu:184-194
+    if (b) return fail(QW38_INVALID_ARGUMENT, op, "FP8 paired SwiGLU is not supported");
+    const hipError_t e = launch_fp8_gemv(
+        static_cast<const uint8_t*>(a.codes.pointer), static_cast<const float*>(a.scales.pointer),
+        a.n, a.k, static_cast<const uint16_t*>(a.input.pointer), a.output.pointer,
+        static_cast<const float*>(a.residual.pointer), a.epilogue, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, op);
+  }
   const WeightView wa = decode_weight(a);
   WeightView wb{};
   if (b) wb = decode_weight(*b);
@@ -430,6 +439,37 @@ hipError_t project(const qw38_weight& w, const Q8View& x, float* out, const floa
                    hipStream_t s) {
   if (x.m <= 8) return launch_gemv(view(w), x, out, residual, s);
   return launch_mmq(view(w), x, out, residual, s);
+}
+
+// ---- FP8 projections (cuda/fp8.cu, restated validation) -----------------
+struct FRegion {
+  const void* p;
+  uint64_t n;
+  uint32_t alignment;
+  bool write;
+};
+
+// Device-resident, aligned spans; a written span overlaps no other
+// (cuda/fp8.cu:46-57).
+int fp8_regions(std::initializer_list<FRegion> regions, int device) {
+  const FRegion* rs = regions.begin();
+  for (size_t i = 0; i < regions.size(); ++i) {
+    if (int st = validate_span(Region{rs[i].p, rs[i].n, rs[i].alignment}, device, "fp8.v1")) return st;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(rs[i].p);
+    for (size_t j = 0; j < i; ++j) {
+      const uintptr_t b = reinterpret_cast<uintptr_t>(rs[j].p);
+      if ((rs[i].write || rs[j].write) && a < b + rs[j].n && b < a + rs[i].n)
+        return fail(QW38_INVALID_ARGUMENT, "fp8.v1", "invalid geometry, extent or alias");
+    }
+  }
+  return QW38_OK;
+}
+
+int fp8_invalid() { return fail(QW38_INVALID_ARGUMENT, "fp8.v1", "invalid geometry, extent or alias"); }
+
+bool fp8_geometry(const qw38_fp8_weight& w) {  // cuda/fp8.cu:58-61
+  return w.n && w.n <= 17408 && w.k && w.k <= 17408 && !(w.n % 128) && !(w.k % 128) &&
+         w.codes_len == uint64_t(w.n) * w.k && w.scales_len == uint64_t(w.n / 128) * (w.k / 128);
 }
 
 }  // namespace
@@ -710,6 +750,79 @@ int qw38_repack_q6k_blocks(const void* blocks, uint64_t blocks_bytes, uint32_t n
     e = launch_repack_q6k(static_cast<const uint8_t*>(blocks), n, k, static_cast<uint8_t*>(codes),
                           static_cast<uint8_t*>(scales), s);
   return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+
+int qw38_fp8_prepare(void* stream, int* sm_count) {
+  constexpr const char* op = "fp8.prepare";
+  if (!sm_count) return fail(QW38_INVALID_ARGUMENT, op, "null output");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  int v = 0;
+  const hipError_t e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device);
+  if (e != hipSuccess) return hip_fail(e, op);
+  *sm_count = v;
+  return ok();
+}
+
+int qw38_fp8_store_bf16(const float* x, uint16_t* y, uint64_t count, void* stream) {
+  if (!count || count > 1024ull * 17408ull) return fp8_invalid();
+  int device = 0;
+  if (int st = stream_device(stream, &device, "fp8.store")) return st;
+  if (int st = fp8_regions({{x, count * 4, 4, false}, {y, count * 2, 2, true}}, device)) return st;
+  DeviceScope scope(device);
+  const hipError_t e = launch_fp8_store_bf16(x, y, count, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "fp8.store");
+}
+
+int qw38_pack_fp8(const uint16_t* input, uint64_t input_len, uint32_t m, uint32_t k,
+                  uint8_t* codes, uint64_t codes_len, float* scales, uint64_t scales_len,
+                  void* stream) {
+  if (!m || m > 1024 || !k || k > 17408 || input_len != uint64_t(m) * k)
+    return fp8_invalid();
+  const uint32_t pm = (m + 127) / 128 * 128, pk = (k + 127) / 128 * 128;
+  if (codes_len != uint64_t(pm) * pk || scales_len != uint64_t(pm) * (pk / 128)) return fp8_invalid();
+  int device = 0;
+  if (int st = stream_device(stream, &device, "fp8.pack")) return st;
+  if (int st = fp8_regions({{input, input_len * 2, 2, false}, {codes, codes_len, 16, true},
+                            {scales, scales_len * 4, 16, true}}, device))
+    return st;
+  DeviceScope scope(device);
+  const hipError_t e = launch_pack_fp8(input, m, k, codes, scales, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "fp8.pack");
+}
+
+int qw38_fp8_gemv(const qw38_fp8_weight* w, const uint16_t* x, uint64_t x_len, float* y,
+                  uint64_t y_len, void* stream) {
+  if (!w || !fp8_geometry(*w) || x_len != w->k || y_len != w->n) return fp8_invalid();
+  int device = 0;
+  if (int st = stream_device(stream, &device, "fp8.gemv")) return st;
+  if (int st = fp8_regions({{w->codes, w->codes_len, 16, false}, {w->scales, w->scales_len * 4, 16, false},
+                            {x, x_len * 2, 2, false}, {y, y_len * 4, 4, true}}, device))
+    return st;
+  DeviceScope scope(device);
+  const hipError_t e = launch_fp8_gemv(w->codes, w->scales, w->n, w->k, x, y, nullptr,
+                                       QW38_DECODE_STORE_FP32, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "fp8.gemv");
+}
+
+int qw38_fp8_gemm(const qw38_fp8_weight* w, const qw38_fp8_input* x, float* y, uint64_t y_len,
+                  void* workspace, uint64_t workspace_bytes, int sm_count, void* stream) {
+  if (!w || !x || !fp8_geometry(*w) || !x->m || x->m > 1024 || x->m % 128 || x->k != w->k ||
+      x->codes_len != uint64_t(x->m) * x->k || x->scales_len != uint64_t(x->m) * (x->k / 128) ||
+      y_len != uint64_t(x->m) * w->n || !workspace || !workspace_bytes || sm_count <= 0)
+    return fp8_invalid();
+  int device = 0;
+  if (int st = stream_device(stream, &device, "fp8.gemm")) return st;
+  if (int st = fp8_regions({{w->codes, w->codes_len, 16, false}, {w->scales, w->scales_len * 4, 16, false},
+                            {x->codes, x->codes_len, 16, false}, {x->scales, x->scales_len * 4, 16, false},
+                            {y, y_len * 4, 16, true}, {workspace, workspace_bytes, 256, true}},
+                           device))
+    return st;
+  DeviceScope scope(device);
+  const hipError_t e = launch_fp8_gemm(w->codes, w->scales, w->n, w->k, x->codes, x->scales, x->m, y,
+                                       static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "fp8.gemm");
 }
 
 int qw38_decode_mmv(const qw38_decode_desc* desc, void* stream) {

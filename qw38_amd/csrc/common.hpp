@@ -154,6 +154,15 @@ hipError_t launch_swiglu_q8(const float* gate, const float* up, uint32_t m, uint
                             hipStream_t s);
 // Compute units of the current device (cached per device).
 int cu_count();
+// FP8 (OCP E4M3FN) path.
+hipError_t launch_pack_fp8(const uint16_t* x, uint32_t m, uint32_t k, uint8_t* codes, float* scales,
+                           hipStream_t s);
+hipError_t launch_fp8_gemv(const uint8_t* codes, const float* scales, uint32_t n, uint32_t k,
+                           const uint16_t* x, void* y, const float* residual, int epilogue,
+                           hipStream_t s);
+hipError_t launch_fp8_gemm(const uint8_t* wc, const float* ws, uint32_t n, uint32_t k,
+                           const uint8_t* xc, const float* xs, uint32_t m, float* y, hipStream_t s);
+hipError_t launch_fp8_store_bf16(const float* x, uint16_t* y, uint64_t count, hipStream_t s);
 hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out,
                        const float* residual, hipStream_t s);
 hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,

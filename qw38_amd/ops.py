@@ -273,6 +273,7 @@ def decode_desc(w: PrefillWeight, x, output, epilogue=DECODE_STORE_FP32, residua
         d.residual = decode_view(residual, DTYPE_FP32, LAYOUT_FP32_VECTOR, w.n, 1, w.n, 1, 4,
                                  output is None)
     d.epilogue = epilogue
+    d._tensors = (w.codes, w.scales, x, output, residual)  # the views hold raw pointers
     return d
 
 
@@ -296,6 +297,91 @@ def decode_mmv_ranges(descs, stream=None) -> None:
     from ._lib import DecodeDesc
     arr = (DecodeDesc * len(descs))(*descs)
     check(lib().qw38_decode_mmv_ranges(arr, len(descs), _stream(stream)))
+
+
+# ---- FP8 (OCP E4M3FN) projections (cuda/fp8.hpp) ----------------------------
+DECODE_LAYOUT_FP8, DECODE_QUANTIZER_FP8, DTYPE_FP8 = 0x020F, 0x0107, 7
+
+
+def _pad128(v: int) -> int:
+    return (v + 127) // 128 * 128
+
+
+def fp8_weight_struct(codes, scales, n: int, k: int):
+    """cuda::Fp8Weight over device tensors: codes uint8 [n][k], scales FP32 [k/128][n/128]."""
+    from ._lib import Fp8Weight
+    w = Fp8Weight(codes.data_ptr(), codes.numel(), scales.data_ptr(), scales.numel(), n, k)
+    w._tensors = (codes, scales)  # the struct holds raw pointers: keep the storage alive with it
+    return w
+
+
+def fp8_input_struct(codes, scales, m: int, k: int):
+    """cuda::Fp8Input over device tensors: codes uint8 [m][k], scales FP32 [k/128][m]."""
+    from ._lib import Fp8Input
+    x = Fp8Input(codes.data_ptr(), codes.numel(), scales.data_ptr(), scales.numel(), m, k)
+    x._tensors = (codes, scales)
+    return x
+
+
+def pack_fp8(x, m: int, k: int, codes=None, scales=None, stream=None):
+    """cuda::pack_fp8: BF16 bits [m][k] (int16 tensor) -> (codes [pm][pk], scales [pk/128][pm])."""
+    pm, pk = _pad128(m), _pad128(k)
+    if codes is None:
+        codes = torch.empty(pm, pk, dtype=torch.uint8, device=x.device)
+    if scales is None:
+        scales = torch.empty(pk // 128, pm, dtype=torch.float32, device=x.device)
+    check(lib().qw38_pack_fp8(x.data_ptr(), x.numel(), m, k, codes.data_ptr(), codes.numel(),
+                              scales.data_ptr(), scales.numel(), _stream(stream)))
+    return codes, scales
+
+
+def fp8_gemv(w, x, y, stream=None) -> None:
+    """cuda::fp8_gemv: w a qw38_fp8_weight, x BF16 bits [k], y FP32 [n]."""
+    check(lib().qw38_fp8_gemv(C.byref(w), x.data_ptr(), x.numel(), y.data_ptr(), y.numel(),
+                              _stream(stream)))
+
+
+def fp8_gemm(w, xin, y, workspace, sm_count: int, stream=None) -> None:
+    """cuda::fp8_gemm: y FP32 [m][n] from packed operands."""
+    check(lib().qw38_fp8_gemm(C.byref(w), C.byref(xin), y.data_ptr(), y.numel(), workspace.data_ptr(),
+                              workspace.numel() * workspace.element_size(), sm_count, _stream(stream)))
+
+
+def fp8_store_bf16(x, y, stream=None) -> None:
+    """cuda::fp8_store_bf16: FP32 -> BF16 bits, round to nearest even."""
+    check(lib().qw38_fp8_store_bf16(x.data_ptr(), y.data_ptr(), x.numel(), _stream(stream)))
+
+
+def fp8_prepare(stream=None) -> int:
+    """cuda::prepare_fp8_gemm: compute units of the stream's device."""
+    v = C.c_int(0)
+    check(lib().qw38_fp8_prepare(_stream(stream), C.byref(v)))
+    return v.value
+
+
+def fp8_decode_desc(codes, scales, n: int, k: int, x, output, epilogue=DECODE_STORE_FP32,
+                    residual=None):
+    """A DecodeMmvDesc over an FP8 weight (layout 0x020F): codes uint8 [n][k],
+    scales FP32 [k/128][n/128] (cuda/prefill.cu:236-246)."""
+    from ._lib import DecodeDesc
+    d = DecodeDesc()
+    d.layout, d.quantizer, d.activation_policy = DECODE_LAYOUT_FP8, DECODE_QUANTIZER_FP8, 1
+    d.n, d.k, d.padded_n, d.padded_k = n, k, pad_n(n), pad_k(k)
+    d.codes = decode_view(codes, DTYPE_FP8, DECODE_LAYOUT_FP8, n, k, pad_n(n), pad_k(k), 16, False)
+    units = scales.numel()
+    d.scales = decode_view(scales, DTYPE_FP32, DECODE_LAYOUT_FP8, 1, units, 1, units, 16, False)
+    d.input = decode_view(x, DTYPE_BF16, LAYOUT_BF16_VECTOR, k, 1, k, 1, 2, False)
+    bf16_out = epilogue == DECODE_STORE_BF16
+    if output is not None:
+        d.output = decode_view(output, DTYPE_BF16 if bf16_out else DTYPE_FP32,
+                               LAYOUT_BF16_VECTOR if bf16_out else LAYOUT_FP32_VECTOR, n, 1, n, 1,
+                               2 if bf16_out else 4, True)
+    if residual is not None:
+        d.residual = decode_view(residual, DTYPE_FP32, LAYOUT_FP32_VECTOR, n, 1, n, 1, 4,
+                                 output is None)
+    d.epilogue = epilogue
+    d._tensors = (codes, scales, x, output, residual)  # the views hold raw pointers
+    return d
 
 
 # ---- BF16 prefill projections (cuda/prefill.hpp) ----------------------------

@@ -132,18 +132,28 @@ def test_decode_rejections_without_device():
         assert L.qw38_decode_mmv(C.byref(desc), None) == 2, needle
         err = _lib.last_error()
         assert err.operation.startswith("decode_mmv") and needle in err.detail, (needle, err.detail)
-    # a reference layout this build does not implement (FP8 V1: 1 B codes, one
-    # FP32 scale per 128x128 block) passes validation and is then rejected
+    # a reference layout this build does not implement (NVFP4 V1: 4-bit codes,
+    # FP16-typed opaque scale span of 256 + 128-row blocks x K/16 bytes) passes
+    # validation and is then rejected before any device call
     d = _decode_desc(n=128, k=256)
-    d.layout, d.quantizer = 0x020F, 0x0107
-    d.codes.layout = 0x020F
-    d.codes.dtype, d.codes.bytes = 7, 128 * 256
-    d.scales = _lib.DecodeView(0x200000, 1, 5, 0x020F, 1, 2, 1, 2, 8, 16, 0)
+    d.layout, d.quantizer = 0x020E, 0x0106
+    d.codes.layout, d.codes.dtype, d.codes.bytes = 0x020E, 6, 128 * 256 // 2
+    units = (256 + 128 * (256 // 16)) // 2
+    d.scales = _lib.DecodeView(0x200000, 1, 4, 0x020E, 1, units, 1, units, 2 * units, 16, 0)
     assert L.qw38_decode_mmv(C.byref(d), None) == 2
     assert "not implemented" in _lib.last_error().detail
-    d.n = d.codes.logical_n = d.output.logical_n = d.output.padded_n = 120
+    # FP8 V1 geometry contract (cuda/decode_mmv.cu:331-332)
+    d = _decode_desc(n=120, k=256)
+    d.layout, d.quantizer = 0x020F, 0x0107
+    d.codes.layout, d.codes.dtype, d.codes.bytes = 0x020F, 7, 120 * 256
     assert L.qw38_decode_mmv(C.byref(d), None) == 2
     assert "FP8 requires aligned mixer geometry" in _lib.last_error().detail
+    # FP8 entries reject bad geometry before touching memory
+    fw = _lib.Fp8Weight(0x100000, 100, 0x200000, 1, 128, 128)  # codes_len != n*k
+    assert L.qw38_fp8_gemv(C.byref(fw), C.c_void_p(0x300000), 128, C.c_void_p(0x400000), 128,
+                           C.c_void_p(0x1)) == 2
+    assert L.qw38_pack_fp8(C.c_void_p(0x100000), 10, 1, 11, C.c_void_p(0x200000), 0,
+                           C.c_void_p(0x300000), 0, C.c_void_p(0x1)) == 2
     # a/b contraction: BF16 dense tiles with FP32 output only
     a, b = _decode_desc(), _decode_desc()
     assert L.qw38_decode_ab_bf16(C.byref(a), C.byref(b), None) == 2

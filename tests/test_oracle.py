@@ -408,3 +408,108 @@ def test_bf16_tile_coordinates_roundtrip():
     tr = ((row // 8) * 3 + col // 256) * 8 + row % 8
     assert _le16(co, tr * 512 + 2 * (col % 256)) == w[row, col]
     assert np.array_equal(oracle.dense_operands(0x0203, co, None, n, k), w)
+
+
+# ---- FP8 (OCP E4M3FN) ---------------------------------------------------------
+def _value(code):
+    """tests/fp8_test.cpp:34-38: independent E4M3 decode."""
+    mag = code & 127
+    e, f = mag >> 3, mag & 7
+    v = np.ldexp(1.0 + f / 8.0, e - 7) if e else f / 512.0
+    return -v if code & 128 else v
+
+
+def _nearest(x):
+    """tests/fp8_test.cpp:39-43: nearest code 0..126 by brute force, ties to
+    the even code, sign from x."""
+    best, err = 0, abs(x)
+    for c in range(1, 127):
+        e = abs(abs(x) - _value(c))
+        if e < err or (e == err and not (c & 1)):
+            err, best = e, c
+    return best | (128 if np.signbit(x) else 0)
+
+
+def test_e4m3_decode_all_codes():
+    got = oracle.e4m3_to_fp32(np.arange(256))
+    for c in range(256):
+        if c & 127 == 127:
+            assert np.isnan(got[c])
+        else:
+            assert got[c] == np.float32(_value(c)), c
+    torch = pytest.importorskip("torch")
+    t = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(np.isnan(t), np.isnan(got))
+    fin = ~np.isnan(got)
+    assert np.array_equal(t[fin].view(np.uint32), got[fin].view(np.uint32))
+
+
+def test_e4m3_encode_rne_saturating():
+    """Every code value, every midpoint between neighbours (ties), values just
+    either side of them, subnormals, saturation and NaN."""
+    vals = oracle.e4m3_to_fp32(np.arange(127)).astype(np.float64)
+    mids = (vals[:-1] + vals[1:]) / 2
+    xs = np.concatenate([vals, mids, np.nextafter(mids, 0), np.nextafter(mids, 1e9),
+                         [448.0, 449.0, 464.0, 500.0, 1e30, 2.0 ** -10, 2.0 ** -11, 3 * 2.0 ** -11]])
+    xs = np.concatenate([xs, -xs]).astype(np.float32)
+    got = oracle.fp32_to_e4m3(xs)
+    for x, g in zip(xs, got):
+        assert g == _nearest(float(x)), (float(x), g)
+    assert oracle.fp32_to_e4m3(np.array([np.nan], np.float32))[0] & 127 == 127
+    torch = pytest.importorskip("torch")
+    inr = np.abs(xs) <= 448
+    t = torch.from_numpy(xs[inr]).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(t, got[inr])
+
+
+def test_pack_fp8_blocks():
+    """tests/fp8_test.cpp:55-92 checks restated: per (row, 128-block) scale
+    absmax/448 floored at the smallest normal, 1 for zero blocks; codes the RNE
+    code of x/scale; zero tails; rows independent of each other; a nonfinite
+    value makes its block's scale NaN."""
+    m, k = 130, 387
+    r = np.arange(m)[:, None]
+    c = np.arange(k)[None, :]
+    x = (((r * 23 + c * 17) % 97) - 48) * 0.03125 * (1 + r // 128 + c // 128)
+    xb = oracle.fp32_to_bf16(x.astype(np.float32))
+    xb[3, 5] = oracle.fp32_to_bf16(np.array([80.0], np.float32))[0]
+    xb[7, :] = 0
+    xb[9, 200] = 0x7F80  # +inf
+    codes, scales = oracle.pack_fp8(xb, m, k)
+    pm, pk = 256, 512
+    assert codes.shape == (pm, pk) and scales.shape == (pk // 128, pm)
+    xf = oracle.bf16_to_fp32(xb)
+    for row in [0, 3, 7, 9, 100, 129]:
+        for b in range(pk // 128):
+            blk = xf[row, b * 128:min(k, b * 128 + 128)]
+            if not np.all(np.isfinite(blk)):
+                assert np.isnan(scales[b, row])
+                continue
+            peak = float(np.abs(blk).max()) if blk.size else 0.0
+            want = 1.0 if peak == 0 else max(np.float32(peak) / np.float32(448), np.float32(2.0 ** -126))
+            assert scales[b, row] == np.float32(want)
+            for col in range(b * 128, min(k, b * 128 + 128), 37):
+                assert codes[row, col] == _nearest(float(np.float32(xf[row, col]) / scales[b, row]))
+    assert not codes[m:].any() and not codes[:, k:].any()
+    one, s1 = oracle.pack_fp8(xb[3:4], 1, k)
+    assert np.array_equal(one[0], codes[3]) and np.array_equal(s1[:, 0], scales[:, 3])
+
+
+def test_fp8_contractions_closed_form():
+    """The double closed forms agree with a dense numpy evaluation of the
+    decoded operands (gemv and gemm, including the scale indexing)."""
+    rng = np.random.Generator(np.random.PCG64(8))
+    n, k, m = 256, 384, 5
+    wc = rng.integers(0, 256, (n, k)).astype(np.uint8)
+    wc[(wc & 127) == 127] = 0
+    ws = rng.random((k // 128, n // 128)).astype(np.float32) + 0.5
+    x = oracle.fp32_to_bf16(rng.standard_normal(k).astype(np.float32))
+    y, _ = oracle.fp8_gemv(wc, ws, n, k, x)
+    wd = oracle.e4m3_to_fp32(wc).astype(np.float64) * np.repeat(np.repeat(ws.T, 128, 0), 128, 1)
+    assert np.allclose(y, wd @ oracle.bf16_to_fp32(x).astype(np.float64), rtol=1e-12, atol=1e-12)
+    xc = rng.integers(0, 256, (m, k)).astype(np.uint8)
+    xc[(xc & 127) == 127] = 1
+    xs = rng.random((k // 128, m)).astype(np.float32)
+    g, _ = oracle.fp8_gemm(wc, ws, n, k, xc, xs, m)
+    xd = oracle.e4m3_to_fp32(xc).astype(np.float64) * np.repeat(xs.T, 128, 1)
+    assert np.allclose(g, xd @ wd.T, rtol=1e-12, atol=1e-12)
