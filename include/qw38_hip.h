@@ -276,6 +276,17 @@ int qw38_fp8_gemv(const qw38_fp8_weight* weight, const uint16_t* x, uint64_t x_l
 int qw38_fp8_gemm(const qw38_fp8_weight* weight, const qw38_fp8_input* input, float* y,
                   uint64_t y_len, void* workspace, uint64_t workspace_bytes, int sm_count,
                   void* stream);
+/* Replaces the FP8 branch of PrefillEngine::project for M > 1
+ * (cuda/prefill.cu:565-593: fp8_gemm into an FP32 scratch, then
+ * epilogue_kernel at cuda/prefill.cu:116-134). Here the epilogue is fused into
+ * the GEMM's store and no scratch is used. input is the pack_fp8 operand of
+ * the tokens (m = tokens rounded up to 128); output [tokens][n] is BF16
+ * (QW38_DECODE_STORE_BF16) or FP32 (_STORE_FP32, _RESIDUAL_ADD_FP32:
+ * output = residual + product, residual [tokens][n] not aliasing output).
+ * Weight geometry: n <= 12288, n % 128 == 0, k <= 6144, k % 256 == 0
+ * (cuda/prefill.cu:218-219). */
+int qw38_fp8_project(const qw38_fp8_weight* weight, const qw38_fp8_input* input, uint32_t tokens,
+                     void* output, const float* residual, int epilogue, void* stream);
 /* Replaces cuda::fp8_store_bf16 (cuda/fp8.hpp:27-28, cuda/fp8.cu:161-171). */
 int qw38_fp8_store_bf16(const float* x, uint16_t* y, uint64_t count, void* stream);
 /* Replaces cuda::prepare_fp8_gemm (cuda/fp8.hpp:26, cuda/fp8.cu:113-123):

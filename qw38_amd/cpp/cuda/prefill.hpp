@@ -1,6 +1,7 @@
-// BF16 prefill engine (interface of cuda/prefill.hpp in Enucatl/qw38). Q4_K
-// 0x020D weights run on this build's BF16 MFMA projection; the Q8 MMQ path is
-// q4k_q8_project. Other weight layouts are rejected as not implemented.
+// Prefill engine (interface of cuda/prefill.hpp in Enucatl/qw38). Q4_K 0x020D
+// weights run on this build's BF16 MFMA projection (the Q8 MMQ path is
+// q4k_q8_project); FP8 0x020F weights run on the FP8 GEMM with a fused
+// epilogue (M > 1) or decode_mmv (M = 1). Other layouts are rejected.
 #pragma once
 
 #include "cuda/buffer.hpp"
@@ -20,6 +21,7 @@ inline constexpr std::uint32_t kPrefillDefaultTokens = 1024;
 inline constexpr std::uint32_t kPrefillDefaultWeightRows = 512;
 inline constexpr std::uint32_t kPrefillMaxK = 17408;
 inline constexpr std::uint32_t kPrefillHeadRows = 8;
+inline constexpr std::uint32_t kFp8MaxK = 6144;  // FP8 prefill projections: k <= 6144
 
 // Validate an externally borrowed device span before a multi-stage layer
 // mutates state: device memory of `device`, aligned, inside one allocation.
@@ -62,7 +64,7 @@ struct PrefillProjection {
   std::uint32_t valid_tokens{};
   std::uint64_t first_position{};
   PrefillEpilogue epilogue{PrefillEpilogue::StoreBf16};
-  Fp8Input packed{};
+  Fp8Input packed{};  // FP8 with M > 1: fp8_operand(valid_tokens, k), packed by the caller
 };
 
 class PrefillEngine {
@@ -76,12 +78,15 @@ class PrefillEngine {
   PrefillEngine& operator=(PrefillEngine const&) = delete;
 
   // Both dispatch policies run the same BF16 MFMA projection here; fp8 = true
-  // is rejected (no FP8 path on this build).
+  // also reserves the engine-owned FP8 activation operand (codes + scales of
+  // up to token_capacity x 6144).
   [[nodiscard]] static expected<PrefillEngine, Error> create(
       Stream const& stream, std::uint32_t token_capacity = kPrefillDefaultTokens,
       std::uint32_t weight_rows = kPrefillDefaultWeightRows,
       PrefillDispatch dispatch = PrefillDispatch::BoundedUnpackBf16Cublas, bool fp8 = false);
 
+  // The engine-owned operand for pack_fp8 of m tokens of width k (k <= 6144,
+  // k % 128 == 0); empty without an FP8 engine or for an invalid shape.
   [[nodiscard]] Fp8Input fp8_operand(unsigned m, unsigned k) const noexcept;
   [[nodiscard]] expected<void, Error> project(PrefillProjection const& projection);
   [[nodiscard]] expected<void, Error> paired_swiglu(PrefillWeight const& gate,
@@ -106,13 +111,16 @@ class PrefillEngine {
       PrefillWeight const& head, std::uint16_t const* normalized, std::uint32_t valid_tokens,
       std::uint64_t first_position, std::span<std::uint32_t const> requested_rows, float* logits);
 
-  [[nodiscard]] std::uint64_t workspace_bytes() const noexcept { return workspace_.bytes(); }
+  [[nodiscard]] std::uint64_t workspace_bytes() const noexcept {
+    return workspace_.bytes() + fp8_workspace_.bytes();
+  }
   [[nodiscard]] std::uint32_t token_capacity() const noexcept { return token_capacity_; }
   [[nodiscard]] std::uint32_t weight_rows() const noexcept { return weight_rows_; }
   [[nodiscard]] Stream const* stream() const noexcept { return stream_; }
 
  private:
   [[nodiscard]] expected<void, Error> ready(char const* op) const;
+  [[nodiscard]] expected<void, Error> project_fp8(PrefillProjection const& projection);
 
   Stream const* stream_{};
   hipStream_t native_stream_{};
@@ -121,6 +129,8 @@ class PrefillEngine {
   std::uint32_t token_capacity_{};
   std::uint32_t weight_rows_{};
   PrefillDispatch dispatch_{PrefillDispatch::BoundedUnpackBf16Cublas};
+  DeviceBuffer fp8_workspace_{};  // FP8 operand: codes [cap][6144], scales [48][cap]
+  int fp8_sm_count_{};
 };
 
 }  // namespace qw38::cuda

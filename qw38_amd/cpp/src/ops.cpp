@@ -1,7 +1,7 @@
 // qw38::cuda operators of the projection path over the C-ABI of libqw38_hip:
 // q4k_q8 (cuda/q4k_q8.hpp), the hidden RMS producers (cuda/activation.hpp),
-// decode_mmv (cuda/decode_mmv.hpp), the FP8 entry points (cuda/fp8.hpp, not
-// implemented) and the BF16 PrefillEngine (cuda/prefill.hpp).
+// decode_mmv (cuda/decode_mmv.hpp), the FP8 entry points (cuda/fp8.hpp) and
+// the PrefillEngine (cuda/prefill.hpp) with its BF16 and FP8 branches.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -174,15 +174,68 @@ expected<void, Error> launch_decode_mmv_ranges(DecodeMmvRangeDesc const& desc, S
   return from_abi(qw38_decode_mmv_ranges(ds.data(), uint32_t(ds.size()), stream.native()));
 }
 
-// ---- FP8 (types only on this build) -------------------------------------------------
-expected<void, Error> pack_fp8(std::span<std::uint16_t const>, unsigned, unsigned,
-                               std::span<std::uint8_t>, std::span<float>, Stream const&) {
-  return unexpected(not_implemented("fp8.pack", "FP8"));
+// ---- FP8 (cuda/fp8.hpp) ------------------------------------------------------------
+namespace {
+qw38_fp8_weight abi(Fp8Weight const& w) {
+  return qw38_fp8_weight{w.codes.data(), w.codes.size(), w.scales.data(), w.scales.size(), w.n, w.k};
+}
+qw38_fp8_input abi(Fp8Input const& x) {
+  return qw38_fp8_input{x.codes.data(), x.codes.size(), x.scales.data(), x.scales.size(), x.m, x.k};
+}
+}  // namespace
+
+expected<void, Error> fp8_decode(DecodeMmvDesc const& desc, Stream const& stream) {
+  if (desc.layout != kDecodeLayoutFp8V1)
+    return unexpected(make_error(ErrorCode::InvalidArgument, "fp8.decode", "not an FP8 descriptor"));
+  return launch_decode_mmv(desc, stream);
 }
 
-expected<void, Error> fp8_gemv(Fp8Weight, std::span<std::uint16_t const>, std::span<float>,
-                               Stream const&) {
-  return unexpected(not_implemented("fp8.gemv", "FP8"));
+expected<int, Error> prepare_fp8_gemm(Stream const& stream) {
+  if (auto st = require_stream(stream, "fp8.prepare"); !st) return unexpected(st.error());
+  int sm = 0;
+  if (auto st = from_abi(qw38_fp8_prepare(stream.native(), &sm)); !st) return unexpected(st.error());
+  return sm;
+}
+
+expected<void, Error> fp8_store_bf16(std::span<float const> input, std::span<std::uint16_t> output,
+                                     Stream const& stream) {
+  if (auto st = require_stream(stream, "fp8.store"); !st) return st;
+  if (input.size() != output.size())
+    return unexpected(make_error(ErrorCode::InvalidArgument, "fp8.v1", "invalid geometry, extent or alias"));
+  auto guard = stream.activate();
+  if (!guard) return unexpected(guard.error());
+  return from_abi(qw38_fp8_store_bf16(input.data(), output.data(), input.size(), stream.native()));
+}
+
+expected<void, Error> pack_fp8(std::span<std::uint16_t const> input, unsigned m, unsigned k,
+                               std::span<std::uint8_t> codes, std::span<float> scales,
+                               Stream const& stream) {
+  if (auto st = require_stream(stream, "fp8.pack"); !st) return st;
+  auto guard = stream.activate();
+  if (!guard) return unexpected(guard.error());
+  return from_abi(qw38_pack_fp8(input.data(), input.size(), m, k, codes.data(), codes.size(),
+                                scales.data(), scales.size(), stream.native()));
+}
+
+expected<void, Error> fp8_gemm(Fp8Weight weight, Fp8Input input, std::span<float> output,
+                               std::span<std::byte> workspace, int sm_count, Stream const& stream) {
+  if (auto st = require_stream(stream, "fp8.gemm"); !st) return st;
+  auto guard = stream.activate();
+  if (!guard) return unexpected(guard.error());
+  const qw38_fp8_weight w = abi(weight);
+  const qw38_fp8_input x = abi(input);
+  return from_abi(qw38_fp8_gemm(&w, &x, output.data(), output.size(), workspace.data(),
+                                workspace.size(), sm_count, stream.native()));
+}
+
+expected<void, Error> fp8_gemv(Fp8Weight weight, std::span<std::uint16_t const> input,
+                               std::span<float> output, Stream const& stream) {
+  if (auto st = require_stream(stream, "fp8.gemv"); !st) return st;
+  auto guard = stream.activate();
+  if (!guard) return unexpected(guard.error());
+  const qw38_fp8_weight w = abi(weight);
+  return from_abi(qw38_fp8_gemv(&w, input.data(), input.size(), output.data(), output.size(),
+                                stream.native()));
 }
 
 // ---- PrefillEngine ---------------------------------------------------------------
@@ -225,6 +278,8 @@ PrefillEngine& PrefillEngine::operator=(PrefillEngine&& other) noexcept {
     token_capacity_ = std::exchange(other.token_capacity_, 0);
     weight_rows_ = std::exchange(other.weight_rows_, 0);
     dispatch_ = other.dispatch_;
+    fp8_workspace_ = std::move(other.fp8_workspace_);
+    fp8_sm_count_ = std::exchange(other.fp8_sm_count_, 0);
   }
   return *this;
 }
@@ -240,7 +295,6 @@ expected<PrefillEngine, Error> PrefillEngine::create(Stream const& stream,
       (dispatch != PrefillDispatch::BoundedUnpackBf16Cublas && dispatch != PrefillDispatch::LocalQ4K))
     return unexpected(make_error(ErrorCode::InvalidArgument, "prefill.create",
                                  "invalid stream or token capacity"));
-  if (fp8) return unexpected(not_implemented("prefill.create", "the FP8 prefill path"));
   auto guard = stream.activate();
   if (!guard) return unexpected(guard.error());
   auto buffer = DeviceBuffer::allocate(qw38_prefill_mlp_workspace_bytes(token_capacity), stream.device());
@@ -253,6 +307,15 @@ expected<PrefillEngine, Error> PrefillEngine::create(Stream const& stream,
   e.token_capacity_ = token_capacity;
   e.weight_rows_ = weight_rows;
   e.dispatch_ = dispatch;
+  if (fp8) {  // cuda/prefill.cu:424-430; no FP32 accumulator: the epilogue is fused
+    auto sm = prepare_fp8_gemm(stream);
+    if (!sm) return unexpected(sm.error());
+    e.fp8_sm_count_ = *sm;
+    const std::uint64_t cap = (token_capacity + 127) / 128 * 128;
+    auto op = DeviceBuffer::allocate(cap * (kFp8MaxK + kFp8MaxK / 128 * 4), stream.device());
+    if (!op) return unexpected(op.error());
+    e.fp8_workspace_ = std::move(*op);
+  }
   return e;
 }
 
@@ -263,7 +326,69 @@ expected<void, Error> PrefillEngine::ready(char const* op) const {
   return {};
 }
 
-Fp8Input PrefillEngine::fp8_operand(unsigned, unsigned) const noexcept { return {}; }
+Fp8Input PrefillEngine::fp8_operand(unsigned m, unsigned k) const noexcept {
+  // cuda/prefill.cu:502-508: codes [pm][k] at the front, scales after the
+  // codes of the full capacity
+  if (fp8_workspace_.empty() || !m || m > token_capacity_ || !k || k > kFp8MaxK || k % 128) return {};
+  const std::uint64_t pm = (m + 127) / 128 * 128, cap = (token_capacity_ + 127) / 128 * 128;
+  auto const* codes = static_cast<std::uint8_t const*>(fp8_workspace_.data());
+  auto const* scales = reinterpret_cast<float const*>(codes + cap * kFp8MaxK);
+  return {{codes, pm * k}, {scales, pm * (k / 128)}, unsigned(pm), k};
+}
+
+expected<void, Error> PrefillEngine::project_fp8(PrefillProjection const& d) {
+  constexpr char const* op = "fp8.project";
+  PrefillWeight const& w = d.weight;
+  // cuda/prefill.cu:534-539: a residual exactly with the residual epilogue
+  if ((d.epilogue == PrefillEpilogue::ResidualAddFp32) != (d.residual != nullptr) ||
+      (d.epilogue != PrefillEpilogue::StoreBf16 && d.epilogue != PrefillEpilogue::StoreFp32 &&
+       d.epilogue != PrefillEpilogue::ResidualAddFp32))
+    return unexpected(make_error(ErrorCode::InvalidArgument, "prefill.project",
+                                 "input, output, position or epilogue contract mismatch"));
+  if (w.quantizer != kDecodeQuantizerFp8V1 || w.n > 12288 || w.k > kFp8MaxK || w.n % 128 ||
+      w.k % 256 || w.padded_n != w.n || w.padded_k != w.k ||
+      w.codes_bytes != std::uint64_t(w.n) * w.k ||
+      w.scales_bytes != std::uint64_t(w.n / 128) * (w.k / 128) * 4)
+    return unexpected(make_error(ErrorCode::InvalidArgument, "prefill.weight",
+                                 "weight, layout or token contract mismatch"));
+  if (d.valid_tokens == 1) {  // cuda/prefill.cu:566-573: decode_mmv, no pack
+    if (!d.packed.codes.empty() || !d.packed.scales.empty())
+      return unexpected(make_error(ErrorCode::InvalidArgument, op, "unused decode pack"));
+    const bool bf16 = d.epilogue == PrefillEpilogue::StoreBf16;
+    DecodeMmvDesc desc;
+    desc.layout = w.layout;
+    desc.quantizer = w.quantizer;
+    desc.n = desc.padded_n = w.n;
+    desc.k = desc.padded_k = w.k;
+    desc.epilogue = static_cast<DecodeEpilogue>(d.epilogue);
+    desc.codes = decode_matrix_view(const_cast<void*>(w.codes), DecodeDtype::Fp8, w.layout, w.n, w.k,
+                                    w.n, w.k, w.codes_bytes, 16);
+    const auto units = static_cast<std::uint32_t>(w.scales_bytes / 4);
+    desc.scales = decode_matrix_view(const_cast<void*>(w.scales), DecodeDtype::Fp32, w.layout, 1,
+                                     units, 1, units, w.scales_bytes, 16);
+    desc.input = decode_vector_view(const_cast<std::uint16_t*>(d.input), DecodeDtype::Bf16,
+                                    kDecodeLayoutBf16VectorV0, w.k, std::uint64_t(w.k) * 2, 2, false);
+    desc.output = decode_vector_view(d.output, bf16 ? DecodeDtype::Bf16 : DecodeDtype::Fp32,
+                                     bf16 ? kDecodeLayoutBf16VectorV0 : kDecodeLayoutFp32VectorV0,
+                                     w.n, std::uint64_t(w.n) * (bf16 ? 2 : 4), bf16 ? 2 : 4, true);
+    if (d.residual)
+      desc.residual = decode_vector_view(const_cast<float*>(d.residual), DecodeDtype::Fp32,
+                                         kDecodeLayoutFp32VectorV0, w.n, std::uint64_t(w.n) * 4, 4,
+                                         false);
+    return fp8_decode(desc, *stream_);
+  }
+  // cuda/prefill.cu:574-578: the engine-owned operand, packed by the caller
+  const Fp8Input owned = fp8_operand(d.valid_tokens, w.k);
+  if (owned.codes.empty() || d.packed.codes.data() != owned.codes.data() ||
+      d.packed.scales.data() != owned.scales.data() || d.packed.codes.size() != owned.codes.size() ||
+      d.packed.scales.size() != owned.scales.size() || d.packed.m != owned.m || d.packed.k != owned.k)
+    return unexpected(make_error(ErrorCode::InvalidArgument, op, "plan-owned packed operand required"));
+  const qw38_fp8_weight fw{static_cast<std::uint8_t const*>(w.codes), w.codes_bytes,
+                           static_cast<float const*>(w.scales), w.scales_bytes / 4, w.n, w.k};
+  const qw38_fp8_input fx = abi(owned);
+  return from_abi(qw38_fp8_project(&fw, &fx, d.valid_tokens, d.output, d.residual,
+                                   static_cast<int>(d.epilogue), native_stream_));
+}
 
 expected<void, Error> PrefillEngine::project(PrefillProjection const& d) {
   if (auto st = ready("prefill.project"); !st) return st;
@@ -276,6 +401,7 @@ expected<void, Error> PrefillEngine::project(PrefillProjection const& d) {
       d.first_position > std::numeric_limits<std::uint64_t>::max() - d.valid_tokens)
     return unexpected(make_error(ErrorCode::InvalidArgument, "prefill.project",
                                  "input, output, position or epilogue contract mismatch"));
+  if (d.weight.layout == kDecodeLayoutFp8V1) return project_fp8(d);
   const qw38_weight w = abi(d.weight);
   return from_abi(qw38_prefill_project(&w, d.input, d.valid_tokens, d.output, d.residual,
                                        static_cast<int>(d.epilogue), native_stream_));

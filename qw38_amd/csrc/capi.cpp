@@ -821,8 +821,37 @@ int qw38_fp8_gemm(const qw38_fp8_weight* w, const qw38_fp8_input* x, float* y, u
     return st;
   DeviceScope scope(device);
   const hipError_t e = launch_fp8_gemm(w->codes, w->scales, w->n, w->k, x->codes, x->scales, x->m, y,
-                                       static_cast<hipStream_t>(stream));
+                                       nullptr, x->m, 0, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? ok() : hip_fail(e, "fp8.gemm");
+}
+
+int qw38_fp8_project(const qw38_fp8_weight* w, const qw38_fp8_input* x, uint32_t tokens,
+                     void* output, const float* residual, int epilogue, void* stream) {
+  // PrefillEngine::project FP8 branch (cuda/prefill.cu:218-219, 565-593)
+  const bool res = epilogue == QW38_DECODE_RESIDUAL_ADD_FP32;
+  if (!w || !x || !fp8_geometry(*w) || w->n > 12288 || w->k > 6144 || w->k % 256 || !tokens ||
+      tokens > 1024 || x->m != (tokens + 127) / 128 * 128 || x->k != w->k ||
+      x->codes_len != uint64_t(x->m) * x->k || x->scales_len != uint64_t(x->m) * (x->k / 128))
+    return fp8_invalid();
+  if (epilogue < QW38_DECODE_STORE_BF16 || epilogue > QW38_DECODE_RESIDUAL_ADD_FP32 ||
+      res != (residual != nullptr) || !output)
+    return fail(QW38_INVALID_ARGUMENT, "prefill.project",
+                "input, output, position or epilogue contract mismatch");
+  int device = 0;
+  if (int st = stream_device(stream, &device, "fp8.project")) return st;
+  const uint64_t cells = uint64_t(tokens) * w->n;
+  const uint32_t ob = epilogue == QW38_DECODE_STORE_BF16 ? 2 : 4;
+  if (int st = fp8_regions({{w->codes, w->codes_len, 16, false}, {w->scales, w->scales_len * 4, 16, false},
+                            {x->codes, x->codes_len, 16, false}, {x->scales, x->scales_len * 4, 16, false},
+                            {residual, res ? cells * 4 : 0, 16, false},
+                            {output, cells * ob, ob == 2 ? 8u : 16u, true}},
+                           device))
+    return st;
+  DeviceScope scope(device);
+  const hipError_t e = launch_fp8_gemm(w->codes, w->scales, w->n, w->k, x->codes, x->scales, x->m,
+                                       output, residual, tokens, epilogue,
+                                       static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "fp8.project");
 }
 
 int qw38_decode_mmv(const qw38_decode_desc* desc, void* stream) {

@@ -160,8 +160,10 @@ hipError_t launch_pack_fp8(const uint16_t* x, uint32_t m, uint32_t k, uint8_t* c
 hipError_t launch_fp8_gemv(const uint8_t* codes, const float* scales, uint32_t n, uint32_t k,
                            const uint16_t* x, void* y, const float* residual, int epilogue,
                            hipStream_t s);
+// epilogue 0: raw FP32 [m][n]; otherwise a QW38_DECODE_* store of the first `valid` tokens.
 hipError_t launch_fp8_gemm(const uint8_t* wc, const float* ws, uint32_t n, uint32_t k,
-                           const uint8_t* xc, const float* xs, uint32_t m, float* y, hipStream_t s);
+                           const uint8_t* xc, const float* xs, uint32_t m, void* y,
+                           const float* residual, uint32_t valid, int epilogue, hipStream_t s);
 hipError_t launch_fp8_store_bf16(const float* x, uint16_t* y, uint64_t count, hipStream_t s);
 hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out,
                        const float* residual, hipStream_t s);

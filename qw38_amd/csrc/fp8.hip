@@ -141,7 +141,9 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const uint8_t* __restrict
                                                        const float* __restrict__ ws, uint32_t n,
                                                        uint32_t k, const uint8_t* __restrict__ xc,
                                                        const float* __restrict__ xsc, uint32_t m,
-                                                       float* __restrict__ y) {
+                                                       void* __restrict__ y,
+                                                       const float* __restrict__ residual,
+                                                       uint32_t valid, int epi) {
   __shared__ __align__(16) uint8_t Wt[2][128 * kStrideB];
   __shared__ __align__(16) uint8_t Xt[2][128 * kStrideB];
   const uint32_t nbs = n / 128, mbs = m / 128;
@@ -214,15 +216,30 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const uint8_t* __restrict
         for (int v = 0; v < 4; ++v) acc[i][j][v] = fmaf(s, P[i][j][v], acc[i][j][v]);
     }
   }
-  // lane holds rows 4lk..4lk+3 of row tile i for token lr of token tile j
+  // lane holds rows 4lk..4lk+3 of row tile i for token lr of token tile j.
+  // epi 0 writes the raw FP32 product of every padded token (fp8_gemm); the
+  // prefill epilogues (cuda/prefill.cu:116-134) write only the first `valid`
+  // tokens: BF16 RNE, FP32, or FP32 residual[t][r] + product.
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t t = mb * 128 + wt * 64 + j * 16 + lr;
+    if (epi != 0 && t >= valid) continue;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t r = nb * 128 + wr * 64 + i * 16 + lk * 4;
-      *reinterpret_cast<float4*>(y + size_t(t) * n + r) =
-          make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      const size_t o = size_t(t) * n + r;
+      float4 v = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      if (epi == QW38_DECODE_STORE_BF16) {
+        const uint2 b{uint32_t(f32_to_bf16_rne(v.x)) | (uint32_t(f32_to_bf16_rne(v.y)) << 16),
+                      uint32_t(f32_to_bf16_rne(v.z)) | (uint32_t(f32_to_bf16_rne(v.w)) << 16)};
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + o) = b;
+        continue;
+      }
+      if (epi == QW38_DECODE_RESIDUAL_ADD_FP32) {
+        const float4 q = *reinterpret_cast<const float4*>(residual + o);
+        v = make_float4(q.x + v.x, q.y + v.y, q.z + v.z, q.w + v.w);
+      }
+      *reinterpret_cast<float4*>(static_cast<float*>(y) + o) = v;
     }
   }
 }
@@ -252,9 +269,10 @@ hipError_t launch_fp8_gemv(const uint8_t* codes, const float* scales, uint32_t n
 }
 
 hipError_t launch_fp8_gemm(const uint8_t* wc, const float* ws, uint32_t n, uint32_t k,
-                           const uint8_t* xc, const float* xs, uint32_t m, float* y, hipStream_t s) {
+                           const uint8_t* xc, const float* xs, uint32_t m, void* y,
+                           const float* residual, uint32_t valid, int epilogue, hipStream_t s) {
   hipLaunchKernelGGL(fp8_gemm_kernel, dim3((n / 128) * (m / 128)), dim3(256), 0, s, wc, ws, n, k,
-                     xc, xs, m, y);
+                     xc, xs, m, y, residual, valid, epilogue);
   return hipGetLastError();
 }
 

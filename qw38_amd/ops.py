@@ -347,6 +347,14 @@ def fp8_gemm(w, xin, y, workspace, sm_count: int, stream=None) -> None:
                               workspace.numel() * workspace.element_size(), sm_count, _stream(stream)))
 
 
+def fp8_project(w, xin, tokens: int, output, epilogue=DECODE_STORE_BF16, residual=None,
+                stream=None) -> None:
+    """PrefillEngine::project FP8 branch for M > 1 (cuda/prefill.cu:565-593):
+    output [tokens][n] through the fused GEMM epilogue."""
+    check(lib().qw38_fp8_project(C.byref(w), C.byref(xin), tokens, output.data_ptr(),
+                                 _ptr(residual), epilogue, _stream(stream)))
+
+
 def fp8_store_bf16(x, y, stream=None) -> None:
     """cuda::fp8_store_bf16: FP32 -> BF16 bits, round to nearest even."""
     check(lib().qw38_fp8_store_bf16(x.data_ptr(), y.data_ptr(), x.numel(), _stream(stream)))

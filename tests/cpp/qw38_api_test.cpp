@@ -19,6 +19,7 @@
 #include "cuda/copy.hpp"
 #include "cuda/decode_mmv.hpp"
 #include "cuda/event.hpp"
+#include "cuda/fp8.hpp"
 #include "cuda/graph.hpp"
 #include "cuda/prefill.hpp"
 #include "cuda/q4k_q8.hpp"
@@ -424,7 +425,6 @@ void test_prefill(Stream const& s) {
   expect(engine.workspace_bytes() > 0 && engine.token_capacity() == 64, "engine owns its workspace");
   expect(!PrefillEngine::create(s, 0), "zero capacity rejected");
   expect(!PrefillEngine::create(s, 64, 300), "invalid weight_rows rejected");
-  expect(!PrefillEngine::create(s, 64, 512, PrefillDispatch::LocalQ4K, true), "FP8 engine rejected");
   // project the fixture weight (K = 512 logical for the BF16 path: k % 256 == 0)
   LogicalQ4K w = fixture_weight();
   w.k = 512;  // codes beyond 259 are zero in the fixture
@@ -473,10 +473,98 @@ void test_prefill(Stream const& s) {
          "head evaluation contract (shape, duplicates) rejected");
 }
 
+// OCP E4M3FN value of a code (bias 7, no infinities, 0x7F / 0xFF NaN).
+double e4m3_value(std::uint8_t c) {
+  const int e = (c >> 3) & 15, m = c & 7;
+  const double v = e == 0 ? std::ldexp(double(m), -9) : std::ldexp(double(8 + m), e - 10);
+  return (c & 0x80) ? -v : v;
+}
+
+// The engine's FP8 consumers (tests/fp8_test.cpp:238-266): the M > 1 projection
+// equals fp8_gemm on the engine-owned pack, siblings keep the pack, missing or
+// incompatible packs are refused, and M = 1 runs decode equal to fp8_gemv.
+void test_fp8(Stream const& s) {
+  constexpr unsigned n = 128, k = 5120, m = 256;
+  auto engine = unwrap(PrefillEngine::create(s, m, 512, PrefillDispatch::BoundedUnpackBf16Cublas, true),
+                       "FP8 engine create");
+  const int sm = unwrap(prepare_fp8_gemm(s), "prepare_fp8_gemm");
+  expect(sm > 0, "prepare_fp8_gemm reports the device's compute units");
+  const Fp8Input op = engine.fp8_operand(m, k);
+  expect(op.m == m && op.k == k && op.codes.size() == std::size_t(m) * k &&
+             op.scales.size() == std::size_t(m) * (k / 128),
+         "fp8_operand spans the engine-owned pack");
+  expect(engine.fp8_operand(m + 1, k).codes.empty() && engine.fp8_operand(m, 6272).codes.empty(),
+         "fp8_operand refuses shapes beyond capacity");
+  std::vector<std::uint8_t> wc(std::size_t(n) * k);
+  for (std::size_t i = 0; i < wc.size(); ++i) {
+    std::uint8_t c = std::uint8_t((i * 37 + i / k * 11) & 0xff);
+    wc[i] = (c & 0x7f) == 0x7f ? 0 : c;
+  }
+  std::vector<float> ws(k / 128);
+  for (unsigned b = 0; b < ws.size(); ++b) ws[b] = std::ldexp(1.0f + float(b % 5) / 8, -9 - int(b % 3));
+  std::vector<std::uint16_t> x(std::size_t(m) * k);
+  for (unsigned t = 0; t < m; ++t)
+    for (unsigned c = 0; c < k; ++c)
+      x[std::size_t(t) * k + c] =
+          float_to_bf16(float(int((t * 23 + c * 17) % 97) - 48) * 0.03125f * float(1 + t % 3));
+  auto dwc = to_device(wc, s), dws = to_device(ws, s), dx = to_device(x, s);
+  must(pack_fp8({dx.as<std::uint16_t>(), x.size()}, m, k,
+                {const_cast<std::uint8_t*>(op.codes.data()), op.codes.size()},
+                {const_cast<float*>(op.scales.data()), op.scales.size()}, s),
+       "pack_fp8 into the engine operand");
+  const Fp8Weight fw{{dwc.as<std::uint8_t>(), wc.size()}, {dws.as<float>(), ws.size()}, n, k};
+  const PrefillWeight pw{dwc.buf.data(), dws.buf.data(), kDecodeLayoutFp8V1, kDecodeQuantizerFp8V1,
+                         n, k, n, k, wc.size(), ws.size() * 4};
+  Dev projected{unwrap(DeviceBuffer::allocate(std::size_t(m) * n * 4), "alloc")};
+  Dev reference{unwrap(DeviceBuffer::allocate(std::size_t(m) * n * 4), "alloc")};
+  Dev work{unwrap(DeviceBuffer::allocate(4096), "alloc")};
+  PrefillProjection p{.weight = pw, .input = dx.as<std::uint16_t>(), .output = projected.buf.data(),
+                      .valid_tokens = m, .epilogue = PrefillEpilogue::StoreFp32, .packed = op};
+  must(engine.project(p), "FP8 engine project");
+  must(fp8_gemm(fw, op, {reference.as<float>(), std::size_t(m) * n},
+                {static_cast<std::byte*>(work.buf.data()), 4096}, sm, s),
+       "fp8_gemm");
+  const auto result = to_host<float>(projected.buf.data(), std::size_t(m) * n, s);
+  expect(result == to_host<float>(reference.buf.data(), std::size_t(m) * n, s),
+         "FP8 prefill projection equals fp8_gemm on the same pack");
+  // closed form in double on the pack actually used
+  const auto pc = to_host<std::uint8_t>(op.codes.data(), op.codes.size(), s);
+  const auto psc = to_host<float>(op.scales.data(), op.scales.size(), s);
+  bool close = true;
+  for (unsigned t : {0u, 1u, 131u, 255u})
+    for (unsigned r = 0; r < n; r += 9) {
+      double acc = 0, l1 = 0;
+      for (unsigned c = 0; c < k; ++c) {
+        const double a = e4m3_value(pc[std::size_t(t) * k + c]) * psc[std::size_t(c / 128) * m + t];
+        const double b = e4m3_value(wc[std::size_t(r) * k + c]) * ws[c / 128];
+        acc += a * b;
+        l1 += std::fabs(a * b);
+      }
+      close &= std::fabs(acc - result[std::size_t(t) * n + r]) < 1e-4 + 1e-5 * l1;
+    }
+  expect(close, "FP8 projection within 1e-4 + 1e-5 * l1 of the double contraction");
+  must(engine.project(p), "FP8 sibling project");
+  expect(result == to_host<float>(projected.buf.data(), std::size_t(m) * n, s),
+         "a sibling consumer preserves the pack");
+  p.packed = {};
+  expect(!engine.project(p), "consumer refuses a missing pack");
+  p.packed = op;
+  p.packed.k = 6144;
+  expect(!engine.project(p), "consumer refuses an incompatible pack");
+  p.packed = {};
+  p.valid_tokens = 1;
+  must(engine.project(p), "FP8 decode project");
+  must(fp8_gemv(fw, {dx.as<std::uint16_t>(), k}, {reference.as<float>(), n}, s), "fp8_gemv");
+  const auto one = to_host<float>(projected.buf.data(), n, s), ref = to_host<float>(reference.buf.data(), n, s);
+  expect(one == ref, "M = 1 decode equals fp8_gemv on the same view");
+  p.packed = op;
+  expect(!engine.project(p), "M = 1 refuses an unused decode pack");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
-  const char* names[] = {"runtime", "q4k_q8", "decode_onehot", "graph_replay", "prefill"};
+  const char* names[] = {"runtime", "q4k_q8", "decode_onehot", "graph_replay", "prefill", "fp8"};
   if (argc > 1 && std::strcmp(argv[1], "--list") == 0) {
     for (auto* n : names) std::printf("%s\n", n);
     return 0;
@@ -492,6 +580,8 @@ int main(int argc, char** argv) {
   test_graph_replay(stream);
   std::printf("== prefill\n");
   test_prefill(stream);
+  std::printf("== fp8\n");
+  test_fp8(stream);
   must(stream.sync(), "final sync");
   std::printf("%d failure(s)\n", g_failures);
   return g_failures == 0 ? 0 : 1;

@@ -154,6 +154,20 @@ def test_decode_rejections_without_device():
                            C.c_void_p(0x1)) == 2
     assert L.qw38_pack_fp8(C.c_void_p(0x100000), 10, 1, 11, C.c_void_p(0x200000), 0,
                            C.c_void_p(0x300000), 0, C.c_void_p(0x1)) == 2
+    # FP8 prefill projection: prefill geometry (k % 256, cuda/prefill.cu:218-219),
+    # operand m = tokens rounded up to 128, epilogue/residual pairing
+    fw = _lib.Fp8Weight(0x100000, 128 * 128, 0x200000, 1, 128, 128)
+    fx = _lib.Fp8Input(0x300000, 128 * 128, 0x400000, 128, 128, 128)
+    assert L.qw38_fp8_project(C.byref(fw), C.byref(fx), 5, C.c_void_p(0x500000), None, 1, None) == 2
+    assert "invalid geometry" in _lib.last_error().detail
+    fw = _lib.Fp8Weight(0x100000, 128 * 256, 0x200000, 2, 128, 256)
+    fx = _lib.Fp8Input(0x300000, 128 * 256, 0x400000, 256, 128, 256)
+    assert L.qw38_fp8_project(C.byref(fw), C.byref(fx), 129, C.c_void_p(0x500000), None, 1, None) == 2
+    assert L.qw38_fp8_project(C.byref(fw), C.byref(fx), 5, C.c_void_p(0x500000), None, 3, None) == 2
+    assert "epilogue contract" in _lib.last_error().detail
+    assert L.qw38_fp8_project(C.byref(fw), C.byref(fx), 5, C.c_void_p(0x500000),
+                              C.c_void_p(0x600000), 2, None) == 2
+    assert "epilogue contract" in _lib.last_error().detail
     # a/b contraction: BF16 dense tiles with FP32 output only
     a, b = _decode_desc(), _decode_desc()
     assert L.qw38_decode_ab_bf16(C.byref(a), C.byref(b), None) == 2

@@ -201,3 +201,39 @@ def test_fp8_store_bf16(torch_gpu):
     fin = np.isfinite(x)
     assert np.array_equal(got[fin], want[fin])
     assert got[0] == 0x7F80 and got[1] == 0xFF80 and (got[2] & 0x7FFF) > 0x7F80
+
+
+@pytest.mark.parametrize("tokens", [1, 77, 300])
+def test_fp8_project_epilogues(torch_gpu, tokens):
+    """The fused prefill epilogues equal the reference's two-pass order:
+    fp8_gemm into FP32, then BF16 RNE / FP32 / residual + value per valid
+    token (cuda/prefill.cu:116-134, 583-593); padded tokens are not written."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 384, 512
+    rng = np.random.Generator(np.random.PCG64(tokens))
+    codes = rng.integers(0, 256, (n, k)).astype(np.uint8)
+    codes[(codes & 127) == 127] = 1
+    scales = (rng.random((k // 128, n // 128)) * 1e-2).astype(np.float32)
+    xb = oracle.fp32_to_bf16(rng.standard_normal((tokens, k)).astype(np.float32))
+    xc, xs = ops.pack_fp8(_dev(torch, xb.view(np.int16)), tokens, k)
+    w = ops.fp8_weight_struct(_dev(torch, codes), _dev(torch, scales), n, k)
+    xin = ops.fp8_input_struct(xc, xs, xc.shape[0], k)
+    raw = torch.empty(xc.shape[0], n, device="cuda")
+    work = torch.empty(256, dtype=torch.uint8, device="cuda")
+    ops.fp8_gemm(w, xin, raw, work, 1)
+    rawv = raw.cpu().numpy()[:tokens]
+    yb = torch.full((tokens + 1, n), -1, dtype=torch.int16, device="cuda")
+    ops.fp8_project(w, xin, tokens, yb, ops.DECODE_STORE_BF16)
+    ybv = yb.cpu().numpy().view(np.uint16)
+    assert np.array_equal(ybv[:tokens], oracle.fp32_to_bf16(rawv))
+    assert np.all(ybv[tokens] == 0xFFFF)
+    yf = torch.full((tokens + 1, n), 7.0, device="cuda")
+    ops.fp8_project(w, xin, tokens, yf, ops.DECODE_STORE_FP32)
+    assert np.array_equal(yf.cpu().numpy()[:tokens], rawv) and torch.all(yf[tokens] == 7.0)
+    res = rng.standard_normal((tokens, n)).astype(np.float32)
+    yr = torch.empty(tokens, n, device="cuda")
+    ops.fp8_project(w, xin, tokens, yr, ops.DECODE_RESIDUAL_ADD_FP32, residual=_dev(torch, res))
+    assert np.array_equal(yr.cpu().numpy(), res + rawv)
+    ref, l1 = oracle.fp8_gemm(codes, scales, n, k, xc.cpu().numpy(), xs.cpu().numpy(), xc.shape[0])
+    _close(rawv, ref[:tokens], l1[:tokens], f"fp8_project tokens={tokens}")
