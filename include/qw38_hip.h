@@ -155,9 +155,9 @@ int qw38_quantize_q6k_blocks(const float* x, uint64_t x_len, uint32_t n, uint32_
  * (cuda/decode_mmv.cu:245-560): typed views, padded geometry, exact byte
  * counts, alignment, writability and non-overlap, all before any launch.
  * This build implements the Q4_K layout 0x020D (quantizer 0x0105), Q4G64
- * (0x0201, 0x020B), Q8G32 (0x0202, 0x020C), BF16 dense tiles (0x0203) and FP8
- * (0x020F, single and ranged launches); NVFP4 (0x020E) is recognised and
- * rejected with QW38_INVALID_ARGUMENT ("not implemented on this build"). */
+ * (0x0201, 0x020B), Q8G32 (0x0202, 0x020C), BF16 dense tiles (0x0203), FP8
+ * (0x020F, single and ranged launches) and NVFP4 (0x020E: single and paired
+ * launches; ranged launches are rejected, cuda/decode_mmv.cu:796-799). */
 #define QW38_DECODE_LAYOUT_Q4G64_V0 0x0201
 #define QW38_DECODE_LAYOUT_Q8G32_V0 0x0202
 #define QW38_DECODE_LAYOUT_BF16_DENSE_TILE_V0 0x0203
@@ -287,6 +287,52 @@ int qw38_fp8_gemm(const qw38_fp8_weight* weight, const qw38_fp8_input* input, fl
  * (cuda/prefill.cu:218-219). */
 int qw38_fp8_project(const qw38_fp8_weight* weight, const qw38_fp8_input* input, uint32_t tokens,
                      void* output, const float* residual, int epilogue, void* stream);
+/* ---- NVFP4 (cuda/nvfp4.hpp, cuda/nvfp4.cu) --------------------------------
+ * Elements are E2M1 nibbles, row-major [rows][pk/2] with element 2j in the
+ * low nibble of byte j; every 16 elements share a UE4M3 scale byte placed by
+ * the CUTLASS SM1xx swizzle over 128-row stripes (src/format/nvfp4.hpp:
+ * 9-18). Weights prepend a 256-byte header whose first 4 bytes are the FP32
+ * global factor. */
+/* Replaces launch_pack_nvfp4 (cuda/nvfp4.hpp:17-19, cuda/nvfp4.cu:72-82):
+ * BF16 [m][k] -> codes [m][pk/2] and scales of pad128(m) rows (padding
+ * rows' scales 0). The byte sizes are checked against m, pad_k(k). */
+int qw38_pack_nvfp4(const uint16_t* input, uint32_t m, uint32_t k, uint8_t* codes,
+                    uint64_t codes_bytes, uint8_t* scales, uint64_t scales_bytes, void* stream);
+/* Replaces launch_hidden_rms_nvfp4 (cuda/activation.hpp:20-22,
+ * cuda/activation.cu:507-520): the RMS of hidden 5120 packed straight to
+ * NVFP4 (codes [m][2560], scales of pad128(m) rows). */
+int qw38_hidden_rms_nvfp4(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                          uint8_t* codes, uint8_t* scales, void* stream);
+/* Replaces launch_hidden_rms_fp8 (cuda/activation.hpp:16-19,
+ * cuda/activation.cu:522-534): the RMS of hidden 5120 packed to FP8 (codes
+ * [pad128(m)][5120], scales [40][pad128(m)]); companion, when non-null,
+ * receives the BF16 row [m][5120]. */
+int qw38_hidden_rms_fp8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                        uint16_t* companion, uint8_t* codes, float* scales, void* stream);
+/* Replaces nvfp4_gemm_tile (cuda/nvfp4.hpp:12-16, cuda/nvfp4.cu:83-116):
+ * output FP32 [m][n] = factor * activation . weight rows row_start ..
+ * row_start + n - 1 (m <= 1024, n <= 17408, n % 8 == 0, k <= 5120,
+ * k % 256 == 0, row_start % 128 == 0). No workspace is needed. */
+int qw38_nvfp4_gemm_tile(const void* codes, const void* scales, const uint8_t* activation,
+                         const uint8_t* activation_scales, uint32_t m, uint32_t n, uint32_t k,
+                         uint32_t row_start, float* output, void* stream);
+/* Scratch of the NVFP4 prefill entries for `tokens` rows: packed codes and
+ * scales, and the FP32 gate projection of the paired SwiGLU. */
+uint64_t qw38_nvfp4_workspace_bytes(uint32_t tokens);
+/* Replaces the NVFP4 branch of PrefillEngine::project (cuda/prefill.cu:
+ * 598-628): pack the BF16 input, W4A4 GEMM, prefill epilogue fused into the
+ * store. Weight: layout 0x020E, quantizer 0x0106, K <= 5120, K % 256 == 0,
+ * N <= 17408, N % 8 == 0 (cuda/prefill.cu:220-221). The packed part of
+ * the workspace (up to the gate region) is required. */
+int qw38_nvfp4_project(const qw38_weight* weight, const uint16_t* input, uint32_t tokens,
+                       void* output, const float* residual, int epilogue, void* workspace,
+                       uint64_t workspace_bytes, void* stream);
+/* Replaces the NVFP4 branch of PrefillEngine::paired_swiglu (cuda/prefill.cu:
+ * 680-715): one pack, gate GEMM to FP32 scratch, up GEMM storing
+ * BF16(SiLU(gate) * up). */
+int qw38_nvfp4_paired_swiglu(const qw38_weight* gate, const qw38_weight* up,
+                             const uint16_t* normalized, uint16_t* swiglu, uint32_t tokens,
+                             void* workspace, uint64_t workspace_bytes, void* stream);
 /* Replaces cuda::fp8_store_bf16 (cuda/fp8.hpp:27-28, cuda/fp8.cu:161-171). */
 int qw38_fp8_store_bf16(const float* x, uint16_t* y, uint64_t count, void* stream);
 /* Replaces cuda::prepare_fp8_gemm (cuda/fp8.hpp:26, cuda/fp8.cu:113-123):
@@ -318,10 +364,13 @@ int qw38_hidden_rms_bf16(const float* residual, const uint16_t* gamma, float eps
                          uint16_t* output, void* stream);
 /* Workspace of qw38_prefill_mlp: BF16 normalized [tokens][5120] and SwiGLU
  * [tokens][17408] (the PrefillEngine's normalized_/swiglu_ buffers,
- * cuda/prefill.cu:388-397). */
+ * cuda/prefill.cu:388-397), then the NVFP4 scratch of
+ * qw38_nvfp4_workspace_bytes(tokens) used when gate/up are NVFP4. */
 uint64_t qw38_prefill_mlp_workspace_bytes(uint32_t tokens);
 /* Replaces PrefillEngine::mlp (cuda/prefill.cu:717-779): RMS -> BF16, paired
- * gate/up SwiGLU, down projection + residual into next_h [tokens][5120]. */
+ * gate/up SwiGLU, down projection + residual into next_h [tokens][5120].
+ * NVFP4 gate/up (layout 0x020E) take the fused RMS -> NVFP4 producer and the
+ * W4A4 pair (cuda/prefill.cu:766-772); down is Q4_K 0x020D. */
 int qw38_prefill_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
                      const float* h_mid, const uint16_t* gamma, float eps, float* next_h,
                      uint32_t tokens, void* workspace, uint64_t workspace_bytes, void* stream);

@@ -79,6 +79,14 @@ def lib():
             "orc_pack_fp8": (None, [V, U32, U32, V, V]),
             "orc_fp8_gemv": (None, [V, V, U32, U32, V, V, V]),
             "orc_fp8_gemm": (None, [V, V, U32, U32, V, V, U32, V, V]),
+            "orc_e2m1_value": (C.c_float, [C.c_uint8]),
+            "orc_ue4m3_value": (C.c_float, [C.c_uint8]),
+            "orc_nvfp4_nearest": (C.c_uint8, [C.c_float, I]),
+            "orc_nvfp4_sf_index": (U64, [U64, U64, U64]),
+            "orc_pack_nvfp4": (None, [V, U32, U32, V, V]),
+            "orc_quantize_nvfp4": (I, [V, U32, U32, V, V]),
+            "orc_nvfp4_gemv": (None, [V, V, U32, U32, V, U32, V, V]),
+            "orc_nvfp4_gemm": (None, [V, V, U32, U32, V, V, U32, V, V]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -416,6 +424,72 @@ def fp8_gemm(wc, ws, n: int, k: int, xc, xs, m: int):
     lib().orc_fp8_gemm(_p(np.ascontiguousarray(wc, np.uint8)), _p(np.ascontiguousarray(ws, np.float32)), n, k,
                        _p(np.ascontiguousarray(xc, np.uint8)), _p(np.ascontiguousarray(xs, np.float32)), m,
                        _p(y), _p(l1))
+    return y, l1
+
+
+# ---- NVFP4 path (cuda/nvfp4.cu, src/format/nvfp4.cpp) -----------------------
+def nvfp4_scale_bytes(rows: int, pk: int) -> int:
+    return pad128(rows) * (pk // 16)
+
+
+def pad_k256(k: int) -> int:
+    return (k + 255) // 256 * 256
+
+
+def e2m1_value(c) -> np.ndarray:
+    table = np.array([lib().orc_e2m1_value(i) for i in range(16)], np.float32)
+    return table[np.asarray(c, np.uint8) & 15]
+
+
+def ue4m3_value(c) -> np.ndarray:
+    table = np.array([lib().orc_ue4m3_value(i) for i in range(128)], np.float32)
+    return table[np.asarray(c, np.uint8) & 127]
+
+
+def nvfp4_nearest(v: float, scale: bool) -> int:
+    return int(lib().orc_nvfp4_nearest(float(v), 1 if scale else 0))
+
+
+def nvfp4_sf_index(row: int, block: int, pk: int) -> int:
+    return int(lib().orc_nvfp4_sf_index(row, block, pk))
+
+
+def pack_nvfp4(x_bf16: np.ndarray, m: int, k: int):
+    """launch_pack_nvfp4 (cuda/nvfp4.cu:72-82): (codes [m][pk/2], scales)."""
+    pk = pad_k256(k)
+    codes = np.zeros((m, pk // 2), np.uint8)
+    scales = np.zeros(nvfp4_scale_bytes(m, pk), np.uint8)
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    lib().orc_pack_nvfp4(_p(x), m, k, _p(codes), _p(scales))
+    return codes, scales
+
+
+def quantize_nvfp4(w_bf16: np.ndarray, n: int, k: int):
+    """quantize_nvfp4 (src/compiler/quantization/nvfp4.cpp:12-61): (codes
+    [pn][pk/2], scales with the 256-byte factor header), pn = pad8(n)."""
+    pk, pn = pad_k256(k), pad8(n)
+    codes = np.zeros((pn, pk // 2), np.uint8)
+    scales = np.zeros(256 + nvfp4_scale_bytes(pn, pk), np.uint8)
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    if lib().orc_quantize_nvfp4(_p(w), n, k, _p(codes), _p(scales)) != 0:
+        raise ValueError("nonfinite BF16 weight")
+    return codes, scales
+
+
+def nvfp4_gemv(codes, scales, n: int, pk: int, x_bf16, k: int):
+    y = np.zeros(n, np.float64)
+    l1 = np.zeros(n, np.float64)
+    lib().orc_nvfp4_gemv(_p(np.ascontiguousarray(codes, np.uint8)), _p(np.ascontiguousarray(scales, np.uint8)),
+                         n, pk, _p(np.ascontiguousarray(x_bf16, np.uint16)), k, _p(y), _p(l1))
+    return y, l1
+
+
+def nvfp4_gemm(wc, ws, n: int, pk: int, xc, xs, m: int):
+    y = np.zeros((m, n), np.float64)
+    l1 = np.zeros((m, n), np.float64)
+    lib().orc_nvfp4_gemm(_p(np.ascontiguousarray(wc, np.uint8)), _p(np.ascontiguousarray(ws, np.uint8)), n, pk,
+                         _p(np.ascontiguousarray(xc, np.uint8)), _p(np.ascontiguousarray(xs, np.uint8)), m,
+                         _p(y), _p(l1))
     return y, l1
 
 

@@ -76,6 +76,17 @@
  *   orc_fp8_gemv/_gemm    cuda/fp8.cu:82-160 contraction in double; pinned as
  *                         the reference test's own closed form
  *                         (tests/fp8_test.cpp:105-116).
+ *   orc_nvfp4_*           src/format/nvfp4.{hpp,cpp}, cuda/nvfp4_device.cuh,
+ *                         src/compiler/quantization/nvfp4.cpp. Element/scale
+ *                         values restate nvfp4_e2m1 / nvfp4_e4m3; the encoders
+ *                         are the exhaustive nearest-value search the reference
+ *                         test uses as its own oracle (tests/nvfp4_test.cpp:
+ *                         47-56). Pinned: the UE4M3 search equals E4M3 RNE on
+ *                         nonnegative values, the midpoint and tie fixtures of
+ *                         tests/nvfp4_test.cpp:127-147, the scale swizzle is a
+ *                         bijection with the documented stripe/chunk layout,
+ *                         and the contraction is the reference test's double
+ *                         closed form (tests/nvfp4_test.cpp:181-196).
  *
  * Build with -ffp-contract=off -fno-fast-math: every FMA here is explicit.
  */
@@ -1053,5 +1064,147 @@ void orc_fp8_gemm(const uint8_t* wc, const float* ws, uint32_t n, uint32_t k, co
       }
       out[(size_t)t * n + r] = acc;
       if (l1) l1[(size_t)t * n + r] = s1;
+    }
+}
+
+/* ---- NVFP4 (src/format/nvfp4.cpp, cuda/nvfp4_device.cuh) ------------------ */
+float orc_e2m1_value(uint8_t c) {
+  static const float v[8] = {0.f, .5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+  return (c & 8u) ? -v[c & 7u] : v[c & 7u];
+}
+
+float orc_ue4m3_value(uint8_t c) {
+  return (c >> 3) == 0 ? ldexpf((float)(c & 7u), -9) : ldexpf(1.f + (float)(c & 7u) / 8.f, (int)(c >> 3) - 7);
+}
+
+/* Nearest code by exhaustive search, ties to the even code
+ * (tests/nvfp4_test.cpp:47-56): scale codes 0..126, element codes 0..7 with
+ * the sign of a nonzero v in bit 3. */
+uint8_t orc_nvfp4_nearest(float v, int scale) {
+  float error = INFINITY;
+  unsigned best = 0;
+  for (unsigned c = 0; c < (scale ? 127u : 8u); ++c) {
+    const float value = scale ? orc_ue4m3_value((uint8_t)c) : orc_e2m1_value((uint8_t)c);
+    const float e = fabsf(fabsf(v) - value);
+    if (e < error || (e == error && !(c & 1u))) { error = e; best = c; }
+  }
+  return (uint8_t)(best | (!scale && signbit(v) && v != 0 ? 8u : 0u));
+}
+
+/* src/format/nvfp4.hpp:14-17 */
+uint64_t orc_nvfp4_sf_index(uint64_t row, uint64_t block, uint64_t pk) {
+  return (row / 128) * 128 * (pk / 16) + (block / 4) * 512 + (row % 32) * 16 + ((row % 128) / 32) * 4 +
+         block % 4;
+}
+
+/* One 16-element block (cuda/nvfp4_device.cuh:20-48): returns the scale code,
+ * writes the 8 code bytes (element 2j in the low nibble of byte j). */
+static uint8_t nvfp4_block(const float v[16], uint8_t out[8]) {
+  float peak = 0.f;
+  int finite = 1;
+  for (int i = 0; i < 16; ++i) {
+    if (!isfinite(v[i])) finite = 0;
+    else if (fabsf(v[i]) > peak) peak = fabsf(v[i]);
+  }
+  uint8_t s = finite ? orc_nvfp4_nearest(peak / 6.f, 1) : 127;
+  if (finite && peak != 0.f && s == 0) s = 1;
+  const float scale = orc_ue4m3_value(s);
+  for (int i = 0; i < 8; ++i) {
+    const float a = v[2 * i], b = v[2 * i + 1];
+    const unsigned lo = (a == 0.f || !finite) ? 0u : orc_nvfp4_nearest(a / scale, 0);
+    const unsigned hi = (b == 0.f || !finite) ? 0u : orc_nvfp4_nearest(b / scale, 0);
+    out[i] = (uint8_t)(lo | (hi << 4));
+  }
+  return s;
+}
+
+/* launch_pack_nvfp4 (cuda/nvfp4.cu:72-82): BF16 [m][k] -> codes [m][pk/2],
+ * scales of pad128(m) rows (padding rows 0; padding rows' codes absent). */
+void orc_pack_nvfp4(const uint16_t* x, uint32_t m, uint32_t k, uint8_t* codes, uint8_t* scales) {
+  const uint32_t pk = (k + 255) / 256 * 256, pm = (m + 127) / 128 * 128;
+  for (uint32_t r = 0; r < pm; ++r)
+    for (uint32_t b = 0; b < pk / 16; ++b) {
+      float v[16];
+      for (uint32_t i = 0; i < 16; ++i) {
+        const uint32_t c = b * 16 + i;
+        v[i] = (r < m && c < k) ? orc_bf16_to_fp32(x[(size_t)r * k + c]) : 0.f;
+      }
+      uint8_t out[8];
+      scales[orc_nvfp4_sf_index(r, b, pk)] = nvfp4_block(v, out);
+      if (r < m) memcpy(codes + ((size_t)r * pk + b * 16) / 2, out, 8);
+    }
+}
+
+/* quantize_nvfp4 (src/compiler/quantization/nvfp4.cpp:12-61): the weight
+ * payload of BF16 [n][k]: codes [pn][pk/2], scales 256-byte header (FP32
+ * factor = 2^ceil(log2(peak / 2688)), at least FLT_MIN) + swizzled scales of
+ * pad128(pn) rows. pn = n rounded up to 8. Returns 0, or -1 for a nonfinite
+ * weight. */
+int orc_quantize_nvfp4(const uint16_t* w, uint32_t n, uint32_t k, uint8_t* codes, uint8_t* scales) {
+  const uint32_t pk = (k + 255) / 256 * 256, pn = (n + 7) / 8 * 8;
+  float peak = 0.f;
+  for (size_t i = 0; i < (size_t)n * k; ++i) {
+    const float v = orc_bf16_to_fp32(w[i]);
+    if (!isfinite(v)) return -1;
+    if (fabsf(v) > peak) peak = fabsf(v);
+  }
+  float factor = peak == 0.f ? 1.f : (float)exp2(ceil(log2((double)peak / 2688.)));
+  if (factor < 0x1p-126f) factor = 0x1p-126f;
+  memset(codes, 0, (size_t)pn * pk / 2);
+  memset(scales, 0, 256 + (size_t)(pn + 127) / 128 * 128 * (pk / 16));
+  memcpy(scales, &factor, 4);
+  for (uint32_t r = 0; r < n; ++r)
+    for (uint32_t b = 0; b < (k + 15) / 16; ++b) {
+      float v[16] = {0};
+      for (uint32_t i = 0; i < 16 && b * 16 + i < k; ++i)
+        v[i] = orc_bf16_to_fp32(w[(size_t)r * k + b * 16 + i]) / factor;
+      uint8_t out[8];
+      scales[256 + orc_nvfp4_sf_index(r, b, pk)] = nvfp4_block(v, out);
+      memcpy(codes + ((size_t)r * pk + b * 16) / 2, out, 8);
+    }
+  return 0;
+}
+
+static inline unsigned nib(const uint8_t* codes, uint64_t i) { return (codes[i / 2] >> (4 * (i & 1))) & 15u; }
+
+/* decode_mmv NVFP4 (cuda/decode_mmv.cu:94-102, 223-239): weight element
+ * RN(RN(ue4m3(sf) * factor) * e2m1(code)) in FP32, times BF16 x, summed in
+ * double; l1 = sum of |products|. */
+void orc_nvfp4_gemv(const uint8_t* codes, const uint8_t* scales, uint32_t n, uint32_t pk,
+                    const uint16_t* x, uint32_t k, double* out, double* l1) {
+  float factor;
+  memcpy(&factor, scales, 4);
+  for (uint32_t r = 0; r < n; ++r) {
+    double acc = 0, s1 = 0;
+    for (uint32_t c = 0; c < k; ++c) {
+      const float sc = orc_ue4m3_value(scales[256 + orc_nvfp4_sf_index(r, c / 16, pk)]) * factor;
+      const float wv = sc * orc_e2m1_value((uint8_t)nib(codes, (uint64_t)r * pk + c));
+      const double z = (double)wv * (double)orc_bf16_to_fp32(x[c]);
+      acc += z;
+      s1 += fabs(z);
+    }
+    out[r] = acc;
+    if (l1) l1[r] = s1;
+  }
+}
+
+/* W4A4 (cuda/nvfp4.cu:83-116): y[t][r] = factor * sum_c (sa*a)(sw*w) in double. */
+void orc_nvfp4_gemm(const uint8_t* wc, const uint8_t* ws, uint32_t n, uint32_t pk, const uint8_t* xc,
+                    const uint8_t* xs, uint32_t m, double* out, double* l1) {
+  float factor;
+  memcpy(&factor, ws, 4);
+  for (uint32_t t = 0; t < m; ++t)
+    for (uint32_t r = 0; r < n; ++r) {
+      double acc = 0, s1 = 0;
+      for (uint32_t c = 0; c < pk; ++c) {
+        const double a = (double)orc_ue4m3_value(xs[orc_nvfp4_sf_index(t, c / 16, pk)]) *
+                         orc_e2m1_value((uint8_t)nib(xc, (uint64_t)t * pk + c));
+        const double b = (double)orc_ue4m3_value(ws[256 + orc_nvfp4_sf_index(r, c / 16, pk)]) *
+                         orc_e2m1_value((uint8_t)nib(wc, (uint64_t)r * pk + c));
+        acc += a * b;
+        s1 += fabs(a * b);
+      }
+      out[(size_t)t * n + r] = (double)factor * acc;
+      if (l1) l1[(size_t)t * n + r] = (double)factor * s1;
     }
 }

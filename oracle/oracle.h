@@ -126,6 +126,19 @@ void orc_fp8_gemv(const uint8_t* codes, const float* wscales, uint32_t n, uint32
 void orc_fp8_gemm(const uint8_t* wc, const float* ws, uint32_t n, uint32_t k, const uint8_t* xc,
                   const float* xs, uint32_t m, double* out, double* l1);
 
+/* ---- NVFP4 (src/format/nvfp4.cpp, cuda/nvfp4.cu) --------------------------- */
+float orc_e2m1_value(uint8_t c);
+float orc_ue4m3_value(uint8_t c);
+uint8_t orc_nvfp4_nearest(float v, int scale);
+uint64_t orc_nvfp4_sf_index(uint64_t row, uint64_t block, uint64_t pk);
+void orc_pack_nvfp4(const uint16_t* x, uint32_t m, uint32_t k, uint8_t* codes, uint8_t* scales);
+int orc_quantize_nvfp4(const uint16_t* w, uint32_t n, uint32_t k, uint8_t* codes, uint8_t* scales);
+void orc_nvfp4_gemv(const uint8_t* codes, const uint8_t* scales, uint32_t n, uint32_t pk,
+                    const uint16_t* x, uint32_t k, double* out, double* l1);
+void orc_nvfp4_gemm(const uint8_t* wc, const uint8_t* ws, uint32_t n, uint32_t pk, const uint8_t* xc,
+                    const uint8_t* xs, uint32_t m, double* out, double* l1);
+
+
 #ifdef __cplusplus
 }
 #endif

@@ -102,6 +102,13 @@ SIGNATURES = {
     "qw38_fp8_gemm": (_I, [_P(Fp8Weight), _P(Fp8Input), _V, _U64, _V, _U64, _I, _V]),
     "qw38_fp8_store_bf16": (_I, [_V, _V, _U64, _V]),
     "qw38_fp8_project": (_I, [_P(Fp8Weight), _P(Fp8Input), _U32, _V, _V, _I, _V]),
+    "qw38_pack_nvfp4": (_I, [_V, _U32, _U32, _V, _U64, _V, _U64, _V]),
+    "qw38_hidden_rms_nvfp4": (_I, [_V, _V, _F, _U32, _V, _V, _V]),
+    "qw38_hidden_rms_fp8": (_I, [_V, _V, _F, _U32, _V, _V, _V, _V]),
+    "qw38_nvfp4_gemm_tile": (_I, [_V, _V, _V, _V, _U32, _U32, _U32, _U32, _V, _V]),
+    "qw38_nvfp4_workspace_bytes": (_U64, [_U32]),
+    "qw38_nvfp4_project": (_I, [_P(Weight), _V, _U32, _V, _V, _I, _V, _U64, _V]),
+    "qw38_nvfp4_paired_swiglu": (_I, [_P(Weight), _P(Weight), _V, _V, _U32, _V, _U64, _V]),
     "qw38_fp8_prepare": (_I, [_V, _P(_I)]),
     "qw38_prefill_project": (_I, [_P(Weight), _V, _U32, _V, _V, _I, _V]),
     "qw38_prefill_paired_swiglu": (_I, [_P(Weight), _P(Weight), _V, _V, _U32, _V]),

@@ -348,11 +348,12 @@ int decode_geometry(const DDesc& d, const char* op, bool paired_b) {
   return QW38_OK;
 }
 
-// Layouts the reference knows but this build does not implement for decode
-// (NVFP4).
+// Layouts this build implements for decode (every layout the reference's
+// decode_mmv accepts).
 int decode_supported(const DDesc& d, const char* op) {
   switch (d.layout) {
     case QW38_DECODE_LAYOUT_FP8_V1:
+    case QW38_DECODE_LAYOUT_NVFP4_V1:
     case QW38_LAYOUT_Q4K_CANDIDATE_V2:
     case QW38_DECODE_LAYOUT_Q4G64_V0:
     case QW38_DECODE_LAYOUT_Q4G64_CANDIDATE_V1:
@@ -407,6 +408,17 @@ int decode_launch(const DDesc& a, const DDesc* b, void* stream, const char* op) 
         static_cast<const uint8_t*>(a.codes.pointer), static_cast<const float*>(a.scales.pointer),
         a.n, a.k, static_cast<const uint16_t*>(a.input.pointer), a.output.pointer,
         static_cast<const float*>(a.residual.pointer), a.epilogue, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, op);
+  }
+  if (a.layout == QW38_DECODE_LAYOUT_NVFP4_V1) {  // cuda/decode_mmv.cu:94-102, 586-587
+    const hipError_t e = launch_nvfp4_gemv(
+        static_cast<const uint8_t*>(a.codes.pointer), static_cast<const uint8_t*>(a.scales.pointer),
+        b ? static_cast<const uint8_t*>(b->codes.pointer) : nullptr,
+        b ? static_cast<const uint8_t*>(b->scales.pointer) : nullptr, a.n, a.padded_n, a.k,
+        a.padded_k, static_cast<const uint16_t*>(a.input.pointer), a.output.pointer,
+        b ? b->output.pointer : nullptr, static_cast<const float*>(a.residual.pointer),
+        b ? static_cast<const float*>(b->residual.pointer) : nullptr, a.epilogue,
+        static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, op);
   }
   const WeightView wa = decode_weight(a);
@@ -470,6 +482,44 @@ int fp8_invalid() { return fail(QW38_INVALID_ARGUMENT, "fp8.v1", "invalid geomet
 bool fp8_geometry(const qw38_fp8_weight& w) {  // cuda/fp8.cu:58-61
   return w.n && w.n <= 17408 && w.k && w.k <= 17408 && !(w.n % 128) && !(w.k % 128) &&
          w.codes_len == uint64_t(w.n) * w.k && w.scales_len == uint64_t(w.n / 128) * (w.k / 128);
+}
+
+// ---- NVFP4 (cuda/nvfp4.cu, cuda/prefill.cu:218-221, 598-628, 680-715) ----
+constexpr uint64_t pad128(uint64_t v) { return (v + 127) / 128 * 128; }
+constexpr uint64_t align256(uint64_t v) { return (v + 255) / 256 * 256; }
+
+// Engine-side NVFP4 scratch of `tokens` rows of K <= 5120: packed codes,
+// swizzled scales, and the FP32 gate projection of the paired SwiGLU.
+struct Nvfp4Scratch {
+  uint64_t codes, scales, gate, bytes;
+};
+Nvfp4Scratch nvfp4_scratch(uint32_t tokens) {
+  Nvfp4Scratch s{};
+  s.codes = 0;
+  s.scales = align256(pad128(tokens) * 2560);
+  s.gate = s.scales + align256(pad128(tokens) * 320);
+  s.bytes = s.gate + uint64_t(tokens) * 17408 * 4;
+  return s;
+}
+
+// PrefillWeight contract of an NVFP4 weight (cuda/prefill.cu:218-221,
+// 434-448): K <= 5120, K % 256 == 0, N <= 17408, N % 8 == 0, exact spans.
+int nvfp4_weight(const qw38_weight& w, uint32_t tokens, const char* op) {
+  if (!tokens || tokens > 1024 || !w.codes || !w.scales || w.layout != QW38_DECODE_LAYOUT_NVFP4_V1 ||
+      w.quantizer != QW38_DECODE_QUANTIZER_NVFP4_V1 || !w.n || w.n > 17408 || w.n % 8 || !w.k ||
+      w.k > 5120 || w.k % 256 || w.padded_n != pad_n(w.n) || w.padded_k != pad_k(w.k) ||
+      w.codes_bytes != uint64_t(w.padded_n) * w.padded_k / 2 ||
+      w.scales_bytes != 256 + pad128(w.padded_n) * (w.padded_k / 16))
+    return fail(QW38_INVALID_ARGUMENT, op, "weight, layout or token contract mismatch");
+  return QW38_OK;
+}
+
+hipError_t nvfp4_gemm(const qw38_weight& w, const uint8_t* xc, const uint8_t* xs, uint32_t tokens,
+                      void* out, const float* residual, int epilogue, hipStream_t s) {
+  const uint8_t* sc = static_cast<const uint8_t*>(w.scales);
+  return launch_nvfp4_gemm(static_cast<const uint8_t*>(w.codes), sc + 256,
+                           reinterpret_cast<const float*>(sc), w.n, w.padded_n, w.padded_k, xc, xs,
+                           tokens, out, residual, epilogue, s);
 }
 
 }  // namespace
@@ -854,6 +904,153 @@ int qw38_fp8_project(const qw38_fp8_weight* w, const qw38_fp8_input* x, uint32_t
   return e == hipSuccess ? ok() : hip_fail(e, "fp8.project");
 }
 
+int qw38_pack_nvfp4(const uint16_t* input, uint32_t m, uint32_t k, uint8_t* codes,
+                    uint64_t codes_bytes, uint8_t* scales, uint64_t scales_bytes, void* stream) {
+  constexpr const char* op = "nvfp4.pack";  // cuda/nvfp4.cu:72-82
+  if (!input || !codes || !scales || !m || m > 1024 || !k || k > 17408)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid operands");
+  const uint64_t pk = pad_k(k);
+  if (codes_bytes < uint64_t(m) * pk / 2 || scales_bytes < pad128(m) * (pk / 16))
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid operands");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = fp8_regions({{input, uint64_t(m) * k * 2, 2, false}, {codes, uint64_t(m) * pk / 2, 8, true},
+                            {scales, pad128(m) * (pk / 16), 1, true}}, device))
+    return st;
+  DeviceScope scope(device);
+  const hipError_t e = launch_pack_nvfp4(input, m, k, codes, scales, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_hidden_rms_nvfp4(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                          uint8_t* codes, uint8_t* scales, void* stream) {
+  constexpr const char* op = "nvfp4.rms";  // cuda/activation.cu:507-520
+  if (!residual || !gamma || !codes || !scales || !m || m > 1024 || !std::isfinite(eps) || eps <= 0.f)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid operands");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = fp8_regions({{residual, uint64_t(m) * 5120 * 4, 4, false}, {gamma, 5120 * 2, 2, false},
+                            {codes, uint64_t(m) * 2560, 8, true}, {scales, pad128(m) * 320, 1, true}},
+                           device))
+    return st;
+  DeviceScope scope(device);
+  const hipError_t e = launch_rms_nvfp4(residual, gamma, eps, m, codes, scales, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_hidden_rms_fp8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                        uint16_t* companion, uint8_t* codes, float* scales, void* stream) {
+  constexpr const char* op = "fp8.rms";  // cuda/activation.cu:522-534
+  if (!residual || !gamma || !codes || !scales || !m || m > 1024 || !std::isfinite(eps) || eps <= 0.f)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid operands");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  const uint64_t pm = pad128(m);
+  if (int st = fp8_regions({{residual, uint64_t(m) * 5120 * 4, 4, false}, {gamma, 5120 * 2, 2, false},
+                            {codes, pm * 5120, 16, true}, {scales, pm * 40 * 4, 4, true},
+                            {companion, companion ? uint64_t(m) * 5120 * 2 : 0, 2, true}},
+                           device))
+    return st;
+  DeviceScope scope(device);
+  const hipError_t e = launch_rms_fp8(residual, gamma, eps, m, companion, codes, scales,
+                                      static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_nvfp4_gemm_tile(const void* codes, const void* scales, const uint8_t* activation,
+                         const uint8_t* activation_scales, uint32_t m, uint32_t n, uint32_t k,
+                         uint32_t row_start, float* output, void* stream) {
+  constexpr const char* op = "nvfp4.gemm";  // cuda/nvfp4.cu:83-116
+  if (!codes || !scales || !activation || !activation_scales || !output || !m || m > 1024 || !n ||
+      n > 17408 || n % 8 || !k || k > 5120 || k % 256 || row_start % 128)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid tile");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  const uint8_t* wc = static_cast<const uint8_t*>(codes) + uint64_t(row_start) * k / 2;
+  const uint8_t* sc = static_cast<const uint8_t*>(scales);
+  const uint8_t* wsf = sc + 256 + uint64_t(row_start) * (k / 16);
+  if (int st = fp8_regions({{wc, uint64_t(n) * k / 2, 16, false}, {sc, 4, 4, false},
+                            {wsf, pad128(n) * (k / 16), 16, false},
+                            {activation, uint64_t(m) * k / 2, 16, false},
+                            {activation_scales, pad128(m) * (k / 16), 16, false},
+                            {output, uint64_t(m) * n * 4, 16, true}},
+                           device))
+    return st;
+  DeviceScope scope(device);
+  const hipError_t e = launch_nvfp4_gemm(wc, wsf, reinterpret_cast<const float*>(sc), n, n, k, activation,
+                                         activation_scales, m, output, nullptr, 0,
+                                         static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+uint64_t qw38_nvfp4_workspace_bytes(uint32_t tokens) { return nvfp4_scratch(tokens).bytes; }
+
+int qw38_nvfp4_project(const qw38_weight* weight, const uint16_t* input, uint32_t tokens,
+                       void* output, const float* residual, int epilogue, void* workspace,
+                       uint64_t workspace_bytes, void* stream) {
+  constexpr const char* op = "prefill.project";  // cuda/prefill.cu:598-628
+  if (!weight) return fail(QW38_INVALID_ARGUMENT, op, "null weight");
+  const qw38_weight& w = *weight;
+  if (int st = nvfp4_weight(w, tokens, "prefill.weight")) return st;
+  const bool res = epilogue == QW38_DECODE_RESIDUAL_ADD_FP32;
+  if (!input || !output || res != (residual != nullptr) ||
+      (epilogue != QW38_DECODE_STORE_BF16 && epilogue != QW38_DECODE_STORE_FP32 && !res))
+    return fail(QW38_INVALID_ARGUMENT, op, "input, output, position or epilogue contract mismatch");
+  const Nvfp4Scratch ws = nvfp4_scratch(tokens);
+  if (!workspace || workspace_bytes < ws.gate)
+    return fail(QW38_INVALID_ARGUMENT, op, "workspace too small");
+  const uint32_t ob = epilogue == QW38_DECODE_STORE_BF16 ? 2u : 4u;
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{w.codes, w.codes_bytes, 16}, {w.scales, w.scales_bytes, 16},
+                         {input, uint64_t(tokens) * w.k * 2, 2},
+                         {output, uint64_t(tokens) * w.n * ob, ob == 2 ? 8u : 16u},
+                         {residual, res ? uint64_t(tokens) * w.n * 4 : 0, 16},
+                         {workspace, ws.gate, 256}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* base = static_cast<uint8_t*>(workspace);
+  hipError_t e = launch_pack_nvfp4(input, tokens, w.k, base + ws.codes, base + ws.scales, s);
+  if (e == hipSuccess)
+    e = nvfp4_gemm(w, base + ws.codes, base + ws.scales, tokens, output, residual, epilogue, s);
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
+int qw38_nvfp4_paired_swiglu(const qw38_weight* gate, const qw38_weight* up,
+                             const uint16_t* normalized, uint16_t* swiglu, uint32_t tokens,
+                             void* workspace, uint64_t workspace_bytes, void* stream) {
+  constexpr const char* op = "prefill.swiglu";  // cuda/prefill.cu:680-715
+  if (!gate || !up) return fail(QW38_INVALID_ARGUMENT, op, "null weight");
+  if (int st = nvfp4_weight(*gate, tokens, "prefill.weight")) return st;
+  if (int st = nvfp4_weight(*up, tokens, "prefill.weight")) return st;
+  if (!normalized || !swiglu || gate->n != up->n || gate->k != up->k)
+    return fail(QW38_INVALID_ARGUMENT, op, "paired weight or activation contract mismatch");
+  const Nvfp4Scratch ws = nvfp4_scratch(tokens);
+  if (!workspace || workspace_bytes < ws.bytes)
+    return fail(QW38_INVALID_ARGUMENT, op, "workspace too small");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{gate->codes, gate->codes_bytes, 16}, {gate->scales, gate->scales_bytes, 16},
+                         {up->codes, up->codes_bytes, 16}, {up->scales, up->scales_bytes, 16},
+                         {normalized, uint64_t(tokens) * gate->k * 2, 2},
+                         {swiglu, uint64_t(tokens) * gate->n * 2, 8}, {workspace, ws.bytes, 256}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* base = static_cast<uint8_t*>(workspace);
+  float* g = reinterpret_cast<float*>(base + ws.gate);
+  hipError_t e = launch_pack_nvfp4(normalized, tokens, gate->k, base + ws.codes, base + ws.scales, s);
+  if (e == hipSuccess) e = nvfp4_gemm(*gate, base + ws.codes, base + ws.scales, tokens, g, nullptr, 0, s);
+  if (e == hipSuccess)
+    e = nvfp4_gemm(*up, base + ws.codes, base + ws.scales, tokens, swiglu, g, QW38_DECODE_SWIGLU_BF16, s);
+  return e == hipSuccess ? ok() : hip_fail(e, op);
+}
+
 int qw38_decode_mmv(const qw38_decode_desc* desc, void* stream) {
   constexpr const char* op = "decode_mmv";
   if (!desc) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
@@ -995,7 +1192,7 @@ int qw38_hidden_rms_bf16(const float* residual, const uint16_t* gamma, float eps
 }
 
 uint64_t qw38_prefill_mlp_workspace_bytes(uint32_t tokens) {
-  return uint64_t(tokens) * (5120u * 2u + 17408u * 2u);
+  return align256(uint64_t(tokens) * (5120u * 2u + 17408u * 2u)) + nvfp4_scratch(tokens).bytes;
 }
 
 int qw38_prefill_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
@@ -1008,8 +1205,13 @@ int qw38_prefill_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_
       up->layout != gate->layout || up->quantizer != gate->quantizer ||
       workspace_bytes < qw38_prefill_mlp_workspace_bytes(tokens))
     return fail(QW38_INVALID_ARGUMENT, op, "MLP shape or pointer contract mismatch");
-  for (const qw38_weight* w : {gate, up, down})
-    if (int st = prefill_weight(*w, tokens, "prefill.weight")) return st;
+  // NVFP4 gate/up run the fused RMS->NVFP4 producer and the W4A4 pair
+  // (cuda/prefill.cu:766-772); the down projection (K = 17408) stays Q4_K.
+  const bool nv = gate->layout == QW38_DECODE_LAYOUT_NVFP4_V1;
+  for (const qw38_weight* w : {gate, up})
+    if (int st = nv ? nvfp4_weight(*w, tokens, "prefill.weight") : prefill_weight(*w, tokens, "prefill.weight"))
+      return st;
+  if (int st = prefill_weight(*down, tokens, "prefill.weight")) return st;
   int device = 0;
   if (int st = stream_device(stream, &device, op)) return st;
   const uint64_t act = uint64_t(tokens) * 5120;
@@ -1025,11 +1227,22 @@ int qw38_prefill_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_
   const hipStream_t s = static_cast<hipStream_t>(stream);
   uint16_t* normalized = static_cast<uint16_t*>(workspace);
   uint16_t* sw = normalized + act;
-  hipError_t e = launch_rms_bf16(h_mid, gamma, eps, tokens, normalized, s);
-  const WeightView u = view(*up);
-  if (e == hipSuccess)
-    e = launch_prefill_bf16(view(*gate), &u, normalized, tokens, sw, nullptr,
-                            QW38_DECODE_STORE_BF16, s);
+  hipError_t e = hipSuccess;
+  if (nv) {
+    uint8_t* nb = static_cast<uint8_t*>(workspace) + align256(uint64_t(tokens) * (5120u * 2u + 17408u * 2u));
+    const Nvfp4Scratch ws = nvfp4_scratch(tokens);
+    float* g = reinterpret_cast<float*>(nb + ws.gate);
+    e = launch_rms_nvfp4(h_mid, gamma, eps, tokens, nb + ws.codes, nb + ws.scales, s);
+    if (e == hipSuccess) e = nvfp4_gemm(*gate, nb + ws.codes, nb + ws.scales, tokens, g, nullptr, 0, s);
+    if (e == hipSuccess)
+      e = nvfp4_gemm(*up, nb + ws.codes, nb + ws.scales, tokens, sw, g, QW38_DECODE_SWIGLU_BF16, s);
+  } else {
+    e = launch_rms_bf16(h_mid, gamma, eps, tokens, normalized, s);
+    const WeightView u = view(*up);
+    if (e == hipSuccess)
+      e = launch_prefill_bf16(view(*gate), &u, normalized, tokens, sw, nullptr,
+                              QW38_DECODE_STORE_BF16, s);
+  }
   if (e == hipSuccess)
     e = launch_prefill_bf16(view(*down), nullptr, sw, tokens, next_h, h_mid,
                             QW38_DECODE_RESIDUAL_ADD_FP32, s);

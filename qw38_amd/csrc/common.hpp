@@ -109,6 +109,19 @@ __device__ __forceinline__ float exp_cw(float x) {
   return ldexpf(p, int(n));
 }
 
+// SiLU with the logistic sigmoid in the reference's two-branch form
+// (cuda/decode_mmv.cu:78-85, cuda/prefill.cu:136-141) on exp_cw.
+__device__ __forceinline__ float silu(float z) {
+  float sg;
+  if (z >= 0.f) {
+    sg = 1.f / (1.f + exp_cw(-z));
+  } else {
+    const float e = exp_cw(z);
+    sg = e / (1.f + e);
+  }
+  return z * sg;
+}
+
 // Byte offsets of the 16-byte code word of (row, super-block kb, K32 group g)
 // and of the 16-byte metadata row of (row, kb).
 // 0x020D: tile row ((row/8)*kbs + kb)*8 + row%8; codes 128 B per tile row
@@ -165,6 +178,28 @@ hipError_t launch_fp8_gemm(const uint8_t* wc, const float* ws, uint32_t n, uint3
                            const uint8_t* xc, const float* xs, uint32_t m, void* y,
                            const float* residual, uint32_t valid, int epilogue, hipStream_t s);
 hipError_t launch_fp8_store_bf16(const float* x, uint16_t* y, uint64_t count, hipStream_t s);
+// NVFP4 (E2M1 + UE4M3 16-blocks, swizzled scales): activation pack (scales of
+// pad128(m) rows), decode GEMV (paired when cb != nullptr) and the W4A4 GEMM
+// (wsf: swizzled scales after the 256-byte header, wfactor: the header's FP32
+// factor; epilogue 0 = raw FP32, a QW38_DECODE_* store, or
+// QW38_DECODE_SWIGLU_BF16 with the gate projection FP32 [m][n] in residual).
+// Fused RMS producers of hidden 5120: NVFP4 pack (codes [m][2560], swizzled
+// scales of pad128(m) rows) and FP8 pack (codes [pm][5120], scales [40][pm],
+// BF16 companion row when non-null).
+hipError_t launch_rms_nvfp4(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                            uint8_t* codes, uint8_t* scales, hipStream_t s);
+hipError_t launch_rms_fp8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                          uint16_t* companion, uint8_t* codes, float* scales, hipStream_t s);
+hipError_t launch_pack_nvfp4(const uint16_t* x, uint32_t m, uint32_t k, uint8_t* codes,
+                             uint8_t* scales, hipStream_t s);
+hipError_t launch_nvfp4_gemv(const uint8_t* ca, const uint8_t* sa, const uint8_t* cb,
+                             const uint8_t* sb, uint32_t n, uint32_t pn, uint32_t k, uint32_t pk,
+                             const uint16_t* x, void* ya, void* yb, const float* ra, const float* rb,
+                             int epilogue, hipStream_t s);
+hipError_t launch_nvfp4_gemm(const uint8_t* wc, const uint8_t* wsf, const float* wfactor,
+                             uint32_t n, uint32_t code_rows, uint32_t pk, const uint8_t* xc,
+                             const uint8_t* xs, uint32_t m, void* y, const float* residual,
+                             int epilogue, hipStream_t s);
 hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out,
                        const float* residual, hipStream_t s);
 hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,

@@ -32,18 +32,6 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
   return uint32_t(__builtin_amdgcn_mov_dpp(int(v), ctrl, 0xf, 0xf, false));
 }
 
-// Logistic sigmoid in the reference's two-branch form (cuda/decode_mmv.cu:
-// 78-85) on this build's exp_cw.
-__device__ __forceinline__ float silu(float z) {
-  float sg;
-  if (z >= 0.f) {
-    sg = 1.f / (1.f + exp_cw(-z));
-  } else {
-    const float e = exp_cw(z);
-    sg = e / (1.f + e);
-  }
-  return z * sg;
-}
 
 struct Tile {
   uint32_t c[8];

@@ -14,7 +14,7 @@
 // MFMA keeps the sum to about 1e-7 (the reference's budget is 1e-5 of it,
 // tests/fp8_test.cpp:100). Codes are staged in LDS as bytes and widened to
 // FP16 per fragment with v_cvt_scalef32_pk_f16_fp8 (scale 1: exact).
-#include "common.hpp"
+#include "lowp.hpp"
 
 namespace qw38hip {
 namespace {
@@ -22,21 +22,6 @@ namespace {
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
-
-// Round to nearest even E4M3FN, finite values saturating at +-448, NaN -> 0x7F.
-__device__ __forceinline__ uint32_t e4m3_rne(float x) {
-  if (x != x) return 0x7Fu;
-  const uint32_t s = (__float_as_uint(x) >> 24) & 0x80u;
-  const float a = fabsf(x);
-  if (a >= 448.f) return s | 0x7Eu;
-  if (a < 0.015625f) return s | uint32_t(rintf(a * 512.f));  // multiples of 2^-9
-  const uint32_t b = __float_as_uint(a);
-  const uint32_t r = b + 0x7ffffu + ((b >> 20) & 1u);  // 3-bit mantissa, half to even
-  const int e = int(r >> 23) - 127;
-  const uint32_t mm = (r >> 20) & 7u;
-  if (e > 8 || (e == 8 && mm == 7)) return s | 0x7Eu;
-  return s | (uint32_t(e + 7) << 3) | mm;
-}
 
 // ---- pack: one block of 128 threads per (row, 128-column block) ----
 __global__ __launch_bounds__(128) void pack_fp8_kernel(const uint16_t* __restrict__ x, uint32_t m,

@@ -81,16 +81,6 @@ __device__ __forceinline__ void store_w(const WFetch& f, uint32_t g, _Float16* d
   for (int i = 0; i < 4; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
 }
 
-__device__ __forceinline__ float silu(float z) {
-  float sg;
-  if (z >= 0.f) {
-    sg = 1.f / (1.f + exp_cw(-z));
-  } else {
-    const float e = exp_cw(z);
-    sg = e / (1.f + e);
-  }
-  return z * sg;
-}
 
 template <bool Paired, bool Fast>
 __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(

@@ -5,7 +5,7 @@
 // Semantics (bit-exact): cuda/q8_device.cuh:6-25 -- peak = max finite |x|,
 // a = peak == 0 ? 1 : RN(peak / 127), z = clamp(rint(RN(x / a)), -127, 127),
 // sum = sum z; a nonfinite group stores a = NaN, z = 0 and raises the flag.
-#include "common.hpp"
+#include "lowp.hpp"
 
 namespace qw38hip {
 namespace {
@@ -78,16 +78,53 @@ __device__ float block256(float v, float* sm) {
 
 constexpr uint32_t kHidden = 5120;
 
-// cuda/activation.cu:134-190 (Pack == 3): absmax prescale, sum of squares,
-// (1+gamma)*x/rms -> BF16 RNE -> Q8. FMAs where nvcc contracts mul+add.
-// Pack: BF16 -> Q8 pack (hidden_rms_kernel<3>); otherwise the BF16 values are
-// the output (hidden_rms_kernel<0>, cuda/activation.cu:134-190).
-template <bool Pack>
+// cuda/activation.cu:134-190: absmax prescale, sum of squares,
+// (1+gamma)*x/rms -> BF16 RNE, then by Mode:
+//   kRmsBf16   the BF16 row is the output (hidden_rms_kernel<0>);
+//   kRmsQ8     Q8 pack of the BF16 row (hidden_rms_kernel<3>);
+//   kRmsNvfp4  NVFP4 pack (hidden_rms_kernel<1>, cuda/nvfp4_device.cuh:18-49);
+//   kRmsFp8    FP8 pack into codes [pm][5120] / scales [40][pm], the BF16 row
+//              also stored when out_bf16 is given (hidden_rms_kernel<2>,
+//              cuda/fp8_device.cuh:8-26).
+// NVFP4/FP8 grids cover pad128(m) rows; padding rows only write their
+// padding scales (NVFP4: 0; FP8: scale 1 and zero codes).
+// FMAs where nvcc contracts mul+add.
+enum RmsMode { kRmsBf16 = 0, kRmsQ8 = 1, kRmsNvfp4 = 2, kRmsFp8 = 3 };
+
+// one 128-element FP8 block per wave: two elements per lane
+__device__ __forceinline__ void fp8_block128(float v0, float v1, uint32_t r, uint32_t b, uint32_t pm,
+                                             uint8_t* codes, float* scales) {
+  float peak = fmaxf(isfinite(v0) ? fabsf(v0) : __builtin_inff(), isfinite(v1) ? fabsf(v1) : __builtin_inff());
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) peak = fmaxf(peak, __shfl_xor(peak, o));
+  const float scale = isfinite(peak) ? (peak == 0.f ? 1.f : fmaxf(__fdiv_rn(peak, 448.f), 0x1p-126f))
+                                     : __builtin_nanf("");
+  const uint32_t lane = threadIdx.x & 63u;
+  if (lane == 0) scales[size_t(b) * pm + r] = scale;
+  codes[size_t(r) * kHidden + b * 128 + lane] = uint8_t(e4m3_rne(__fdiv_rn(v0, scale)));
+  codes[size_t(r) * kHidden + b * 128 + 64 + lane] = uint8_t(e4m3_rne(__fdiv_rn(v1, scale)));
+}
+
+template <int Mode>
 __global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ residual,
                                                   const uint16_t* __restrict__ gamma, float eps,
-                                                  uint16_t* out_bf16, int8_t* codes, float* scales,
-                                                  int32_t* sums, int* failure) {
-  __shared__ uint16_t rounded[Pack ? kHidden : 1];
+                                                  uint16_t* out_bf16, uint32_t m, uint8_t* codes,
+                                                  float* scales, int32_t* sums, int* failure,
+                                                  uint8_t* sf_bytes) {
+  constexpr bool Pack = Mode != kRmsBf16;
+  if constexpr (Mode == kRmsNvfp4 || Mode == kRmsFp8) {
+    if (blockIdx.x >= m) {
+      if constexpr (Mode == kRmsNvfp4) {
+        for (uint32_t b = threadIdx.x; b < kHidden / 16; b += 256)
+          sf_bytes[nvfp4_sf_index(blockIdx.x, b, kHidden)] = 0;
+      } else {
+        for (uint32_t b = threadIdx.x >> 6; b < kHidden / 128; b += 4)
+          fp8_block128(0.f, 0.f, blockIdx.x, b, gridDim.x, codes, scales);
+      }
+      return;
+    }
+  }
+  __shared__ __align__(16) uint16_t rounded[Pack ? kHidden : 1];
   __shared__ float sm[9];
   const float* x = residual + size_t(blockIdx.x) * kHidden;
   uint16_t* y = Pack ? rounded : out_bf16 + size_t(blockIdx.x) * kHidden;
@@ -106,12 +143,30 @@ __global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ resi
   for (uint32_t i = threadIdx.x; i < kHidden; i += 256) {
     const float g = bf16_to_f32(gamma[i]);
     y[i] = f32_to_bf16_rne((1.0f + g) * ((x[i] / safe) * inv));
+    if constexpr (Mode == kRmsFp8)
+      if (out_bf16) out_bf16[size_t(blockIdx.x) * kHidden + i] = y[i];
   }
   if constexpr (Pack) {
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < kHidden; i += 256)
-      q8_group32(bf16_to_f32(rounded[i]), codes, scales, sums,
-                 (size_t(blockIdx.x) * kHidden + i) / 32, failure);
+    if constexpr (Mode == kRmsQ8) {
+      for (uint32_t i = threadIdx.x; i < kHidden; i += 256)
+        q8_group32(bf16_to_f32(rounded[i]), reinterpret_cast<int8_t*>(codes), scales, sums,
+                   (size_t(blockIdx.x) * kHidden + i) / 32, failure);
+    } else if constexpr (Mode == kRmsNvfp4) {
+      for (uint32_t b = threadIdx.x; b < kHidden / 16; b += 256) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = bf16_to_f32(rounded[b * 16 + i]);
+        uint32_t cw[2];
+        sf_bytes[nvfp4_sf_index(blockIdx.x, b, kHidden)] = uint8_t(nvfp4_encode_block(v, cw));
+        *reinterpret_cast<uint2*>(codes + (size_t(blockIdx.x) * kHidden + b * 16) / 2) = make_uint2(cw[0], cw[1]);
+      }
+    } else {
+      const uint32_t lane = threadIdx.x & 63u;
+      for (uint32_t b = threadIdx.x >> 6; b < kHidden / 128; b += 4)
+        fp8_block128(bf16_to_f32(rounded[b * 128 + lane]), bf16_to_f32(rounded[b * 128 + 64 + lane]),
+                     blockIdx.x, b, gridDim.x, codes, scales);
+    }
   }
 }
 
@@ -145,15 +200,29 @@ hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t p
 hipError_t launch_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
                          int8_t* codes, float* scales, int32_t* sums, int* failure,
                          hipStream_t s) {
-  hipLaunchKernelGGL(rms_kernel<true>, dim3(m), dim3(256), 0, s, residual, gamma, eps, nullptr,
-                     codes, scales, sums, failure);
+  hipLaunchKernelGGL(rms_kernel<kRmsQ8>, dim3(m), dim3(256), 0, s, residual, gamma, eps, nullptr, m,
+                     reinterpret_cast<uint8_t*>(codes), scales, sums, failure, nullptr);
   return hipGetLastError();
 }
 
 hipError_t launch_rms_bf16(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
                            uint16_t* out, hipStream_t s) {
-  hipLaunchKernelGGL(rms_kernel<false>, dim3(m), dim3(256), 0, s, residual, gamma, eps, out,
-                     nullptr, nullptr, nullptr, nullptr);
+  hipLaunchKernelGGL(rms_kernel<kRmsBf16>, dim3(m), dim3(256), 0, s, residual, gamma, eps, out, m,
+                     nullptr, nullptr, nullptr, nullptr, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_nvfp4(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                            uint8_t* codes, uint8_t* scales, hipStream_t s) {
+  hipLaunchKernelGGL(rms_kernel<kRmsNvfp4>, dim3((m + 127) / 128 * 128), dim3(256), 0, s, residual,
+                     gamma, eps, nullptr, m, codes, nullptr, nullptr, nullptr, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_fp8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
+                          uint16_t* companion, uint8_t* codes, float* scales, hipStream_t s) {
+  hipLaunchKernelGGL(rms_kernel<kRmsFp8>, dim3((m + 127) / 128 * 128), dim3(256), 0, s, residual,
+                     gamma, eps, companion, m, codes, scales, nullptr, nullptr, nullptr);
   return hipGetLastError();
 }
 

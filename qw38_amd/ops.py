@@ -392,6 +392,99 @@ def fp8_decode_desc(codes, scales, n: int, k: int, x, output, epilogue=DECODE_ST
     return d
 
 
+# ---- NVFP4 (cuda/nvfp4.hpp) ---------------------------------------------------
+DECODE_LAYOUT_NVFP4, DECODE_QUANTIZER_NVFP4, DTYPE_NVFP4 = 0x020E, 0x0106, 6
+
+
+def nvfp4_scale_count(rows: int, pk: int) -> int:
+    """Swizzled scale bytes of `rows` rows (src/format/nvfp4.hpp:12-14)."""
+    return _pad128(rows) * (pk // 16)
+
+
+def pack_nvfp4(x, m: int, k: int, codes=None, scales=None, stream=None):
+    """launch_pack_nvfp4: BF16 bits [m][k] -> (codes uint8 [m][pk/2], swizzled scales)."""
+    pk = pad_k(k)
+    if codes is None:
+        codes = torch.zeros(m, pk // 2, dtype=torch.uint8, device=x.device)
+    if scales is None:
+        scales = torch.zeros(nvfp4_scale_count(m, pk), dtype=torch.uint8, device=x.device)
+    check(lib().qw38_pack_nvfp4(x.data_ptr(), m, k, codes.data_ptr(), codes.numel(),
+                                scales.data_ptr(), scales.numel(), _stream(stream)))
+    return codes, scales
+
+
+def hidden_rms_nvfp4(residual, gamma, eps, m, codes, scales, stream=None) -> None:
+    """launch_hidden_rms_nvfp4 (cuda/activation.cu:507-520)."""
+    check(lib().qw38_hidden_rms_nvfp4(residual.data_ptr(), gamma.data_ptr(), eps, m,
+                                      codes.data_ptr(), scales.data_ptr(), _stream(stream)))
+
+
+def hidden_rms_fp8(residual, gamma, eps, m, codes, scales, companion=None, stream=None) -> None:
+    """launch_hidden_rms_fp8 (cuda/activation.cu:522-534)."""
+    check(lib().qw38_hidden_rms_fp8(residual.data_ptr(), gamma.data_ptr(), eps, m, _ptr(companion),
+                                    codes.data_ptr(), scales.data_ptr(), _stream(stream)))
+
+
+def nvfp4_gemm_tile(codes, scales, act, act_scales, m, n, k, row_start, out, stream=None) -> None:
+    """nvfp4_gemm_tile (cuda/nvfp4.cu:83-116): out FP32 [m][n]."""
+    check(lib().qw38_nvfp4_gemm_tile(codes.data_ptr(), scales.data_ptr(), act.data_ptr(),
+                                     act_scales.data_ptr(), m, n, k, row_start, out.data_ptr(),
+                                     _stream(stream)))
+
+
+def nvfp4_weight(codes, scales, n: int, k: int) -> PrefillWeight:
+    """A PrefillWeight over an NVFP4 payload (layout 0x020E)."""
+    return PrefillWeight(codes, scales, DECODE_LAYOUT_NVFP4, DECODE_QUANTIZER_NVFP4, n, k,
+                         pad_n(n), pad_k(k))
+
+
+def nvfp4_workspace_bytes(tokens: int) -> int:
+    return int(lib().qw38_nvfp4_workspace_bytes(tokens))
+
+
+def nvfp4_project(w: PrefillWeight, x, tokens: int, output, workspace, epilogue=DECODE_STORE_FP32,
+                  residual=None, stream=None) -> None:
+    """NVFP4 branch of PrefillEngine::project (cuda/prefill.cu:598-628)."""
+    ws = w.struct()
+    check(lib().qw38_nvfp4_project(C.byref(ws), x.data_ptr(), tokens, output.data_ptr(),
+                                   _ptr(residual), epilogue, workspace.data_ptr(), workspace.numel(),
+                                   _stream(stream)))
+
+
+def nvfp4_paired_swiglu(gate: PrefillWeight, up: PrefillWeight, x, swiglu, tokens: int, workspace,
+                        stream=None) -> None:
+    """NVFP4 branch of PrefillEngine::paired_swiglu (cuda/prefill.cu:680-715)."""
+    g, u = gate.struct(), up.struct()
+    check(lib().qw38_nvfp4_paired_swiglu(C.byref(g), C.byref(u), x.data_ptr(), swiglu.data_ptr(),
+                                         tokens, workspace.data_ptr(), workspace.numel(),
+                                         _stream(stream)))
+
+
+def nvfp4_decode_desc(w: PrefillWeight, x, output, epilogue=DECODE_STORE_FP32, residual=None):
+    """A DecodeMmvDesc over an NVFP4 weight (cuda/prefill.cu:236-246): scales
+    are an FP16-typed opaque span of one row."""
+    from ._lib import DecodeDesc
+    d = DecodeDesc()
+    d.layout, d.quantizer, d.activation_policy = DECODE_LAYOUT_NVFP4, DECODE_QUANTIZER_NVFP4, 1
+    d.n, d.k, d.padded_n, d.padded_k = w.n, w.k, w.padded_n, w.padded_k
+    d.codes = decode_view(w.codes, DTYPE_NVFP4, DECODE_LAYOUT_NVFP4, w.n, w.k, w.padded_n,
+                          w.padded_k, 16, False)
+    units = w.scales.numel() // 2
+    d.scales = decode_view(w.scales, DTYPE_FP16, DECODE_LAYOUT_NVFP4, 1, units, 1, units, 16, False)
+    d.input = decode_view(x, DTYPE_BF16, LAYOUT_BF16_VECTOR, w.k, 1, w.k, 1, 2, False)
+    bf16_out = epilogue in (DECODE_STORE_BF16, DECODE_SWIGLU_BF16)
+    if output is not None:
+        d.output = decode_view(output, DTYPE_BF16 if bf16_out else DTYPE_FP32,
+                               LAYOUT_BF16_VECTOR if bf16_out else LAYOUT_FP32_VECTOR, w.n, 1, w.n,
+                               1, 2 if bf16_out else 4, True)
+    if residual is not None:
+        d.residual = decode_view(residual, DTYPE_FP32, LAYOUT_FP32_VECTOR, w.n, 1, w.n, 1, 4,
+                                 output is None)
+    d.epilogue = epilogue
+    d._tensors = (w.codes, w.scales, x, output, residual)
+    return d
+
+
 # ---- BF16 prefill projections (cuda/prefill.hpp) ----------------------------
 def prefill_project(w: PrefillWeight, x, tokens: int, output, epilogue=DECODE_STORE_FP32,
                     residual=None, stream=None) -> None:

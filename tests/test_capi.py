@@ -132,16 +132,17 @@ def test_decode_rejections_without_device():
         assert L.qw38_decode_mmv(C.byref(desc), None) == 2, needle
         err = _lib.last_error()
         assert err.operation.startswith("decode_mmv") and needle in err.detail, (needle, err.detail)
-    # a reference layout this build does not implement (NVFP4 V1: 4-bit codes,
-    # FP16-typed opaque scale span of 256 + 128-row blocks x K/16 bytes) passes
-    # validation and is then rejected before any device call
-    d = _decode_desc(n=128, k=256)
+    # NVFP4 V1 (4-bit codes, FP16-typed opaque scale span of 256 + 128-row
+    # blocks x K/16 bytes): N beyond the model geometry is rejected
+    # (cuda/decode_mmv.cu:391-393)
+    n = 248328
+    d = _decode_desc(n=n, k=256)
     d.layout, d.quantizer = 0x020E, 0x0106
-    d.codes.layout, d.codes.dtype, d.codes.bytes = 0x020E, 6, 128 * 256 // 2
-    units = (256 + 128 * (256 // 16)) // 2
+    d.codes.layout, d.codes.dtype, d.codes.bytes = 0x020E, 6, n * 256 // 2
+    units = (256 + (n + 127) // 128 * 128 * (256 // 16)) // 2
     d.scales = _lib.DecodeView(0x200000, 1, 4, 0x020E, 1, units, 1, units, 2 * units, 16, 0)
     assert L.qw38_decode_mmv(C.byref(d), None) == 2
-    assert "not implemented" in _lib.last_error().detail
+    assert "NVFP4 N exceeds model geometry" in _lib.last_error().detail
     # FP8 V1 geometry contract (cuda/decode_mmv.cu:331-332)
     d = _decode_desc(n=120, k=256)
     d.layout, d.quantizer = 0x020F, 0x0107
@@ -168,6 +169,26 @@ def test_decode_rejections_without_device():
     assert L.qw38_fp8_project(C.byref(fw), C.byref(fx), 5, C.c_void_p(0x500000),
                               C.c_void_p(0x600000), 2, None) == 2
     assert "epilogue contract" in _lib.last_error().detail
+    # NVFP4 entries reject before touching memory
+    # (cuda/nvfp4.cu:74-75, 87-90; cuda/prefill.cu:220-221)
+    assert L.qw38_pack_nvfp4(C.c_void_p(0x100000), 0, 16, C.c_void_p(0x200000), 8,
+                             C.c_void_p(0x300000), 2048, None) == 2
+    assert L.qw38_pack_nvfp4(C.c_void_p(0x100000), 2, 256, C.c_void_p(0x200000), 255,
+                             C.c_void_p(0x300000), 2048, None) == 2
+    assert L.qw38_nvfp4_gemm_tile(C.c_void_p(0x100000), C.c_void_p(0x200000), C.c_void_p(0x300000),
+                                  C.c_void_p(0x400000), 4, 12, 256, 0, C.c_void_p(0x500000), None) == 2
+    assert "invalid tile" in _lib.last_error().detail
+    assert L.qw38_nvfp4_gemm_tile(C.c_void_p(0x100000), C.c_void_p(0x200000), C.c_void_p(0x300000),
+                                  C.c_void_p(0x400000), 4, 16, 256, 64, C.c_void_p(0x500000), None) == 2
+    nw = _lib.Weight(0x100000, 0x200000, 0x020E, 0x0106, 16, 6144, 16, 6144, 16 * 6144 // 2,
+                     256 + 128 * 6144 // 16)
+    assert L.qw38_nvfp4_project(C.byref(nw), C.c_void_p(0x300000), 4, C.c_void_p(0x400000), None, 2,
+                                C.c_void_p(0x500000), 1 << 20, None) == 2
+    assert "weight, layout or token contract" in _lib.last_error().detail
+    assert L.qw38_hidden_rms_nvfp4(C.c_void_p(0x100000), C.c_void_p(0x200000), -1.0, 4,
+                                   C.c_void_p(0x300000), C.c_void_p(0x400000), None) == 2
+    assert L.qw38_hidden_rms_fp8(C.c_void_p(0x100000), C.c_void_p(0x200000), 1e-6, 1025, None,
+                                 C.c_void_p(0x300000), C.c_void_p(0x400000), None) == 2
     # a/b contraction: BF16 dense tiles with FP32 output only
     a, b = _decode_desc(), _decode_desc()
     assert L.qw38_decode_ab_bf16(C.byref(a), C.byref(b), None) == 2

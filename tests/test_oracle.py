@@ -513,3 +513,161 @@ def test_fp8_contractions_closed_form():
     g, _ = oracle.fp8_gemm(wc, ws, n, k, xc, xs, m)
     xd = oracle.e4m3_to_fp32(xc).astype(np.float64) * np.repeat(xs.T, 128, 1)
     assert np.allclose(g, xd @ wd.T, rtol=1e-12, atol=1e-12)
+
+
+# ---- NVFP4 (src/format/nvfp4.cpp, cuda/nvfp4_device.cuh) ---------------------
+def _np_nvfp4_block(v):
+    """Numpy restatement of one block, written independently of the oracle's
+    exhaustive search: the scale through E4M3 RNE (orc_fp32_to_e4m3 on a
+    nonnegative value), elements through the E2M1 tie table."""
+    v = np.asarray(v, np.float32)
+    if not np.all(np.isfinite(v)):
+        return 127, np.zeros(16, np.uint8)
+    peak = np.float32(np.abs(v).max())
+    s = int(oracle.fp32_to_e4m3(np.array([peak / np.float32(6)], np.float32))[0])
+    if peak != 0 and s == 0:
+        s = 1
+    scale = oracle.ue4m3_value(s)
+    out = np.zeros(16, np.uint8)
+    for i, x in enumerate(v):
+        if x == 0:
+            continue
+        q = np.float32(x / scale)
+        a = abs(float(q))
+        mag = (0 if a <= .25 else 1 if a < .75 else 2 if a <= 1.25 else 3 if a < 1.75 else
+               4 if a <= 2.5 else 5 if a < 3.5 else 6 if a <= 5 else 7)
+        out[i] = mag | (8 if np.signbit(q) else 0)
+    return s, out
+
+
+def test_nvfp4_values_and_encoders():
+    # nvfp4_e2m1 / nvfp4_e4m3 (src/format/nvfp4.cpp:8-16)
+    assert list(oracle.e2m1_value(np.arange(8))) == [0, .5, 1, 1.5, 2, 3, 4, 6]
+    assert list(oracle.e2m1_value(np.arange(8, 16))) == [-0.0, -.5, -1, -1.5, -2, -3, -4, -6]
+    assert oracle.ue4m3_value(1) == 2.0 ** -9 and oracle.ue4m3_value(8) == 2.0 ** -6
+    assert oracle.ue4m3_value(126) == 448.0
+    # E2M1 ties to the even code (tests/nvfp4_test.cpp:139-140 tie set)
+    ties = [.25, .75, 1.25, 1.75, 2.5, 3.5, 5.0, 6.0]
+    want = [0, 2, 2, 4, 4, 6, 6, 7]
+    assert [oracle.nvfp4_nearest(t, False) for t in ties] == want
+    assert [oracle.nvfp4_nearest(-t, False) for t in ties] == [w | 8 for w in want]
+    assert oracle.nvfp4_nearest(100.0, False) == 7 and oracle.nvfp4_nearest(-1e-3, False) == 8
+    # the exhaustive UE4M3 search equals E4M3 RNE on nonnegative values:
+    # every midpoint, both neighbours of it, and a log-uniform sample
+    vals = [oracle.ue4m3_value(c) for c in range(127)]
+    mids = [(a + b) / 2 for a, b in zip(vals, vals[1:])]
+    rng = np.random.Generator(np.random.PCG64(5))
+    probe = np.concatenate([np.array(mids, np.float32),
+                            np.nextafter(np.array(mids, np.float32), np.float32(0)),
+                            np.nextafter(np.array(mids, np.float32), np.float32(1e9)),
+                            np.exp2(rng.uniform(-12, 10, 4000)).astype(np.float32),
+                            np.array([0, 448, 460, 1e6], np.float32)])
+    got = np.array([oracle.nvfp4_nearest(float(p), True) for p in probe])
+    assert np.array_equal(got, oracle.fp32_to_e4m3(probe))
+
+
+def test_nvfp4_scale_swizzle_bijection():
+    # src/format/nvfp4.hpp:14-17: a bijection of (row, block) over pad128 rows,
+    # 128-row stripes of pk/16 bytes, 512-byte chunks of four blocks
+    pk, rows = 512, 256
+    idx = np.array([[oracle.nvfp4_sf_index(r, b, pk) for b in range(pk // 16)] for r in range(rows)])
+    assert np.array_equal(np.sort(idx.ravel()), np.arange(rows * pk // 16))
+    assert np.all(idx[:128].max() < 128 * pk // 16) and np.all(idx[128:].min() >= 128 * pk // 16)
+    # one chunk = rows 0..127 x blocks 0..3: contiguous 512 bytes
+    assert sorted(idx[:128, :4].ravel()) == list(range(512))
+    assert oracle.nvfp4_sf_index(33, 5, 512) == 512 + 16 + 4 + 1
+
+
+def test_nvfp4_pack_blocks_and_fixtures():
+    rng = np.random.Generator(np.random.PCG64(6))
+    m, k = 5, 387   # ragged K (pk 512), rows padded to 128 in the scales
+    x = oracle.fp32_to_bf16((rng.standard_normal((m, k)) * 3).astype(np.float32))
+    x[1, :] = 0
+    x[2, 40] = 0x7F80                       # +inf: block 2 of row 2 gets scale 127
+    # tests/nvfp4_test.cpp:133-140: midpoints of consecutive scales x 6, ties
+    for b in range(1, 8):
+        x[3, 16 * b:16 * b + 16] = oracle.fp32_to_bf16(
+            np.float32((oracle.ue4m3_value(b) + oracle.ue4m3_value(b + 1)) * 3))
+    t = np.array([.25, .75, 1.25, 1.75, 2.5, 3.5, 5., 6.], np.float32)
+    x[4, 256:272] = oracle.fp32_to_bf16(np.concatenate([t, -t]))
+    codes, scales = oracle.pack_nvfp4(x, m, k)
+    pk = 512
+    xf = np.zeros((m, pk), np.float32)
+    xf[:, :k] = oracle.bf16_to_fp32(x)
+    for r in range(128):
+        for b in range(pk // 16):
+            si = oracle.nvfp4_sf_index(r, b, pk)
+            if r >= m:
+                assert scales[si] == 0
+                continue
+            s, c = _np_nvfp4_block(xf[r, 16 * b:16 * b + 16])
+            assert scales[si] == s, (r, b)
+            got = np.zeros(16, np.uint8)
+            got[0::2] = codes[r, 8 * b:8 * b + 8] & 15
+            got[1::2] = codes[r, 8 * b:8 * b + 8] >> 4
+            assert np.array_equal(got, c), (r, b)
+    assert scales[oracle.nvfp4_sf_index(2, 2, pk)] == 127
+    assert np.all(codes[2, 16:24] == 0)
+
+
+def test_nvfp4_quantizer_invariants():
+    rng = np.random.Generator(np.random.PCG64(7))
+    n, k = 13, 300
+    w = oracle.fp32_to_bf16((rng.standard_normal((n, k)) * 0.05).astype(np.float32))
+    codes, scales = oracle.quantize_nvfp4(w, n, k)
+    pk, pn = 512, 16
+    factor = scales[:4].view(np.float32)[0]
+    peak = np.abs(oracle.bf16_to_fp32(w)).max()
+    # power-of-two factor with peak / factor in (1344, 2688] (src/compiler/quantization/nvfp4.cpp:25-28)
+    assert np.frexp(factor)[0] == 0.5 and 1344 < peak / factor <= 2688
+    assert np.all(scales[4:256] == 0)
+    # padding rows and columns carry zero codes and zero scales
+    assert np.all(codes[n:] == 0) and np.all(codes[:, (k + 1) // 2 + 8:] == 0)
+    for r in range(pn, 128):
+        assert scales[256 + oracle.nvfp4_sf_index(r, 0, pk)] == 0
+    # reconstruction error: at most half an E2M1 step of the block scale
+    wf = oracle.bf16_to_fp32(w)
+    for r in range(n):
+        for c in range(0, k, 7):
+            sf = scales[256 + oracle.nvfp4_sf_index(r, c // 16, pk)]
+            code = (codes[r, c // 2] >> (4 * (c & 1))) & 15
+            rec = factor * oracle.ue4m3_value(sf) * oracle.e2m1_value(code)
+            assert abs(rec - wf[r, c]) <= factor * oracle.ue4m3_value(sf) * 1.0 + 1e-30
+    with pytest.raises(ValueError):
+        bad = w.copy()
+        bad[0, 0] = 0x7FC0
+        oracle.quantize_nvfp4(bad, n, k)
+
+
+def _nvfp4_dense(codes, scales, rows, pk, header):
+    """Dequantize in float64 from the layout definition."""
+    nib = np.zeros((rows, pk), np.uint8)
+    nib[:, 0::2] = codes[:rows] & 15
+    nib[:, 1::2] = codes[:rows] >> 4
+    sf = np.array([[scales[header + oracle.nvfp4_sf_index(r, b, pk)] for b in range(pk // 16)]
+                   for r in range(rows)])
+    return oracle.e2m1_value(nib).astype(np.float64) * np.repeat(oracle.ue4m3_value(sf), 16, axis=1)
+
+
+def test_nvfp4_contractions_closed_form():
+    rng = np.random.Generator(np.random.PCG64(8))
+    n, k, m = 24, 512, 5
+    wc, ws = oracle.quantize_nvfp4(oracle.fp32_to_bf16(rng.standard_normal((n, k)).astype(np.float32)), n, k)
+    x = oracle.fp32_to_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    xc, xs = oracle.pack_nvfp4(x, m, k)
+    factor = float(ws[:4].view(np.float32)[0])
+    W = _nvfp4_dense(wc, ws, n, k, 256)
+    A = _nvfp4_dense(xc, xs, m, k, 0)
+    y, l1 = oracle.nvfp4_gemm(wc, ws, n, k, xc, xs, m)
+    assert np.allclose(y, factor * (A @ W.T), rtol=1e-12, atol=1e-12)
+    assert np.all(l1 >= np.abs(y) - 1e-9)
+    # decode: FP32 element RN(RN(scale * factor) * value), times BF16 x
+    sf = np.array([[ws[256 + oracle.nvfp4_sf_index(r, b, k)] for b in range(k // 16)] for r in range(n)])
+    sc = (oracle.ue4m3_value(sf) * np.float32(factor)).astype(np.float32)
+    nib = np.zeros((n, k), np.uint8)
+    nib[:, 0::2] = wc[:n] & 15
+    nib[:, 1::2] = wc[:n] >> 4
+    wf = (np.repeat(sc, 16, axis=1) * oracle.e2m1_value(nib)).astype(np.float32)
+    yd, _ = oracle.nvfp4_gemv(wc, ws, n, k, x[0], k)
+    assert np.allclose(yd, wf.astype(np.float64) @ oracle.bf16_to_fp32(x[0]).astype(np.float64),
+                       rtol=1e-12, atol=1e-12)
