@@ -3,7 +3,8 @@
 Headline (BASELINE.json metric): Q4_K x Q8 decode GEMV GB/s at M=1 on config
 2 (fused gate+up, N=2x17408=34816, K=5120), as a fraction of 8 TB/s HBM; the
 same JSON line carries the MMQ int8-equivalent TOPS at M=512 (config 4,
-Q4_K N=34816) and the other decode M values.
+Q4_K N=34816), the other decode M values, and the config-5 full-model weight
+pass (64 synthetic layers, one decode step and one 512-token prefill chunk).
 
 A "step" is one projection launch over one weight copy with the Q8
 activations resident in HBM. Weight copies rotate (>= 1.2 GB in total) so
@@ -216,6 +217,76 @@ def bench_mmq(torch, ops, n, k, m, steps, warmup, layout, seed=21):
             "m": m, "n": n, "k": k}
 
 
+# Config 5: one layer of the synthetic 27B-class stack (out rows, in columns, format)
+MODEL_LAYER = (("qkv_gate", 12288, 5120, "q4k"), ("out", 5120, 6144, "q4k"),
+               ("gate_up", 34816, 5120, "q4k"), ("down", 5120, 17408, "q6k"))
+
+
+def weight_bytes(fmt, n, k):
+    return n * k // 256 * (144 if fmt == "q4k" else 210)
+
+
+def bench_model(torch, ops, layers, q4_layout, prefill_m, reps, seed=1000):
+    """Config 5: a full weight pass over `layers` synthetic layers (about
+    14.5 GB of quantized weights resident in HBM at 64 layers): one decode step
+    (M=1, every projection of every layer once) and one prefill chunk
+    (M=prefill_m). Each (layer, projection) has its own seeded ~N(0, 0.02)
+    weights, quantized on the GPU, and its own fresh seeded ~N(0,1) Q8
+    activation rows. Both passes are captured in one hipGraph each and timed
+    with events; the aggregate rate covers every byte / op of the pass."""
+    t0 = time.perf_counter()
+    g = torch.Generator(device="cuda")
+    fail = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = []
+    for l in range(layers):
+        row = []
+        for j, (name, n, k, fmt) in enumerate(MODEL_LAYER):
+            g.manual_seed(seed + 16 * l + j)
+            x = torch.randn(n, k, generator=g, device="cuda", dtype=torch.float32) * 0.02
+            if fmt == "q4k":
+                blocks = ops.quantize_q4k_blocks(x, n, k, fail)
+                w = ops.upload_q4k_blocks(blocks, n, k, layout=q4_layout)
+            else:
+                blocks = ops.quantize_q6k_blocks(x, n, k)
+                w = ops.upload_q6k_blocks(blocks, n, k)
+            del x, blocks
+            row.append(w)
+        ws.append(row)
+    torch.cuda.synchronize()
+    assert int(fail.item()) == 0
+    t_gen = time.perf_counter() - t0
+    res = {"layers": layers, "q4k_layout": f"{q4_layout:#06x}", "q6k_layout": "0x0241",
+           "weight_bytes": layers * sum(weight_bytes(f, n, k) for _, n, k, f in MODEL_LAYER),
+           "setup_s": round(t_gen, 1)}
+    for m in (1, prefill_m):
+        qs = [[make_q8(torch, ops, m, k, seed + 7919 + 16 * l + j, outliers=False)[0]
+               for j, (_, n, k, _) in enumerate(MODEL_LAYER)] for l in range(layers)]
+        outs = [torch.empty(m, n, device="cuda") for _, n, _, _ in MODEL_LAYER]
+
+        def run_pass(_i):
+            for l in range(layers):
+                for j in range(len(MODEL_LAYER)):
+                    ops.q4k_q8_project(ws[l][j], qs[l][j], outs[j])
+
+        ms_pass, npass, mode = time_launches(torch, run_pass, 1, reps, 1)
+        nbytes = layers * sum(weight_bytes(f, n, k) + m * k * 1.25 + m * n * 4
+                              for _, n, k, f in MODEL_LAYER)
+        nops = layers * sum(2.0 * m * n * k for _, n, k, _ in MODEL_LAYER)
+        gbs = nbytes / (ms_pass * 1e-3) / 1e9
+        tops = nops / (ms_pass * 1e-3) / 1e12
+        key = "decode_m1" if m == 1 else f"prefill_m{m}"
+        res[key] = {"ms": round(ms_pass, 4), "gbs": round(gbs, 1),
+                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "tops": round(tops, 2),
+                    "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                    "launches": layers * len(MODEL_LAYER), "passes": npass, "mode": mode}
+        log(f"model pass M={m} ({layers} layers, {res['weight_bytes']/1e9:.2f} GB): "
+            f"{ms_pass:.3f} ms, {gbs:.0f} GB/s, {tops:.1f} TOPS ({mode})")
+        del qs, outs
+    del ws
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(torch, blocks, n, k, m, budget_s):
     """Oracle (C restatement, OpenMP) on the host cores: same contraction."""
     import numpy as np
@@ -252,6 +323,9 @@ def main():
     ap.add_argument("--no-mmq", action="store_true")
     ap.add_argument("--no-bf16", action="store_true", help="skip the BF16-activation decode_mmv")
     ap.add_argument("--decode-m", default="1,2,4,8", help="decode token counts to time")
+    ap.add_argument("--no-model", action="store_true", help="skip the config-5 model pass")
+    ap.add_argument("--model-layers", type=int, default=64)
+    ap.add_argument("--model-layout", default="0x020D", help="Q4_K layout of the model pass")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (counter scale for rocprof --pmc)")
     args = ap.parse_args()
@@ -286,6 +360,8 @@ def main():
     dbf16 = None if args.no_bf16 else bench_decode_bf16(torch, ops, n, k, args.steps, args.warmup)
     pbf16 = None if (args.no_bf16 or args.no_mmq) else bench_prefill_bf16(
         torch, ops, n, k, 512, max(20, args.steps // 8), max(3, args.warmup // 4))
+    model = None if args.no_model else bench_model(
+        torch, ops, args.model_layers, int(args.model_layout, 16), 512, 3)
     cpu = None
     if not args.no_cpu:
         _, blocks = make_weight(torch, ops, n, k, 11, layout)
@@ -322,6 +398,7 @@ def main():
         "mmq_m512": mmq,
         "decode_bf16_m1": dbf16,
         "prefill_bf16_m512": pbf16,
+        "config5_model_pass": model,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

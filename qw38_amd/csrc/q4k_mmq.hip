@@ -25,6 +25,7 @@
 // v_perm with 0x64 high bytes, then one packed FP16 FMA/add recovers the exact
 // integer value (scaled by s for Q4_K weights). Rows of the LDS tiles are
 // 64 halfs + 8 pad; all stores are 16 B.
+#include <cmath>
 #include <cstdlib>
 #include <type_traits>
 
@@ -94,7 +95,7 @@ struct Fetch {
   int32_t su[GPT];   // only): this thread's GPT groups of token kt
 };
 
-template <uint16_t Layout, int WR, int WT, int NI, int NJ>
+template <uint16_t Layout, bool Vec, int WR, int WT, int NI, int NJ>
 __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) void mmq_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n,
     uint32_t pn, uint32_t kbs, const int8_t* __restrict__ xc, const float* __restrict__ xa,
@@ -195,13 +196,27 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
       }
       const uint4 mw = *reinterpret_cast<const uint4*>(mp);
       F.x[0] = mw.x; F.x[1] = mw.y; F.x[2] = mw.z; F.x[3] = mw.w;
-    } else if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2) {  // 4 B / 2 B aligned
-      const uint32_t* c4 = reinterpret_cast<const uint32_t*>(codes + a_base + kb * 1024 + q * 32);
-      const uint16_t* m2 = reinterpret_cast<const uint16_t*>(meta + m_base + kb * 128);
+    } else if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2) {
+      const uint8_t* cp = codes + a_base + kb * 1024 + q * 32;
+      const uint8_t* mp = meta + m_base + kb * 128;
+      if constexpr (Vec) {  // 16-byte aligned spans: one wide load each
+        if constexpr (AW == 4) {
+          const uint4 cw = reinterpret_cast<const uint4*>(cp)[ah];
+          F.w[0] = cw.x; F.w[1] = cw.y; F.w[2] = cw.z; F.w[3] = cw.w;
+        } else {
+          const uint2 cw = reinterpret_cast<const uint2*>(cp)[ah];
+          F.w[0] = cw.x; F.w[1] = cw.y;
+        }
+        const uint4 mw = *reinterpret_cast<const uint4*>(mp);
+        F.x[0] = mw.x; F.x[1] = mw.y; F.x[2] = mw.z; F.x[3] = mw.w;
+      } else {  // 4-byte aligned codes, 2-byte aligned metadata
+        const uint32_t* c4 = reinterpret_cast<const uint32_t*>(cp);
+        const uint16_t* m2 = reinterpret_cast<const uint16_t*>(mp);
 #pragma unroll
-      for (int i = 0; i < AW; ++i) F.w[i] = c4[ah * AW + i];
+        for (int i = 0; i < AW; ++i) F.w[i] = c4[ah * AW + i];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) F.x[i] = uint32_t(m2[2 * i]) | (uint32_t(m2[2 * i + 1]) << 16);
+        for (int i = 0; i < 4; ++i) F.x[i] = uint32_t(m2[2 * i]) | (uint32_t(m2[2 * i + 1]) << 16);
+      }
     } else {
       const uint32_t g = 2 * q + asel;
       const uint64_t tr = a_base + kb * 8;
@@ -529,7 +544,13 @@ hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const fl
   const uint32_t tok_blocks = (x.m + C::BT - 1) / C::BT;
   if (row_blocks == 0) return hipSuccess;
   const dim3 grid(row_blocks * tok_blocks);
-  hipLaunchKernelGGL((mmq_kernel<Layout, WR, WT, NI, NJ>), grid, dim3(WR * WT * 64), 0, s, w.codes, w.scales,
+  // 0x020D spans are 4-byte (codes) / 2-byte (metadata) aligned in general;
+  // 16-byte aligned ones (every span this library allocates) load wide.
+  const bool vec = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales)) % 16) == 0;
+  auto kern = mmq_kernel<Layout, true, WR, WT, NI, NJ>;
+  if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2)
+    if (!vec) kern = mmq_kernel<Layout, false, WR, WT, NI, NJ>;
+  hipLaunchKernelGGL(kern, grid, dim3(WR * WT * 64), 0, s, w.codes, w.scales,
                      w.n, w.pn, w.pk / 256, x.codes, x.scales, x.sums, x.m, x.pk, out, residual,
                      row_begin, row_blocks, tok_blocks);
   return hipGetLastError();
@@ -549,29 +570,55 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
     const char* e = std::getenv("QW38_MMQ_SPLIT");
     return !(e && std::atoi(e) == 0);
   }();
-  const int bt = forced ? forced : (x.m <= 32 ? 32 : x.m <= 64 ? 64 : 256);
+  // Tile choice by a cost model of the busiest CU: with b blocks on it, a
+  // shape that runs two blocks per CU costs floor(b/2) * t2 + (b % 2) * t1
+  // per K step, a one-per-CU shape b * t1. Step times measured on MI355X
+  // (microseconds per two-group K step): 256 x 128 t1 = 1.9 (Q6_K's 128 x 128:
+  // 2.05); 128 x 64 t1 = 1.07, t2 = 1.39 (Q6_K 1.33, 2.65); 128 x 32
+  // t1 = 0.70, t2 = 0.89 (Q6_K 1.0, 2.0). Small grids thus take smaller tiles
+  // so that every CU has work.
   const uint32_t pn = w.pn;
-  if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2>(w, x, out, residual, s, 0, pn);  // 128 x 32
-  if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4>(w, x, out, residual, s, 0, pn);  // 128 x 64
-  if constexpr (Layout == QW38_LAYOUT_Q6K_WAVE64) {  // Q6_K's two A planes: 128 x 128 at most
-    return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s, 0, pn);
-  } else {
-    if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s, 0, pn);  // 128 x 128
-    // 256 x 128 tiles, one block per CU. When the last round of tiles would
-    // leave most CUs idle, the big tiles cover whole rounds of row blocks and
-    // the remaining rows run as 128 x 32 tiles (two blocks per CU) when they
-    // fit one such round, which takes about half as long as a big round.
-    const uint32_t cus = uint32_t(cu_count());
+  const uint32_t cus = uint32_t(cu_count());
+  constexpr bool q6 = Layout == QW38_LAYOUT_Q6K_WAVE64;
+  auto per_cu = [&](uint32_t rows, uint32_t toks) {
+    const uint64_t tiles = uint64_t((pn + rows - 1) / rows) * ((x.m + toks - 1) / toks);
+    return double((tiles + cus - 1) / cus);
+  };
+  auto two = [](double b, double t1, double t2) { return std::floor(b / 2) * t2 + std::fmod(b, 2.0) * t1; };
+  // 256 x 128 tiles, one block per CU. When the last round of tiles would
+  // leave most CUs idle, the big tiles cover whole rounds of row blocks and
+  // the remaining rows run as 128 x 32 tiles (two blocks per CU) when they
+  // fit one such round, which takes about half as long as a big round.
+  uint32_t big_rows = pn;
+  double b_big = per_cu(q6 ? 128u : 256u, 128);
+  if constexpr (!q6) {
     const uint32_t rb = (pn + 255) / 256, tb = (x.m + 127) / 128;
-    uint32_t big_rows = pn;
     if (split && !forced && uint64_t(rb) * tb > cus) {
       const uint32_t full_rb = uint32_t(uint64_t(rb * tb / cus) * cus / tb);
       if (full_rb > 0 && full_rb < rb) {
         const uint64_t tail_blocks = uint64_t((pn - full_rb * 256 + 127) / 128) * ((x.m + 31) / 32);
         const uint64_t tail_rounds = (tail_blocks + 2 * cus - 1) / (2 * cus);
-        if (tail_rounds <= 1) big_rows = full_rb * 256;
+        if (tail_rounds <= 1) {
+          big_rows = full_rb * 256;
+          b_big = double(uint64_t(full_rb) * tb / cus) + 0.5;
+        }
       }
     }
+  }
+  const double c_big = b_big * (q6 ? 2.05 : 1.9);
+  const double c64 = q6 ? two(per_cu(128, 64), 1.33, 2.65) : two(per_cu(128, 64), 1.07, 1.39);
+  const double c32 = q6 ? two(per_cu(128, 32), 1.0, 2.0) : two(per_cu(128, 32), 0.70, 0.89);
+  int bt = 32;
+  if (x.m > 32 && c64 < c32) bt = 64;
+  if (x.m > 64 && c_big < (bt == 64 ? c64 : c32)) bt = 256;
+  if (forced) bt = forced;
+  if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2>(w, x, out, residual, s, 0, pn);  // 128 x 32
+  if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4>(w, x, out, residual, s, 0, pn);  // 128 x 64
+  if constexpr (q6) {  // Q6_K's two A planes: 128 x 128 at most
+    return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s, 0, pn);
+  } else {
+    if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s, 0, pn);  // 128 x 128
+    if (forced) big_rows = pn;
     hipError_t e = launch_cfg<Layout, 4, 2, 4, 4>(w, x, out, residual, s, 0, big_rows);
     if (e != hipSuccess || big_rows == pn) return e;
     return launch_cfg<Layout, 4, 1, 2, 2>(w, x, out, residual, s, big_rows, pn);
