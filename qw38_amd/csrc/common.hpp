@@ -205,6 +205,9 @@ hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out,
 hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,
                               const float* residual, hipStream_t s, int ws_override,
                               uint32_t max_blocks);
+// Q6_K (0x0241) streaming GEMV for M <= 2; hipErrorNotSupported otherwise.
+hipError_t launch_q6k_stream(const WeightView& w, const Q8View& x, float* out,
+                             const float* residual, hipStream_t s);
 hipError_t launch_gemv_w64(const WeightView& w, const Q8View& x, float* out,
                            const float* residual, hipStream_t s);
 hipError_t launch_mmq(const WeightView& w, const Q8View& x, float* out,

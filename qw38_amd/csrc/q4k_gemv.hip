@@ -360,7 +360,10 @@ hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out, const f
                   : gemv_m<QW38_LAYOUT_Q4K_CANDIDATE_V2, false>(w, x, out, residual, s);
     case QW38_LAYOUT_Q4K_WAVE64:
       return launch_gemv_w64(w, x, out, residual, s);
-    case QW38_LAYOUT_Q6K_WAVE64:
+    case QW38_LAYOUT_Q6K_WAVE64: {
+      const hipError_t e = launch_q6k_stream(w, x, out, residual, s);
+      if (e != hipErrorNotSupported) return e;
+    }
       // Q6_K layout requires 16-byte aligned codes (validated by the caller).
       return (reinterpret_cast<uintptr_t>(x.codes) % 16 == 0)
                  ? gemv_m<QW38_LAYOUT_Q6K_WAVE64, true>(w, x, out, residual, s)

@@ -94,7 +94,7 @@ def test_config3_q6k_down(torch_gpu):
     import qw38_amd.ops as ops
     n, k = 5120, 17408
     w, wl = _fit_q6k(torch, ops, n, k, 301)
-    for m in (1, 8, 40):
+    for m in (1, 2, 8, 40):
         q, ob = _q8(torch, ops, silu_rows(m, k, 302 + m))
         y = _project(torch, ops, w, q, m, n)
         ref, _, _ = oracle.q6k_q8_contract(wl, ob)
@@ -108,7 +108,7 @@ def test_q6k_small_shapes_and_dots(torch_gpu):
         wl = random_q6k(n, k, n + k)
         co, mo = wl.physical()
         w = ops.PrefillWeight.from_bytes(co, mo, oracle.LAYOUT_Q6K_W64, n, k)
-        for m in (1, 3, 8, 9, 33, 130):
+        for m in (1, 2, 3, 8, 9, 33, 130):
             q, ob = _q8(torch, ops, normal((m, k), m + 7))
             y = _project(torch, ops, w, q, m, n)
             ref, _, dots = oracle.q6k_q8_contract(wl, ob, want_dots=True)
@@ -120,12 +120,15 @@ def test_q6k_small_shapes_and_dots(torch_gpu):
                 assert np.array_equal(d.cpu().numpy().reshape(dots.shape), dots)
 
 
+@pytest.mark.parametrize("layout", [oracle.LAYOUT_Q4K_SEQ, oracle.LAYOUT_Q4K_W64], ids=["020D", "0240"])
 @pytest.mark.parametrize("n,k,m", [(12288, 5120, 128), (34816, 5120, 512), (12288, 5120, 2048)])
-def test_config4_mmq_row_sample(torch_gpu, n, k, m):
-    """MMQ at the config-4 shapes; the oracle checks a seeded sample of 512 rows."""
+def test_config4_mmq_row_sample(torch_gpu, n, k, m, layout):
+    """MMQ at the config-4 shapes (the tile shape follows the cost model:
+    128x32 at M=128, 256x128 with the tail split at M=512, 256x128 at 2048);
+    the oracle checks a seeded sample of 512 rows."""
     torch = torch_gpu
     import qw38_amd.ops as ops
-    w, wl = _fit_q4k(torch, ops, n, k, 401 + m, oracle.LAYOUT_Q4K_W64)
+    w, wl = _fit_q4k(torch, ops, n, k, 401 + m, layout)
     q, ob = _q8(torch, ops, normal((m, k), 402 + m))
     y = _project(torch, ops, w, q, m, n)
     rows = np.sort(np.random.Generator(np.random.PCG64(m)).choice(n, 512, replace=False))
@@ -145,3 +148,70 @@ def test_config4_q6k_mmq_row_sample(torch_gpu):
     sub = oracle.Q6K(wl.q[rows], wl.sc[rows], wl.d[rows], len(rows), k)
     ref, _, _ = oracle.q6k_q8_contract(sub, ob)
     _check(y[:, rows], ref, "config4 Q6_K M=512")
+
+
+@pytest.mark.parametrize("m", [1, 8, 128, 512])
+def test_config5_out_projection(torch_gpu, m):
+    """Config-5 out projection (N=5120, K=6144, Q4_K on the reference layout
+    0x020D): GEMV at M=1 and 8, MMQ at 128 (128x32 tiles) and 512 (128x64
+    tiles); the oracle checks a seeded sample of 256 rows."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 5120, 6144
+    w, wl = _fit_q4k(torch, ops, n, k, 601 + m, oracle.LAYOUT_Q4K_SEQ)
+    q, ob = _q8(torch, ops, normal((m, k), 602 + m))
+    y = _project(torch, ops, w, q, m, n)
+    rows = np.sort(np.random.Generator(np.random.PCG64(60 + m)).choice(n, 256, replace=False))
+    sub = oracle.Q4K(wl.codes[rows], wl.meta[rows], len(rows), k)
+    ref, _, _ = oracle.q4k_q8_contract(sub, ob)
+    _check(y[:, rows], ref, f"config5 out M={m}")
+
+
+def test_config5_q6k_down_m128(torch_gpu):
+    """Config-5 down projection at M=128 (Q6_K, the cost model picks 128x32
+    tiles); 256 sampled rows against the oracle."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k, m = 5120, 17408, 128
+    w, wl = _fit_q6k(torch, ops, n, k, 701)
+    q, ob = _q8(torch, ops, normal((m, k), 702))
+    y = _project(torch, ops, w, q, m, n)
+    rows = np.sort(np.random.Generator(np.random.PCG64(7)).choice(n, 256, replace=False))
+    sub = oracle.Q6K(wl.q[rows], wl.sc[rows], wl.d[rows], len(rows), k)
+    ref, _, _ = oracle.q6k_q8_contract(sub, ob)
+    _check(y[:, rows], ref, "config5 Q6_K down M=128")
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_q6k_stream_unaligned_and_residual(torch_gpu, m):
+    """Q6_K decode (M <= 2 streams the strip): Q8 codes at a 4-byte offset give
+    bitwise the aligned result, the residual is added exactly, and the words
+    around a row-tail output span stay untouched (tests/q4k_q8_test.cpp:96-117
+    carried over to the Q6_K layout)."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 37, 2560
+    wl = random_q6k(n, k, 4242)
+    co, mo = wl.physical()
+    w = ops.PrefillWeight.from_bytes(co, mo, oracle.LAYOUT_Q6K_W64, n, k)
+    q, ob = _q8(torch, ops, normal((m, k), 99 + m))
+    y = _project(torch, ops, w, q, m, n)
+    ref, _, _ = oracle.q6k_q8_contract(wl, ob)
+    _check(y, ref, f"Q6_K stream n={n} k={k} M={m}")
+    z = q.codes.cpu().numpy().reshape(-1)
+    shifted = np.full(z.size + 8, 99, np.int8)
+    shifted[4:4 + z.size] = z
+    dshift = _dev(torch, shifted)
+    residual = ((np.arange(m * n) % 13).astype(np.float32) - 6) * 0.25
+    dres = _dev(torch, residual)
+    qv = ops.Q8Input(q.codes, q.scales, q.sums, q.m, q.k, q.padded_k)
+    qv.codes = dshift
+    qv.codes_ptr = dshift.data_ptr() + 4
+    qv.codes_len = z.size
+    guards = torch.full((m * n + 2,), -12345.0, device="cuda")
+    ops.q4k_q8_project(w, qv, guards, residual=dres, output_ptr=guards.data_ptr() + 4,
+                       output_len=m * n)
+    torch.cuda.synchronize()
+    r = guards.cpu().numpy()
+    assert np.array_equal(r[1:-1], (y.reshape(-1) + residual).astype(np.float32))
+    assert r[0] == -12345.0 and r[-1] == -12345.0
