@@ -2,7 +2,8 @@
 
     python -m qw38_amd.rocprof_summary <results.db> [--match SUBSTR] [--top N]
 
-Prints, per kernel: dispatch count and average / min / max duration (us), and,
+Prints, per kernel instantiation and grid size: dispatch count and average /
+min / max duration (us), and,
 when the run collected ``--pmc`` counters, the per-dispatch average of every
 counter. Used to turn rocprofv3 runs into the text summaries under profiles/.
 """
@@ -16,15 +17,22 @@ import sys
 
 
 def _short(name: str) -> str:
+    """Kernel base name with its template arguments (balanced <...>), without
+    namespaces and the parameter list."""
     name = re.sub(r"\s+", " ", name)
-    m = re.search(r"(\w+)<", name)
-    base = name
-    if "qw38hip" in name:
-        m2 = re.search(r"qw38hip::(?:\(anonymous namespace\)::)?(\w+)(<[^()]*>)?", name)
-        if m2:
-            base = m2.group(1) + (m2.group(2) or "")
-    elif m:
-        base = name[:120]
+    m2 = re.search(r"qw38hip::(?:\(anonymous namespace\)::)?(\w+)", name)
+    if not m2:
+        return name[:120]
+    base, i = m2.group(1), m2.end()
+    if i < len(name) and name[i] == "<":
+        depth, j = 0, i
+        while j < len(name):
+            depth += name[j] == "<"
+            depth -= name[j] == ">"
+            j += 1
+            if depth == 0:
+                break
+        base += name[i:j]
     return base[:140]
 
 
@@ -33,18 +41,22 @@ def summarize(path: str, match: str | None = None, top: int = 12) -> str:
     names = [r[0] for r in db.execute("select name from sqlite_master where type in ('table','view')")]
     out = []
     # kernel durations
-    rows = db.execute("select id, name, start, end from kernels").fetchall()
+    # one line per (kernel instantiation, grid): shapes launched with the same
+    # kernel stay apart
+    kcols = [r[1] for r in db.execute("pragma table_info(kernels)")]
+    has_grid = "grid_x" in kcols and "workgroup_x" in kcols
+    q = "select id, name, start, end" + (", grid_x, workgroup_x" if has_grid else "") + " from kernels"
     by = collections.defaultdict(list)
-    ids = {}
-    for kid, name, s, e in rows:
+    for row in db.execute(q).fetchall():
+        kid, name, s, e = row[:4]
         if match and match not in name:
             continue
-        by[name].append((e - s) / 1e3)
-        ids.setdefault(name, []).append(kid)
+        blocks = (row[4] // max(row[5], 1)) if has_grid else 0
+        by[(name, blocks)].append((e - s) / 1e3)
     tot = sum(sum(v) for v in by.values()) or 1.0
-    out.append(f"{'kernel':<72} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'time%':>6}")
-    for name, v in sorted(by.items(), key=lambda kv: -sum(kv[1]))[:top]:
-        out.append(f"{_short(name):<72} {len(v):>6} {sum(v)/len(v):>9.3f} {min(v):>9.3f} "
+    out.append(f"{'kernel':<72} {'blocks':>7} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'time%':>6}")
+    for (name, blocks), v in sorted(by.items(), key=lambda kv: -sum(kv[1]))[:top]:
+        out.append(f"{_short(name):<72} {blocks:>7} {len(v):>6} {sum(v)/len(v):>9.3f} {min(v):>9.3f} "
                    f"{max(v):>9.3f} {100*sum(v)/tot:>6.1f}")
     # counters, when present
     if "counters_collection" in names:
