@@ -1,8 +1,7 @@
 // BF16-activation decode GEMV (interface of cuda/decode_mmv.hpp in
 // Enucatl/qw38). The descriptor types, wire IDs, padding and byte-count
 // helpers are the reference's; this build implements the Q4_K (0x020D), Q4G64,
-// Q8G32 and BF16 dense-tile layouts and rejects FP8 and NVFP4 as not
-// implemented.
+// Q8G32, BF16 dense-tile, FP8 (0x020F) and NVFP4 (0x020E) layouts.
 #pragma once
 
 #include "cuda/error.hpp"

@@ -121,6 +121,9 @@ class PrefillEngine {
  private:
   [[nodiscard]] expected<void, Error> ready(char const* op) const;
   [[nodiscard]] expected<void, Error> project_fp8(PrefillProjection const& projection);
+  // NVFP4 scratch: the region after the MLP slabs of workspace_.
+  [[nodiscard]] void* nvfp4_scratch() const noexcept;
+  [[nodiscard]] std::uint64_t nvfp4_scratch_bytes() const noexcept;
 
   Stream const* stream_{};
   hipStream_t native_stream_{};

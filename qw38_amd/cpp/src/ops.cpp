@@ -12,6 +12,7 @@
 #include "cuda/activation.hpp"
 #include "cuda/decode_mmv.hpp"
 #include "cuda/fp8.hpp"
+#include "cuda/nvfp4.hpp"
 #include "cuda/graph.hpp"
 #include "cuda/prefill.hpp"
 #include "cuda/q4k_q8.hpp"
@@ -238,6 +239,72 @@ expected<void, Error> fp8_gemv(Fp8Weight weight, std::span<std::uint16_t const> 
                                 stream.native()));
 }
 
+// ---- NVFP4 (cuda/nvfp4.hpp) --------------------------------------------------------
+namespace {
+std::uint32_t pad256(std::uint32_t k) { return (k + 255u) / 256u * 256u; }
+std::uint64_t pad128_rows(std::uint32_t m) { return (std::uint64_t(m) + 127u) / 128u * 128u; }
+}  // namespace
+
+expected<int, Error> prepare_nvfp4_gemm(std::uint32_t max_m, std::uint64_t workspace_bytes,
+                                        Stream const& stream) {
+  (void)workspace_bytes;
+  if (auto st = require_stream(stream, "nvfp4.prepare"); !st) return unexpected(st.error());
+  if (max_m == 0 || max_m > 1024)
+    return unexpected(make_error(ErrorCode::InvalidArgument, "nvfp4.prepare", "invalid token capacity"));
+  int sm = 0;
+  if (auto st = from_abi(qw38_fp8_prepare(stream.native(), &sm)); !st) return unexpected(st.error());
+  return sm;
+}
+
+expected<void, Error> nvfp4_gemm_tile(void const* codes, void const* scales,
+                                      std::uint8_t const* activation,
+                                      std::uint8_t const* activation_scales, std::uint32_t m,
+                                      std::uint32_t n, std::uint32_t k, std::uint32_t row_start,
+                                      float* output, void* workspace, std::uint64_t workspace_bytes,
+                                      int sm_count, Stream const& stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  (void)sm_count;
+  if (auto st = require_stream(stream, "nvfp4.gemm"); !st) return st;
+  auto guard = stream.activate();
+  if (!guard) return unexpected(guard.error());
+  return from_abi(qw38_nvfp4_gemm_tile(codes, scales, activation, activation_scales, m, n, k,
+                                       row_start, output, stream.native()));
+}
+
+expected<void, Error> launch_pack_nvfp4(std::uint16_t const* input, std::uint8_t* codes,
+                                        std::uint8_t* scales, std::uint32_t m, std::uint32_t k,
+                                        Stream const& stream) {
+  if (auto st = require_stream(stream, "nvfp4.pack"); !st) return st;
+  auto guard = stream.activate();
+  if (!guard) return unexpected(guard.error());
+  const std::uint32_t pk = pad256(k);
+  return from_abi(qw38_pack_nvfp4(input, m, k, codes, std::uint64_t(m) * (pk / 2), scales,
+                                  pad128_rows(m) * (pk / 16), stream.native()));
+}
+
+expected<void, Error> launch_hidden_rms_fp8(float const* residual, std::uint16_t const* gamma,
+                                            float eps, std::uint32_t n_tokens,
+                                            std::uint16_t* companion, std::uint8_t* codes,
+                                            float* scales, Stream const& stream) {
+  if (auto st = require_stream(stream, "hidden_rms_fp8"); !st) return st;
+  auto guard = stream.activate();
+  if (!guard) return unexpected(guard.error());
+  return from_abi(qw38_hidden_rms_fp8(residual, gamma, eps, n_tokens, companion, codes, scales,
+                                      stream.native()));
+}
+
+expected<void, Error> launch_hidden_rms_nvfp4(float const* residual, std::uint16_t const* gamma,
+                                              float eps, std::uint32_t n_tokens,
+                                              std::uint8_t* codes, std::uint8_t* scales,
+                                              Stream const& stream) {
+  if (auto st = require_stream(stream, "hidden_rms_nvfp4"); !st) return st;
+  auto guard = stream.activate();
+  if (!guard) return unexpected(guard.error());
+  return from_abi(qw38_hidden_rms_nvfp4(residual, gamma, eps, n_tokens, codes, scales,
+                                        stream.native()));
+}
+
 // ---- PrefillEngine ---------------------------------------------------------------
 expected<void, Error> validate_prefill_device_span(void const* pointer, std::uint64_t bytes,
                                                    std::uint32_t alignment, int device) {
@@ -390,6 +457,17 @@ expected<void, Error> PrefillEngine::project_fp8(PrefillProjection const& d) {
                                    static_cast<int>(d.epilogue), native_stream_));
 }
 
+void* PrefillEngine::nvfp4_scratch() const noexcept {
+  // qw38_prefill_mlp_workspace_bytes: the normalized and SwiGLU BF16 slabs,
+  // then (256-byte aligned) the NVFP4 scratch of the token capacity
+  const std::uint64_t slabs = (std::uint64_t(token_capacity_) * (5120u * 2u + 17408u * 2u) + 255u) / 256u * 256u;
+  return static_cast<std::byte*>(const_cast<void*>(workspace_.data())) + slabs;
+}
+
+std::uint64_t PrefillEngine::nvfp4_scratch_bytes() const noexcept {
+  return qw38_nvfp4_workspace_bytes(token_capacity_);
+}
+
 expected<void, Error> PrefillEngine::project(PrefillProjection const& d) {
   if (auto st = ready("prefill.project"); !st) return st;
   auto guard = stream_->activate();
@@ -403,6 +481,10 @@ expected<void, Error> PrefillEngine::project(PrefillProjection const& d) {
                                  "input, output, position or epilogue contract mismatch"));
   if (d.weight.layout == kDecodeLayoutFp8V1) return project_fp8(d);
   const qw38_weight w = abi(d.weight);
+  if (d.weight.layout == kDecodeLayoutNvFp4V1)  // cuda/prefill.cu:598-628: pack, W4A4, epilogue
+    return from_abi(qw38_nvfp4_project(&w, d.input, d.valid_tokens, d.output, d.residual,
+                                       static_cast<int>(d.epilogue), nvfp4_scratch(),
+                                       nvfp4_scratch_bytes(), native_stream_));
   return from_abi(qw38_prefill_project(&w, d.input, d.valid_tokens, d.output, d.residual,
                                        static_cast<int>(d.epilogue), native_stream_));
 }
@@ -419,6 +501,9 @@ expected<void, Error> PrefillEngine::paired_swiglu(PrefillWeight const& gate, Pr
     return unexpected(make_error(ErrorCode::InvalidArgument, "prefill.swiglu",
                                  "paired weight or activation contract mismatch"));
   const qw38_weight g = abi(gate), u = abi(up);
+  if (gate.layout == kDecodeLayoutNvFp4V1)  // cuda/prefill.cu:680-715: one pack, two W4A4 GEMMs
+    return from_abi(qw38_nvfp4_paired_swiglu(&g, &u, normalized, swiglu, valid_tokens, nvfp4_scratch(),
+                                             nvfp4_scratch_bytes(), native_stream_));
   return from_abi(qw38_prefill_paired_swiglu(&g, &u, normalized, swiglu, valid_tokens, native_stream_));
 }
 

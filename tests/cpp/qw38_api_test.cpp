@@ -20,6 +20,7 @@
 #include "cuda/decode_mmv.hpp"
 #include "cuda/event.hpp"
 #include "cuda/fp8.hpp"
+#include "cuda/nvfp4.hpp"
 #include "cuda/graph.hpp"
 #include "cuda/prefill.hpp"
 #include "cuda/q4k_q8.hpp"
@@ -561,10 +562,84 @@ void test_fp8(Stream const& s) {
   expect(!engine.project(p), "M = 1 refuses an unused decode pack");
 }
 
+// NVFP4 weight from BF16 rows: packed like an activation, behind a 256-byte
+// header that holds the FP32 global factor 1.
+struct Nvfp4W {
+  Dev codes, scales;
+  PrefillWeight view;
+};
+Nvfp4W nvfp4_weight(unsigned n, unsigned k, unsigned seed, Stream const& s) {
+  std::vector<std::uint16_t> w(std::size_t(n) * k);
+  for (std::size_t i = 0; i < w.size(); ++i)
+    w[i] = float_to_bf16(float(int((i * 29 + seed * 7 + i / k * 3) % 61) - 30) / 16.0f);
+  auto dw = to_device(w, s);
+  const std::uint64_t cb = std::uint64_t(n) * k / 2, sb = (n + 127) / 128 * 128ull * (k / 16);
+  std::vector<std::uint8_t> hdr(256 + sb, 0);
+  const float one = 1.0f;
+  std::memcpy(hdr.data(), &one, 4);
+  Nvfp4W r{Dev{unwrap(DeviceBuffer::allocate(cb), "alloc")}, to_device(hdr, s), {}};
+  must(launch_pack_nvfp4(dw.as<std::uint16_t>(), r.codes.as<std::uint8_t>(), r.scales.as<std::uint8_t>() + 256,
+                         n, k, s),
+       "pack NVFP4 weight");
+  r.view = PrefillWeight{r.codes.buf.data(), r.scales.buf.data(), kDecodeLayoutNvFp4V1,
+                         kDecodeQuantizerNvFp4V1, n, k, n, k, cb, 256 + sb};
+  return r;
+}
+
+void test_nvfp4(Stream const& s) {
+  constexpr unsigned n = 136, k = 5120, m = 77;
+  auto engine = unwrap(PrefillEngine::create(s, 128, 512), "NVFP4 engine create");
+  const int sm = unwrap(prepare_nvfp4_gemm(128, 0, s), "prepare_nvfp4_gemm");
+  expect(sm > 0, "prepare_nvfp4_gemm reports the device's compute units");
+  auto gate = nvfp4_weight(n, k, 1, s), up = nvfp4_weight(n, k, 2, s);
+  std::vector<std::uint16_t> x(std::size_t(m) * k);
+  for (std::size_t i = 0; i < x.size(); ++i)
+    x[i] = float_to_bf16(float(int((i * 17 + 5) % 131) - 65) / 27.0f);
+  auto dx = to_device(x, s);
+  // the engine's NVFP4 projection equals pack + nvfp4_gemm_tile
+  Dev proj{unwrap(DeviceBuffer::allocate(std::size_t(m) * n * 4), "alloc")};
+  PrefillProjection p{.weight = gate.view, .input = dx.as<std::uint16_t>(), .output = proj.buf.data(),
+                      .valid_tokens = m, .epilogue = PrefillEpilogue::StoreFp32};
+  must(engine.project(p), "NVFP4 engine project");
+  Dev xc{unwrap(DeviceBuffer::allocate(std::size_t(m) * k / 2), "alloc")};
+  Dev xs{unwrap(DeviceBuffer::allocate(std::size_t(128) * (k / 16)), "alloc")};
+  must(launch_pack_nvfp4(dx.as<std::uint16_t>(), xc.as<std::uint8_t>(), xs.as<std::uint8_t>(), m, k, s),
+       "pack NVFP4 activations");
+  Dev g{unwrap(DeviceBuffer::allocate(std::size_t(m) * n * 4), "alloc")};
+  Dev u{unwrap(DeviceBuffer::allocate(std::size_t(m) * n * 4), "alloc")};
+  must(nvfp4_gemm_tile(gate.view.codes, gate.view.scales, xc.as<std::uint8_t>(), xs.as<std::uint8_t>(), m, n,
+                       k, 0, g.as<float>(), nullptr, 0, sm, s),
+       "nvfp4_gemm_tile gate");
+  must(nvfp4_gemm_tile(up.view.codes, up.view.scales, xc.as<std::uint8_t>(), xs.as<std::uint8_t>(), m, n, k,
+                       0, u.as<float>(), nullptr, 0, sm, s),
+       "nvfp4_gemm_tile up");
+  const auto yp = to_host<float>(proj.buf.data(), std::size_t(m) * n, s);
+  const auto yg = to_host<float>(g.buf.data(), std::size_t(m) * n, s);
+  const auto yu = to_host<float>(u.buf.data(), std::size_t(m) * n, s);
+  expect(yp == yg, "NVFP4 engine projection equals pack + nvfp4_gemm_tile bitwise");
+  // paired SwiGLU: BF16(SiLU(gate) * up) of the same two tiles, within one BF16 ulp
+  Dev sw{unwrap(DeviceBuffer::allocate(std::size_t(m) * n * 2), "alloc")};
+  must(engine.paired_swiglu(gate.view, up.view, dx.as<std::uint16_t>(), sw.as<std::uint16_t>(), m, 0),
+       "NVFP4 paired SwiGLU");
+  const auto ys = to_host<std::uint16_t>(sw.buf.data(), std::size_t(m) * n, s);
+  bool close = true;
+  for (std::size_t i = 0; i < ys.size(); ++i) {
+    const double gv = yg[i], want = gv / (1.0 + std::exp(-gv)) * yu[i];
+    const std::uint16_t wb = float_to_bf16(float(want));
+    close &= std::abs(int(ys[i]) - int(wb)) <= 1;
+  }
+  expect(close, "NVFP4 paired SwiGLU within one BF16 ulp of SiLU(gate) * up");
+  // a Q4_K down projection is not an NVFP4 pair partner
+  PrefillWeight mixed = up.view;
+  mixed.layout = 0x020D;
+  expect(!engine.paired_swiglu(gate.view, mixed, dx.as<std::uint16_t>(), sw.as<std::uint16_t>(), m, 0),
+         "NVFP4 gate with a non-NVFP4 up rejected");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
-  const char* names[] = {"runtime", "q4k_q8", "decode_onehot", "graph_replay", "prefill", "fp8"};
+  const char* names[] = {"runtime", "q4k_q8", "decode_onehot", "graph_replay", "prefill", "fp8", "nvfp4"};
   if (argc > 1 && std::strcmp(argv[1], "--list") == 0) {
     for (auto* n : names) std::printf("%s\n", n);
     return 0;
@@ -582,6 +657,8 @@ int main(int argc, char** argv) {
   test_prefill(stream);
   std::printf("== fp8\n");
   test_fp8(stream);
+  std::printf("== nvfp4\n");
+  test_nvfp4(stream);
   must(stream.sync(), "final sync");
   std::printf("%d failure(s)\n", g_failures);
   return g_failures == 0 ? 0 : 1;
