@@ -408,7 +408,58 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
         for (int i = 0; i < NI; ++i)
 #pragma unroll
           for (int j = 0; j < NJ; ++j) scale_add(q == 0 && gsel == 0, at[gsel][j], P[gsel][i][j], X[i][j]);
-    } else {
+    } else if constexpr (WR * WT <= 4) {
+      // One wave per SIMD (512 registers): software pipeline over the 2 * NI
+      // (group, row tile) items of the
+      // step. The MFMAs of item u are issued before the scaling FMAs of item
+      // u - 1, whose results are complete by then, so the matrix core and the
+      // VALU work side by side instead of the FMAs waiting on the MFMAs they
+      // read. The sched_group_barrier hints keep one MFMA and four FMAs
+      // interleaved.
+      float at[2][NJ];
+      half8 bf[2][NJ];
+      f4 Pp[NJ];
+#pragma unroll
+      for (uint32_t u = 0; u <= 2 * NI; ++u) {
+        const uint32_t gsel = u / NI, i = u % NI;
+        f4 Pc[NJ];
+        if (u < 2 * NI) {
+          if (i == 0) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              const uint32_t t = wt * NJ * 16 + j * 16 + lr;
+              at[gsel][j] = Aa[kp][t * 8 + 2 * q + gsel];
+              bf[gsel][j] = *reinterpret_cast<const half8*>(&Bs[buf][t * kStride + gsel * 32 + lk * 8]);
+            }
+          }
+          const uint32_t ro = (wr * NI * 16 + i * 16 + lr) * kStride + gsel * 32 + lk * 8;
+          const half8 af = *reinterpret_cast<const half8*>(&As[buf][0][ro]);
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            Pc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[gsel][j], f4{0, 0, 0, 0}, 0, 0, 0);
+          if constexpr (kQ6) {
+            const half8 al = *reinterpret_cast<const half8*>(&As[buf][kPlanes - 1][ro]);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)  // hi + lo partial sums stay exact integers below 2^24
+              Pc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[gsel][j], Pc[j], 0, 0, 0);
+          }
+        }
+        if (u > 0) {
+          const uint32_t pg = (u - 1) / NI, pi = (u - 1) % NI;
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) scale_add(q == 0 && pg == 0, at[pg][j], Pp[j], X[pi][j]);
+        }
+        if (u > 0 && u < 2 * NI) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            __builtin_amdgcn_sched_group_barrier(0x008, kQ6 ? 2 : 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);            // VALU
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) Pp[j] = Pc[j];
+      }
+    } else {  // two waves per SIMD: row tile i is scaled while row tile i + 1's MFMAs run
 #pragma unroll
       for (uint32_t gsel = 0; gsel < 2; ++gsel) {
         const uint32_t g = 2 * q + gsel;
@@ -581,7 +632,7 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   // shape that runs two blocks per CU costs floor(b/2) * t2 + (b % 2) * t1
   // per K step, a one-per-CU shape b * t1. Step times measured on MI355X
   // (microseconds per two-group K step): 256 x 128 t1 = 1.9 (Q6_K's 128 x 128:
-  // 2.05); 128 x 64 t1 = 1.07, t2 = 1.39 (Q6_K 1.33, 2.65); 128 x 32
+  // 1.77); 128 x 64 t1 = 1.07, t2 = 1.39 (Q6_K 1.33, 2.65); 128 x 32
   // t1 = 0.70, t2 = 0.89 (Q6_K 1.0, 2.0). Small grids thus take smaller tiles
   // so that every CU has work.
   const uint32_t pn = w.pn;
@@ -612,7 +663,7 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
       }
     }
   }
-  const double c_big = b_big * (q6 ? 2.05 : 1.9);
+  const double c_big = b_big * (q6 ? 1.77 : 1.9);
   const double c64 = q6 ? two(per_cu(128, 64), 1.33, 2.65) : two(per_cu(128, 64), 1.07, 1.39);
   const double c32 = q6 ? two(per_cu(128, 32), 1.0, 2.0) : two(per_cu(128, 32), 0.70, 0.89);
   int bt = 32;
