@@ -417,7 +417,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
       // read. The sched_group_barrier hints keep one MFMA and four FMAs
       // interleaved.
       float at[2][NJ];
-      half8 bf[2][NJ];
+      half8 bf[NJ];  // reloaded per group: all MFMAs of group 0 precede group 1's
       f4 Pp[NJ];
 #pragma unroll
       for (uint32_t u = 0; u <= 2 * NI; ++u) {
@@ -429,19 +429,19 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
             for (int j = 0; j < NJ; ++j) {
               const uint32_t t = wt * NJ * 16 + j * 16 + lr;
               at[gsel][j] = Aa[kp][t * 8 + 2 * q + gsel];
-              bf[gsel][j] = *reinterpret_cast<const half8*>(&Bs[buf][t * kStride + gsel * 32 + lk * 8]);
+              bf[j] = *reinterpret_cast<const half8*>(&Bs[buf][t * kStride + gsel * 32 + lk * 8]);
             }
           }
           const uint32_t ro = (wr * NI * 16 + i * 16 + lr) * kStride + gsel * 32 + lk * 8;
           const half8 af = *reinterpret_cast<const half8*>(&As[buf][0][ro]);
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
-            Pc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[gsel][j], f4{0, 0, 0, 0}, 0, 0, 0);
+            Pc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], f4{0, 0, 0, 0}, 0, 0, 0);
           if constexpr (kQ6) {
             const half8 al = *reinterpret_cast<const half8*>(&As[buf][kPlanes - 1][ro]);
 #pragma unroll
             for (int j = 0; j < NJ; ++j)  // hi + lo partial sums stay exact integers below 2^24
-              Pc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[gsel][j], Pc[j], 0, 0, 0);
+              Pc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[j], Pc[j], 0, 0, 0);
           }
         }
         if (u > 0) {
