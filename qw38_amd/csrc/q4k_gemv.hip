@@ -123,8 +123,10 @@ __device__ __forceinline__ float reduce_rows(const float acc[8]) {
 }
 
 // Block = 4 waves; WS waves split the K chunks of one strip; 4/WS strips per block.
+// At least two waves per SIMD (at most 256 registers): Q6_K at M=8 would take
+// 266 and run one wave per SIMD (62.6 us at config 3 against 52.6 us here).
 template <uint16_t Layout, int MT, bool Fast, int WS>
-__global__ __launch_bounds__(256) void gemv_kernel(
+__global__ __launch_bounds__(256, 2) void gemv_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n,
     uint32_t strips, uint32_t kbs, const int8_t* __restrict__ xc,
     const float* __restrict__ xa, const int32_t* __restrict__ xs, uint32_t pk,
