@@ -55,32 +55,34 @@ __global__ __launch_bounds__(128) void pack_nvfp4_kernel(const uint16_t* __restr
 
 // ---- decode GEMV: one wave per row, 32 contiguous elements per lane ----
 // Two consecutive 16-blocks per lane step; their scale bytes are adjacent in
-// the swizzle (b even -> b % 4 in {0, 2}).
+// the swizzle (b even -> b % 4 in {0, 2}). A weight element is
+// RN(RN(scale * factor) * value) (cuda/decode_mmv.cu:94-102): the UE4M3 scale
+// has at most 4 significant bits and factor is a power of two, so
+// scale * factor and its product with an E2M1 value (at most 2 significant
+// bits) are exact in FP32. Each block is therefore summed as sum(value * x)
+// with exact BF16 operands (v_cvt_scalef32_pk_bf16_fp4, then v_dot2_f32_bf16
+// on element pairs) and scaled once: acc += (scale * factor) * block.
 __device__ __forceinline__ float nvfp4_dot32(uint4 c, uint32_t sf2, float factor,
-                                             const uint16_t* xs, float acc) {
+                                             const uint32_t (&xw)[16], float acc) {
+  typedef __bf16 bfx2 __attribute__((ext_vector_type(2)));
   const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    // RN(UE4M3 * factor), then RN(that * E2M1) per element
     const float sc = __fmul_rn(e4m3_value((sf2 >> (8 * h)) & 0xffu), factor);
-    const uint4 xa = *reinterpret_cast<const uint4*>(xs + 16 * h);
-    const uint4 xb = *reinterpret_cast<const uint4*>(xs + 16 * h + 8);
-    const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    float bs = 0.f;
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
       const uint32_t word = cw[2 * h + w];
-      const f2 vs[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.f, 0),
-                        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.f, 1),
-                        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.f, 2),
-                        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.f, 3)};
+      const bfx2 v[4] = {__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, 1.f, 0),
+                         __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, 1.f, 1),
+                         __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, 1.f, 2),
+                         __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, 1.f, 3)};
 #pragma unroll
-      for (int bsel = 0; bsel < 4; ++bsel) {
-        const f2 v = vs[bsel];
-        const uint32_t pair = xw[4 * w + bsel];
-        acc = fmaf(__fmul_rn(sc, v[0]), __uint_as_float(pair << 16), acc);
-        acc = fmaf(__fmul_rn(sc, v[1]), __uint_as_float(pair & 0xffff0000u), acc);
-      }
+      for (int bsel = 0; bsel < 4; ++bsel)
+        bs = __builtin_amdgcn_fdot2_f32_bf16(v[bsel], __builtin_bit_cast(bfx2, xw[8 * h + 4 * w + bsel]), bs,
+                                             false);
     }
+    acc = fmaf(sc, bs, acc);
   }
   return acc;
 }
@@ -97,44 +99,113 @@ __device__ __forceinline__ void decode_store(int epi, void* y, const float* resi
   }
 }
 
+// Block: four waves x kRowsPerWave rows. A lane takes 32 contiguous elements
+// per step (16 code bytes per row and the 32 BF16 inputs, read from LDS once
+// for all the wave's rows); all steps' code and scale loads of a row are
+// issued before the first is consumed when K <= 8192.
+constexpr uint32_t kRowsPerWave = 4;
+
 template <bool Paired>
 __global__ __launch_bounds__(256) void nvfp4_gemv_kernel(
     const uint8_t* __restrict__ ca, const uint8_t* __restrict__ sa, const uint8_t* __restrict__ cb,
     const uint8_t* __restrict__ sb, uint32_t n, uint32_t pn, uint32_t k, uint32_t pk,
     const uint16_t* __restrict__ x, void* ya, void* yb, const float* ra, const float* rb, int epi) {
+  constexpr uint32_t R = kRowsPerWave, kMaxSteps = 4, BR = 4 * R;
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-  for (uint32_t i = threadIdx.x; i < pk; i += 256) xs[i] = i < k ? x[i] : uint16_t(0);
+  // Scales of the block's BR rows, one dword per (row, quad of blocks): in
+  // the swizzle a row's blocks 4q..4q+3 share one aligned dword, and the
+  // dwords of consecutive rows are 16 B apart.
+  const uint32_t quads = pk / 64;
+  uint32_t* sfa_l = reinterpret_cast<uint32_t*>(smem + size_t(pk) * 2);
+  uint32_t* sfb_l = sfa_l + BR * quads;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t brow0 = blockIdx.x * BR;  // BR divides 128: the block lies in one stripe
+  const uint32_t row0 = brow0 + (threadIdx.x >> 6) * R;
+  const uint32_t nsteps = (pk + 2047) / 2048;
+  const bool hoist = nsteps <= kMaxSteps;
+
+  // This wave's code loads go out first (rows past pn re-read the last row
+  // and are never stored), so they overlap the block's staging below.
+  auto load = [&](uint32_t c0, uint4 (&wa)[R], uint4 (&wb)[R]) {
+#pragma unroll
+    for (uint32_t r = 0; r < R; ++r) {
+      const size_t co = (size_t(min(row0 + r, pn - 1)) * pk + c0) / 2;
+      wa[r] = *reinterpret_cast<const uint4*>(ca + co);
+      if constexpr (Paired) wb[r] = *reinterpret_cast<const uint4*>(cb + co);
+    }
+  };
+  uint4 wa[kMaxSteps][R], wb[kMaxSteps][R];
+  if (hoist && row0 < pn) {
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxSteps; ++i)
+      if (i < nsteps && lane * 32 + i * 2048 < pk) load(lane * 32 + i * 2048, wa[i], wb[i]);
+  }
+
+  if ((reinterpret_cast<uintptr_t>(x) % 16) == 0 && k % 8 == 0) {
+    for (uint32_t i = threadIdx.x; i < pk / 8; i += 256)
+      reinterpret_cast<uint4*>(xs)[i] = 8 * i < k ? reinterpret_cast<const uint4*>(x)[i] : make_uint4(0, 0, 0, 0);
+  } else {
+    for (uint32_t i = threadIdx.x; i < pk; i += 256) xs[i] = i < k ? x[i] : uint16_t(0);
+  }
+  for (uint32_t i = threadIdx.x; i < BR * quads; i += 256) {
+    const uint32_t rl = i % BR, q = i / BR;
+    const uint64_t o = 256 + nvfp4_sf_index(brow0 + rl, 4 * q, pk);
+    sfa_l[rl * quads + q] = *reinterpret_cast<const uint32_t*>(sa + o);
+    if constexpr (Paired) sfb_l[rl * quads + q] = *reinterpret_cast<const uint32_t*>(sb + o);
+  }
   __syncthreads();
-  const uint32_t lane = threadIdx.x & 63u, row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= pn) return;
+  if (row0 >= pn) return;
   const float fa = *reinterpret_cast<const float*>(sa);
   const float fb = Paired ? *reinterpret_cast<const float*>(sb) : 0.f;
-  float acc_a = 0.f, acc_b = 0.f;
-  for (uint32_t c0 = lane * 32; c0 < pk; c0 += 2048) {
-    const size_t co = (size_t(row) * pk + c0) / 2;
-    const uint64_t so = 256 + nvfp4_sf_index(row, c0 / 16, pk);
-    const uint4 wa = *reinterpret_cast<const uint4*>(ca + co);
-    const uint32_t sfa = *reinterpret_cast<const uint16_t*>(sa + so);
-    acc_a = nvfp4_dot32(wa, sfa, fa, xs + c0, acc_a);
-    if constexpr (Paired) {
-      const uint4 wb = *reinterpret_cast<const uint4*>(cb + co);
-      const uint32_t sfb = *reinterpret_cast<const uint16_t*>(sb + so);
-      acc_b = nvfp4_dot32(wb, sfb, fb, xs + c0, acc_b);
+  float acc_a[R], acc_b[R];
+#pragma unroll
+  for (uint32_t r = 0; r < R; ++r) acc_a[r] = acc_b[r] = 0.f;
+  auto step = [&](uint32_t c0, const uint4 (&wa_)[R], const uint4 (&wb_)[R]) {
+    uint32_t xw[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4*>(xs + c0 + 8 * i);
+      xw[4 * i] = v.x; xw[4 * i + 1] = v.y; xw[4 * i + 2] = v.z; xw[4 * i + 3] = v.w;
+    }
+    const uint32_t sh = 8 * ((c0 / 16) % 4);
+#pragma unroll
+    for (uint32_t r = 0; r < R; ++r) {
+      const uint32_t li = (row0 + r - brow0) * quads + c0 / 64;
+      acc_a[r] = nvfp4_dot32(wa_[r], (sfa_l[li] >> sh) & 0xffffu, fa, xw, acc_a[r]);
+      if constexpr (Paired) acc_b[r] = nvfp4_dot32(wb_[r], (sfb_l[li] >> sh) & 0xffffu, fb, xw, acc_b[r]);
+    }
+  };
+  if (hoist) {
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxSteps; ++i)
+      if (i < nsteps && lane * 32 + i * 2048 < pk) step(lane * 32 + i * 2048, wa[i], wb[i]);
+  } else {
+    for (uint32_t c0 = lane * 32; c0 < pk; c0 += 2048) {
+      uint4 ta[R], tb[R];
+      load(c0, ta, tb);
+      step(c0, ta, tb);
     }
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    acc_a += __shfl_xor(acc_a, o);
-    if constexpr (Paired) acc_b += __shfl_xor(acc_b, o);
+  for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      acc_a[r] += __shfl_xor(acc_a[r], o);
+      if constexpr (Paired) acc_b[r] += __shfl_xor(acc_b[r], o);
+    }
+  if (lane != 0) return;
+#pragma unroll
+  for (uint32_t r = 0; r < R; ++r) {
+    const uint32_t row = row0 + r;
+    if (row >= n) break;
+    if (Paired && epi == QW38_DECODE_SWIGLU_BF16) {
+      static_cast<uint16_t*>(ya)[row] = f32_to_bf16_rne(silu(acc_a[r]) * acc_b[r]);
+      continue;
+    }
+    decode_store(epi, ya, ra, row, acc_a[r]);
+    if constexpr (Paired) decode_store(epi, yb, rb, row, acc_b[r]);
   }
-  if (lane != 0 || row >= n) return;
-  if (Paired && epi == QW38_DECODE_SWIGLU_BF16) {
-    static_cast<uint16_t*>(ya)[row] = f32_to_bf16_rne(silu(acc_a) * acc_b);
-    return;
-  }
-  decode_store(epi, ya, ra, row, acc_a);
-  if constexpr (Paired) decode_store(epi, yb, rb, row, acc_b);
 }
 
 // ---- W4A4 GEMM: 128 weight rows x 128 tokens per block, 4 waves of 64 x 64 ----
@@ -315,12 +386,13 @@ hipError_t launch_nvfp4_gemv(const uint8_t* ca, const uint8_t* sa, const uint8_t
                              const uint8_t* sb, uint32_t n, uint32_t pn, uint32_t k, uint32_t pk,
                              const uint16_t* x, void* ya, void* yb, const float* ra, const float* rb,
                              int epilogue, hipStream_t s) {
-  const dim3 grid((pn + 3) / 4);
+  const dim3 grid((pn + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave));
+  const size_t lds = size_t(pk) * 2 + size_t(2) * 4 * kRowsPerWave * (pk / 64) * 4;
   if (cb)
-    hipLaunchKernelGGL(nvfp4_gemv_kernel<true>, grid, dim3(256), size_t(pk) * 2, s, ca, sa, cb, sb, n,
+    hipLaunchKernelGGL(nvfp4_gemv_kernel<true>, grid, dim3(256), lds, s, ca, sa, cb, sb, n,
                        pn, k, pk, x, ya, yb, ra, rb, epilogue);
   else
-    hipLaunchKernelGGL(nvfp4_gemv_kernel<false>, grid, dim3(256), size_t(pk) * 2, s, ca, sa, cb, sb,
+    hipLaunchKernelGGL(nvfp4_gemv_kernel<false>, grid, dim3(256), lds, s, ca, sa, cb, sb,
                        n, pn, k, pk, x, ya, yb, ra, rb, epilogue);
   return hipGetLastError();
 }
