@@ -5,18 +5,21 @@
 // row: 128 B of low nibbles, then 64 B of high bit pairs), 128 contiguous
 // bytes of int8 sub-block scales and 16 contiguous bytes of fp16 d, and the
 // tiles of an 8-row strip follow one another. One wave streams one tile per
-// step: lane l = 8 r + g owns row r, K32 group g (16 low-nibble bytes, 8
+// step: lane l = 8 g + r owns row r, K32 group g (16 low-nibble bytes, 8
 // high-pair bytes, the group's two sub-block scales and the row's d), so each
-// wave load instruction reads whole contiguous runs. WS waves of a block
-// split a strip's tiles into contiguous ranges; loads (weights and the lane's
-// 32 activation codes and scale a, which stay cache-resident) run D tiles
+// wave load instruction reads whole contiguous runs. The activations of a
+// tile (8 groups x 32 codes) are loaded once per wave, one dword per lane
+// (lane 8 g + i holds codes 4i..4i+3 of group g), and each lane gathers its
+// group's eight dwords with ds_swizzle broadcasts inside its 8-lane group, so
+// no lane re-reads another row's copy through the vector cache. WS waves of a
+// block split a strip's tiles into contiguous ranges; loads run D tiles
 // ahead, and nothing is staged in LDS.
 //
 // With codes q = 0..63, sub-block scales sc0, sc1 and the 16-code sums s0, s1
 // of the activations (v_dot4 against ones), the reference's per-group integer
 // is I = sc0 (sum_{16} q z - 32 s0) + sc1 (sum_{16} q z - 32 s1), from exact
 // v_dot4_i32_i8 dots; each lane accumulates a d I in FP32 in K order, the
-// group partials of a row are summed over its 8 lanes (xor 1, 2, 4), then
+// group partials of a row are summed over its 8 lanes (xor 8, 16, 32), then
 // over the waves in ascending order, so results do not depend on the grid.
 #include <cstdlib>
 
@@ -33,7 +36,7 @@ struct Q6Step {
   uint32_t hi[2];      // 8 high-pair bytes
   uint32_t sc;         // the group's two int8 sub-block scales (low half)
   uint32_t d;          // fp16 d of the row (low half)
-  uint32_t z[MT][8];   // 32 activation codes per token
+  uint32_t z[MT];      // activation dword r of the lane's group, per token
   float a[MT];         // activation scale per token
 };
 
@@ -58,18 +61,16 @@ __device__ __forceinline__ void load_q6(const uint8_t* crow, uint32_t g, const u
   t.d = *reinterpret_cast<const uint16_t*>(drow);
 #pragma unroll
   for (int tk = 0; tk < MT; ++tk) {
-    const int8_t* z = zp + size_t(tk) * pk;
-    if constexpr (Fast) {
-      const uint4 u = reinterpret_cast<const uint4*>(z)[0];
-      const uint4 v = reinterpret_cast<const uint4*>(z)[1];
-      t.z[tk][0] = u.x; t.z[tk][1] = u.y; t.z[tk][2] = u.z; t.z[tk][3] = u.w;
-      t.z[tk][4] = v.x; t.z[tk][5] = v.y; t.z[tk][6] = v.z; t.z[tk][7] = v.w;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) t.z[tk][i] = reinterpret_cast<const uint32_t*>(z)[i];
-    }
+    t.z[tk] = *reinterpret_cast<const uint32_t*>(zp + size_t(tk) * pk);
     t.a[tk] = ap[size_t(tk) * groups];
   }
+}
+
+// Lane (lane & ~7) | I's value, for every lane: ds_swizzle in bit mode with
+// and-mask 0x18, or-mask I (lanes are remapped within each 32-lane half).
+template <int I>
+__device__ __forceinline__ uint32_t bcast8(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), 0x18 | (I << 5)));
 }
 
 template <int MT>
@@ -85,16 +86,19 @@ __device__ __forceinline__ void consume_q6(const Q6Step<MT>& t, float acc[MT]) {
   const float d = f16_to_f32(t.d);
 #pragma unroll
   for (int tk = 0; tk < MT; ++tk) {
+    // dword i of the lane's group comes from lane (lane & ~7) | i
+    const uint32_t z[8] = {bcast8<0>(t.z[tk]), bcast8<1>(t.z[tk]), bcast8<2>(t.z[tk]), bcast8<3>(t.z[tk]),
+                           bcast8<4>(t.z[tk]), bcast8<5>(t.z[tk]), bcast8<6>(t.z[tk]), bcast8<7>(t.z[tk])};
     int d0 = 0, d1 = 0, s0 = 0, s1 = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      d0 = dot4(v[i], t.z[tk][i], d0);
-      s0 = dot4(0x01010101u, t.z[tk][i], s0);
+      d0 = dot4(v[i], z[i], d0);
+      s0 = dot4(0x01010101u, z[i], s0);
     }
 #pragma unroll
     for (int i = 4; i < 8; ++i) {
-      d1 = dot4(v[i], t.z[tk][i], d1);
-      s1 = dot4(0x01010101u, t.z[tk][i], s1);
+      d1 = dot4(v[i], z[i], d1);
+      s1 = dot4(0x01010101u, z[i], s1);
     }
     const int I = sc0 * (d0 - 32 * s0) + sc1 * (d1 - 32 * s1);
     acc[tk] = fmaf(t.a[tk] * d, float(I), acc[tk]);
@@ -112,12 +116,12 @@ __global__ __launch_bounds__(256) void q6_stream_kernel(
   __shared__ float red[WS > 1 ? NW * MT * 8 : 1];
   const uint32_t groups = pk / 32;
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-  const uint32_t r = lane >> 3, g = lane & 7u;
+  const uint32_t g = lane >> 3, r = lane & 7u;
   const uint32_t ks = wave % WS;
   const uint32_t kb0 = uint32_t(uint64_t(kbs) * ks / WS);
   const uint32_t nkb = uint32_t(uint64_t(kbs) * (ks + 1) / WS) - kb0;
   const uint64_t tiles = uint64_t(strips) * kbs * 8;  // tile rows: the d array follows the scales
-  const int8_t* zbase = xc + (size_t(kb0) * 8 + g) * 32;
+  const int8_t* zbase = xc + (size_t(kb0) * 8 + g) * 32 + r * 4;
   const float* abase = xa + size_t(kb0) * 8 + g;
 
   const uint32_t stride = persistent ? gridDim.x * SPB : SPB * gridDim.x + strips;
@@ -154,12 +158,12 @@ __global__ __launch_bounds__(256) void q6_stream_kernel(
       for (int u = 0; u < D; ++u)
         if (i + u < nkb) consume_q6<MT>(ring[u], acc);
     }
-    // a row's partials live in lanes 8r..8r+7
+    // a row's partials live in lanes r, r + 8, ..., r + 56
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      acc[t] += __shfl_xor(acc[t], 1);
-      acc[t] += __shfl_xor(acc[t], 2);
-      acc[t] += __shfl_xor(acc[t], 4);
+      acc[t] += __shfl_xor(acc[t], 8);
+      acc[t] += __shfl_xor(acc[t], 16);
+      acc[t] += __shfl_xor(acc[t], 32);
     }
     const uint32_t row = strip * 8 + r;
     const bool writer = g == 0;
@@ -232,10 +236,10 @@ hipError_t launch_q6k_stream(const WeightView& w, const Q8View& x, float* out, c
     return e ? std::atoi(e) : 0;
   }();
   if (!env) return hipErrorNotSupported;
-  // Fast: 16-byte aligned codes and activations; otherwise 4-byte loads with
-  // identical arithmetic (the scales are read as 2-byte words, the
-  // reference's minimum alignment of the scales span).
-  const bool fast = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(x.codes)) % 16) == 0;
+  // Fast: 16-byte aligned codes; otherwise 4-byte loads with identical
+  // arithmetic (activations are read as dwords and the scales as 2-byte
+  // words, the reference's minimum alignment of the scales span).
+  const bool fast = (reinterpret_cast<uintptr_t>(w.codes) % 16) == 0;
   const uint32_t strips = w.pn / 8, kbs = w.pk / 256;
   int ws = 1;  // split K over more waves when the strips alone cannot fill the chip
   if (strips < 4096 && kbs >= 8) ws = 2;
