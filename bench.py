@@ -166,6 +166,33 @@ def bench_decode(torch, ops, n, k, ms, steps, warmup, layout, seed=11):
     return res, base
 
 
+def bench_decode_q6(torch, ops, n, k, ms, steps, warmup, seed=61):
+    """Config 3: Q6_K down-projection decode (layout 0x0241) at each M in ms,
+    rotating weight copies so every launch streams its weights from HBM."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn(n, k, generator=g, device="cuda") * 0.02
+    base = ops.upload_q6k_blocks(ops.quantize_q6k_blocks(x, n, k), n, k)
+    del x
+    wbytes = weight_bytes("q6k", n, k)
+    copies = max(2, math.ceil(1.2e9 / wbytes))
+    ws = [base] + [clone_weight(ops, base) for _ in range(copies - 1)]
+    res = {}
+    for m in ms:
+        q, _ = make_q8(torch, ops, m, k, seed + 100 + m, outliers=False)
+        outs = [torch.empty(m, n, device="cuda") for _ in range(copies)]
+        ms_step, nsteps, mode = time_launches(
+            torch, lambda i: ops.q4k_q8_project(ws[i], q, outs[i]), copies, steps, warmup)
+        algo = wbytes + m * k * 1.25 + m * n * 4
+        res[str(m)] = {"us": round(ms_step * 1e3, 3), "gbs": round(algo / (ms_step * 1e-3) / 1e9, 1),
+                       "frac_hbm": round(algo / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                       "mode": mode}
+        log(f"decode Q6_K N={n} K={k} M={m}: {ms_step*1e3:.2f} us/launch, "
+            f"{res[str(m)]['gbs']:.0f} GB/s ({mode})")
+    del ws
+    return res
+
+
 def bench_decode_bf16(torch, ops, n, k, steps, warmup, seed=31):
     """BF16-activation decode_mmv (Q4_K 0x020D, M=1, StoreFp32) on the config-2
     shape, rotating weight copies like the Q8 decode."""
@@ -324,6 +351,7 @@ def main():
     ap.add_argument("--no-bf16", action="store_true", help="skip the BF16-activation decode_mmv")
     ap.add_argument("--decode-m", default="1,2,4,8", help="decode token counts to time")
     ap.add_argument("--no-model", action="store_true", help="skip the config-5 model pass")
+    ap.add_argument("--no-q6", action="store_true", help="skip the config-3 Q6_K decode leg")
     ap.add_argument("--model-layers", type=int, default=64)
     ap.add_argument("--model-layout", default="0x020D", help="Q4_K layout of the model pass")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -357,6 +385,8 @@ def main():
     mmq_layout = int(args.mmq_layout, 16)
     mmq = None if args.no_mmq else bench_mmq(torch, ops, n, k, 512, max(20, args.steps // 8),
                                               max(3, args.warmup // 4), mmq_layout)
+    q6 = None if args.no_q6 else bench_decode_q6(torch, ops, 5120, 17408, [1, 8], args.steps,
+                                                 args.warmup)
     dbf16 = None if args.no_bf16 else bench_decode_bf16(torch, ops, n, k, args.steps, args.warmup)
     pbf16 = None if (args.no_bf16 or args.no_mmq) else bench_prefill_bf16(
         torch, ops, n, k, 512, max(20, args.steps // 8), max(3, args.warmup // 4))
@@ -395,6 +425,7 @@ def main():
         "decode_m": {str(m): {"gbs": round(v["gbs"], 1), "us": round(v["ms"] * 1e3, 3),
                               "frac_hbm": round(v["gbs"] / HBM_PEAK_GBS, 4)}
                      for m, v in dec.items()},
+        "config3_q6k_decode": q6,
         "mmq_m512": mmq,
         "decode_bf16_m1": dbf16,
         "prefill_bf16_m512": pbf16,
