@@ -6,15 +6,19 @@ same JSON line carries the MMQ int8-equivalent TOPS at M=512 (config 4,
 Q4_K N=34816), the other decode M values, and the config-5 full-model weight
 pass (64 synthetic layers, one decode step and one 512-token prefill chunk).
 
-A "step" is one projection launch over one weight copy with the Q8
-activations resident in HBM. Weight copies rotate (>= 1.2 GB in total) so
-MI355X's 256 MB Infinity Cache cannot serve repeats. Weights are seeded fp32
+A "step" is one rotation over the rotated weight copies of the headline
+shape: one projection launch per copy (12 launches over 1.2 GB for config 2),
+with the Q8 activations resident in HBM. Copies rotate (>= 1.2 GB in total) so
+MI355X's 256 MB Infinity Cache cannot serve repeats; every leg times at least
+100 launches. Weights are seeded fp32
 ~N(0, 0.02) quantized ON THE GPU by the library's Q4_K fitter (bit-exact with
 the reference's pinned llama.cpp fitter); activations ~N(0,1) with 1% of the
 channels x20, rounded to BF16 and Q8-packed by the library.
 
-The cpu_baseline leg times the oracle's C restatement of the same contraction
-(test infrastructure, OpenMP) on the host cores for a bounded sample.
+The cpu_baseline leg compiles oracle/cpu_baseline.c (the reference's closed-form
+contraction as an FP32 CPU kernel over the packed GGML blocks, test
+infrastructure) with -O3 -march=native -fopenmp on the host that runs the
+bench and times it on the host cores for a bounded sample.
 """
 from __future__ import annotations
 
@@ -57,8 +61,9 @@ def measured_traffic(layout):
         return None
     vals = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        g = re.search(kernel + r"[^\n]*\(dispatches=\d+\): " + counter + r"=([\d.e+]+)", text)
-        c = re.search(r"__amd_rocclr_copyBuffer \(dispatches=\d+\): " + counter + r"=([\d.e+]+)", text)
+        g = re.search(kernel + r"[^\n]*\(dispatches=\d+\):[^\n]*\b" + counter + r"=([\d.e+]+)", text)
+        c = re.search(r"__amd_rocclr_copyBuffer[^\n]*\(dispatches=\d+\):[^\n]*\b" + counter +
+                      r"=([\d.e+]+)", text)
         if not g or not c:
             return None
         scale = (1 << 20) / float(c.group(1))  # KiB the counter should read for 1 GiB
@@ -109,86 +114,132 @@ def make_q8(torch, ops, m, k, seed, outliers=True):
     return q, bf
 
 
-def time_launches(torch, fn, copies, steps, warmup, use_graph=True):
-    """Runs `steps` launches rotating over `copies`; returns (ms_per_step, mode)."""
+def time_launches(torch, fn, copies, steps, warmup, use_graph=True, min_launches=100):
+    """Times launches of fn(i) rotating over `copies` inputs.
+
+    One rotation (fn(0) .. fn(copies-1), one launch per weight copy) is
+    captured in a hipGraph. `warmup` untimed replays, then the timed region
+    replays the rotation `steps` times, or more when needed to reach
+    `min_launches` launches (rounded up to whole rotations), bracketed by HIP
+    events recorded on the launch stream. Returns (ms per launch, launches
+    timed, rotations timed, mode)."""
     stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        fn(i % copies)
-    torch.cuda.synchronize()
     mode = "eager"
     graph = None
+    for i in range(copies):  # first calls outside capture (lazy set-up)
+        fn(i)
+    torch.cuda.synchronize()
     if use_graph:
         try:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, capture_error_mode="thread_local"):
                 for i in range(copies):
                     fn(i)
-            graph.replay()
             torch.cuda.synchronize()
             mode = "hipgraph"
         except Exception as e:  # fall back to eager launches
             log(f"graph capture unavailable ({e}); timing eager launches")
             graph = None
+    rot = max(steps, -(-min_launches // copies))
+    for _ in range(max(1, warmup)):
+        if graph is not None:
+            graph.replay()
+        else:
+            for i in range(copies):
+                fn(i)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    reps = max(1, steps // copies) if graph is not None else steps
     torch.cuda.synchronize()
     start.record(stream)
-    if graph is not None:
-        for _ in range(reps):
+    for _ in range(rot):
+        if graph is not None:
             graph.replay()
-        n = reps * copies
-    else:
-        for i in range(steps):
-            fn(i % copies)
-        n = steps
+        else:
+            for i in range(copies):
+                fn(i)
     end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / n, n, mode
+    n = rot * copies
+    return start.elapsed_time(end) / n, n, rot, mode
 
 
-def bench_decode(torch, ops, n, k, ms, steps, warmup, layout, seed=11):
-    wbytes = q4k_bytes(n, k)
-    copies = max(2, math.ceil(1.2e9 / wbytes))
-    base, _ = make_weight(torch, ops, n, k, seed, layout)
-    ws = [base] + [clone_weight(ops, base) for _ in range(copies - 1)]
-    res = {}
-    for m in ms:
-        q, _ = make_q8(torch, ops, m, k, seed + 100 + m)
-        outs = [torch.empty(m, n, device="cuda") for _ in range(copies)]
-        ms_step, nsteps, mode = time_launches(
-            torch, lambda i: ops.q4k_q8_project(ws[i], q, outs[i]), copies, steps, warmup)
-        algo = wbytes + m * k * 1.25 + m * n * 4  # weights + Q8 (1.25 B/elem) + fp32 out
-        res[m] = {"ms": ms_step, "gbs": algo / (ms_step * 1e-3) / 1e9, "bytes": algo,
-                  "steps": nsteps, "mode": mode}
-        log(f"decode N={n} K={k} M={m}: {ms_step*1e3:.2f} us/launch, "
-            f"{res[m]['gbs']:.0f} GB/s ({mode})")
-    return res, base
+def time_eager(torch, fn, copies, launches):
+    """Eager (no graph) launches rotating over copies: device time per launch
+    from events on the launch stream, and host wall time per call."""
+    stream = torch.cuda.current_stream()
+    for i in range(copies):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    t0 = time.perf_counter()
+    for i in range(launches):
+        fn(i % copies)
+    host = (time.perf_counter() - t0) / launches
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / launches, host * 1e3
 
 
-def bench_decode_q6(torch, ops, n, k, ms, steps, warmup, seed=61):
-    """Config 3: Q6_K down-projection decode (layout 0x0241) at each M in ms,
-    rotating weight copies so every launch streams its weights from HBM."""
+def hbm_roofline(nbytes, ms, **extra):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "us": round(ms * 1e3, 3),
+            "algorithmic_bytes": int(nbytes), **extra}
+
+
+def mfma_roofline(nops, ms, peak_sclk=None, **extra):
+    tops = nops / (ms * 1e-3) / 1e12
+    r = {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+         "frac": round(tops / INT8_PEAK_TOPS, 4), "us": round(ms * 1e3, 2),
+         "ops": int(nops), "frac_fp16_mfma_peak": round(tops / FP16_PEAK_TFLOPS, 4), **extra}
+    if peak_sclk:
+        r["peak_at_measured_sclk"] = round(peak_sclk, 1)
+        r["frac_at_measured_sclk"] = round(tops / peak_sclk, 4)
+    return r
+
+
+def weight_bytes(fmt, n, k):
+    return n * k // 256 * (144 if fmt == "q4k" else 210)
+
+
+def make_any_weight(torch, ops, fmt, n, k, seed, layout):
+    if fmt == "q4k":
+        return make_weight(torch, ops, n, k, seed, layout)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     x = torch.randn(n, k, generator=g, device="cuda") * 0.02
-    base = ops.upload_q6k_blocks(ops.quantize_q6k_blocks(x, n, k), n, k)
+    blocks = ops.quantize_q6k_blocks(x, n, k)
     del x
-    wbytes = weight_bytes("q6k", n, k)
+    w = ops.upload_q6k_blocks(blocks, n, k)
+    torch.cuda.synchronize()
+    return w, blocks
+
+
+def bench_decode(torch, ops, fmt, n, k, ms, steps, warmup, layout, seed, outliers=True,
+                 eager_m1=False):
+    """Decode GEMV at each M in ms, rotating >= 1.2 GB of weight copies so every
+    launch streams its weights from HBM. Returns {M: hbm roofline entry}."""
+    wbytes = weight_bytes(fmt, n, k)
     copies = max(2, math.ceil(1.2e9 / wbytes))
+    base, _ = make_any_weight(torch, ops, fmt, n, k, seed, layout)
     ws = [base] + [clone_weight(ops, base) for _ in range(copies - 1)]
     res = {}
     for m in ms:
-        q, _ = make_q8(torch, ops, m, k, seed + 100 + m, outliers=False)
+        q, _ = make_q8(torch, ops, m, k, seed + 100 + m, outliers=outliers)
         outs = [torch.empty(m, n, device="cuda") for _ in range(copies)]
-        ms_step, nsteps, mode = time_launches(
-            torch, lambda i: ops.q4k_q8_project(ws[i], q, outs[i]), copies, steps, warmup)
-        algo = wbytes + m * k * 1.25 + m * n * 4
-        res[str(m)] = {"us": round(ms_step * 1e3, 3), "gbs": round(algo / (ms_step * 1e-3) / 1e9, 1),
-                       "frac_hbm": round(algo / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                       "mode": mode}
-        log(f"decode Q6_K N={n} K={k} M={m}: {ms_step*1e3:.2f} us/launch, "
-            f"{res[str(m)]['gbs']:.0f} GB/s ({mode})")
+        fn = lambda i: ops.q4k_q8_project(ws[i], q, outs[i])  # noqa: E731
+        ms_launch, launches, rot, mode = time_launches(torch, fn, copies, steps, warmup)
+        algo = wbytes + m * k * 1.25 + m * n * 4  # weights + Q8 (1.25 B/elem) + fp32 out
+        res[m] = hbm_roofline(algo, ms_launch, launches=launches, rotations=rot, copies=copies,
+                              timing=mode)
+        if eager_m1 and m == 1:
+            dev_ms, host_ms = time_eager(torch, fn, copies, 600)
+            res[m]["eager_us_per_launch"] = round(dev_ms * 1e3, 3)
+            res[m]["eager_host_us_per_call"] = round(host_ms * 1e3, 3)
+        log(f"decode {fmt} N={n} K={k} M={m}: {ms_launch*1e3:.2f} us/launch, "
+            f"{res[m]['achieved']:.0f} GB/s ({mode}, {launches} launches)")
     del ws
     return res
 
@@ -205,13 +256,13 @@ def bench_decode_bf16(torch, ops, n, k, steps, warmup, seed=31):
     x = torch.randn(k, generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
     outs = [torch.empty(n, device="cuda") for _ in range(copies)]
     descs = [ops.decode_desc(ws[i], x, outs[i], ops.DECODE_STORE_FP32) for i in range(copies)]
-    ms_step, nsteps, mode = time_launches(torch, lambda i: ops.decode_mmv(descs[i]), copies,
-                                          steps, warmup)
-    algo = wbytes + k * 2 + n * 4
-    gbs = algo / (ms_step * 1e-3) / 1e9
-    log(f"decode_bf16 N={n} K={k}: {ms_step*1e3:.2f} us/launch, {gbs:.0f} GB/s ({mode})")
-    return {"us": round(ms_step * 1e3, 3), "gbs": round(gbs, 1),
-            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "layout": "0x020d", "steps": nsteps}
+    ms_launch, launches, _, mode = time_launches(torch, lambda i: ops.decode_mmv(descs[i]), copies,
+                                                 steps, warmup)
+    r = hbm_roofline(wbytes + k * 2 + n * 4, ms_launch, launches=launches, layout="0x020d",
+                     timing=mode)
+    log(f"decode_bf16 N={n} K={k}: {ms_launch*1e3:.2f} us/launch, {r['achieved']:.0f} GB/s ({mode})")
+    del ws
+    return r
 
 
 def bench_prefill_bf16(torch, ops, n, k, m, steps, warmup, seed=41):
@@ -222,26 +273,33 @@ def bench_prefill_bf16(torch, ops, n, k, m, steps, warmup, seed=41):
     g.manual_seed(seed + 1)
     x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
     out = torch.empty(m, n, device="cuda")
-    ms_step, nsteps, mode = time_launches(
+    ms_launch, launches, _, mode = time_launches(
         torch, lambda i: ops.prefill_project(w, x, m, out, ops.DECODE_STORE_FP32), 1, steps, warmup)
-    tf = 2.0 * m * n * k / (ms_step * 1e-3) / 1e12
-    log(f"prefill_bf16 N={n} K={k} M={m}: {ms_step*1e3:.1f} us/launch, {tf:.1f} TFLOP/s ({mode})")
-    return {"us": round(ms_step * 1e3, 2), "tflops": round(tf, 1),
-            "frac_bf16_mfma_peak": round(tf / FP16_PEAK_TFLOPS, 4), "m": m, "n": n, "k": k}
+    tf = 2.0 * m * n * k / (ms_launch * 1e-3) / 1e12
+    log(f"prefill_bf16 N={n} K={k} M={m}: {ms_launch*1e3:.1f} us/launch, {tf:.1f} TFLOP/s ({mode})")
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / FP16_PEAK_TFLOPS, 4), "us": round(ms_launch * 1e3, 2),
+            "launches": launches, "m": m, "n": n, "k": k}
 
 
-def bench_mmq(torch, ops, n, k, m, steps, warmup, layout, seed=21):
-    w, _ = make_weight(torch, ops, n, k, seed, layout)
-    q, _ = make_q8(torch, ops, m, k, seed + 1)
-    out = torch.empty(m, n, device="cuda")
-    ms_step, nsteps, mode = time_launches(
-        torch, lambda i: ops.q4k_q8_project(w, q, out), 1, steps, warmup)
-    ops_count = 2.0 * m * n * k
-    tops = ops_count / (ms_step * 1e-3) / 1e12
-    log(f"mmq N={n} K={k} M={m}: {ms_step*1e3:.1f} us/launch, {tops:.1f} TOPS ({mode})")
-    return {"ms": ms_step, "tops": tops, "frac_int8_peak": tops / INT8_PEAK_TOPS,
-            "frac_fp16_mfma_peak": tops / FP16_PEAK_TFLOPS, "steps": nsteps, "mode": mode,
-            "m": m, "n": n, "k": k}
+def bench_mmq(torch, ops, shapes, steps, warmup, layout, peak_sclk, seed=21):
+    """Config 4: MMQ at each (format, N, K, M); weights resident (the MMQ is
+    MFMA-bound: 2*M*N*K ops against the int8 dense peak)."""
+    res = {}
+    for fmt, n, k, mlist in shapes:
+        w, _ = make_any_weight(torch, ops, fmt, n, k, seed + n, layout)
+        for m in mlist:
+            q, _ = make_q8(torch, ops, m, k, seed + 1 + m, outliers=(fmt == "q4k"))
+            out = torch.empty(m, n, device="cuda")
+            ms_launch, launches, _, mode = time_launches(
+                torch, lambda i: ops.q4k_q8_project(w, q, out), 1, steps, warmup)
+            key = f"{fmt}_n{n}_k{k}_m{m}"
+            res[key] = mfma_roofline(2.0 * m * n * k, ms_launch, peak_sclk, launches=launches,
+                                     layout=f"{w.layout:#06x}", timing=mode)
+            log(f"mmq {key}: {ms_launch*1e3:.1f} us/launch, {res[key]['achieved']:.1f} TOPS ({mode})")
+            del q, out
+        del w
+    return res
 
 
 # Config 5: one layer of the synthetic 27B-class stack (out rows, in columns, format)
@@ -249,38 +307,26 @@ MODEL_LAYER = (("qkv_gate", 12288, 5120, "q4k"), ("out", 5120, 6144, "q4k"),
                ("gate_up", 34816, 5120, "q4k"), ("down", 5120, 17408, "q6k"))
 
 
-def weight_bytes(fmt, n, k):
-    return n * k // 256 * (144 if fmt == "q4k" else 210)
-
-
-def bench_model(torch, ops, layers, q4_layout, prefill_m, reps, seed=1000):
+def bench_model(torch, ops, layers, q4_layout, prefill_m, reps, peak_sclk, seed=1000):
     """Config 5: a full weight pass over `layers` synthetic layers (about
     14.5 GB of quantized weights resident in HBM at 64 layers): one decode step
     (M=1, every projection of every layer once) and one prefill chunk
     (M=prefill_m). Each (layer, projection) has its own seeded ~N(0, 0.02)
     weights, quantized on the GPU, and its own fresh seeded ~N(0,1) Q8
-    activation rows. Both passes are captured in one hipGraph each and timed
-    with events; the aggregate rate covers every byte / op of the pass."""
+    activation rows. Each pass is captured in one hipGraph and timed with
+    events. After timing, the last layer's four projections are re-run eagerly
+    and must equal the graph-replay outputs bitwise (the oracle parity of the
+    same pass is a GPU test)."""
     t0 = time.perf_counter()
-    g = torch.Generator(device="cuda")
-    fail = torch.zeros(1, dtype=torch.int32, device="cuda")
     ws = []
     for l in range(layers):
         row = []
         for j, (name, n, k, fmt) in enumerate(MODEL_LAYER):
-            g.manual_seed(seed + 16 * l + j)
-            x = torch.randn(n, k, generator=g, device="cuda", dtype=torch.float32) * 0.02
-            if fmt == "q4k":
-                blocks = ops.quantize_q4k_blocks(x, n, k, fail)
-                w = ops.upload_q4k_blocks(blocks, n, k, layout=q4_layout)
-            else:
-                blocks = ops.quantize_q6k_blocks(x, n, k)
-                w = ops.upload_q6k_blocks(blocks, n, k)
-            del x, blocks
+            w, blocks = make_any_weight(torch, ops, fmt, n, k, seed + 16 * l + j, q4_layout)
+            del blocks
             row.append(w)
         ws.append(row)
     torch.cuda.synchronize()
-    assert int(fail.item()) == 0
     t_gen = time.perf_counter() - t0
     res = {"layers": layers, "q4k_layout": f"{q4_layout:#06x}", "q6k_layout": "0x0241",
            "weight_bytes": layers * sum(weight_bytes(f, n, k) for _, n, k, f in MODEL_LAYER),
@@ -295,54 +341,120 @@ def bench_model(torch, ops, layers, q4_layout, prefill_m, reps, seed=1000):
                 for j in range(len(MODEL_LAYER)):
                     ops.q4k_q8_project(ws[l][j], qs[l][j], outs[j])
 
-        ms_pass, npass, mode = time_launches(torch, run_pass, 1, reps, 1)
+        ms_pass, npass, _, mode = time_launches(torch, run_pass, 1, reps, 1, min_launches=1)
+        same = True
+        for j, (_, n, _, _) in enumerate(MODEL_LAYER):
+            again = torch.empty(m, n, device="cuda")
+            ops.q4k_q8_project(ws[-1][j], qs[-1][j], again)
+            torch.cuda.synchronize()
+            same = same and bool(torch.equal(again, outs[j]))
         nbytes = layers * sum(weight_bytes(f, n, k) + m * k * 1.25 + m * n * 4
                               for _, n, k, f in MODEL_LAYER)
         nops = layers * sum(2.0 * m * n * k for _, n, k, _ in MODEL_LAYER)
-        gbs = nbytes / (ms_pass * 1e-3) / 1e9
-        tops = nops / (ms_pass * 1e-3) / 1e12
         key = "decode_m1" if m == 1 else f"prefill_m{m}"
-        res[key] = {"ms": round(ms_pass, 4), "gbs": round(gbs, 1),
-                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "tops": round(tops, 2),
-                    "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                    "launches": layers * len(MODEL_LAYER), "passes": npass, "mode": mode}
+        entry = (hbm_roofline(nbytes, ms_pass) if m == 1 else mfma_roofline(nops, ms_pass, peak_sclk))
+        entry.update({"ms": round(ms_pass, 4), "launches": layers * len(MODEL_LAYER),
+                      "passes": npass, "timing": mode, "replay_equals_eager": same})
+        res[key] = entry
         log(f"model pass M={m} ({layers} layers, {res['weight_bytes']/1e9:.2f} GB): "
-            f"{ms_pass:.3f} ms, {gbs:.0f} GB/s, {tops:.1f} TOPS ({mode})")
+            f"{ms_pass:.3f} ms, {entry['achieved']} {entry['unit']} ({mode}), replay==eager {same}")
         del qs, outs
     del ws
     torch.cuda.empty_cache()
     return res
 
 
+def clock_probe(torch, ops):
+    """Shader clock under a full int8 MFMA load (qw38_mfma_clock_probe) and the
+    int8 dense peak at that clock: CUs x 8192 ops/cycle x sclk."""
+    import ctypes as C
+
+    from qw38_amd._lib import lib
+    ticks = torch.zeros(4, dtype=torch.int64, device="cuda")
+    blocks = C.c_uint32(0)
+    iters = 40000
+    stream = torch.cuda.current_stream()
+    for _ in range(2):
+        st = lib().qw38_mfma_clock_probe(iters, ticks.data_ptr(), C.byref(blocks), stream.cuda_stream)
+        assert st == 0
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    lib().qw38_mfma_clock_probe(iters, ticks.data_ptr(), C.byref(blocks), stream.cuda_stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    cyc, rt = (int(v) for v in ticks[:2].cpu())
+    sclk = cyc / (rt / 100e6) if rt else float("nan")
+    cus = blocks.value
+    loop_ops = cus * 4 * iters * 4 * 32 * 32 * 32 * 2.0
+    r = {"sclk_mhz": round(sclk / 1e6, 1), "cus": cus,
+         "int8_peak_tops_at_sclk": round(cus * 8192 * sclk / 1e12, 1),
+         "pure_mfma_loop_tops": round(loop_ops / (ms * 1e-3) / 1e12, 1)}
+    log(f"clock probe: {r}")
+    return r
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(torch, blocks, n, k, m, budget_s):
-    """Oracle (C restatement, OpenMP) on the host cores: same contraction."""
+    """oracle/cpu_baseline.c compiled here with -O3 -march=native -fopenmp
+    (FP32 closed-form contraction straight from the packed GGML blocks, rows
+    in parallel) on the config-2 M=1 workload: median of >= 5 full passes."""
+    import ctypes as C
+    import subprocess
+    import tempfile
+
     import numpy as np
 
     import oracle
+    src = os.path.join(ROOT, "oracle", "cpu_baseline.c")
+    so = os.path.join(tempfile.mkdtemp(prefix="qw38_cpub_"), "libcpu_baseline.so")
+    cmd = ["gcc", "-O3", "-march=native", "-fopenmp", "-fPIC", "-shared", "-o", so, src]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        log(f"cpu baseline build failed: {r.stderr[-400:]}")
+        return None
+    L = C.CDLL(so)
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    w = oracle.Q4K.from_ggml(blocks.cpu().numpy(), n, k)
+    gb = np.ascontiguousarray(blocks.cpu().numpy(), np.uint8)
     rng = np.random.Generator(np.random.PCG64(5))
-    x = oracle.fp32_to_bf16(rng.standard_normal((m, k), dtype=np.float32))
-    q = oracle.pack_q8(x, m, k)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        oracle.q4k_q8_contract(w, q, threads=threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    per = el / reps
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    x[:, rng.choice(k, k // 100, replace=False)] *= 20
+    q = oracle.pack_q8(oracle.fp32_to_bf16(x), m, k)
+    out = np.zeros((m, n), np.float32)
+    P = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
+    args = (P(gb), n, k, P(q.codes), P(q.scales), P(q.sums), m, P(out), threads)
+    L.cpub_q4k.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
+                           C.c_uint32, C.c_void_p, C.c_int]
+    times, t_all = [], time.perf_counter()
+    while len(times) < 5 or time.perf_counter() - t_all < budget_s:
+        t0 = time.perf_counter()
+        assert L.cpub_q4k(*args) == 0
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
     algo = q4k_bytes(n, k) + m * k * 1.25 + m * n * 4
-    return {"value": algo / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} full passes of the N={n} K={k} M={m} Q4_K x Q8 contraction "
-                      f"(oracle/oracle.c, exact int32 K32 dots + affine), {el:.1f} s"}
+    return {"value": round(algo / med / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "build": "gcc -O3 -march=native -fopenmp oracle/cpu_baseline.c",
+            "sample": f"median of {len(times)} full passes ({time.perf_counter() - t_all:.1f} s) of "
+                      f"the config-2 workload N={n} K={k} M={m}: FP32 closed-form contraction "
+                      "over the packed Q4_K blocks, exact int32 K32 dots, rows in parallel"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=240)
-    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--steps", type=int, default=20, help="timed rotations of the headline leg")
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layout", default="0x020D", help="decode weight layout")
     ap.add_argument("--mmq-layout", default="0x0240", help="MMQ weight layout")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -352,6 +464,8 @@ def main():
     ap.add_argument("--decode-m", default="1,2,4,8", help="decode token counts to time")
     ap.add_argument("--no-model", action="store_true", help="skip the config-5 model pass")
     ap.add_argument("--no-q6", action="store_true", help="skip the config-3 Q6_K decode leg")
+    ap.add_argument("--no-config1", action="store_true")
+    ap.add_argument("--mmq-shapes", default="all", help="'all' (config 4) or 'headline'")
     ap.add_argument("--model-layers", type=int, default=64)
     ap.add_argument("--model-layout", default="0x020D", help="Q4_K layout of the model pass")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -376,35 +490,58 @@ def main():
         log("copy calibration: 5 x 1 GiB device-to-device copies done")
         return
     layout = int(args.layout, 16)
-    n, k = 34816, 5120
-    ms_list = [int(v) for v in args.decode_m.split(",")]
-    if 1 not in ms_list:
-        ms_list = [1] + ms_list
-    dec, base = bench_decode(torch, ops, n, k, ms_list, args.steps, args.warmup, layout)
-    head = dec[1]
     mmq_layout = int(args.mmq_layout, 16)
-    mmq = None if args.no_mmq else bench_mmq(torch, ops, n, k, 512, max(20, args.steps // 8),
-                                              max(3, args.warmup // 4), mmq_layout)
-    q6 = None if args.no_q6 else bench_decode_q6(torch, ops, 5120, 17408, [1, 8], args.steps,
-                                                 args.warmup)
-    dbf16 = None if args.no_bf16 else bench_decode_bf16(torch, ops, n, k, args.steps, args.warmup)
-    pbf16 = None if (args.no_bf16 or args.no_mmq) else bench_prefill_bf16(
-        torch, ops, n, k, 512, max(20, args.steps // 8), max(3, args.warmup // 4))
+    n, k = 34816, 5120
+    ms_list = sorted({1, *[int(v) for v in args.decode_m.split(",")]})
+    clock = clock_probe(torch, ops)
+    peak_sclk = clock["int8_peak_tops_at_sclk"]
+    rooflines = {}
+    dec = bench_decode(torch, ops, "q4k", n, k, ms_list, args.steps, args.warmup, layout, 11,
+                       eager_m1=True)
+    head = dec[1]
+    for m, v in dec.items():
+        rooflines[f"config2_m{m}"] = v
+    if not args.no_config1:
+        c1 = bench_decode(torch, ops, "q4k", 5120, 5120, [1], args.steps, args.warmup, layout, 71,
+                          outliers=False)
+        rooflines["config1_m1"] = c1[1]
+    if not args.no_q6:
+        c3 = bench_decode(torch, ops, "q6k", 5120, 17408, [1, 8], args.steps, args.warmup,
+                          0x0241, 61, outliers=False)
+        for m, v in c3.items():
+            rooflines[f"config3_m{m}"] = v
+    if not args.no_mmq:
+        shapes = ([("q4k", 34816, 5120, [512])] if args.mmq_shapes == "headline" else
+                  [("q4k", 12288, 5120, [128, 512, 2048]), ("q4k", 34816, 5120, [128, 512, 2048]),
+                   ("q6k", 5120, 17408, [128, 512, 2048])])
+        mmq = bench_mmq(torch, ops, shapes, args.steps, args.warmup, mmq_layout, peak_sclk)
+        for key, v in mmq.items():
+            rooflines["config4_" + key] = v
+    if not args.no_bf16:
+        rooflines["decode_bf16_config2_m1"] = bench_decode_bf16(torch, ops, n, k, args.steps,
+                                                                args.warmup)
+        if not args.no_mmq:
+            rooflines["prefill_bf16_config4_m512"] = bench_prefill_bf16(
+                torch, ops, n, k, 512, args.steps, args.warmup)
     model = None if args.no_model else bench_model(
-        torch, ops, args.model_layers, int(args.model_layout, 16), 512, 3)
+        torch, ops, args.model_layers, int(args.model_layout, 16), 512, 3, peak_sclk)
+    if model:
+        rooflines["config5_decode_m1"] = model["decode_m1"]
+        rooflines["config5_prefill_m512"] = model["prefill_m512"]
     cpu = None
     if not args.no_cpu:
         _, blocks = make_weight(torch, ops, n, k, 11, layout)
         cpu = cpu_baseline(torch, blocks, n, k, 1, args.cpu_seconds)
     traffic = measured_traffic(layout)
+    rot_bytes = head["algorithmic_bytes"] * head["copies"]
     line = {
         "metric": METRIC,
-        "value": round(head["gbs"], 2),
+        "value": head["achieved"],
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": head["steps"],
+        "steps": head["rotations"],
         "warmup": args.warmup,
-        "ms_per_step": head["ms"],
+        "ms_per_step": round(rot_bytes / (head["achieved"] * 1e9) * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -412,23 +549,19 @@ def main():
         "data": "synthetic (seeded fp32 ~N(0,0.02) weights quantized to Q4_K on the GPU; "
                 "~N(0,1) activations with 1% channels x20 -> BF16 -> Q8)",
         "config": {"workload": "config 2: fused gate+up Q4_K x Q8 decode GEMV, N=34816, "
-                               "K=5120, M=1", "layout": f"{layout:#06x}",
-                   "mmq_layout": f"{mmq_layout:#06x}",
-                   "weight_copies_rotated": max(2, math.ceil(1.2e9 / q4k_bytes(n, k))),
-                   "timing": head["mode"]},
-        "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
+                               "K=5120, M=1; one step = one launch on each of "
+                               f"{head['copies']} rotated weight copies",
+                   "layout": f"{layout:#06x}", "mmq_layout": f"{mmq_layout:#06x}",
+                   "weight_copies_rotated": head["copies"], "launches_timed": head["launches"],
+                   "us_per_launch": head["us"], "timing": head["timing"]},
+        "roofline": {"bound": "hbm", "achieved": head["achieved"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": head["frac"],
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                                      "copy-calibrated)",
-                     "algorithmic_bytes": q4k_bytes(n, k) + k * 5 // 4 + n * 4},
-        "decode_m": {str(m): {"gbs": round(v["gbs"], 1), "us": round(v["ms"] * 1e3, 3),
-                              "frac_hbm": round(v["gbs"] / HBM_PEAK_GBS, 4)}
-                     for m, v in dec.items()},
-        "config3_q6k_decode": q6,
-        "mmq_m512": mmq,
-        "decode_bf16_m1": dbf16,
-        "prefill_bf16_m512": pbf16,
+                     "algorithmic_bytes": head["algorithmic_bytes"]},
+        "rooflines": rooflines,
+        "mfma_clock": clock,
         "config5_model_pass": model,
         "cpu_baseline": cpu,
     }

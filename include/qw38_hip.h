@@ -375,6 +375,13 @@ int qw38_prefill_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_
                      const float* h_mid, const uint16_t* gamma, float eps, float* next_h,
                      uint32_t tokens, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* Measurement aid with no reference counterpart: one wave per SIMD on every
+ * CU runs `iterations` x 4 independent v_mfma_i32_32x32x32_i8; ticks (device
+ * memory, 3 x uint64) receives the shader-clock cycles and the 100 MHz
+ * real-time ticks wave 0 spent in its loop; *blocks the grid size. Used by the
+ * bench to recompute the int8 MFMA dense peak at the measured sclk. */
+int qw38_mfma_clock_probe(uint32_t iterations, uint64_t* ticks, uint32_t* blocks, void* stream);
+
 /* Byte sizes of a tiled weight (cuda/decode_mmv.hpp:330-369 for 0x020D,
  * extended with this build's layouts). 0 for an unknown layout. */
 uint64_t qw38_code_bytes(uint16_t layout, uint32_t padded_n, uint32_t padded_k);

@@ -8,7 +8,8 @@ The arithmetic lives in ``oracle.c`` (plain C, built with -ffp-contract=off);
 this module wraps it with numpy. ``ref()`` loads ``_ref/libref_llama_q4k.so``,
 the reference's own pinned llama.cpp Q4_K header compiled in place, used to pin
 the oracle's quantizer. The header of ``oracle.c`` states how every function is
-pinned; the Q6_K quantizer is "parity unpinned" (no reference code exists).
+pinned; the Q6_K quantizer (no reference code or vectors exist) is pinned by
+exact-block round trips and closed-form properties of its last steps.
 """
 from __future__ import annotations
 

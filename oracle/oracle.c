@@ -39,9 +39,16 @@
  *                         and lossless round trip. 0x0240 (this build's plane
  *                         order) pinned by round trip + explicit coordinates.
  *   orc_quantize_q6k_*    llama.cpp quantize_row_q6_K_ref / make_qx_quants
- *                         (ggml-quants.c at e6ab7c1a4, not vendored in the
- *                         reference). PARITY UNPINNED: no reference code or
- *                         vectors exist; only invariants are tested.
+ *                         (ggml-quants.c at e6ab7c1a4, MIT, not vendored in the
+ *                         reference; no reference vectors exist). Pinned by
+ *                         the mathematics: blocks built exactly as
+ *                         d*sc*(q-32) (one sub-block at sc=-128) come back
+ *                         byte-exact; on random data every code is the clamped
+ *                         round-half-even nearest of x/(d*sc) (restated in
+ *                         numpy), the largest sub-block scale is -128, and the
+ *                         error is <= d|sc|/2 off the clamp. The perturbed-
+ *                         iscale least-squares search inside make_qx_quants is
+ *                         pinned only where its result is exact.
  *   orc_q6k_*ggml*        ggml block_q6_K byte order (ggml-common.h). Pinned by
  *                         round trip only.
  *   orc_q4k_q8_contract   tests/q4k_q8_test.cpp:121-131 (double closed form),
@@ -574,7 +581,7 @@ int orc_unpack_q4k_layout(uint16_t layout, const uint8_t* ci, const uint8_t* mi,
   return 0;
 }
 
-/* ---- Q6_K quantizer (GGML published algorithm; parity unpinned) --------- */
+/* ---- Q6_K quantizer (llama.cpp quantize_row_q6_K_ref, published algorithm) */
 #define Q6_GROUP_MAX_EPS 1e-15f
 static float fit_qx(int n, int nmax, const float* x, uint8_t* L) {
   float max = 0, amax = 0;

@@ -58,26 +58,39 @@ def summarize(path: str, match: str | None = None, top: int = 12) -> str:
     for (name, blocks), v in sorted(by.items(), key=lambda kv: -sum(kv[1]))[:top]:
         out.append(f"{_short(name):<72} {blocks:>7} {len(v):>6} {sum(v)/len(v):>9.3f} {min(v):>9.3f} "
                    f"{max(v):>9.3f} {100*sum(v)/tot:>6.1f}")
-    # counters, when present
+    # counters, when present: keyed by (kernel instantiation, grid) exactly
+    # like the timing rows above and printed in the same order, so two grids of
+    # one kernel can never swap their counter lines
     if "counters_collection" in names:
         cols = [r[1] for r in db.execute("pragma table_info(counters_collection)")]
-        kcol = "kernel_name" if "kernel_name" in cols else None
         vcol = "value" if "value" in cols else "counter_value"
         ncol = "counter_name" if "counter_name" in cols else "name"
-        if kcol:
-            q = f"select {kcol}, {ncol}, avg({vcol}), count(*) from (select {kcol}, {ncol}, dispatch_id, sum({vcol}) as {vcol} from counters_collection group by {kcol}, {ncol}, dispatch_id) group by {kcol}, {ncol}"
+        grid = None
+        if "grid_size" in cols and "workgroup_size" in cols:
+            grid = "grid_size / max(workgroup_size, 1)"
+        elif "grid_size_x" in cols and "workgroup_size_x" in cols:
+            grid = "grid_size_x / max(workgroup_size_x, 1)"
+        if "kernel_name" in cols and grid is not None:
+            q = (f"select kernel_name, blocks, {ncol}, avg(v), count(*) from ("
+                 f"select kernel_name, {grid} as blocks, {ncol}, dispatch_id, sum({vcol}) as v "
+                 f"from counters_collection group by kernel_name, blocks, {ncol}, dispatch_id) "
+                 f"group by kernel_name, blocks, {ncol}")
             agg = collections.defaultdict(dict)
-            for kname, cname, avg, cnt in db.execute(q):
+            for kname, blocks, cname, avg, cnt in db.execute(q):
                 if match and match not in kname:
                     continue
-                agg[kname][cname] = (avg, cnt)
+                agg[(kname, int(blocks))][cname] = (avg, cnt)
+            order = {key: -sum(v) for key, v in by.items()}
             if agg:
                 out.append("")
-                out.append("per-dispatch counter averages:")
-                for kname, cs in sorted(agg.items(), key=lambda kv: kv[0]):
+                out.append("per-dispatch counter averages (kernel, blocks):")
+                for key, cs in sorted(agg.items(), key=lambda kv: (order.get(kv[0], 0.0), kv[0][0])):
                     vals = "  ".join(f"{c}={a:.6g}" for c, (a, _) in sorted(cs.items()))
                     n = max(c for _, c in cs.values())
-                    out.append(f"  {_short(kname)} (dispatches={n}): {vals}")
+                    out.append(f"  {_short(key[0])} blocks={key[1]} (dispatches={n}): {vals}")
+        elif "kernel_name" in cols:
+            out.append("")
+            out.append("counters present but no grid column: " + ", ".join(cols))
     return "\n".join(out)
 
 

@@ -121,7 +121,8 @@ def test_q6k_small_shapes_and_dots(torch_gpu):
 
 
 @pytest.mark.parametrize("layout", [oracle.LAYOUT_Q4K_SEQ, oracle.LAYOUT_Q4K_W64], ids=["020D", "0240"])
-@pytest.mark.parametrize("n,k,m", [(12288, 5120, 128), (34816, 5120, 512), (12288, 5120, 2048)])
+@pytest.mark.parametrize("n,k,m", [(12288, 5120, 128), (12288, 5120, 512), (12288, 5120, 2048),
+                                   (34816, 5120, 128), (34816, 5120, 512), (34816, 5120, 2048)])
 def test_config4_mmq_row_sample(torch_gpu, n, k, m, layout):
     """MMQ at the config-4 shapes (the tile shape follows the cost model:
     128x32 at M=128, 256x128 with the tail split at M=512, 256x128 at 2048);
@@ -137,17 +138,50 @@ def test_config4_mmq_row_sample(torch_gpu, n, k, m, layout):
     _check(y[:, rows], ref, f"config4 N={n} M={m}")
 
 
-def test_config4_q6k_mmq_row_sample(torch_gpu):
+@pytest.mark.parametrize("m", [128, 512, 2048])
+def test_config4_q6k_mmq_row_sample(torch_gpu, m):
+    """Config-4 Q6_K down projection (5120x17408) at M = 128, 512, 2048."""
     torch = torch_gpu
     import qw38_amd.ops as ops
-    n, k, m = 5120, 17408, 512
-    w, wl = _fit_q6k(torch, ops, n, k, 501)
-    q, ob = _q8(torch, ops, silu_rows(m, k, 502))
+    n, k = 5120, 17408
+    w, wl = _fit_q6k(torch, ops, n, k, 501 + m)
+    q, ob = _q8(torch, ops, silu_rows(m, k, 502 + m))
     y = _project(torch, ops, w, q, m, n)
-    rows = np.sort(np.random.Generator(np.random.PCG64(5)).choice(n, 256, replace=False))
+    rows = np.sort(np.random.Generator(np.random.PCG64(5 + m)).choice(n, 128, replace=False))
     sub = oracle.Q6K(wl.q[rows], wl.sc[rows], wl.d[rows], len(rows), k)
     ref, _, _ = oracle.q6k_q8_contract(sub, ob)
-    _check(y[:, rows], ref, "config4 Q6_K M=512")
+    _check(y[:, rows], ref, f"config4 Q6_K M={m}")
+
+
+@pytest.mark.parametrize("layout", [oracle.LAYOUT_Q4K_SEQ, oracle.LAYOUT_Q4K_W64], ids=["020D", "0240"])
+@pytest.mark.parametrize("m", [512, 2048])
+def test_config4_mmq_outlier_rows(torch_gpu, m, layout):
+    """MMQ on config 2's activations (1% of channels x20): the per-token
+    power-of-two and FP16 hi+lo split of a*sum is the MMQ's one lossy step,
+    and wide ranges of a stress it. Gate+up N=34816, 384 sampled rows."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 34816, 5120
+    w, wl = _fit_q4k(torch, ops, n, k, 801 + m, layout)
+    q, ob = _q8(torch, ops, outlier_rows(m, k, 802 + m))
+    y = _project(torch, ops, w, q, m, n)
+    rows = np.sort(np.random.Generator(np.random.PCG64(80 + m)).choice(n, 384, replace=False))
+    sub = oracle.Q4K(wl.codes[rows], wl.meta[rows], len(rows), k)
+    ref, _, _ = oracle.q4k_q8_contract(sub, ob)
+    _check(y[:, rows], ref, f"config4 outlier rows N={n} M={m}")
+
+
+def test_config5_qkv_decode(torch_gpu):
+    """Config-5 QKV/gate projection (12288x5120, Q4_K on 0x020D) at M=1, the
+    full output against the oracle."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 12288, 5120
+    w, wl = _fit_q4k(torch, ops, n, k, 901, oracle.LAYOUT_Q4K_SEQ)
+    q, ob = _q8(torch, ops, normal((1, k), 902))
+    y = _project(torch, ops, w, q, 1, n)
+    ref, _, _ = oracle.q4k_q8_contract(wl, ob)
+    _check(y, ref, "config5 QKV M=1")
 
 
 @pytest.mark.parametrize("m", [1, 8, 128, 512])
@@ -215,3 +249,53 @@ def test_q6k_stream_unaligned_and_residual(torch_gpu, m):
     r = guards.cpu().numpy()
     assert np.array_equal(r[1:-1], (y.reshape(-1) + residual).astype(np.float32))
     assert r[0] == -12345.0 and r[-1] == -12345.0
+
+
+@pytest.mark.parametrize("m", [1, 512])
+def test_config5_pass_graph_replay(torch_gpu, m):
+    """The config-5 pass as the bench runs it (every projection of each layer
+    captured in one hipGraph; Q4_K on 0x020D, Q6_K on 0x0241), here over two
+    layers: after two replays, each projection of the last layer matches the
+    oracle on 128 sampled rows (all rows at M=1 for the small shapes)."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    shapes = [(12288, 5120, "q4k"), (5120, 6144, "q4k"), (34816, 5120, "q4k"), (5120, 17408, "q6k")]
+    layers = 2
+    ws, wl, qs, obs = [], [], [], []
+    for l in range(layers):
+        for j, (n, k, fmt) in enumerate(shapes):
+            seed = 1000 + 16 * l + j
+            if fmt == "q4k":
+                w, lw = _fit_q4k(torch, ops, n, k, seed, oracle.LAYOUT_Q4K_SEQ)
+            else:
+                w, lw = _fit_q6k(torch, ops, n, k, seed)
+            q, ob = _q8(torch, ops, normal((m, k), seed + 7919))
+            ws.append(w), wl.append(lw), qs.append(q), obs.append(ob)
+    outs = [torch.full((m, n), float("nan"), device="cuda") for n, _, _ in shapes]
+
+    def run_pass():
+        for l in range(layers):
+            for j in range(len(shapes)):
+                ops.q4k_q8_project(ws[l * len(shapes) + j], qs[l * len(shapes) + j], outs[j])
+
+    run_pass()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run_pass()
+    for o in outs:
+        o.fill_(float("nan"))
+    for _ in range(2):
+        g.replay()
+        torch.cuda.synchronize()
+    for j, (n, k, fmt) in enumerate(shapes):
+        i = (layers - 1) * len(shapes) + j
+        rows = np.sort(np.random.Generator(np.random.PCG64(j)).choice(n, 128, replace=False))
+        y = outs[j].cpu().numpy()[:, rows]
+        if fmt == "q4k":
+            sub = oracle.Q4K(wl[i].codes[rows], wl[i].meta[rows], len(rows), k)
+            ref, _, _ = oracle.q4k_q8_contract(sub, obs[i])
+        else:
+            sub = oracle.Q6K(wl[i].q[rows], wl[i].sc[rows], wl[i].d[rows], len(rows), k)
+            ref, _, _ = oracle.q6k_q8_contract(sub, obs[i])
+        _check(y, ref, f"config5 pass graph M={m} projection {j} ({n}x{k} {fmt})")

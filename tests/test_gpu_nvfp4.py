@@ -169,7 +169,8 @@ def test_paired_swiglu(torch_gpu):
         sw = torch.empty(m, n, dtype=torch.int16, device="cuda")
         ops.nvfp4_paired_swiglu(wa, wb, x, sw, m, work)
         gv, uv = g.cpu().numpy().astype(np.float64), u.cpu().numpy().astype(np.float64)
-        sig = np.where(gv >= 0, 1 / (1 + np.exp(-gv)), np.exp(gv) / (1 + np.exp(gv)))
+        e = np.exp(-np.abs(gv))  # never overflows; logistic(gv) on both signs
+        sig = np.where(gv >= 0, 1 / (1 + e), e / (1 + e))
         want = oracle.bf16_to_fp32(oracle.fp32_to_bf16((gv * sig * uv).astype(np.float32)))
         got = oracle.bf16_to_fp32(sw.cpu().numpy().view(np.uint16))
         assert np.all(np.isfinite(got))
@@ -206,7 +207,9 @@ def test_decode_single_paired_and_ranges(torch_gpu):
     ops.decode_mmv_paired(ops.nvfp4_decode_desc(wa, x, sw, ops.DECODE_SWIGLU_BF16),
                           ops.nvfp4_decode_desc(wb, x, None, ops.DECODE_SWIGLU_BF16))
     g, u = yav.astype(np.float64), o2.cpu().numpy().astype(np.float64)
-    want = oracle.bf16_to_fp32(oracle.fp32_to_bf16((g / (1 + np.exp(-g)) * u).astype(np.float32)))
+    e = np.exp(-np.abs(g))
+    sig = np.where(g >= 0, 1 / (1 + e), e / (1 + e))
+    want = oracle.bf16_to_fp32(oracle.fp32_to_bf16((g * sig * u).astype(np.float32)))
     got = oracle.bf16_to_fp32(sw.cpu().numpy().view(np.uint16))
     assert np.all(np.abs(got - want) <= .008 * np.abs(want) + .001)
     # ranged launches reject NVFP4 before any write (tests/nvfp4_test.cpp:236-244)

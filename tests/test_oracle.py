@@ -252,7 +252,80 @@ def test_q6k_fitter_invariants():
     err = np.abs(q.dequantize() - x)
     assert err.max() < 0.01 and err.mean() < 1e-3
     z = oracle.quantize_q6k(np.zeros((1, 256), np.float32))
-    assert np.all(z.d == 0) and np.all(z.sc == 0)
+    assert np.all(z.d == 0) and np.all(z.sc == 0) and np.all(z.q == 0)
+
+
+# ---- Q6_K fitter pins ------------------------------------------------------
+# The fitter restates llama.cpp quantize_row_q6_K_ref at e6ab7c1a4 (MIT), which
+# the reference does not vendor (third_party/llama.cpp-q4k/README.md:27-54):
+# per 16-element sub-block, make_qx_quants(n=16, nmax=32, rmse_type=1,
+# weights x^2) picks the signed scale whose extreme element maps to -32
+# (iscale = -32/max, then 18 perturbed iscales -(32 + 0.1 i)/max refined by
+# weighted least squares); the block's largest-magnitude sub-block scale maps to
+# -128 (iscale = -128/max_scale, d = fp16(1/iscale)); sc = min(127,
+# nearest(iscale * scale)); finally q = clamp(nearest(x / (d sc)), -32, 31) + 32.
+# nearest() rounds half to even (the 1.5 * 2^23 bias trick). The checks below
+# pin each step with a property a plausible mistake breaks.
+
+
+def _fp16_bits_to_f32(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def _exact_q6k_blocks(nblocks, seed):
+    """Blocks that are exactly d * sc_j * (q - 32): d a normal fp16, sc_j
+    nonzero with exactly one sub-block at -128 (the largest magnitude), every
+    sub-block holding a q = 0 element (its extreme value, -32 d sc_j)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    d = rng.integers(0x1000, 0x2400, size=nblocks).astype(np.uint16)
+    sc = rng.integers(-127, 128, size=(nblocks, 16))
+    sc[sc == 0] = 1
+    sc[np.arange(nblocks), rng.integers(0, 16, size=nblocks)] = -128
+    q = rng.integers(1, 64, size=(nblocks, 16, 16))
+    q[np.arange(nblocks)[:, None], np.arange(16)[None, :], rng.integers(0, 16, size=(nblocks, 16))] = 0
+    dd = _fp16_bits_to_f32(d)[:, None] * sc.astype(np.float32)  # exact: 11-bit x 8-bit
+    x = (dd[:, :, None] * (q - 32).astype(np.float32)).astype(np.float32)  # exact
+    return x.reshape(nblocks, 256), d, sc.astype(np.int8), q.reshape(nblocks, 256).astype(np.uint8)
+
+
+def test_q6k_fitter_recovers_exact_blocks():
+    """A block built exactly from (d, sc, q) comes back byte-exact: pins the
+    sign convention (extreme -> -32), the -128 mapping of the largest scale,
+    the fp16 rounding of d, the sc rounding and the final code mapping
+    (an off-by-one in the -32 offset or a dropped clamp fails here)."""
+    x, d, sc, q = _exact_q6k_blocks(512, 77)
+    got = oracle.quantize_q6k(x.reshape(-1, 256))
+    assert np.array_equal(got.d.reshape(-1), d)
+    assert np.array_equal(got.sc.reshape(-1, 16), sc)
+    assert np.array_equal(got.q.reshape(-1, 256), q)
+    assert np.array_equal(got.dequantize().astype(np.float32).reshape(-1, 256), x)
+
+
+def test_q6k_fitter_final_step_and_scale_map():
+    """On random N(0, 0.02) rows: every code is the clamped round-half-even
+    nearest of x / (d sc) (llama.cpp's last pass), restated here in float32
+    numpy; the largest-magnitude sub-block scale of each block is -128; and the
+    per-sub-block reconstruction error is at most d |sc| / 2 except where the
+    clamp at +31 applies."""
+    x = normal((64, 1024), 9, 0.02).reshape(-1, 256)
+    w = oracle.quantize_q6k(x)
+    d = _fp16_bits_to_f32(w.d.reshape(-1))
+    sc = w.sc.reshape(-1, 16).astype(np.float32)
+    q = w.q.reshape(-1, 16, 16).astype(np.int32)
+    dd = (d[:, None] * sc).astype(np.float32)
+    xs = x.reshape(-1, 16, 16)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        l = np.rint((xs / dd[:, :, None]).astype(np.float32))
+    expect = np.clip(l, -32, 31) + 32
+    live = dd != 0
+    assert np.array_equal(q[live], expect[live].astype(np.int32))
+    assert np.all(np.abs(w.sc.reshape(-1, 16).astype(np.int32)).max(axis=1) == 128)
+    assert np.all(w.sc.reshape(-1, 16).min(axis=1) == -128)
+    rec = dd[:, :, None] * (q - 32).astype(np.float32)
+    err = np.abs(rec - xs)
+    unclamped = (l > -32.5) & (l < 31.5)
+    tol = np.abs(dd)[:, :, None] / 2 * (1 + 2 ** -20)
+    assert np.all((err <= tol) | ~unclamped)
 
 
 def test_linearity_of_contraction_in_activation_scale():
