@@ -108,6 +108,21 @@ int qw38_q4k_q8_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_w
                     uint32_t m, void* workspace, uint64_t workspace_bytes, void* stream,
                     int* submitted, int* pending_failure);
 
+/* No counterpart in the reference: an allocation-free qw38_q4k_q8_mlp for
+ * callers that cannot allocate or pass device memory (code under HIP graph
+ * capture, tight serving loops). Same operands, semantics and errors as
+ * qw38_q4k_q8_mlp, but the workspace is a static device array of the library
+ * (qw38_q8_mlp_static_scratch_bytes(), held on each GPU until the process
+ * ends), so m <= QW38_Q8_MLP_STATIC_MAX_TOKENS; larger m is rejected with
+ * QW38_INVALID_ARGUMENT before any launch. Every call on one GPU shares that
+ * GPU's scratch: calls that overlap on one GPU (two streams, two threads)
+ * race. The failure flag is cleared by a kernel on each call. */
+#define QW38_Q8_MLP_STATIC_MAX_TOKENS 64u
+uint64_t qw38_q8_mlp_static_scratch_bytes(void);
+int qw38_q4k_q8_mlp_static(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
+                           const float* residual, const uint16_t* gamma, float eps, float* output,
+                           uint32_t m, void* stream, int* submitted, int* pending_failure);
+
 /* Replaces launch_hidden_rms_q8 (cuda/activation.hpp:11-14,
  * cuda/activation.cu:536-548): zero-centred RMS over hidden 5120 ->
  * BF16 -> Q8 pack. codes [m][5120], scales/sums [m][160]. */

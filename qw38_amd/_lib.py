@@ -86,6 +86,9 @@ SIGNATURES = {
     "qw38_q8_mlp_workspace_bytes": (_U64, [_U32]),
     "qw38_q4k_q8_mlp": (_I, [_P(Weight), _P(Weight), _P(Weight), _V, _V, _F, _V, _U32, _V, _U64,
                              _V, _P(_I), _V]),
+    "qw38_q8_mlp_static_scratch_bytes": (_U64, []),
+    "qw38_q4k_q8_mlp_static": (_I, [_P(Weight), _P(Weight), _P(Weight), _V, _V, _F, _V, _U32, _V,
+                                    _P(_I), _V]),
     "qw38_hidden_rms_q8": (_I, [_V, _V, _F, _U32, _V, _V, _V, _V, _V]),
     "qw38_swiglu_q8": (_I, [_V, _V, _U32, _U32, _V, _V, _V, _V, _V]),
     "qw38_q8_group_dots": (_I, [_P(Weight), _P(Q8Input), _V, _U64, _V]),

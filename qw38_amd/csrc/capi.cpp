@@ -11,6 +11,7 @@
 #include <cstring>
 #include <initializer_list>
 #include <limits>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -609,10 +610,17 @@ uint64_t qw38_q8_mlp_workspace_bytes(uint32_t m) {
   return uint64_t(m) * (17408 + 17408 / 32 * 8 + 2 * 17408 * 4) + 4;
 }
 
-int qw38_q4k_q8_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
-                    const float* residual, const uint16_t* gamma, float eps, float* output,
-                    uint32_t m, void* workspace, uint64_t workspace_bytes, void* stream,
-                    int* submitted, int* pending_failure) {
+}  // extern "C"
+
+namespace {
+// Q8 MLP body shared by qw38_q4k_q8_mlp (caller workspace) and
+// qw38_q4k_q8_mlp_static (the library's static scratch, own_workspace): the
+// workspace of the static variant is private to the library, so it is left
+// out of the caller-operand residency and aliasing checks.
+int mlp_run(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
+            const float* residual, const uint16_t* gamma, float eps, float* output, uint32_t m,
+            void* workspace, uint64_t workspace_bytes, void* stream, int* submitted,
+            int* pending_failure, bool own_workspace) {
   constexpr const char* op = "q8.mlp";
   if (submitted) *submitted = 0;
   if (!gate || !up || !down || !submitted) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
@@ -644,7 +652,7 @@ int qw38_q4k_q8_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_w
                          {residual, uint64_t(m) * 5120 * 4, 4},
                          {gamma, 5120 * 2, 2},
                          {output, uint64_t(m) * 5120 * 4, 4},
-                         {workspace, workspace_bytes, 4},
+                         {workspace, own_workspace ? 0 : workspace_bytes, 4},
                          {pending_failure, pending_failure ? 4u : 0u, 4}},
                         device, op))
     return st;
@@ -681,6 +689,74 @@ int qw38_q4k_q8_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_w
   if (bad)
     return fail(QW38_INVALID_ARGUMENT, "q8.producer", "nonfinite producer or invalid Q8 scale");
   return ok();
+}
+}  // namespace
+
+extern "C" {
+
+int qw38_q4k_q8_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
+                    const float* residual, const uint16_t* gamma, float eps, float* output,
+                    uint32_t m, void* workspace, uint64_t workspace_bytes, void* stream,
+                    int* submitted, int* pending_failure) {
+  return mlp_run(gate, up, down, residual, gamma, eps, output, m, workspace, workspace_bytes,
+                 stream, submitted, pending_failure, false);
+}
+
+}  // extern "C"
+
+// ---- allocation-free Q8 MLP --------------------------------------------------
+// The workspace of qw38_q4k_q8_mlp_static lives in this file-scope device array
+// (each GPU holds its own copy, at its own address, until the process ends).
+// In host code `scratch` only names the symbol: its device address on the
+// current device comes from hipGetSymbolAddress, looked up once per device and
+// kept in g_scratch_ptr; kernels and copies only ever see that address.
+namespace {
+constexpr uint32_t kStaticMlpMaxTokens = QW38_Q8_MLP_STATIC_MAX_TOKENS;
+constexpr uint64_t kStaticMlpBytes =
+    uint64_t(kStaticMlpMaxTokens) * (17408 + 17408 / 32 * 8 + 2 * 17408 * 4) + 4;
+__device__ __align__(256) uint8_t scratch[kStaticMlpBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+// Device address of this device's scratch (device must be current).
+int scratch_address(int device, void** out) {
+  if (device < 0 || device >= 64) return fail(QW38_INVALID_ARGUMENT, "q8.mlp_static", "device index");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "q8.mlp_static.symbol");
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return QW38_OK;
+}
+}  // namespace
+
+extern "C" {
+
+uint64_t qw38_q8_mlp_static_scratch_bytes(void) { return kStaticMlpBytes; }
+
+int qw38_q4k_q8_mlp_static(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,
+                           const float* residual, const uint16_t* gamma, float eps, float* output,
+                           uint32_t m, void* stream, int* submitted, int* pending_failure) {
+  constexpr const char* op = "q8.mlp_static";
+  if (submitted) *submitted = 0;
+  if (!submitted) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
+  if (m > kStaticMlpMaxTokens)
+    return fail(QW38_INVALID_ARGUMENT, op,
+                "m exceeds the static scratch capacity (QW38_Q8_MLP_STATIC_MAX_TOKENS = 64)");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  void* ws = nullptr;
+  {
+    DeviceScope scope(device);
+    if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+    if (int st = scratch_address(device, &ws)) return st;
+  }
+  return mlp_run(gate, up, down, residual, gamma, eps, output, m, ws,
+                 qw38_q8_mlp_workspace_bytes(m), stream, submitted, pending_failure, true);
 }
 
 int qw38_hidden_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
