@@ -34,6 +34,14 @@ COMMON = [
 ]
 
 
+# Per-source extra hipcc flags. The batched decode kernel keeps its MFMA results
+# in VGPRs (no v_accvgpr_read per result); the 512-register MMQ tiles keep the
+# compiler's AGPR choice.
+EXTRA = {
+    "q4k_decode_mfma.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"],
+}
+
+
 def sources():
     srcs = sorted(glob.glob(os.path.join(PKG, "csrc", "*.hip")))
     srcs += sorted(glob.glob(os.path.join(PKG, "csrc", "*.cpp")))
@@ -43,7 +51,7 @@ def sources():
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)

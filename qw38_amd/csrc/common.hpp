@@ -208,6 +208,13 @@ hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,
 // Q6_K (0x0241) streaming GEMV for M <= 2; hipErrorNotSupported otherwise.
 hipError_t launch_q6k_stream(const WeightView& w, const Q8View& x, float* out,
                              const float* residual, hipStream_t s);
+// Q4_K 0x020D at M = 2..8 on int8 MFMA; hipErrorNotSupported when the shape,
+// alignment or LDS budget does not fit (the caller then uses the dot4 kernels).
+hipError_t launch_q4k_mfma_decode(const WeightView& w, const Q8View& x, float* out,
+                                  const float* residual, hipStream_t s);
+// Q6_K 0x0241 at M = 3..8 on int8 MFMA; hipErrorNotSupported otherwise.
+hipError_t launch_q6k_mfma_decode(const WeightView& w, const Q8View& x, float* out,
+                                  const float* residual, hipStream_t s);
 hipError_t launch_gemv_w64(const WeightView& w, const Q8View& x, float* out,
                            const float* residual, hipStream_t s);
 hipError_t launch_mmq(const WeightView& w, const Q8View& x, float* out,

@@ -349,6 +349,10 @@ hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out, const f
     const char* e = std::getenv("QW38_GEMV_STREAM_BLOCKS");
     return e ? std::atoi(e) : 0;
   }();
+  {
+    const hipError_t e = launch_q4k_mfma_decode(w, x, out, residual, s);
+    if (e != hipErrorNotSupported) return e;
+  }
   if (env_stream) {
     const hipError_t e = launch_gemv_stream(w, x, out, residual, s, env_ws, uint32_t(env_blocks));
     if (e != hipErrorNotSupported) return e;
@@ -363,7 +367,9 @@ hipError_t launch_gemv(const WeightView& w, const Q8View& x, float* out, const f
     case QW38_LAYOUT_Q4K_WAVE64:
       return launch_gemv_w64(w, x, out, residual, s);
     case QW38_LAYOUT_Q6K_WAVE64: {
-      const hipError_t e = launch_q6k_stream(w, x, out, residual, s);
+      hipError_t e = launch_q6k_mfma_decode(w, x, out, residual, s);
+      if (e != hipErrorNotSupported) return e;
+      e = launch_q6k_stream(w, x, out, residual, s);
       if (e != hipErrorNotSupported) return e;
     }
       // Q6_K layout requires 16-byte aligned codes (validated by the caller).

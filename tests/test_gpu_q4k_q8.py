@@ -135,8 +135,10 @@ def test_project_m_sweep(torch_gpu, weights, layout):
             mmq_prev[m] = y
         else:
             # Batched GEMV: token 0 equals the same kernel family's first result
-            # bitwise (M <= 2 streams the strip linearly; 3..8 reuse 8 rows).
-            fam = 0 if m <= 2 else 1
+            # bitwise. 0x020D: M=1 streams the strip linearly, M=2..8 run the
+            # int8-MFMA kernel (T=4 and T=8 share one operation order per
+            # (row, token)); 0x0240: M <= 2 and 3..8.
+            fam = 0 if (m == 1 if layout == oracle.LAYOUT_Q4K_SEQ else m <= 2) else 1
             if fam not in gemv_first:
                 gemv_first[fam] = y[0].copy()
             assert np.array_equal(gemv_first[fam].view(np.uint32), y[0].view(np.uint32))
