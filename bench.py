@@ -468,6 +468,9 @@ def main():
     ap.add_argument("--mmq-shapes", default="all", help="'all' (config 4) or 'headline'")
     ap.add_argument("--model-layers", type=int, default=64)
     ap.add_argument("--model-layout", default="0x020D", help="Q4_K layout of the model pass")
+    ap.add_argument("--eager-leg", default=None, metavar="FMT:N:K:M:CALLS",
+                    help="only run CALLS eager projections of one shape (q4k on --layout, q6k on "
+                         "0x0241) over 12 rotated weight copies, for rocprofv3 traces and counters")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (counter scale for rocprof --pmc)")
     args = ap.parse_args()
@@ -491,6 +494,18 @@ def main():
         return
     layout = int(args.layout, 16)
     mmq_layout = int(args.mmq_layout, 16)
+    if args.eager_leg:
+        fmt, n_, k_, m_, calls = args.eager_leg.split(":")
+        n_, k_, m_, calls = int(n_), int(k_), int(m_), int(calls)
+        w, _ = make_any_weight(torch, ops, fmt, n_, k_, 11, layout if fmt == "q4k" else 0x0241)
+        ws = [w] + [clone_weight(ops, w) for _ in range(11)]
+        q, _ = make_q8(torch, ops, m_, k_, 5, outliers=(fmt == "q4k"))
+        out = torch.empty(m_, n_, device="cuda")
+        for i in range(calls):
+            ops.q4k_q8_project(ws[i % len(ws)], q, out)
+        torch.cuda.synchronize()
+        log(f"eager leg {args.eager_leg}: done")
+        return
     n, k = 34816, 5120
     ms_list = sorted({1, *[int(v) for v in args.decode_m.split(",")]})
     clock = clock_probe(torch, ops)

@@ -397,6 +397,12 @@ int qw38_prefill_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_
  * bench to recompute the int8 MFMA dense peak at the measured sclk. */
 int qw38_mfma_clock_probe(uint32_t iterations, uint64_t* ticks, uint32_t* blocks, void* stream);
 
+/* Replaces qw38::runtime::profiling::enabled (src/runtime/profiling.hpp:9-10):
+ * turns the calling thread's roctx ranges ("qw38:op name=q4k_project ...",
+ * the reference's NVTX strings) on or off. QW38_PROFILE=1 in the environment
+ * turns them on for every thread. */
+void qw38_set_profiling(int enabled);
+
 /* Byte sizes of a tiled weight (cuda/decode_mmv.hpp:330-369 for 0x020D,
  * extended with this build's layouts). 0 for an unknown layout. */
 uint64_t qw38_code_bytes(uint16_t layout, uint32_t padded_n, uint32_t padded_k);

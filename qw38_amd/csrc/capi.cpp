@@ -14,6 +14,7 @@
 #include <mutex>
 
 #include "common.hpp"
+#include "profiling.hpp"
 
 namespace {
 using namespace qw38hip;
@@ -403,6 +404,9 @@ int decode_launch(const DDesc& a, const DDesc* b, void* stream, const char* op) 
   if (int st = stream_device(stream, &device, op)) return st;
   DeviceScope scope(device);
   if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  profiling::ScopedRange range(
+      "qw38:op name=decode_mmv m=%u n=%u k=%u paired=%u layout=%u epilogue=%u compute=scalar_fp32", 1u,
+      unsigned(a.n), unsigned(a.k), unsigned(b != nullptr), unsigned(a.layout), unsigned(a.epilogue));
   if (a.layout == QW38_DECODE_LAYOUT_FP8_V1) {  // cuda/fp8.cu:184-194
     if (b) return fail(QW38_INVALID_ARGUMENT, op, "FP8 paired SwiGLU is not supported");
     const hipError_t e = launch_fp8_gemv(
@@ -449,7 +453,10 @@ int prefill_weight(const qw38_weight& w, uint32_t tokens, const char* op) {
 }
 
 hipError_t project(const qw38_weight& w, const Q8View& x, float* out, const float* residual,
-                   hipStream_t s) {
+                   hipStream_t s, const char* role = "projection") {
+  profiling::ScopedRange range("qw38:op name=q4k_project m=%u n=%u k=%u role=%s residual=%u compute=%s",
+                               unsigned(x.m), unsigned(w.n), unsigned(w.k), role,
+                               unsigned(residual != nullptr), x.m <= 8 ? "integer_dot4_mfma" : "mfma_f16_exact");
   if (x.m <= 8) return launch_gemv(view(w), x, out, residual, s);
   return launch_mmq(view(w), x, out, residual, s);
 }
@@ -535,6 +542,8 @@ int qw38_last_error(int* hip_status, char* operation, size_t operation_cap, char
   return g_err.status;
 }
 
+void qw38_set_profiling(int enabled) { profiling::enabled = enabled != 0; }
+
 uint64_t qw38_code_bytes(uint16_t layout, uint32_t padded_n, uint32_t padded_k) {
   const uint64_t nk = uint64_t(padded_n) * padded_k;
   switch (layout) {
@@ -571,6 +580,7 @@ int qw38_pack_q8(const uint16_t* input, uint64_t input_len, const qw38_q8_input*
     return st;
   DeviceScope scope(device);
   if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  profiling::ScopedRange range("qw38:op name=q8_pack m=%u n=%u k=%u", unsigned(x.m), unsigned(x.k), 1u);
   hipError_t e = launch_pack_q8(input, x.m, x.k, x.padded_k, x.codes, x.scales, x.sums, failure,
                                 static_cast<hipStream_t>(stream));
   return e == hipSuccess ? ok() : hip_fail(e, op);
@@ -670,21 +680,30 @@ int mlp_run(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* d
     return hip_fail(e, what);
   };
   hipError_t e = hipSuccess;
-  if (!pending_failure && (e = launch_fill_zero_i32(flag, 1, s)) != hipSuccess)
-    return bail(e, "q8.clear_failure");
+  if (!pending_failure) {
+    profiling::ScopedRange range("qw38:op name=q8_clear_failure bytes=4");
+    if ((e = launch_fill_zero_i32(flag, 1, s)) != hipSuccess) return bail(e, "q8.clear_failure");
+  }
   if ((e = launch_rms_q8(residual, gamma, eps, m, codes, scales, sums, flag, s)) != hipSuccess)
     return bail(e, "q8.rms_pack");
   Q8View x{codes, scales, sums, m, 5120, 5120};
-  if ((e = project(*gate, x, g, nullptr, s)) != hipSuccess) return bail(e, "q4k_q8.project");
-  if ((e = project(*up, x, u, nullptr, s)) != hipSuccess) return bail(e, "q4k_q8.project");
-  if ((e = launch_swiglu_q8(g, u, m, 17408, codes, scales, sums, flag, s)) != hipSuccess)
-    return bail(e, "q8.swiglu_pack");
+  if ((e = project(*gate, x, g, nullptr, s, "gate")) != hipSuccess) return bail(e, "q4k_q8.project");
+  if ((e = project(*up, x, u, nullptr, s, "up")) != hipSuccess) return bail(e, "q4k_q8.project");
+  {
+    profiling::ScopedRange range("qw38:op name=swiglu_q8_pack m=%u n=%u k=%u", unsigned(m), 17408u, 1u);
+    if ((e = launch_swiglu_q8(g, u, m, 17408, codes, scales, sums, flag, s)) != hipSuccess)
+      return bail(e, "q8.swiglu_pack");
+  }
   x = Q8View{codes, scales, sums, m, 17408, 17408};
-  if ((e = project(*down, x, output, residual, s)) != hipSuccess) return bail(e, "q4k_q8.project");
+  if ((e = project(*down, x, output, residual, s, "down")) != hipSuccess)
+    return bail(e, "q4k_q8.project");
   if (pending_failure) return ok();
   int bad = 0;
-  if ((e = hipMemcpyAsync(&bad, flag, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
-    return bail(e, "q8.failure");
+  {
+    profiling::ScopedRange range("qw38:op name=q8_failure_readback bytes=4");
+    if ((e = hipMemcpyAsync(&bad, flag, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+      return bail(e, "q8.failure");
+  }
   if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "stream.sync");
   if (bad)
     return fail(QW38_INVALID_ARGUMENT, "q8.producer", "nonfinite producer or invalid Q8 scale");
