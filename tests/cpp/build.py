@@ -9,7 +9,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-TESTS = ("qw38_api_test", "qw38_artifact_test")
+TESTS = ("qw38_api_test", "qw38_artifact_test", "qw38_runtime_test")
 
 
 def build_one(name: str) -> str:
