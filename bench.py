@@ -302,6 +302,62 @@ def bench_mmq(torch, ops, shapes, steps, warmup, layout, peak_sclk, seed=21):
     return res
 
 
+def bench_mlp(torch, ops, layouts, steps, warmup, peak_sclk, seed=500):
+    """The whole Q8 MLP (q4k_q8_mlp: RMS->Q8, gate+up, SwiGLU->Q8, down +
+    residual; Q4_K gate/up 17408x5120, Q6_K down 5120x17408) at M=1 on the
+    decode layout and M=512 on the MMQ layout, captured in a hipGraph (with
+    the device failure flag, as a captured decode token runs it). Beside it
+    the unfused chain of the same stages as separate launches (two FP32
+    [m][17408] slabs and a standalone SwiGLU->Q8 pack); both end in the same
+    bits."""
+    res = {}
+    for m, layout in ((1, layouts[0]), (512, layouts[1])):
+        gate, _ = make_any_weight(torch, ops, "q4k", 17408, 5120, seed, layout)
+        up, _ = make_any_weight(torch, ops, "q4k", 17408, 5120, seed + 1, layout)
+        down, _ = make_any_weight(torch, ops, "q6k", 5120, 17408, seed + 2, 0x0241)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed + 3)
+        resid = torch.randn(m, 5120, generator=g, device="cuda")
+        gamma = (0.1 * torch.randn(5120, generator=g, device="cuda")).to(torch.bfloat16).view(torch.int16)
+        ws = torch.zeros(ops.q8_mlp_workspace_bytes(m), dtype=torch.uint8, device="cuda")
+        flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+        out = torch.empty(m, 5120, device="cuda")
+        ms_f, launches, _, mode = time_launches(
+            torch, lambda i: ops.q4k_q8_mlp(gate, up, down, resid, gamma, 1e-6, out, m, ws,
+                                            pending_failure=flag), 1, steps, warmup)
+        fused_out = out.clone()
+        qx = ops.Q8Input.empty(m, 5120)
+        qh = ops.Q8Input.empty(m, 17408)
+        gs = torch.empty(m, 17408, device="cuda")
+        us = torch.empty(m, 17408, device="cuda")
+        out2 = torch.empty(m, 5120, device="cuda")
+
+        def chain(_i):
+            ops.hidden_rms_q8(resid, gamma, 1e-6, m, qx, flag)
+            ops.q4k_q8_project(gate, qx, gs)
+            ops.q4k_q8_project(up, qx, us)
+            ops.swiglu_q8(gs, us, m, 17408, qh, flag)
+            ops.q4k_q8_project(down, qh, out2, residual=resid)
+
+        ms_c, _, _, _ = time_launches(torch, chain, 1, steps, warmup)
+        torch.cuda.synchronize()
+        same = bool(torch.equal(fused_out, out2))
+        nops = 2.0 * m * 5120 * (3 * 17408)
+        nbytes = 2 * q4k_bytes(17408, 5120) + weight_bytes("q6k", 5120, 17408)
+        key = f"mlp_m{m}"
+        res[key] = {"us": round(ms_f * 1e3, 2), "unfused_chain_us": round(ms_c * 1e3, 2),
+                    "layout": f"{layout:#06x}", "down": "q6k 0x0241", "launches": launches,
+                    "timing": mode, "equals_unfused": same}
+        if m == 1:
+            res[key]["weight_gbs"] = round(nbytes / (ms_f * 1e-3) / 1e9, 1)
+        else:
+            res[key]["tops"] = round(nops / (ms_f * 1e-3) / 1e12, 1)
+            res[key]["frac_int8_peak_at_sclk"] = round(nops / (ms_f * 1e-3) / 1e12 / peak_sclk, 4)
+        log(f"mlp m={m}: {ms_f*1e3:.1f} us (unfused chain {ms_c*1e3:.1f} us), equal {same} ({mode})")
+        del gate, up, down, ws, gs, us
+    return res
+
+
 # Config 5: one layer of the synthetic 27B-class stack (out rows, in columns, format)
 MODEL_LAYER = (("qkv_gate", 12288, 5120, "q4k"), ("out", 5120, 6144, "q4k"),
                ("gate_up", 34816, 5120, "q4k"), ("down", 5120, 17408, "q6k"))
@@ -463,6 +519,7 @@ def main():
     ap.add_argument("--no-bf16", action="store_true", help="skip the BF16-activation decode_mmv")
     ap.add_argument("--decode-m", default="1,2,4,8", help="decode token counts to time")
     ap.add_argument("--no-model", action="store_true", help="skip the config-5 model pass")
+    ap.add_argument("--no-mlp", action="store_true", help="skip the whole-MLP leg")
     ap.add_argument("--no-q6", action="store_true", help="skip the config-3 Q6_K decode leg")
     ap.add_argument("--no-config1", action="store_true")
     ap.add_argument("--mmq-shapes", default="all", help="'all' (config 4) or 'headline'")
@@ -471,6 +528,9 @@ def main():
     ap.add_argument("--eager-leg", default=None, metavar="FMT:N:K:M:CALLS",
                     help="only run CALLS eager projections of one shape (q4k on --layout, q6k on "
                          "0x0241) over 12 rotated weight copies, for rocprofv3 traces and counters")
+    ap.add_argument("--mlp-leg", default=None, metavar="M:CALLS",
+                    help="only run CALLS eager whole-MLP calls at M tokens (Q4_K gate/up on --layout "
+                         "for M <= 8, else --mmq-layout; Q6_K down), for rocprofv3 traces")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (counter scale for rocprof --pmc)")
     args = ap.parse_args()
@@ -506,6 +566,21 @@ def main():
         torch.cuda.synchronize()
         log(f"eager leg {args.eager_leg}: done")
         return
+    if args.mlp_leg:
+        m_, calls = (int(v) for v in args.mlp_leg.split(":"))
+        lay = layout if m_ <= 8 else mmq_layout
+        gate, _ = make_any_weight(torch, ops, "q4k", 17408, 5120, 500, lay)
+        up, _ = make_any_weight(torch, ops, "q4k", 17408, 5120, 501, lay)
+        down, _ = make_any_weight(torch, ops, "q6k", 5120, 17408, 502, 0x0241)
+        resid = torch.randn(m_, 5120, device="cuda")
+        gamma = torch.zeros(5120, dtype=torch.int16, device="cuda")
+        ws = torch.zeros(ops.q8_mlp_workspace_bytes(m_), dtype=torch.uint8, device="cuda")
+        out = torch.empty(m_, 5120, device="cuda")
+        for _ in range(calls):
+            ops.q4k_q8_mlp(gate, up, down, resid, gamma, 1e-6, out, m_, ws)
+        torch.cuda.synchronize()
+        log(f"mlp leg {args.mlp_leg}: done")
+        return
     n, k = 34816, 5120
     ms_list = sorted({1, *[int(v) for v in args.decode_m.split(",")]})
     clock = clock_probe(torch, ops)
@@ -538,6 +613,8 @@ def main():
         if not args.no_mmq:
             rooflines["prefill_bf16_config4_m512"] = bench_prefill_bf16(
                 torch, ops, n, k, 512, args.steps, args.warmup)
+    mlp = None if args.no_mlp else bench_mlp(torch, ops, (layout, mmq_layout), args.steps,
+                                             args.warmup, peak_sclk)
     model = None if args.no_model else bench_model(
         torch, ops, args.model_layers, int(args.model_layout, 16), 512, 3, peak_sclk)
     if model:
@@ -578,6 +655,7 @@ def main():
         "rooflines": rooflines,
         "mfma_clock": clock,
         "config5_model_pass": model,
+        "mlp": mlp,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

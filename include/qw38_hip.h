@@ -94,6 +94,21 @@ int qw38_q4k_q8_project(const qw38_weight* weight, const qw38_q8_input* input,
                         float* output, uint64_t output_len, const float* residual,
                         uint64_t residual_len, void* stream);
 
+/* The gate + up half of q4k_q8_mlp (cuda/q4k_q8.cu:378-385: two
+ * q4k_q8_project calls, then the SwiGLU->Q8 producer of cuda/q4k_q8.cu:52-61)
+ * as ONE launch: output = Q8 pack of BF16(SiLU(gate x) * (up x)), written by
+ * the projection's epilogue (no FP32 [m][n] intermediates). Bit-identical to
+ * the unfused chain. gate/up: Q4_K (0x020D or 0x0240), same layout and
+ * geometry, n % 32 == 0; output: m x n Q8 operand; *failure is set to 1 on a
+ * nonfinite group (failure_len must be 1). m == 1 on layout 0x020D runs the
+ * streaming decode GEMV's arithmetic, every other case the MFMA MMQ's; each
+ * equals the unfused chain at the m where q4k_q8_project runs the same
+ * kernel family. q4k_q8_mlp uses it wherever it applies (m > 8, or m == 1 on
+ * 0x020D). No reference counterpart as an entry point. */
+int qw38_q4k_q8_gate_up_swiglu(const qw38_weight* gate, const qw38_weight* up,
+                               const qw38_q8_input* input, const qw38_q8_input* output,
+                               int* failure, uint64_t failure_len, void* stream);
+
 /* Replaces cuda::q8_mlp_workspace_bytes (cuda/q4k_q8.hpp:28-30). */
 uint64_t qw38_q8_mlp_workspace_bytes(uint32_t m);
 

@@ -83,6 +83,7 @@ SIGNATURES = {
     "qw38_last_error": (_I, [_P(_I), C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t]),
     "qw38_pack_q8": (_I, [_V, _U64, _P(Q8Input), _V, _U64, _V]),
     "qw38_q4k_q8_project": (_I, [_P(Weight), _P(Q8Input), _V, _U64, _V, _U64, _V]),
+    "qw38_q4k_q8_gate_up_swiglu": (_I, [_P(Weight), _P(Weight), _P(Q8Input), _P(Q8Input), _V, _U64, _V]),
     "qw38_q8_mlp_workspace_bytes": (_U64, [_U32]),
     "qw38_q4k_q8_mlp": (_I, [_P(Weight), _P(Weight), _P(Weight), _V, _V, _F, _V, _U32, _V, _U64,
                              _V, _P(_I), _V]),

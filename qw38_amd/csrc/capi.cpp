@@ -8,6 +8,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <initializer_list>
 #include <limits>
@@ -616,6 +617,49 @@ int qw38_q4k_q8_project(const qw38_weight* weight, const qw38_q8_input* input, f
   return e == hipSuccess ? ok() : hip_fail(e, "q4k_q8.project");
 }
 
+int qw38_q4k_q8_gate_up_swiglu(const qw38_weight* gate, const qw38_weight* up,
+                               const qw38_q8_input* input, const qw38_q8_input* output,
+                               int* failure, uint64_t failure_len, void* stream) {
+  constexpr const char* op = "q8.gate_up";
+  if (!gate || !up || !input || !output) return fail(QW38_INVALID_ARGUMENT, op, "null descriptor");
+  const qw38_q8_input& x = *input;
+  const qw38_q8_input& y = *output;
+  for (const qw38_weight* w : {gate, up})
+    if (int st = valid_weight(*w, "q8.weight")) return st;
+  if (gate->layout == QW38_LAYOUT_Q6K_WAVE64 || gate->layout != up->layout)
+    return fail(QW38_INVALID_ARGUMENT, "q8.weight", "gate/up must be Q4_K in one layout");
+  if (!valid_q8(x, QW38_PROJECT_MAX_TOKENS) || !valid_q8(y, QW38_PROJECT_MAX_TOKENS) ||
+      x.k != gate->k || up->k != gate->k || up->n != gate->n || gate->n % 32 != 0 ||
+      gate->n != gate->padded_n || y.m != x.m || y.k != gate->n || y.padded_k != gate->n ||
+      failure_len != 1 || !failure)
+    return fail(QW38_INVALID_ARGUMENT, op, "invalid geometry");
+  int device = 0;
+  if (int st = stream_device(stream, &device, op)) return st;
+  if (int st = distinct({{gate->codes, gate->codes_bytes, codes_alignment(*gate)},
+                         {gate->scales, gate->scales_bytes, scales_alignment(*gate)},
+                         {up->codes, up->codes_bytes, codes_alignment(*up)},
+                         {up->scales, up->scales_bytes, scales_alignment(*up)},
+                         {x.codes, x.codes_len, 4},
+                         {x.scales, x.scales_len * 4, 4},
+                         {x.sums, x.sums_len * 4, 4},
+                         {y.codes, y.codes_len, 4},
+                         {y.scales, y.scales_len * 4, 4},
+                         {y.sums, y.sums_len * 4, 4},
+                         {failure, 4, 4}},
+                        device, op))
+    return st;
+  DeviceScope scope(device);
+  if (scope.status != hipSuccess) return hip_fail(scope.status, op);
+  profiling::ScopedRange range("qw38:op name=q4k_gate_up_swiglu_q8 m=%u n=%u k=%u", unsigned(x.m),
+                               unsigned(2 * gate->n), unsigned(gate->k));
+  const Q8View xv{x.codes, x.scales, x.sums, x.m, x.k, x.padded_k};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = gemv_glu_applies(view(*gate), view(*up), x.m)
+                     ? launch_gemv_glu(view(*gate), view(*up), xv, y.codes, y.scales, y.sums, failure, s)
+                     : launch_mmq_glu(view(*gate), view(*up), xv, y.codes, y.scales, y.sums, failure, s);
+  return e == hipSuccess ? ok() : hip_fail(e, "q4k_q8.gate_up");
+}
+
 uint64_t qw38_q8_mlp_workspace_bytes(uint32_t m) {
   return uint64_t(m) * (17408 + 17408 / 32 * 8 + 2 * 17408 * 4) + 4;
 }
@@ -674,6 +718,19 @@ int mlp_run(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* d
   auto* g = reinterpret_cast<float*>(sums + size_t(m) * 544);
   auto* u = g + size_t(m) * 17408;
   int* flag = pending_failure ? pending_failure : reinterpret_cast<int*>(u + size_t(m) * 17408);
+  // Prefill (m > 8) runs gate + up as one fused MMQ launch whose epilogue
+  // writes the down operand's Q8 codes directly; its input operand then lives
+  // in the (unused) gate slab so it does not alias the codes being written.
+  // QW38_MLP_FUSED=0 selects the unfused chain (same bits; a tuning aid).
+  static const bool fused_env = [] {
+    const char* e = std::getenv("QW38_MLP_FUSED");
+    return !(e && std::atoi(e) == 0);
+  }();
+  const bool fused = fused_env && gate->layout == up->layout &&
+                     (m > 8 || gemv_glu_applies(view(*gate), view(*up), m));
+  int8_t* in_codes = fused ? reinterpret_cast<int8_t*>(g) : codes;
+  float* in_scales = fused ? reinterpret_cast<float*>(in_codes + size_t(m) * 5120) : scales;
+  int32_t* in_sums = fused ? reinterpret_cast<int32_t*>(in_scales + size_t(m) * 160) : sums;
   *submitted = 1;
   auto bail = [&](hipError_t e, const char* what) {
     if (!pending_failure) (void)hipStreamSynchronize(s);
@@ -684,12 +741,18 @@ int mlp_run(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* d
     profiling::ScopedRange range("qw38:op name=q8_clear_failure bytes=4");
     if ((e = launch_fill_zero_i32(flag, 1, s)) != hipSuccess) return bail(e, "q8.clear_failure");
   }
-  if ((e = launch_rms_q8(residual, gamma, eps, m, codes, scales, sums, flag, s)) != hipSuccess)
+  if ((e = launch_rms_q8(residual, gamma, eps, m, in_codes, in_scales, in_sums, flag, s)) != hipSuccess)
     return bail(e, "q8.rms_pack");
-  Q8View x{codes, scales, sums, m, 5120, 5120};
-  if ((e = project(*gate, x, g, nullptr, s, "gate")) != hipSuccess) return bail(e, "q4k_q8.project");
-  if ((e = project(*up, x, u, nullptr, s, "up")) != hipSuccess) return bail(e, "q4k_q8.project");
-  {
+  Q8View x{in_codes, in_scales, in_sums, m, 5120, 5120};
+  if (fused) {
+    profiling::ScopedRange range("qw38:op name=q4k_gate_up_swiglu_q8 m=%u n=%u k=%u", unsigned(m), 34816u,
+                                 5120u);
+    e = m > 8 ? launch_mmq_glu(view(*gate), view(*up), x, codes, scales, sums, flag, s)
+              : launch_gemv_glu(view(*gate), view(*up), x, codes, scales, sums, flag, s);
+    if (e != hipSuccess) return bail(e, "q4k_q8.gate_up");
+  } else {
+    if ((e = project(*gate, x, g, nullptr, s, "gate")) != hipSuccess) return bail(e, "q4k_q8.project");
+    if ((e = project(*up, x, u, nullptr, s, "up")) != hipSuccess) return bail(e, "q4k_q8.project");
     profiling::ScopedRange range("qw38:op name=swiglu_q8_pack m=%u n=%u k=%u", unsigned(m), 17408u, 1u);
     if ((e = launch_swiglu_q8(g, u, m, 17408, codes, scales, sums, flag, s)) != hipSuccess)
       return bail(e, "q8.swiglu_pack");

@@ -122,6 +122,45 @@ __device__ __forceinline__ float silu(float z) {
   return z * sg;
 }
 
+// Q8 MLP producer value (cuda/q4k_q8.cu:52-61): BF16(SiLU(g) * u) with the
+// plain g / (1 + e^-g) form, widened back to FP32; nonfinite g or u give NaN.
+__device__ __forceinline__ float swiglu_q8_value(float g, float u) {
+  float v = (g / (1.f + exp_cw(-g))) * u;
+  if (!isfinite(g) || !isfinite(u)) v = __uint_as_float(0x7fc00000u);
+  return bf16_to_f32(f32_to_bf16_rne(v));
+}
+
+// Q8 K32 group pack (cuda/q8_device.cuh:6-25): peak = max finite |x|,
+// a = peak == 0 ? 1 : RN(peak / 127), z = clamp(rint(RN(x / a)), -127, 127),
+// sum = sum z; a nonfinite group stores a = NaN, z = 0 and raises the flag.
+// One K32 group per 32-lane half of a wave64 (lane = threadIdx.x % 32; the
+// reductions stay inside the half). `active` false: the half takes part in
+// the shuffles but stores nothing.
+__device__ __forceinline__ void q8_group32(float x, int8_t* codes, float* scales,
+                                           int32_t* sums, size_t group, int* failure,
+                                           bool active = true) {
+  const unsigned lane = threadIdx.x & 31u;
+  const bool finite = isfinite(x);
+  float peak = finite ? fabsf(x) : 0.f;
+#pragma unroll
+  for (int off = 16; off; off >>= 1) peak = fmaxf(peak, __shfl_xor(peak, off, 32));
+  const uint64_t ballot = __ballot(finite);
+  const uint32_t half = uint32_t(ballot >> (threadIdx.x & 32u));
+  const float a = peak == 0.f ? 1.f : peak / 127.f;
+  const bool valid = half == 0xffffffffu && isfinite(a) && a > 0.f;
+  int z = 0;
+  if (valid) z = max(-127, min(127, int(rintf(x / a))));
+  if (active) codes[group * 32 + lane] = int8_t(z);
+  int sum = z;
+#pragma unroll
+  for (int off = 16; off; off >>= 1) sum += __shfl_xor(sum, off, 32);
+  if (active && lane == 0) {
+    scales[group] = valid ? a : __uint_as_float(0x7fc00000u);
+    sums[group] = sum;
+    if (!valid) *failure = 1;  // sticky flag, plain vector store
+  }
+}
+
 // Byte offsets of the 16-byte code word of (row, super-block kb, K32 group g)
 // and of the 16-byte metadata row of (row, kb).
 // 0x020D: tile row ((row/8)*kbs + kb)*8 + row%8; codes 128 B per tile row
@@ -219,6 +258,17 @@ hipError_t launch_gemv_w64(const WeightView& w, const Q8View& x, float* out,
                            const float* residual, hipStream_t s);
 hipError_t launch_mmq(const WeightView& w, const Q8View& x, float* out,
                       const float* residual, hipStream_t s);
+// Fused gate + up MMQ (same geometry, Q4_K): one launch whose epilogue applies
+// SwiGLU -> BF16 -> Q8 and writes the down projection's Q8 operand
+// (codes [m][n], scales / sums [m][n / 32]) without FP32 gate / up slabs.
+// Decode form of launch_mmq_glu (M = 1, layout 0x020D, n % 32 == 0): the
+// streaming GEMV's arithmetic; hipErrorNotSupported where it does not apply.
+bool gemv_glu_applies(const WeightView& gate, const WeightView& up, uint32_t m);
+hipError_t launch_gemv_glu(const WeightView& gate, const WeightView& up, const Q8View& x, int8_t* codes,
+                           float* scales, int32_t* sums, int* failure, hipStream_t s);
+hipError_t launch_mmq_glu(const WeightView& gate, const WeightView& up, const Q8View& x,
+                          int8_t* codes, float* scales, int32_t* sums, int* failure,
+                          hipStream_t s);
 hipError_t launch_prefill_bf16(const WeightView& a, const WeightView* b, const uint16_t* x,
                                uint32_t m, void* out, const float* residual, int epilogue,
                                hipStream_t s);

@@ -127,6 +127,105 @@ __device__ __forceinline__ void consume(const Tile& t, uint32_t kb, uint32_t g0,
   }
 }
 
+// K is cut into four quarters of whole tile pairs (the odd tail tile joins
+// the last); every row's result is 0 + p0 + p1 + p2 + p3 over the quarter
+// partials p_i, each reduced over the row's lanes (xor 1, 2, 32) first,
+// whatever number of waves splits K. So the WS = 1, 2, 4 kernels and the fused
+// gate + up kernel below give bitwise-identical rows.
+__device__ __forceinline__ uint32_t quarter_begin(uint32_t pairs, uint32_t i) {
+  return uint32_t(uint64_t(pairs) * i / 4);
+}
+
+// Streams quarter qi of one strip into part[MT] (zeroed here).
+template <uint16_t Layout, int MT, bool Fast>
+__device__ __forceinline__ void stream_quarter(const uint8_t* cstrip, const uint8_t* mstrip, uint32_t kbs,
+                                               uint32_t qi, uint32_t lane, const int8_t* sz,
+                                               const float2* sau, uint32_t groups, float part[MT]) {
+  const uint32_t h = lane >> 5;         // tile of the pair
+  const uint32_t j = lane & 3u;         // group pair 2j, 2j+1
+  const uint32_t g0 = 2 * j;
+  const bool hi = j >= 2;
+  const uint32_t sh = 16u * (j & 1u);   // bit offset of group g0 % 4
+  const uint32_t coff = lane * 32, moff = lane * 4;
+  const uint32_t pairs = kbs / 2;
+  const uint32_t q0 = quarter_begin(pairs, qi), q1 = quarter_begin(pairs, qi + 1);
+#pragma unroll
+  for (int t = 0; t < MT; ++t) part[t] = 0.f;
+  // Double-buffered tile pairs: the loads of pair q+1 are issued before pair
+  // q is consumed, so memory stays busy while this wave computes.
+  uint32_t q = q0;
+  const uint32_t nb = q1 - q0;
+  if (nb > 0) {
+    Tile A, B;
+    auto ld = [&](Tile& T, uint32_t qq) {
+      load_tile<Fast>(cstrip + size_t(qq) * 2048, mstrip + size_t(qq) * 256, coff, moff, T);
+    };
+    auto cs = [&](const Tile& T, uint32_t qq) {
+      consume<Layout, MT, Fast>(T, 2 * qq + h, g0, hi, sh, sz, sau, groups, part);
+    };
+    ld(A, q);
+    uint32_t b = 0;
+    for (; b + 2 <= nb; b += 2) {
+      ld(B, q + 1);
+      cs(A, q);
+      ++q;
+      if (b + 2 < nb) ld(A, q + 1);
+      cs(B, q);
+      ++q;
+    }
+    if (b < nb) {
+      cs(A, q);
+      ++q;
+    }
+  }
+  if ((kbs & 1u) && qi == 3) {  // odd last tile: only lanes of tile 0 hold data
+    const uint32_t kb = kbs - 1;
+    Tile T;
+    if (h == 0) {
+      load_tile<Fast>(cstrip + size_t(kb) * 1024, mstrip + size_t(kb) * 128, coff, moff, T);
+    } else {
+      for (int i = 0; i < 8; ++i) T.c[i] = 0;
+      T.m = 0;
+    }
+    float tp[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) tp[t] = 0.f;
+    consume<Layout, MT, Fast>(T, h == 0 ? kb : 0, g0, hi, sh, sz, sau, groups, tp);
+    if (h == 0) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) part[t] += tp[t];
+    }
+  }
+  // a row's partials live in lanes {4r..4r+3} and {32+4r..32+4r+3}
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    part[t] += __shfl_xor(part[t], 1);
+    part[t] += __shfl_xor(part[t], 2);
+    part[t] += __shfl_xor(part[t], 32);
+  }
+}
+
+// Stages the Q8 activations of MT tokens in LDS: codes and (a, a*sum).
+template <int MT, bool Fast, int NT>
+__device__ __forceinline__ void stage_q8(const int8_t* __restrict__ xc, const float* __restrict__ xa,
+                                         const int32_t* __restrict__ xs, uint32_t pk, int8_t* sz,
+                                         float2* sau) {
+  const uint32_t groups = pk / 32;
+  if constexpr (Fast) {
+    const uint4* src = reinterpret_cast<const uint4*>(xc);
+    uint4* dst = reinterpret_cast<uint4*>(sz);
+    for (uint32_t i = threadIdx.x; i < MT * pk / 16; i += NT) dst[i] = src[i];
+  } else {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(xc);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(sz);
+    for (uint32_t i = threadIdx.x; i < MT * pk / 4; i += NT) dst[i] = src[i];
+  }
+  for (uint32_t i = threadIdx.x; i < MT * groups; i += NT) {
+    const float a = xa[i];
+    sau[i] = make_float2(a, a * float(xs[i]));
+  }
+}
+
 template <uint16_t Layout, int MT, bool Fast, int WS>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n,
@@ -134,41 +233,17 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const float* __restrict__ xa, const int32_t* __restrict__ xs, uint32_t pk,
     float* __restrict__ out, const float* __restrict__ residual, uint32_t persistent) {
   extern __shared__ __align__(16) uint8_t smem[];
-  constexpr int SPB = 4 / WS;
+  constexpr int SPB = 4 / WS, QPW = 4 / WS;  // strips per block, quarters per wave
   const uint32_t groups = pk / 32;
   int8_t* sz = reinterpret_cast<int8_t*>(smem);
   float2* sau = reinterpret_cast<float2*>(smem + MT * pk);
   float* red = reinterpret_cast<float*>(smem + MT * pk + MT * groups * 8);
-
-  // ---- stage the Q8 activations once per block: codes and (a, a*sum) ----
-  if constexpr (Fast) {
-    const uint4* src = reinterpret_cast<const uint4*>(xc);
-    uint4* dst = reinterpret_cast<uint4*>(sz);
-    for (uint32_t i = threadIdx.x; i < MT * pk / 16; i += 256) dst[i] = src[i];
-  } else {
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(xc);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(sz);
-    for (uint32_t i = threadIdx.x; i < MT * pk / 4; i += 256) dst[i] = src[i];
-  }
-  for (uint32_t i = threadIdx.x; i < MT * groups; i += 256) {
-    const float a = xa[i];
-    sau[i] = make_float2(a, a * float(xs[i]));
-  }
+  stage_q8<MT, Fast, 256>(xc, xa, xs, pk, sz, sau);
   __syncthreads();
 
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-  const uint32_t h = lane >> 5;              // tile of the pair
   const uint32_t r = (lane >> 2) & 7u;       // row in the strip
-  const uint32_t j = lane & 3u;              // group pair 2j, 2j+1
-  const uint32_t g0 = 2 * j;
-  const bool hi = j >= 2;
-  const uint32_t sh = 16u * (j & 1u);        // bit offset of group g0 % 4
   const uint32_t ks = wave % WS;
-  const uint32_t pairs = kbs / 2;            // full tile pairs; an odd tail tile follows
-  const uint32_t q0 = uint32_t(uint64_t(pairs) * ks / WS);
-  const uint32_t q1 = uint32_t(uint64_t(pairs) * (ks + 1) / WS);
-  const bool tail = (kbs & 1u) && ks == WS - 1;
-  const uint32_t coff = lane * 32, moff = lane * 4;
 
   // Blocks walk strip groups with a block-uniform stride (a persistent grid
   // when it is smaller than the strip groups); with WS > 1 every wave of the
@@ -178,77 +253,13 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const uint32_t strip = base + wave / WS;
     const bool live = strip < strips;
     if (WS == 1 && !live) break;
-    float acc[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = 0.f;
+    float part[QPW][MT];
     if (live) {
       const uint8_t* cstrip = codes + size_t(strip) * kbs * 1024;
       const uint8_t* mstrip = meta + size_t(strip) * kbs * 128;
-      // Batches of kBatch tile pairs: every load of a batch is issued before the
-      // first is consumed, so up to kBatch * 2 KB per wave is in flight.
-      // Double-buffered batches of kB tile pairs: the loads of batch b+1 are
-      // issued before batch b is consumed, so memory stays busy while this wave
-      // computes.
-      constexpr uint32_t kB = 1;
-      uint32_t q = q0;
-      const uint32_t nb = (q1 - q0) / kB;
-      if (nb > 0) {
-        Tile A[kB], B[kB];
-        auto ld = [&](Tile (&T)[kB], uint32_t qq) {
 #pragma unroll
-          for (uint32_t u = 0; u < kB; ++u)
-            load_tile<Fast>(cstrip + size_t(qq + u) * 2048, mstrip + size_t(qq + u) * 256, coff, moff, T[u]);
-        };
-        auto cs = [&](const Tile (&T)[kB], uint32_t qq) {
-#pragma unroll
-          for (uint32_t u = 0; u < kB; ++u)
-            consume<Layout, MT, Fast>(T[u], 2 * (qq + u) + h, g0, hi, sh, sz, sau, groups, acc);
-        };
-        ld(A, q);
-        uint32_t b = 0;
-        for (; b + 2 <= nb; b += 2) {
-          ld(B, q + kB);
-          cs(A, q);
-          q += kB;
-          if (b + 2 < nb) ld(A, q + kB);
-          cs(B, q);
-          q += kB;
-        }
-        if (b < nb) {
-          cs(A, q);
-          q += kB;
-        }
-      }
-      for (; q < q1; ++q) {
-        Tile T;
-        load_tile<Fast>(cstrip + size_t(q) * 2048, mstrip + size_t(q) * 256, coff, moff, T);
-        consume<Layout, MT, Fast>(T, 2 * q + h, g0, hi, sh, sz, sau, groups, acc);
-      }
-      if (tail) {  // odd last tile: only lanes of tile 0 hold data
-        const uint32_t kb = kbs - 1;
-        Tile T;
-        if (h == 0) {
-          load_tile<Fast>(cstrip + size_t(kb) * 1024, mstrip + size_t(kb) * 128, coff, moff, T);
-        } else {
-          for (int i = 0; i < 8; ++i) T.c[i] = 0;
-          T.m = 0;
-        }
-        float part[MT];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) part[t] = 0.f;
-        consume<Layout, MT, Fast>(T, h == 0 ? kb : 0, g0, hi, sh, sz, sau, groups, part);
-        if (h == 0) {
-#pragma unroll
-          for (int t = 0; t < MT; ++t) acc[t] += part[t];
-        }
-      }
-    }
-    // a row's partials live in lanes {4r..4r+3} and {32+4r..32+4r+3}
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      acc[t] += __shfl_xor(acc[t], 1);
-      acc[t] += __shfl_xor(acc[t], 2);
-      acc[t] += __shfl_xor(acc[t], 32);
+      for (int u = 0; u < QPW; ++u)
+        stream_quarter<Layout, MT, Fast>(cstrip, mstrip, kbs, ks * QPW + u, lane, sz, sau, groups, part[u]);
     }
     const uint32_t row = strip * 8 + r;
     const bool writer = (lane & 35u) == 0;
@@ -256,14 +267,19 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
       if (writer && row < n) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
+          float total = 0.f;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) total += part[u][t];
           const size_t i = size_t(t) * n + row;
-          out[i] = acc[t] + (residual ? residual[i] : 0.f);
+          out[i] = total + (residual ? residual[i] : 0.f);
         }
       }
     } else {
-      if (writer) {
+      if (writer && live) {
 #pragma unroll
-        for (int t = 0; t < MT; ++t) red[(wave * MT + t) * 8 + r] = acc[t];
+        for (int u = 0; u < QPW; ++u)
+#pragma unroll
+          for (int t = 0; t < MT; ++t) red[((wave * QPW + u) * MT + t) * 8 + r] = part[u][t];
       }
       __syncthreads();
       if (live && ks == 0 && writer && row < n) {
@@ -271,7 +287,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
         for (int t = 0; t < MT; ++t) {
           float total = 0.f;
 #pragma unroll
-          for (int q = 0; q < WS; ++q) total += red[((wave + q) * MT + t) * 8 + r];
+          for (int q = 0; q < 4; ++q) total += red[((wave * QPW + q) * MT + t) * 8 + r];
           const size_t i = size_t(t) * n + row;
           out[i] = total + (residual ? residual[i] : 0.f);
         }
@@ -286,7 +302,7 @@ hipError_t stream_ws(const WeightView& w, const Q8View& x, float* out, const flo
                      hipStream_t s, int ws, uint32_t max_blocks) {
   const uint32_t strips = w.pn / 8, kbs = w.pk / 256;
   const uint32_t groups = w.pk / 32;
-  const size_t lds = size_t(MT) * w.pk + size_t(MT) * groups * 8 + 4 * MT * 8 * 4;
+  const size_t lds = size_t(MT) * w.pk + size_t(MT) * groups * 8 + 8 * MT * 8 * 4;
 #define QW38_STREAM_LAUNCH(WSV)                                                          \
   do {                                                                                   \
     const uint32_t need = (strips + (4 / WSV) - 1) / (4 / WSV);                          \
@@ -310,6 +326,67 @@ hipError_t stream_m(const WeightView& w, const Q8View& x, float* out, const floa
                   : stream_ws<Layout, 2, Fast>(w, x, out, residual, s, ws, max_blocks);
 }
 
+// Fused decode gate + up with the SwiGLU -> Q8 epilogue (M = 1, layout
+// 0x020D): block G owns K32 feature group G, i.e. gate strips 4G..4G+3 (waves
+// 0-3) and up strips 4G..4G+3 (waves 4-7), one whole strip per wave in K
+// quarters. The rows meet in LDS, and wave 0 packs the group: per token one
+// 32-lane half computes BF16(SiLU(g) u) and its Q8 codes, scale and sum. The
+// gate / up values are those of gemv_stream_kernel (same quarter sums), so
+// the codes equal swiglu_q8 of two separate projections bit for bit; no FP32
+// slab is written.
+template <uint16_t Layout, int MT, bool Fast>
+__global__ __launch_bounds__(512) void glu_stream_kernel(
+    const uint8_t* __restrict__ gcodes, const uint8_t* __restrict__ gmeta,
+    const uint8_t* __restrict__ ucodes, const uint8_t* __restrict__ umeta, uint32_t n, uint32_t kbs,
+    const int8_t* __restrict__ xc, const float* __restrict__ xa, const int32_t* __restrict__ xs,
+    uint32_t pk, int8_t* __restrict__ qc, float* __restrict__ qa, int32_t* __restrict__ qs, int* failure) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float rows[8][MT][8];  // [wave][token][row in strip]
+  const uint32_t groups = pk / 32;
+  int8_t* sz = reinterpret_cast<int8_t*>(smem);
+  float2* sau = reinterpret_cast<float2*>(smem + MT * pk);
+  stage_q8<MT, Fast, 512>(xc, xa, xs, pk, sz, sau);
+  __syncthreads();
+
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t G = blockIdx.x;
+  const uint32_t strip = G * 4 + (wave & 3u);
+  const bool up = wave >= 4;
+  const uint8_t* cstrip = (up ? ucodes : gcodes) + size_t(strip) * kbs * 1024;
+  const uint8_t* mstrip = (up ? umeta : gmeta) + size_t(strip) * kbs * 128;
+  float part[4][MT];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    stream_quarter<Layout, MT, Fast>(cstrip, mstrip, kbs, u, lane, sz, sau, groups, part[u]);
+  if ((lane & 35u) == 0) {
+    const uint32_t r = (lane >> 2) & 7u;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      float total = 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) total += part[u][t];
+      rows[wave][t][r] = total;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const uint32_t t = lane >> 5, i = lane & 31u;  // token, feature in the group
+  const bool on = t < uint32_t(MT);
+  const uint32_t tt = on ? t : 0u;
+  const float x = swiglu_q8_value(rows[i >> 3][tt][i & 7u], rows[4 + (i >> 3)][tt][i & 7u]);
+  q8_group32(x, qc, qa, qs, size_t(tt) * (n / 32) + G, failure, on);
+}
+
+template <uint16_t Layout, int MT, bool Fast>
+hipError_t glu_launch(const WeightView& g, const WeightView& u, const Q8View& x, int8_t* qc, float* qa,
+                      int32_t* qs, int* failure, hipStream_t s) {
+  const size_t lds = size_t(MT) * g.pk + size_t(MT) * (g.pk / 32) * 8;
+  hipLaunchKernelGGL((glu_stream_kernel<Layout, MT, Fast>), dim3(g.n / 32), dim3(512), lds, s, g.codes,
+                     g.scales, u.codes, u.scales, g.n, g.pk / 256, x.codes, x.scales, x.sums, x.pk, qc, qa,
+                     qs, failure);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 // Returns hipErrorNotSupported when this path does not apply (caller falls back).
@@ -317,7 +394,7 @@ hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,
                               const float* residual, hipStream_t s, int ws_override,
                               uint32_t max_blocks) {
   if (x.m > 2 || w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2) return hipErrorNotSupported;
-  const size_t lds = size_t(x.m) * w.pk * 5 / 4 + 4 * x.m * 8 * 4;
+  const size_t lds = size_t(x.m) * w.pk * 5 / 4 + 8 * x.m * 8 * 4;
   if (lds > 56 * 1024) return hipErrorNotSupported;
   const bool fast = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(x.codes)) %
                          16 == 0) &&
@@ -342,6 +419,23 @@ hipError_t launch_gemv_stream(const WeightView& w, const Q8View& x, float* out,
                 : stream_m<QW38_LAYOUT_Q4K_CANDIDATE_V2, false>(w, x, out, residual, s, ws, max_blocks);
   return fast ? stream_m<QW38_LAYOUT_Q4K_WAVE64, true>(w, x, out, residual, s, ws, max_blocks)
               : stream_m<QW38_LAYOUT_Q4K_WAVE64, false>(w, x, out, residual, s, ws, max_blocks);
+}
+
+bool gemv_glu_applies(const WeightView& gate, const WeightView& up, uint32_t m) {
+  return m == 1 && gate.layout == QW38_LAYOUT_Q4K_CANDIDATE_V2 && up.layout == gate.layout &&
+         gate.n == up.n && gate.k == up.k && gate.pk == up.pk && gate.n % 32 == 0 && gate.pn == gate.n &&
+         size_t(m) * gate.pk * 5 / 4 <= 48 * 1024;
+}
+
+hipError_t launch_gemv_glu(const WeightView& gate, const WeightView& up, const Q8View& x, int8_t* codes,
+                           float* scales, int32_t* sums, int* failure, hipStream_t s) {
+  if (!gemv_glu_applies(gate, up, x.m)) return hipErrorNotSupported;
+  const bool fast = ((reinterpret_cast<uintptr_t>(gate.codes) | reinterpret_cast<uintptr_t>(up.codes) |
+                      reinterpret_cast<uintptr_t>(x.codes)) % 16 == 0) &&
+                    ((reinterpret_cast<uintptr_t>(gate.scales) | reinterpret_cast<uintptr_t>(up.scales)) % 4 == 0);
+  constexpr uint16_t L = QW38_LAYOUT_Q4K_CANDIDATE_V2;
+  return fast ? glu_launch<L, 1, true>(gate, up, x, codes, scales, sums, failure, s)
+              : glu_launch<L, 1, false>(gate, up, x, codes, scales, sums, failure, s);
 }
 
 }  // namespace qw38hip

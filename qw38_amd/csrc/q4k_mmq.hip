@@ -25,6 +25,7 @@
 // v_perm with 0x64 high bytes, then one packed FP16 FMA/add recovers the exact
 // integer value (scaled by s for Q4_K weights). Rows of the LDS tiles are
 // 64 halfs + 8 pad; all stores are 16 B.
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <type_traits>
@@ -95,17 +96,41 @@ struct Fetch {
   int32_t su[GPT];   // only): this thread's GPT groups of token kt
 };
 
-template <uint16_t Layout, bool Vec, int WR, int WT, int NI, int NJ>
+// Fused gate + up (Glu): the up projection's weight and the down
+// projection's Q8 operand, written by the SwiGLU -> Q8 epilogue.
+struct GluOut {
+  const uint8_t* codes2;  // up weight codes / metadata (same geometry as gate)
+  const uint8_t* meta2;
+  int8_t* qc;             // [m][n] codes
+  float* qa;              // [m][n / 32] scales
+  int32_t* qs;            // [m][n / 32] code sums
+  int* failure;           // sticky nonfinite-producer flag
+};
+
+// Glu: a tile's first BR / 2 rows are gate rows and its last BR / 2 the up rows
+// of the same BR / 2 features (row_begin and the tile height in features); the
+// gate waves hand their outputs to the up waves through LDS, which apply
+// SwiGLU -> BF16 -> Q8 per K32 feature group in the up waves' registers. The
+// per-(row, token) arithmetic is that of the unfused kernel, so the fused
+// codes equal swiglu_q8 of the two separate projections bit for bit.
+template <uint16_t Layout, bool Vec, int WR, int WT, int NI, int NJ, bool Glu = false>
 __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) void mmq_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n,
     uint32_t pn, uint32_t kbs, const int8_t* __restrict__ xc, const float* __restrict__ xa,
     const int32_t* __restrict__ xs, uint32_t m, uint32_t pk, float* __restrict__ out,
-    const float* __restrict__ residual, uint32_t row_begin, uint32_t row_blocks, uint32_t tok_blocks) {
+    const float* __restrict__ residual, uint32_t row_begin, uint32_t row_blocks, uint32_t tok_blocks,
+    GluOut glu) {
   constexpr bool kQ6 = Layout == QW38_LAYOUT_Q6K_WAVE64;
   using C = Cfg<WR, WT, NI, NJ>;
   constexpr int BR = C::BR, BT = C::BT, NT = WR * WT * 64;
-  constexpr int APT = NT / (2 * BR), AW = 4 / APT;  // A staging: threads per (row, group), code words each
-  static_assert(APT * 2 * BR == NT && (APT == 1 || (APT == 2 && !kQ6)), "A staging share");
+  constexpr int HR = Glu ? BR / 2 : BR;  // features (output rows) per tile
+  static_assert(!Glu || (!kQ6 && WR % 2 == 0 && NI % 2 == 0), "Glu tiles: Q4_K, gate / up wave halves");
+  // A staging: APT threads per (row, group), AW code words each. Tiles with
+  // fewer (row, group) items than threads (80 rows) leave the last threads
+  // out of A staging: they load a duplicate item and store nothing.
+  constexpr int APT = NT / (2 * BR) > 0 ? NT / (2 * BR) : 1, AW = 4 / APT;
+  static_assert((APT * 2 * BR == NT || (APT == 1 && 2 * BR < NT)) && (APT == 1 || (APT == 2 && !kQ6)),
+                "A staging share");
   constexpr int BB = BT * 64 / NT;  // B bytes staged per thread per step
   static_assert(BB == 8 || BB == 16 || BB == 32, "B staging share");
   constexpr int ZW = BB / 4, PARTS = 32 / BB;
@@ -123,7 +148,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   __shared__ float2 Dd[2][BR];                     // (d, -dmin) | (d, 0)
 
   const uint32_t tile = xcd_tile(blockIdx.x, row_blocks * tok_blocks);
-  const uint32_t row0 = row_begin + (tile / tok_blocks) * BR, tok0 = (tile % tok_blocks) * BT;
+  const uint32_t row0 = row_begin + (tile / tok_blocks) * HR, tok0 = (tile % tok_blocks) * BT;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wr = wave / WT, wt = wave % WT;
   const uint32_t lr = lane & 15u, lk = lane >> 4;
@@ -138,9 +163,17 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   // groups of one row, whose bytes are adjacent in the tile row.
   constexpr bool kRowMajorA = Layout == QW38_LAYOUT_Q4K_WAVE64;
   const uint32_t ah = tid % APT;
-  const uint32_t ar = kRowMajorA ? (tid / APT) % BR : (tid / APT) >> 1;
-  const uint32_t asel = kRowMajorA ? (tid / APT) / BR : (tid / APT) & 1u;
-  const uint32_t arow = min(row0 + ar, pn - 1);
+  const uint32_t aslot = (tid / APT) % (2 * BR);
+  const bool a_on = tid / APT < uint32_t(2 * BR);
+  const uint32_t ar = kRowMajorA ? aslot % BR : aslot >> 1;
+  const uint32_t asel = kRowMajorA ? aslot / BR : aslot & 1u;
+  const uint32_t arow = min(row0 + (Glu ? ar % HR : ar), pn - 1);
+  if constexpr (Glu) {  // the tile's up half reads the up weight
+    if (ar >= uint32_t(HR)) {
+      codes = glu.codes2;
+      meta = glu.meta2;
+    }
+  }
   // B staging role: token bt, group-in-step bsel, byte part bpart of BB bytes
   const uint32_t bpart = tid % PARTS, bsel = (tid / PARTS) & 1u, bt = tid / (2 * PARTS);
   const uint32_t btok = min(tok0 + bt, m - 1);
@@ -268,8 +301,8 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     if constexpr (!kQ6) {
       float sf, mf;
       q4_scale_min_lane(F.x[1], F.x[2], F.x[3], g, sf, mf);
-      if (ah == 0) Mq[kp][ar * 8 + g] = _Float16(mf);
-      if (q == 0 && asel == 0 && ah == 0)
+      if (ah == 0 && a_on) Mq[kp][ar * 8 + g] = _Float16(mf);
+      if (q == 0 && asel == 0 && ah == 0 && a_on)
         Dd[kp][ar] = make_float2(f16_to_f32(F.x[0] & 0xffffu), -f16_to_f32(F.x[0] >> 16));
       uint32_t v[2 * AW];
       q4_vectors<Layout, AW>(F.w, v);
@@ -282,10 +315,12 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
         o[2 * j + 1] = as_u32(__builtin_elementwise_fma(hi_pair(v[j]), s2, b2));
       }
       uint4* dst = reinterpret_cast<uint4*>(&As[buf][0][ar * kStride + asel * 32 + ah * 8 * AW]);
+      if (a_on) {
 #pragma unroll
-      for (int i = 0; i < AW; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+        for (int i = 0; i < AW; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+      }
     } else {
-      if (q == 0 && asel == 0) Dd[kp][ar] = make_float2(f16_to_f32(F.x[3]), 0.f);
+      if (q == 0 && asel == 0 && a_on) Dd[kp][ar] = make_float2(f16_to_f32(F.x[3]), 0.f);
       const h2 off = {_Float16(-1056.f), _Float16(-1056.f)};  // 1024 + q -> q - 32
       uint32_t oh[16], ol[16];
 #pragma unroll
@@ -306,10 +341,12 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
       }
       uint4* dh = reinterpret_cast<uint4*>(&As[buf][0][ar * kStride + asel * 32]);
       uint4* dl = reinterpret_cast<uint4*>(&As[buf][kPlanes - 1][ar * kStride + asel * 32]);
+      if (a_on) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        dh[i] = make_uint4(oh[4 * i], oh[4 * i + 1], oh[4 * i + 2], oh[4 * i + 3]);
-        dl[i] = make_uint4(ol[4 * i], ol[4 * i + 1], ol[4 * i + 2], ol[4 * i + 3]);
+        for (int i = 0; i < 4; ++i) {
+          dh[i] = make_uint4(oh[4 * i], oh[4 * i + 1], oh[4 * i + 2], oh[4 * i + 3]);
+          dl[i] = make_uint4(ol[4 * i], ol[4 * i + 1], ol[4 * i + 2], ol[4 * i + 3]);
+        }
       }
     }
     // ---- B: this thread's BB codes z of (token bt, group) as FP16 ----
@@ -561,6 +598,85 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     step(std::integral_constant<uint32_t, 3>{}, kb);
   }
   __syncthreads();  // Ti visible (also when kbs is small)
+  if constexpr (Glu) {
+    // ---- SwiGLU -> Q8 epilogue. Gate waves (wr < WR / 2) park g in LDS (the
+    // A tiles are free now); up wave wr + WR / 2 holds u of the same features
+    // in the same register positions. A K32 feature group of token lr is row
+    // tiles 2p, 2p + 1 of lanes lr + 16 lk: eight values in each of 4 lanes. ----
+    static_assert(sizeof(As) >= size_t(HR) * BT * sizeof(float), "g tile fits the A tiles");
+    float* gl = reinterpret_cast<float*>(&As[0][0][0]);
+    const bool gate_wave = wr < uint32_t(WR / 2);
+    const uint32_t wq = gate_wave ? wr : wr - WR / 2;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float inv = Ti[wt * NJ * 16 + j * 16 + lr];
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[i][j][v] *= inv;
+    }
+    if (gate_wave) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            gl[(wq * NI * 16 + i * 16 + lk * 4 + v) * BT + wt * NJ * 16 + j * 16 + lr] = acc[i][j][v];
+    }
+    __syncthreads();
+    if (gate_wave) return;
+    const uint32_t groups_out = n / 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t tl = wt * NJ * 16 + j * 16 + lr, tok = tok0 + tl;
+#pragma unroll
+      for (int p = 0; p < NI / 2; ++p) {
+        float x[8];
+        float peak = 0.f;
+        int finite = 1;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float g = gl[(wq * NI * 16 + (2 * p + h) * 16 + lk * 4 + v) * BT + tl];
+            const float y = swiglu_q8_value(g, acc[2 * p + h][j][v]);
+            x[4 * h + v] = y;
+            const bool f = isfinite(y);
+            finite &= int(f);
+            peak = fmaxf(peak, f ? fabsf(y) : 0.f);
+          }
+        peak = fmaxf(peak, __shfl_xor(peak, 16));
+        peak = fmaxf(peak, __shfl_xor(peak, 32));
+        finite &= __shfl_xor(finite, 16);
+        finite &= __shfl_xor(finite, 32);
+        const float a = peak == 0.f ? 1.f : peak / 127.f;
+        const bool valid = finite && isfinite(a) && a > 0.f;
+        uint32_t word[2] = {0u, 0u};
+        int sum = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int z = valid ? max(-127, min(127, int(rintf(x[e] / a)))) : 0;
+          sum += z;
+          word[e / 4] |= uint32_t(uint8_t(int8_t(z))) << (8 * (e % 4));
+        }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        const uint32_t f0 = row0 + wq * NI * 16 + p * 32;  // first feature of the group
+        if (tok >= m || f0 >= n) continue;
+        int8_t* cp = glu.qc + size_t(tok) * n + f0 + lk * 4;
+        *reinterpret_cast<uint32_t*>(cp) = word[0];
+        *reinterpret_cast<uint32_t*>(cp + 16) = word[1];
+        if (lk == 0) {
+          const size_t gi = size_t(tok) * groups_out + f0 / 32;
+          glu.qa[gi] = valid ? a : __uint_as_float(0x7fc00000u);
+          glu.qs[gi] = sum;
+          if (!valid) *glu.failure = 1;  // sticky flag, plain vector store
+        }
+      }
+    }
+    return;
+  }
   // ---- store: lane holds rows 4*lk..4*lk+3 of token lr in each tile ----
   const bool vec = (n % 4 == 0) &&
                    ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0;
@@ -594,29 +710,35 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
 
 // Launches one tile shape over weight rows [row_begin, row_end) (row_begin a
 // multiple of the tile height; row_end = pn or a multiple of it).
-template <uint16_t Layout, int WR, int WT, int NI, int NJ>
+// Glu: rows are features, glu carries the up weight and the Q8 outputs.
+template <uint16_t Layout, int WR, int WT, int NI, int NJ, bool Glu = false>
 hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const float* residual,
-                      hipStream_t s, uint32_t row_begin, uint32_t row_end) {
+                      hipStream_t s, uint32_t row_begin, uint32_t row_end, GluOut glu = {}) {
   using C = Cfg<WR, WT, NI, NJ>;
-  const uint32_t row_blocks = (row_end - row_begin + C::BR - 1) / C::BR;
+  constexpr uint32_t H = Glu ? C::BR / 2 : C::BR;
+  const uint32_t row_blocks = (row_end - row_begin + H - 1) / H;
   const uint32_t tok_blocks = (x.m + C::BT - 1) / C::BT;
   if (row_blocks == 0) return hipSuccess;
   const dim3 grid(row_blocks * tok_blocks);
   // 0x020D spans are 4-byte (codes) / 2-byte (metadata) aligned in general;
   // 16-byte aligned ones (every span this library allocates) load wide.
-  const bool vec = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales)) % 16) == 0;
-  auto kern = mmq_kernel<Layout, true, WR, WT, NI, NJ>;
+  const bool vec = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
+                     reinterpret_cast<uintptr_t>(glu.codes2) | reinterpret_cast<uintptr_t>(glu.meta2)) %
+                    16) == 0;
+  auto kern = mmq_kernel<Layout, true, WR, WT, NI, NJ, Glu>;
   if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2)
-    if (!vec) kern = mmq_kernel<Layout, false, WR, WT, NI, NJ>;
+    if (!vec) kern = mmq_kernel<Layout, false, WR, WT, NI, NJ, Glu>;
   hipLaunchKernelGGL(kern, grid, dim3(WR * WT * 64), 0, s, w.codes, w.scales,
                      w.n, w.pn, w.pk / 256, x.codes, x.scales, x.sums, x.m, x.pk, out, residual,
-                     row_begin, row_blocks, tok_blocks);
+                     row_begin, row_blocks, tok_blocks, glu);
   return hipGetLastError();
 }
 
-template <uint16_t Layout>
+// Glu: the tile cost model runs over the 2 n virtual rows of gate and up, and
+// the launches get feature ranges (virtual rows / 2).
+template <uint16_t Layout, bool Glu = false>
 hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const float* residual,
-                        hipStream_t s) {
+                        hipStream_t s, GluOut glu = {}) {
   // QW38_MMQ_TILE=32|64|128 pins the token tile (256: 256 rows x 128 tokens);
   // QW38_MMQ_SPLIT=0 disables the tail split (tuning aids; every tile shape
   // and split gives bitwise-identical results).
@@ -635,7 +757,8 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   // 1.77); 128 x 64 t1 = 1.07, t2 = 1.39 (Q6_K 1.33, 2.65); 128 x 32
   // t1 = 0.70, t2 = 0.89 (Q6_K 1.0, 2.0). Small grids thus take smaller tiles
   // so that every CU has work.
-  const uint32_t pn = w.pn;
+  const uint32_t pn = Glu ? 2 * w.pn : w.pn;
+  constexpr uint32_t kv = Glu ? 2 : 1;  // virtual rows per feature
   const uint32_t cus = uint32_t(cu_count());
   constexpr bool q6 = Layout == QW38_LAYOUT_Q6K_WAVE64;
   auto per_cu = [&](uint32_t rows, uint32_t toks) {
@@ -666,20 +789,27 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   const double c_big = b_big * (q6 ? 1.77 : 1.9);
   const double c64 = q6 ? two(per_cu(128, 64), 1.33, 2.65) : two(per_cu(128, 64), 1.07, 1.39);
   const double c32 = q6 ? two(per_cu(128, 32), 1.0, 2.0) : two(per_cu(128, 32), 0.70, 0.89);
+  // 80 x 128 (one block per CU): 5120-row weights make 64 row blocks, so a
+  // 512-token chunk fills 256 CUs in one round where 128-row tiles leave 96
+  // idle. Step time about 0.7 of the 128 x 128 tile's.
+  const double c80 = per_cu(80, 128) * (q6 ? 1.77 : 1.9) * 0.7;
   int bt = 32;
   if (x.m > 32 && c64 < c32) bt = 64;
   if (x.m > 64 && c_big < (bt == 64 ? c64 : c32)) bt = 256;
+  if (x.m > 64 && !Glu && c80 < std::min({c_big, c64, c32})) bt = 80;
   if (forced) bt = forced;
-  if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2>(w, x, out, residual, s, 0, pn);  // 128 x 32
-  if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4>(w, x, out, residual, s, 0, pn);  // 128 x 64
+  if (bt == 80) return launch_cfg<Layout, 1, 4, 5, 2>(w, x, out, residual, s, 0, pn);  // 80 x 128
+  const uint32_t end = pn / kv;
+  if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 32
+  if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 64
   if constexpr (q6) {  // Q6_K's two A planes: 128 x 128 at most
     return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s, 0, pn);
   } else {
-    if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4>(w, x, out, residual, s, 0, pn);  // 128 x 128
+    if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 128
     if (forced) big_rows = pn;
-    hipError_t e = launch_cfg<Layout, 4, 2, 4, 4>(w, x, out, residual, s, 0, big_rows);
+    hipError_t e = launch_cfg<Layout, 4, 2, 4, 4, Glu>(w, x, out, residual, s, 0, big_rows / kv, glu);
     if (e != hipSuccess || big_rows == pn) return e;
-    return launch_cfg<Layout, 4, 1, 2, 2>(w, x, out, residual, s, big_rows, pn);
+    return launch_cfg<Layout, 4, 1, 2, 2, Glu>(w, x, out, residual, s, big_rows / kv, end, glu);
   }
 }
 
@@ -707,6 +837,23 @@ hipError_t launch_mmq(const WeightView& w, const Q8View& x, float* out, const fl
       return mmq_dispatch<QW38_LAYOUT_Q4K_WAVE64>(w, x, out, residual, s);
     case QW38_LAYOUT_Q6K_WAVE64:
       return mmq_dispatch<QW38_LAYOUT_Q6K_WAVE64>(w, x, out, residual, s);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_mmq_glu(const WeightView& gate, const WeightView& up, const Q8View& x,
+                          int8_t* codes, float* scales, int32_t* sums, int* failure,
+                          hipStream_t s) {
+  if (gate.layout != up.layout || gate.n != up.n || gate.pn != up.pn || gate.pk != up.pk ||
+      gate.n % 32 != 0 || gate.pn != gate.n)
+    return hipErrorInvalidValue;
+  const GluOut glu{up.codes, up.scales, codes, scales, sums, failure};
+  switch (gate.layout) {
+    case QW38_LAYOUT_Q4K_CANDIDATE_V2:
+      return mmq_dispatch<QW38_LAYOUT_Q4K_CANDIDATE_V2, true>(gate, x, nullptr, nullptr, s, glu);
+    case QW38_LAYOUT_Q4K_WAVE64:
+      return mmq_dispatch<QW38_LAYOUT_Q4K_WAVE64, true>(gate, x, nullptr, nullptr, s, glu);
     default:
       return hipErrorInvalidValue;
   }

@@ -10,30 +10,6 @@
 namespace qw38hip {
 namespace {
 
-__device__ __forceinline__ void q8_group32(float x, int8_t* codes, float* scales,
-                                           int32_t* sums, size_t group, int* failure) {
-  const unsigned lane = threadIdx.x & 31u;
-  const bool finite = isfinite(x);
-  float peak = finite ? fabsf(x) : 0.f;
-#pragma unroll
-  for (int off = 16; off; off >>= 1) peak = fmaxf(peak, __shfl_xor(peak, off, 32));
-  const uint64_t ballot = __ballot(finite);
-  const uint32_t half = uint32_t(ballot >> (threadIdx.x & 32u));
-  const float a = peak == 0.f ? 1.f : peak / 127.f;
-  const bool valid = half == 0xffffffffu && isfinite(a) && a > 0.f;
-  int z = 0;
-  if (valid) z = max(-127, min(127, int(rintf(x / a))));
-  codes[group * 32 + lane] = int8_t(z);
-  int sum = z;
-#pragma unroll
-  for (int off = 16; off; off >>= 1) sum += __shfl_xor(sum, off, 32);
-  if (lane == 0) {
-    scales[group] = valid ? a : __uint_as_float(0x7fc00000u);
-    sums[group] = sum;
-    if (!valid) *failure = 1;  // sticky flag, plain vector store
-  }
-}
-
 // cuda/q4k_q8.cu:44-50: grid (pk/256, m); padding columns pack as zeros.
 __global__ __launch_bounds__(256) void pack_q8_kernel(const uint16_t* __restrict__ in,
                                                       uint32_t k, uint32_t pk,
@@ -111,7 +87,6 @@ __global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ resi
                                                   uint16_t* out_bf16, uint32_t m, uint8_t* codes,
                                                   float* scales, int32_t* sums, int* failure,
                                                   uint8_t* sf_bytes) {
-  constexpr bool Pack = Mode != kRmsBf16;
   if constexpr (Mode == kRmsNvfp4 || Mode == kRmsFp8) {
     if (blockIdx.x >= m) {
       if constexpr (Mode == kRmsNvfp4) {
@@ -124,35 +99,54 @@ __global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ resi
       return;
     }
   }
-  __shared__ __align__(16) uint16_t rounded[Pack ? kHidden : 1];
+  // Thread t owns elements t + 256 j (j < 20), held in registers: one round
+  // of loads for the whole row, the per-thread sums run in increasing j (the
+  // order of the strided loops of the reference kernel).
+  constexpr int kPer = kHidden / 256;
+  constexpr bool Lds = Mode == kRmsNvfp4 || Mode == kRmsFp8;
+  __shared__ __align__(16) uint16_t rounded[Lds ? kHidden : 1];
   __shared__ float sm[9];
   const float* x = residual + size_t(blockIdx.x) * kHidden;
-  uint16_t* y = Pack ? rounded : out_bf16 + size_t(blockIdx.x) * kHidden;
+  float xv[kPer], gv[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    xv[j] = x[threadIdx.x + 256 * j];
+    gv[j] = bf16_to_f32(gamma[threadIdx.x + 256 * j]);
+  }
   float s = 0.f;
-  for (uint32_t i = threadIdx.x; i < kHidden; i += 256) s = fmaxf(s, fabsf(x[i]));
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) s = fmaxf(s, fabsf(xv[j]));
   const float scale = block256<true>(s, sm);
   const float safe = scale == 0.f ? 1.f : scale;
   float sq = 0.f;
-  for (uint32_t i = threadIdx.x; i < kHidden; i += 256) {
-    const float q = x[i] / safe;
-    sq = fmaf(q, q, sq);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    xv[j] = xv[j] / safe;
+    sq = fmaf(xv[j], xv[j], sq);
   }
   const float sumsq = block256<false>(sq, sm);
   const float se = sqrtf(eps) / safe;
   const float inv = 1.0f / sqrtf(fmaf(se, se, sumsq / float(kHidden)));
-  for (uint32_t i = threadIdx.x; i < kHidden; i += 256) {
-    const float g = bf16_to_f32(gamma[i]);
-    y[i] = f32_to_bf16_rne((1.0f + g) * ((x[i] / safe) * inv));
+  uint16_t yv[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const uint32_t i = threadIdx.x + 256 * j;
+    yv[j] = f32_to_bf16_rne((1.0f + gv[j]) * (xv[j] * inv));
+    if constexpr (Mode == kRmsBf16) out_bf16[size_t(blockIdx.x) * kHidden + i] = yv[j];
+    if constexpr (Lds) rounded[i] = yv[j];
     if constexpr (Mode == kRmsFp8)
-      if (out_bf16) out_bf16[size_t(blockIdx.x) * kHidden + i] = y[i];
+      if (out_bf16) out_bf16[size_t(blockIdx.x) * kHidden + i] = yv[j];
   }
-  if constexpr (Pack) {
+  if constexpr (Mode == kRmsQ8) {
+    // element t + 256 j sits in group 8 j + t / 32 at lane t % 32 of its half
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      q8_group32(bf16_to_f32(yv[j]), reinterpret_cast<int8_t*>(codes), scales, sums,
+                 (size_t(blockIdx.x) * kHidden + threadIdx.x + 256 * j) / 32, failure);
+  }
+  if constexpr (Lds) {
     __syncthreads();
-    if constexpr (Mode == kRmsQ8) {
-      for (uint32_t i = threadIdx.x; i < kHidden; i += 256)
-        q8_group32(bf16_to_f32(rounded[i]), reinterpret_cast<int8_t*>(codes), scales, sums,
-                   (size_t(blockIdx.x) * kHidden + i) / 32, failure);
-    } else if constexpr (Mode == kRmsNvfp4) {
+    if constexpr (Mode == kRmsNvfp4) {
       for (uint32_t b = threadIdx.x; b < kHidden / 16; b += 256) {
         float v[16];
 #pragma unroll
@@ -176,10 +170,7 @@ __global__ __launch_bounds__(256) void swiglu_q8_kernel(const float* __restrict_
                                                         int8_t* codes, float* scales,
                                                         int32_t* sums, int* failure) {
   const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
-  const float g = gate[i], u = up[i];
-  float v = (g / (1.f + exp_cw(-g))) * u;
-  if (!isfinite(g) || !isfinite(u)) v = __uint_as_float(0x7fc00000u);
-  q8_group32(bf16_to_f32(f32_to_bf16_rne(v)), codes, scales, sums, i / 32, failure);
+  q8_group32(swiglu_q8_value(gate[i], up[i]), codes, scales, sums, i / 32, failure);
 }
 
 __global__ void fill_zero_i32_kernel(int* p, uint32_t count) {

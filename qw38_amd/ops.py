@@ -16,7 +16,7 @@ import torch
 from ._lib import (LAYOUT_Q4K_SEQ, LAYOUT_Q4K_W64, LAYOUT_Q6K_W64, QUANTIZER_Q4K, QUANTIZER_Q6K,
                    Q8Input as _Q8, Weight as _W, check, lib)
 
-__all__ = ["PrefillWeight", "Q8Input", "pack_q8", "q4k_q8_project", "q4k_q8_mlp",
+__all__ = ["PrefillWeight", "Q8Input", "pack_q8", "q4k_q8_project", "q4k_q8_mlp", "q4k_q8_gate_up_swiglu",
            "hidden_rms_q8", "swiglu_q8", "group_dots", "quantize_q4k_blocks", "quantize_q6k_blocks", "upload_q4k_blocks", "upload_q6k_blocks",
            "q8_mlp_workspace_bytes", "code_bytes", "scale_bytes", "pad_k", "pad_n",
            "decode_view", "decode_desc", "decode_mmv", "decode_mmv_paired", "decode_mmv_ranges",
@@ -129,6 +129,15 @@ def q4k_q8_project(weight: PrefillWeight, x: Q8Input, output: torch.Tensor, stre
     olen = output_len if output_len is not None else output.numel()
     check(lib().qw38_q4k_q8_project(C.byref(w), C.byref(q), optr, olen, _ptr(residual),
                                     0 if residual is None else residual.numel(), _stream(stream)))
+
+
+def q4k_q8_gate_up_swiglu(gate: PrefillWeight, up: PrefillWeight, x: Q8Input, out: Q8Input,
+                          failure: torch.Tensor, stream=None):
+    """Fused gate + up projections with the SwiGLU->Q8 epilogue: ``out`` is the
+    down projection's Q8 operand (cuda/q4k_q8.cu:378-385 as one launch)."""
+    g, u, q, o = gate.struct(), up.struct(), x.struct(), out.struct()
+    check(lib().qw38_q4k_q8_gate_up_swiglu(C.byref(g), C.byref(u), C.byref(q), C.byref(o),
+                                           _ptr(failure), failure.numel(), _stream(stream)))
 
 
 def q8_mlp_workspace_bytes(m: int) -> int:

@@ -117,6 +117,18 @@ def test_q8_mlp_end_to_end(torch_gpu, mlp_weights, down):
         y = out.cpu().numpy()
         codes, scales, sums, g, u = _workspace_views(ws, m)
         q1, _ = oracle.rms_q8(res, gamma, 1e-6)
+        if m > 8:
+            # the fused gate+up launch writes no FP32 slabs: take the device's
+            # own projections of the same (bit-exact) RMS->Q8 operand
+            qx = ops.Q8Input.empty(m, 5120)
+            flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+            ops.hidden_rms_q8(dres, dgam, 1e-6, m, qx, flag)
+            gd = torch.empty(m, 17408, device="cuda")
+            ud = torch.empty(m, 17408, device="cuda")
+            ops.q4k_q8_project(gate, qx, gd)
+            ops.q4k_q8_project(up, qx, ud)
+            torch.cuda.synchronize()
+            g, u = gd.cpu().numpy(), ud.cpu().numpy()
         g64, _, _ = oracle.q4k_q8_contract(gl, q1)
         u64, _, _ = oracle.q4k_q8_contract(ul, q1)
         for name, dev, ref in (("gate", g, g64), ("up", u, u64)):
@@ -165,3 +177,67 @@ def test_q8_mlp_failure_semantics(torch_gpu, mlp_weights):
     assert not e.value.submitted
     with pytest.raises(Qw38Error):
         ops.q4k_q8_mlp(gate, up, dn, dres, dgam, 1e-6, out, m, ws[:-8])
+
+
+@pytest.mark.parametrize("layout", [oracle.LAYOUT_Q4K_W64, oracle.LAYOUT_Q4K_SEQ])
+def test_gate_up_swiglu_fused_bitwise(torch_gpu, mlp_weights, layout):
+    """The fused gate+up launch (SwiGLU->Q8 in the projection's epilogue)
+    equals the unfused chain -- two projections, then the oracle-pinned
+    SwiGLU->Q8 pack -- bit for bit: the decode kernel at m = 1 on 0x020D, and
+    the MMQ at m covering every tile shape and the big-tile + tail split; a
+    group whose input scale is NaN is flagged in both."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    _, gl = mlp_weights["gate"]
+    _, ul = mlp_weights["up"]
+    gate = ops.PrefillWeight.from_bytes(*gl.physical(layout), layout, gl.n, gl.k)
+    up = ops.PrefillWeight.from_bytes(*ul.physical(layout), layout, ul.n, ul.k)
+    gamma = oracle.fp32_to_bf16(normal(5120, 80, 0.1))
+    dgam = _dev(torch, gamma.view(np.int16))
+    # m = 1 on 0x020D: the streaming-GEMV family (fused: one wave per strip,
+    # unfused: four waves split K); m > 8: the MMQ family
+    ms = ((1,) if layout == oracle.LAYOUT_Q4K_SEQ else ()) + (9, 40, 64, 130, 512)
+    for m in ms:
+        print(f"gate_up layout=0x{layout:04x} m={m}", flush=True)
+        res = normal((m, 5120), 90 + m) * 2
+        qx = ops.Q8Input.empty(m, 5120)
+        flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+        ops.hidden_rms_q8(_dev(torch, res), dgam, 1e-6, m, qx, flag)
+        if m >= 40:
+            qx.scales.view(m, 160)[m - 3, 17] = float("nan")
+        gd = torch.empty(m, 17408, device="cuda")
+        ud = torch.empty(m, 17408, device="cuda")
+        ops.q4k_q8_project(gate, qx, gd)
+        ops.q4k_q8_project(up, qx, ud)
+        ref = ops.Q8Input.empty(m, 17408)
+        rflag = torch.zeros(1, dtype=torch.int32, device="cuda")
+        ops.swiglu_q8(gd, ud, m, 17408, ref, rflag)
+        out = ops.Q8Input.empty(m, 17408)
+        out.codes.fill_(55)
+        out.scales.fill_(7.0)
+        out.sums.fill_(-1)
+        fflag = torch.zeros(1, dtype=torch.int32, device="cuda")
+        ops.q4k_q8_gate_up_swiglu(gate, up, qx, out, fflag)
+        torch.cuda.synchronize()
+        assert int(fflag.item()) == int(rflag.item()) == (1 if m >= 40 else 0)
+        assert torch.equal(out.codes, ref.codes)
+        assert torch.equal(out.scales.view(torch.int32), ref.scales.view(torch.int32))
+        assert torch.equal(out.sums, ref.sums)
+
+
+def test_gate_up_swiglu_rejections(torch_gpu, mlp_weights):
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    from qw38_amd import Qw38Error
+    gate, _ = mlp_weights["gate"]
+    up, _ = mlp_weights["up"]
+    dn6, _ = mlp_weights["down6"]
+    qx = ops.Q8Input.empty(16, 5120)
+    out = ops.Q8Input.empty(16, 17408)
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    with pytest.raises(Qw38Error):  # Q6_K gate
+        ops.q4k_q8_gate_up_swiglu(dn6, up, qx, out, flag)
+    with pytest.raises(Qw38Error):  # output token count mismatch
+        ops.q4k_q8_gate_up_swiglu(gate, up, qx, ops.Q8Input.empty(8, 17408), flag)
+    with pytest.raises(Qw38Error):  # failure flag length
+        ops.q4k_q8_gate_up_swiglu(gate, up, qx, out, torch.zeros(2, dtype=torch.int32, device="cuda"))
