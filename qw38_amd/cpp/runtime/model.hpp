@@ -35,8 +35,11 @@ struct ConstTensorView {
   std::uint64_t bytes{};
 };
 
+// Target of GGML-order Q4_K blocks. 0x020D by default: the decode kernels
+// for M = 2..8 (int8 MFMA) and the fused M = 1 gate+up launch run on it, and
+// the prefill MMQ runs within a few percent of 0x0240 there.
 struct UploadOptions {
-  std::uint16_t q4k_layout{QW38_LAYOUT_Q4K_WAVE64};  // target of GGML-order Q4_K blocks
+  std::uint16_t q4k_layout{QW38_LAYOUT_Q4K_CANDIDATE_V2};
 };
 
 class Model {

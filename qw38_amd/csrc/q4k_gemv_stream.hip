@@ -19,6 +19,8 @@
 // and, when WS waves split K, across those waves in LDS in a fixed order.
 // Unaligned (4-byte) code / activation spans and 2-byte metadata spans use
 // narrower loads with identical arithmetic, so results are bitwise equal.
+#include <cstdlib>
+
 #include "common.hpp"
 
 namespace qw38hip {
@@ -89,10 +91,12 @@ __device__ __forceinline__ void scale_min_pair(uint32_t p0, uint32_t p1, uint32_
   }
 }
 
-template <uint16_t Layout, int MT, bool Fast>
-__device__ __forceinline__ void consume(const Tile& t, uint32_t kb, uint32_t g0, bool hi,
-                                        uint32_t sh, const int8_t* sz, const float2* sau,
-                                        uint32_t groups, float acc[MT]) {
+// One lane's share of a tile: 32 code bytes = K32 groups g0, g0+1 of one
+// row. z: the two groups' 64 activation codes; au = (a0, a0*sum0, a1,
+// a1*sum1). acc += d * sum_e a_e s_e dot_e - dmin * sum_e (a_e sum_e) m_e.
+template <uint16_t Layout>
+__device__ __forceinline__ void consume_core(const Tile& t, bool hi, uint32_t sh, const uint4 (&z)[4],
+                                             float4 au, float& acc) {
   const uint32_t dd = quad_bcast<0>(t.m), p0 = quad_bcast<1>(t.m), p1 = quad_bcast<2>(t.m),
                  p2 = quad_bcast<3>(t.m);
   float s[2], m[2];
@@ -101,29 +105,38 @@ __device__ __forceinline__ void consume(const Tile& t, uint32_t kb, uint32_t g0,
   uint32_t v[2][8];
   unpack8<Layout>(t.c[0], t.c[1], t.c[2], t.c[3], v[0]);
   unpack8<Layout>(t.c[4], t.c[5], t.c[6], t.c[7], v[1]);
+  float X = 0.f, Y = 0.f;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const uint4 za = z[2 * e], zb = z[2 * e + 1];
+    int dot = 0;
+    dot = dot4(v[e][0], za.x, dot);
+    dot = dot4(v[e][1], za.y, dot);
+    dot = dot4(v[e][2], za.z, dot);
+    dot = dot4(v[e][3], za.w, dot);
+    dot = dot4(v[e][4], zb.x, dot);
+    dot = dot4(v[e][5], zb.y, dot);
+    dot = dot4(v[e][6], zb.z, dot);
+    dot = dot4(v[e][7], zb.w, dot);
+    const float a = e ? au.z : au.x, u = e ? au.w : au.y;
+    X = fmaf(a * s[e], float(dot), X);
+    Y = fmaf(u, m[e], Y);
+  }
+  acc = fmaf(-dmin, Y, fmaf(d, X, acc));
+}
+
+// consume_core per token with the activations of tile kb read from LDS.
+template <uint16_t Layout, int MT, bool Fast>
+__device__ __forceinline__ void consume(const Tile& t, uint32_t kb, uint32_t g0, bool hi,
+                                        uint32_t sh, const int8_t* sz, const float2* sau,
+                                        uint32_t groups, float acc[MT]) {
 #pragma unroll
   for (int tk = 0; tk < MT; ++tk) {
     const uint32_t gi = tk * groups + kb * 8 + g0;
     const uint4* zp = reinterpret_cast<const uint4*>(sz + size_t(gi) * 32);
+    const uint4 z[4] = {zp[0], zp[1], zp[2], zp[3]};
     const float4 au = *reinterpret_cast<const float4*>(sau + gi);  // (a0, u0, a1, u1)
-    float X = 0.f, Y = 0.f;
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const uint4 za = zp[2 * e], zb = zp[2 * e + 1];
-      int dot = 0;
-      dot = dot4(v[e][0], za.x, dot);
-      dot = dot4(v[e][1], za.y, dot);
-      dot = dot4(v[e][2], za.z, dot);
-      dot = dot4(v[e][3], za.w, dot);
-      dot = dot4(v[e][4], zb.x, dot);
-      dot = dot4(v[e][5], zb.y, dot);
-      dot = dot4(v[e][6], zb.z, dot);
-      dot = dot4(v[e][7], zb.w, dot);
-      const float a = e ? au.z : au.x, u = e ? au.w : au.y;
-      X = fmaf(a * s[e], float(dot), X);
-      Y = fmaf(u, m[e], Y);
-    }
-    acc[tk] = fmaf(-dmin, Y, fmaf(d, X, acc[tk]));
+    consume_core<Layout>(t, hi, sh, z, au, acc[tk]);
   }
 }
 

@@ -57,7 +57,7 @@ constexpr uint32_t kHidden = 5120;
 // cuda/activation.cu:134-190: absmax prescale, sum of squares,
 // (1+gamma)*x/rms -> BF16 RNE, then by Mode:
 //   kRmsBf16   the BF16 row is the output (hidden_rms_kernel<0>);
-//   kRmsQ8     Q8 pack of the BF16 row (hidden_rms_kernel<3>);
+//   (the Q8 pack of the BF16 row, hidden_rms_kernel<3>, is rms_q8_wide_kernel)
 //   kRmsNvfp4  NVFP4 pack (hidden_rms_kernel<1>, cuda/nvfp4_device.cuh:18-49);
 //   kRmsFp8    FP8 pack into codes [pm][5120] / scales [40][pm], the BF16 row
 //              also stored when out_bf16 is given (hidden_rms_kernel<2>,
@@ -137,13 +137,6 @@ __global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ resi
     if constexpr (Mode == kRmsFp8)
       if (out_bf16) out_bf16[size_t(blockIdx.x) * kHidden + i] = yv[j];
   }
-  if constexpr (Mode == kRmsQ8) {
-    // element t + 256 j sits in group 8 j + t / 32 at lane t % 32 of its half
-#pragma unroll
-    for (int j = 0; j < kPer; ++j)
-      q8_group32(bf16_to_f32(yv[j]), reinterpret_cast<int8_t*>(codes), scales, sums,
-                 (size_t(blockIdx.x) * kHidden + threadIdx.x + 256 * j) / 32, failure);
-  }
   if constexpr (Lds) {
     __syncthreads();
     if constexpr (Mode == kRmsNvfp4) {
@@ -161,6 +154,71 @@ __global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ resi
         fp8_block128(bf16_to_f32(rounded[b * 128 + lane]), bf16_to_f32(rounded[b * 128 + 64 + lane]),
                      blockIdx.x, b, gridDim.x, codes, scales);
     }
+  }
+}
+
+// RMS -> Q8 with 16 waves per row (the fused producer of the Q8 MLP). The
+// sum of squares keeps rms_kernel's order: waves 0-3 run the 256 strided
+// per-thread chains and the same two-level tree; the absmax (order-free)
+// and the Q8 pack are spread over all 1024 threads, a K32 group per 32-lane
+// half, so a row's 160 groups take 5 pack steps per half instead of 20.
+// The same arithmetic as rms_kernel with the Q8 pack of the BF16 row.
+__global__ __launch_bounds__(1024) void rms_q8_wide_kernel(const float* __restrict__ residual,
+                                                           const uint16_t* __restrict__ gamma, float eps,
+                                                           int8_t* codes, float* scales, int32_t* sums,
+                                                           int* failure) {
+  constexpr int kPer = kHidden / 256, kGroups = kHidden / 32, kHalves = 32, kSteps = kGroups / kHalves;
+  __shared__ float sm[16];
+  __shared__ float bc[2];
+  const uint32_t tid = threadIdx.x, lane32 = tid & 31u, half = tid >> 5;
+  const float* x = residual + size_t(blockIdx.x) * kHidden;
+  // pack mapping: half h owns groups h + 32 s, lane l element 32 g + l
+  float xv[kSteps], gv[kSteps];
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    const uint32_t i = (half + kHalves * st) * 32 + lane32;
+    xv[st] = x[i];
+    gv[st] = bf16_to_f32(gamma[i]);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) s = fmaxf(s, fabsf(xv[st]));
+#pragma unroll
+  for (int off = 32; off; off >>= 1) s = fmaxf(s, __shfl_xor(s, off));
+  if ((tid & 63u) == 0) sm[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.f;
+    for (int w = 0; w < 16; ++w) t = fmaxf(t, sm[w]);
+    bc[0] = t;
+  }
+  __syncthreads();
+  const float scale = bc[0];
+  const float safe = scale == 0.f ? 1.f : scale;
+  if (tid < 256) {  // rms_kernel's chains: element tid + 256 j in increasing j
+    float sq = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const float q = x[tid + 256 * j] / safe;
+      sq = fmaf(q, q, sq);
+    }
+    sq = tree32_sum(sq);
+    if (lane32 == 0) sm[tid >> 5] = sq;
+  }
+  __syncthreads();
+  if (tid < 32) {
+    float t = lane32 < 8 ? sm[lane32] : 0.f;
+    t = tree32_sum(t);
+    if (lane32 == 0) bc[1] = t;
+  }
+  __syncthreads();
+  const float sumsq = bc[1];
+  const float se = sqrtf(eps) / safe;
+  const float inv = 1.0f / sqrtf(fmaf(se, se, sumsq / float(kHidden)));
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    const float y = bf16_to_f32(f32_to_bf16_rne((1.0f + gv[st]) * ((xv[st] / safe) * inv)));
+    q8_group32(y, codes, scales, sums, size_t(blockIdx.x) * kGroups + half + kHalves * st, failure);
   }
 }
 
@@ -191,8 +249,8 @@ hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t p
 hipError_t launch_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
                          int8_t* codes, float* scales, int32_t* sums, int* failure,
                          hipStream_t s) {
-  hipLaunchKernelGGL(rms_kernel<kRmsQ8>, dim3(m), dim3(256), 0, s, residual, gamma, eps, nullptr, m,
-                     reinterpret_cast<uint8_t*>(codes), scales, sums, failure, nullptr);
+  hipLaunchKernelGGL(rms_q8_wide_kernel, dim3(m), dim3(1024), 0, s, residual, gamma, eps, codes, scales, sums,
+                     failure);
   return hipGetLastError();
 }
 
