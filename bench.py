@@ -59,11 +59,21 @@ def measured_traffic(layout):
         text = open(path).read()
     except OSError:
         return None
+    # sections start at their "command:" line; the kernel's value comes from the
+    # section that profiled the decode leg, the copy's from --copy-calibration
+    sections = re.split(r"(?m)^(?=command:)", text)
     vals = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        g = re.search(kernel + r"[^\n]*\(dispatches=\d+\):[^\n]*\b" + counter + r"=([\d.e+]+)", text)
-        c = re.search(r"__amd_rocclr_copyBuffer[^\n]*\(dispatches=\d+\):[^\n]*\b" + counter +
-                      r"=([\d.e+]+)", text)
+        g = c = None
+        for sec in sections:
+            head = sec.split("\n", 1)[0]
+            if not head.startswith("command:") or ("--pmc " + counter) not in head:
+                continue
+            if "--copy-calibration" in head:
+                c = c or re.search(r"__amd_rocclr_copyBuffer[^\n]*\(dispatches=\d+\):[^\n]*\b" + counter +
+                                   r"=([\d.e+]+)", sec)
+            else:
+                g = g or re.search(kernel + r"[^\n]*\(dispatches=\d+\):[^\n]*\b" + counter + r"=([\d.e+]+)", sec)
         if not g or not c:
             return None
         scale = (1 << 20) / float(c.group(1))  # KiB the counter should read for 1 GiB

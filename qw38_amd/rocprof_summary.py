@@ -5,12 +5,14 @@
 Prints, per kernel instantiation and grid size: dispatch count and average /
 min / max duration (us), and,
 when the run collected ``--pmc`` counters, the per-dispatch average of every
-counter. Used to turn rocprofv3 runs into the text summaries under profiles/.
+counter; with ``--marker-trace``, the host-side duration of every roctx range
+name. Used to turn rocprofv3 runs into the text summaries under profiles/.
 """
 from __future__ import annotations
 
 import argparse
 import collections
+import json
 import re
 import sqlite3
 import sys
@@ -91,6 +93,24 @@ def summarize(path: str, match: str | None = None, top: int = 12) -> str:
         elif "kernel_name" in cols:
             out.append("")
             out.append("counters present but no grid column: " + ", ".join(cols))
+    # roctx ranges (--marker-trace): host-side duration per range name
+    if "regions" in names:
+        rows = db.execute("select category, name, start, end, extdata from regions "
+                          "where upper(category) like '%MARKER%'").fetchall()
+        rng = collections.defaultdict(list)
+        for cat, name, s, e, ext in rows:
+            try:  # the range's message, when the profiler recorded one
+                name = json.loads(ext).get("message", name) if ext else name
+            except (ValueError, AttributeError):
+                pass
+            if match and match not in name:
+                continue
+            rng[name].append((e - s) / 1e3)
+        if rng:
+            out.append("")
+            out.append(f"{'roctx range (host)':<96} {'calls':>6} {'avg_us':>9} {'min_us':>9}")
+            for name, v in sorted(rng.items(), key=lambda kv: -sum(kv[1]))[:top]:
+                out.append(f"{name[:96]:<96} {len(v):>6} {sum(v)/len(v):>9.3f} {min(v):>9.3f}")
     return "\n".join(out)
 
 

@@ -7,6 +7,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -49,14 +50,21 @@ struct Bytes {
   void pad_to(std::size_t a) { while (b.size() % a) b.push_back(0); }
 };
 
+// Payload / scale spans of one tensor record (offset, length).
+struct WSpans {
+  std::uint64_t po, pl, so, sl;
+};
+
 // payload_length_override != 0 writes that length into the first tensor's
-// payload span (the bytes written stay the real ones): a sealed manifest with a
-// span the reader must reject.
+// payload span (the bytes written stay the real ones); edit, when given,
+// rewrites the recorded spans before the manifest is sealed: manifests with a
+// valid digest and spans the reader must reject.
 inline std::vector<std::uint8_t> write_artifact(std::vector<WTensor> const& ts, std::vector<WShared> const& sh,
-                                         std::uint64_t payload_length_override = 0) {
+                                         std::uint64_t payload_length_override = 0,
+                                         std::function<void(std::vector<WSpans>&)> const& edit = {}) {
   Bytes f;
   f.zeros(64);  // header, filled last
-  struct Spans { std::uint64_t po, pl, so, sl; };
+  using Spans = WSpans;
   std::vector<Spans> spans;
   for (auto const& t : ts) {
     Spans s{0, 0, 0, 0};
@@ -75,6 +83,7 @@ inline std::vector<std::uint8_t> write_artifact(std::vector<WTensor> const& ts, 
     spans.push_back(s);
   }
   f.pad_to(256);
+  if (edit) edit(spans);
   const std::uint64_t moff = f.b.size();
   Bytes m;
   m.u16(1);                 // manifest version

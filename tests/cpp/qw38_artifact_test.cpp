@@ -145,6 +145,17 @@ void test_reader() {
     expect(bool(r), "odd-length payload still parses (length checks belong to the upload)");
   }
   {
+    auto r = parse(write_artifact(ts, sh, 0, [](std::vector<WSpans>& sp) { sp[1].po += 16; }));
+    expect(!r && r.error().code == F::FormatErrorCode::Misaligned, "span offset off the 256-byte grid rejected");
+  }
+  {
+    // the second payload starts 256 bytes into the first
+    auto r = parse(write_artifact(ts, sh, 0, [](std::vector<WSpans>& sp) { sp[1].po = sp[0].po + 256; }));
+    expect(!r && (r.error().code == F::FormatErrorCode::OverlappingSpan ||
+                  r.error().code == F::FormatErrorCode::InvalidSpan),
+           "overlapping payload spans rejected" + (r ? std::string() : " (" + F::error_message(r.error()) + ")"));
+  }
+  {
     // alias record whose owner has no payload
     auto r = parse(write_artifact(ts, {{4, 1}}));
     expect(!r && r.error().code == F::FormatErrorCode::SharedBinding, "alias of a byte-less owner rejected");
