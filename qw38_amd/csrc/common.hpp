@@ -161,6 +161,83 @@ __device__ __forceinline__ void q8_group32(float x, int8_t* codes, float* scales
   }
 }
 
+// 32-lane shuffle-down tree (lane i += lane i+off), result valid in lane 0 of
+// each half: the warp-32 order of cuda/activation.cu:36-50.
+__device__ __forceinline__ float tree32_sum(float v) {
+#pragma unroll
+  for (int off = 16; off; off >>= 1) v += __shfl_down(v, off, 32);
+  return v;
+}
+
+constexpr uint32_t kRmsHidden = 5120;
+
+// RMS -> BF16 -> Q8 of one 5120-element row by a block of NT threads (512 or
+// 1024): cuda/activation.cu:134-190 with the Q8 pack of hidden_rms_kernel<3>.
+// The sum of squares keeps the reference kernel's order: threads 0..255 run
+// the strided per-thread chains (element t + 256 j, increasing j) and the
+// two-level tree (eight 32-lane trees, then one over the 8 partials and 24
+// zeros). The absmax (order-free) and the Q8 pack are spread over all NT
+// threads, a K32 group per 32-lane half. sm is >= 18 floats of LDS. Ends
+// with the block synchronised.
+template <int NT>
+__device__ __forceinline__ void rms_q8_row(const float* __restrict__ x, const uint16_t* __restrict__ gamma,
+                                           float eps, int8_t* codes, float* scales, int32_t* sums,
+                                           int* failure, float* sm) {
+  constexpr int kPer = kRmsHidden / 256, kGroups = kRmsHidden / 32, kHalves = NT / 32;
+  constexpr int kSteps = kGroups / kHalves, kWaves = NT / 64;
+  static_assert(kSteps * kHalves == kGroups && kWaves <= 16, "block shape");
+  const uint32_t tid = threadIdx.x, lane32 = tid & 31u, half = tid >> 5;
+  float xv[kSteps], gv[kSteps];
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {  // half h owns groups h + kHalves s
+    const uint32_t i = (half + kHalves * st) * 32 + lane32;
+    xv[st] = x[i];
+    gv[st] = bf16_to_f32(gamma[i]);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) s = fmaxf(s, fabsf(xv[st]));
+#pragma unroll
+  for (int off = 32; off; off >>= 1) s = fmaxf(s, __shfl_xor(s, off));
+  if ((tid & 63u) == 0) sm[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.f;
+    for (int w = 0; w < kWaves; ++w) t = fmaxf(t, sm[w]);
+    sm[16] = t;
+  }
+  __syncthreads();
+  const float scale = sm[16];
+  const float safe = scale == 0.f ? 1.f : scale;
+  __syncthreads();  // sm[0..7] is rewritten below
+  if (tid < 256) {
+    float sq = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const float q = x[tid + 256 * j] / safe;
+      sq = fmaf(q, q, sq);
+    }
+    sq = tree32_sum(sq);
+    if (lane32 == 0) sm[tid >> 5] = sq;
+  }
+  __syncthreads();
+  if (tid < 32) {
+    float t = lane32 < 8 ? sm[lane32] : 0.f;
+    t = tree32_sum(t);
+    if (lane32 == 0) sm[17] = t;
+  }
+  __syncthreads();
+  const float sumsq = sm[17];
+  const float se = sqrtf(eps) / safe;
+  const float inv = 1.0f / sqrtf(fmaf(se, se, sumsq / float(kRmsHidden)));
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    const float y = bf16_to_f32(f32_to_bf16_rne((1.0f + gv[st]) * ((xv[st] / safe) * inv)));
+    q8_group32(y, codes, scales, sums, half + kHalves * st, failure);
+  }
+  __syncthreads();
+}
+
 // Byte offsets of the 16-byte code word of (row, super-block kb, K32 group g)
 // and of the 16-byte metadata row of (row, kb).
 // 0x020D: tile row ((row/8)*kbs + kb)*8 + row%8; codes 128 B per tile row

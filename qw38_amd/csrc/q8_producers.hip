@@ -21,13 +21,6 @@ __global__ __launch_bounds__(256) void pack_q8_kernel(const uint16_t* __restrict
   q8_group32(x, codes, scales, sums, (size_t(row) * pk + c) / 32, failure);
 }
 
-// 32-lane shuffle-down tree (lane i += lane i+off), result valid in lane 0 of
-// each half: the warp-32 order of cuda/activation.cu:36-50.
-__device__ __forceinline__ float tree32_sum(float v) {
-#pragma unroll
-  for (int off = 16; off; off >>= 1) v += __shfl_down(v, off, 32);
-  return v;
-}
 __device__ __forceinline__ float tree32_max(float v) {
 #pragma unroll
   for (int off = 16; off; off >>= 1) v = fmaxf(v, __shfl_down(v, off, 32));
@@ -157,69 +150,15 @@ __global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ resi
   }
 }
 
-// RMS -> Q8 with 16 waves per row (the fused producer of the Q8 MLP). The
-// sum of squares keeps rms_kernel's order: waves 0-3 run the 256 strided
-// per-thread chains and the same two-level tree; the absmax (order-free)
-// and the Q8 pack are spread over all 1024 threads, a K32 group per 32-lane
-// half, so a row's 160 groups take 5 pack steps per half instead of 20.
-// The same arithmetic as rms_kernel with the Q8 pack of the BF16 row.
+// RMS -> Q8 with 16 waves per row (rms_q8_row in common.hpp).
 __global__ __launch_bounds__(1024) void rms_q8_wide_kernel(const float* __restrict__ residual,
                                                            const uint16_t* __restrict__ gamma, float eps,
                                                            int8_t* codes, float* scales, int32_t* sums,
                                                            int* failure) {
-  constexpr int kPer = kHidden / 256, kGroups = kHidden / 32, kHalves = 32, kSteps = kGroups / kHalves;
-  __shared__ float sm[16];
-  __shared__ float bc[2];
-  const uint32_t tid = threadIdx.x, lane32 = tid & 31u, half = tid >> 5;
-  const float* x = residual + size_t(blockIdx.x) * kHidden;
-  // pack mapping: half h owns groups h + 32 s, lane l element 32 g + l
-  float xv[kSteps], gv[kSteps];
-#pragma unroll
-  for (int st = 0; st < kSteps; ++st) {
-    const uint32_t i = (half + kHalves * st) * 32 + lane32;
-    xv[st] = x[i];
-    gv[st] = bf16_to_f32(gamma[i]);
-  }
-  float s = 0.f;
-#pragma unroll
-  for (int st = 0; st < kSteps; ++st) s = fmaxf(s, fabsf(xv[st]));
-#pragma unroll
-  for (int off = 32; off; off >>= 1) s = fmaxf(s, __shfl_xor(s, off));
-  if ((tid & 63u) == 0) sm[tid >> 6] = s;
-  __syncthreads();
-  if (tid == 0) {
-    float t = 0.f;
-    for (int w = 0; w < 16; ++w) t = fmaxf(t, sm[w]);
-    bc[0] = t;
-  }
-  __syncthreads();
-  const float scale = bc[0];
-  const float safe = scale == 0.f ? 1.f : scale;
-  if (tid < 256) {  // rms_kernel's chains: element tid + 256 j in increasing j
-    float sq = 0.f;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const float q = x[tid + 256 * j] / safe;
-      sq = fmaf(q, q, sq);
-    }
-    sq = tree32_sum(sq);
-    if (lane32 == 0) sm[tid >> 5] = sq;
-  }
-  __syncthreads();
-  if (tid < 32) {
-    float t = lane32 < 8 ? sm[lane32] : 0.f;
-    t = tree32_sum(t);
-    if (lane32 == 0) bc[1] = t;
-  }
-  __syncthreads();
-  const float sumsq = bc[1];
-  const float se = sqrtf(eps) / safe;
-  const float inv = 1.0f / sqrtf(fmaf(se, se, sumsq / float(kHidden)));
-#pragma unroll
-  for (int st = 0; st < kSteps; ++st) {
-    const float y = bf16_to_f32(f32_to_bf16_rne((1.0f + gv[st]) * ((xv[st] / safe) * inv)));
-    q8_group32(y, codes, scales, sums, size_t(blockIdx.x) * kGroups + half + kHalves * st, failure);
-  }
+  __shared__ float sm[18];
+  const size_t row = blockIdx.x;
+  rms_q8_row<1024>(residual + row * kRmsHidden, gamma, eps, codes + row * kRmsHidden,
+                   scales + row * (kRmsHidden / 32), sums + row * (kRmsHidden / 32), failure, sm);
 }
 
 // cuda/q4k_q8.cu:52-61: v = BF16(SiLU(g) * u); nonfinite g/u -> NaN -> flag.

@@ -241,3 +241,50 @@ def test_gate_up_swiglu_rejections(torch_gpu, mlp_weights):
         ops.q4k_q8_gate_up_swiglu(gate, up, qx, ops.Q8Input.empty(8, 17408), flag)
     with pytest.raises(Qw38Error):  # failure flag length
         ops.q4k_q8_gate_up_swiglu(gate, up, qx, out, torch.zeros(2, dtype=torch.int32, device="cuda"))
+
+
+@pytest.mark.parametrize("down", ["down4", "down6"])
+def test_q8_mlp_m1_fused_equals_chain(torch_gpu, mlp_weights, down):
+    """M = 1 on 0x020D runs the RMS->Q8 producer, then gate, up and SwiGLU->Q8
+    as ONE streaming launch, then down + residual. The output and the down
+    operand equal the unfused chain of separate entry points bit for bit; a
+    NaN in the residual raises the flag."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    from qw38_amd import Qw38Error
+    _, gl = mlp_weights["gate"]
+    _, ul = mlp_weights["up"]
+    seq = oracle.LAYOUT_Q4K_SEQ
+    gate = ops.PrefillWeight.from_bytes(*gl.physical(seq), seq, gl.n, gl.k)
+    up = ops.PrefillWeight.from_bytes(*ul.physical(seq), seq, ul.n, ul.k)
+    dn, _ = mlp_weights[down]
+    gamma = oracle.fp32_to_bf16(normal(5120, 110, 0.1))
+    dgam = _dev(torch, gamma.view(np.int16))
+    for seed in (111, 112):
+        res = _dev(torch, normal((1, 5120), seed) * 3)
+        ws = torch.zeros(ops.q8_mlp_workspace_bytes(1), dtype=torch.uint8, device="cuda")
+        out = torch.empty(1, 5120, device="cuda")
+        ops.q4k_q8_mlp(gate, up, dn, res, dgam, 1e-6, out, 1, ws)
+        qx = ops.Q8Input.empty(1, 5120)
+        flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+        ops.hidden_rms_q8(res, dgam, 1e-6, 1, qx, flag)
+        gd = torch.empty(1, 17408, device="cuda")
+        ud = torch.empty(1, 17408, device="cuda")
+        ops.q4k_q8_project(gate, qx, gd)
+        ops.q4k_q8_project(up, qx, ud)
+        qh = ops.Q8Input.empty(1, 17408)
+        ops.swiglu_q8(gd, ud, 1, 17408, qh, flag)
+        ref = torch.empty(1, 5120, device="cuda")
+        ops.q4k_q8_project(dn, qh, ref, residual=res)
+        torch.cuda.synchronize()
+        assert int(flag.item()) == 0
+        codes, scales, sums, _, _ = _workspace_views(ws, 1)
+        assert np.array_equal(codes, qh.codes.cpu().numpy())
+        assert np.array_equal(scales.view(np.uint32), qh.scales.cpu().numpy().view(np.uint32))
+        assert np.array_equal(sums, qh.sums.cpu().numpy())
+        assert torch.equal(out, ref)
+    bad = res.clone()
+    bad[0, 4000] = float("nan")
+    with pytest.raises(Qw38Error) as e:
+        ops.q4k_q8_mlp(gate, up, dn, bad, dgam, 1e-6, out, 1, ws)
+    assert e.value.operation == "q8.producer"
