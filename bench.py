@@ -531,6 +531,7 @@ def main():
     ap.add_argument("--no-model", action="store_true", help="skip the config-5 model pass")
     ap.add_argument("--no-mlp", action="store_true", help="skip the whole-MLP leg")
     ap.add_argument("--no-q6", action="store_true", help="skip the config-3 Q6_K decode leg")
+    ap.add_argument("--q6-decode-m", default="1,8", help="config-3 token counts to time")
     ap.add_argument("--no-config1", action="store_true")
     ap.add_argument("--mmq-shapes", default="all", help="'all' (config 4) or 'headline'")
     ap.add_argument("--model-layers", type=int, default=64)
@@ -606,8 +607,8 @@ def main():
                           outliers=False)
         rooflines["config1_m1"] = c1[1]
     if not args.no_q6:
-        c3 = bench_decode(torch, ops, "q6k", 5120, 17408, [1, 8], args.steps, args.warmup,
-                          0x0241, 61, outliers=False)
+        c3 = bench_decode(torch, ops, "q6k", 5120, 17408, [int(v) for v in args.q6_decode_m.split(",")],
+                          args.steps, args.warmup, 0x0241, 61, outliers=False)
         for m, v in c3.items():
             rooflines[f"config3_m{m}"] = v
     if not args.no_mmq:

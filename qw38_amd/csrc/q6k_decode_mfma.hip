@@ -36,8 +36,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-template <int TP, int W, int PD>
-__global__ __launch_bounds__(W * 64) void q6k_mfma_decode_kernel(
+template <int TP, int W, int PD, int Occ = 1>
+__global__ __launch_bounds__(W * 64, Occ) void q6k_mfma_decode_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n, uint32_t pn,
     uint32_t kbs, const int8_t* __restrict__ xc, const float* __restrict__ xa, uint32_t m,
     uint32_t pk, float* __restrict__ out, const float* __restrict__ residual, uint32_t tiles) {
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(W * 64) void q6k_mfma_decode_kernel(
   }
 }
 
-template <int TP, int W, int PD>
+template <int TP, int W, int PD, int Occ = 1>
 hipError_t launch_t(const WeightView& w, const Q8View& x, float* out, const float* residual,
                     hipStream_t s, uint32_t per_cu_cap) {
   constexpr int T = 4 * TP;
@@ -206,7 +206,7 @@ hipError_t launch_t(const WeightView& w, const Q8View& x, float* out, const floa
   uint32_t per_cu = std::max<uint32_t>(1, std::min<uint32_t>(uint32_t(160 * 1024 / lds), 32u / W));
   if (per_cu_cap) per_cu = std::min(per_cu, per_cu_cap);
   const uint32_t grid = std::min<uint32_t>(tiles, uint32_t(cu_count()) * per_cu);
-  auto kern = q6k_mfma_decode_kernel<TP, W, PD>;
+  auto kern = q6k_mfma_decode_kernel<TP, W, PD, Occ>;
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
@@ -236,8 +236,13 @@ hipError_t launch_q6k_mfma_decode(const WeightView& w, const Q8View& x, float* o
   if ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(x.codes)) % 16 ||
       reinterpret_cast<uintptr_t>(w.scales) % 4)
     return hipErrorNotSupported;
+  // M 5..8 (two token passes): no load ring, bounded to four waves per SIMD
+  // (112 VGPRs), so all 320 tiles of the 5120-row down projection are
+  // resident at once; with the ring it needs 186 VGPRs, one block per CU and
+  // a second round (config 3, M=8: 38.2 against 43.1 us). M 3..4 keeps the
+  // ring (118 VGPRs either way).
   return x.m <= 4 ? launch_t<1, 8, 1>(w, x, out, residual, s, cap)
-                  : launch_t<2, 8, 1>(w, x, out, residual, s, cap);
+                  : launch_t<2, 8, 0, 4>(w, x, out, residual, s, cap);
 }
 
 }  // namespace qw38hip
