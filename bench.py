@@ -522,7 +522,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20, help="timed rotations of the headline leg")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layout", default="0x020D", help="decode weight layout")
-    ap.add_argument("--mmq-layout", default="0x0240", help="MMQ weight layout")
+    ap.add_argument("--mmq-layout", default="0x020D", help="MMQ weight layout")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-mmq", action="store_true")

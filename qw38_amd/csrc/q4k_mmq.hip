@@ -739,7 +739,8 @@ hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const fl
 template <uint16_t Layout, bool Glu = false>
 hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const float* residual,
                         hipStream_t s, GluOut glu = {}) {
-  // QW38_MMQ_TILE=32|64|128 pins the token tile (256: 256 rows x 128 tokens);
+  // QW38_MMQ_TILE=32|64|128 pins the token tile (256: 256 rows x 128 tokens;
+  // 80: 80 x 128; 129: 128 x 128 with eight waves);
   // QW38_MMQ_SPLIT=0 disables the tail split (tuning aids; every tile shape
   // and split gives bitwise-identical results).
   static const int forced = [] {
@@ -793,12 +794,21 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   // 512-token chunk fills 256 CUs in one round where 128-row tiles leave 96
   // idle. Step time about 0.7 of the 128 x 128 tile's.
   const double c80 = per_cu(80, 128) * (q6 ? 1.77 : 1.9) * 0.7;
+  // 128 x 128 with eight waves (two per SIMD, like the 256 x 128 tile; Q4_K
+  // only): 1.18 us per step at one block per CU. It wins where 256-row
+  // tiles leave CUs idle and the four-wave tiles lack the second wave per
+  // SIMD, e.g. the 5120 x 6144 projection at M = 512 (114 against 133 us).
+  const double c129 = q6 ? 1e30 : per_cu(128, 128) * 1.18;
   int bt = 32;
-  if (x.m > 32 && c64 < c32) bt = 64;
-  if (x.m > 64 && c_big < (bt == 64 ? c64 : c32)) bt = 256;
-  if (x.m > 64 && !Glu && c80 < std::min({c_big, c64, c32})) bt = 80;
+  double best = c32;
+  if (x.m > 32 && c64 < best) bt = 64, best = c64;
+  if (x.m > 64 && c_big < best) bt = 256, best = c_big;
+  if (x.m > 64 && !Glu && c80 < best) bt = 80, best = c80;
+  if (x.m > 64 && c129 < best) bt = 129, best = c129;
   if (forced) bt = forced;
   if (bt == 80) return launch_cfg<Layout, 1, 4, 5, 2>(w, x, out, residual, s, 0, pn);  // 80 x 128
+  if constexpr (!q6)
+    if (bt == 129) return launch_cfg<Layout, 2, 4, 4, 2, Glu>(w, x, out, residual, s, 0, pn / kv, glu);  // 128 x 128, 8 waves
   const uint32_t end = pn / kv;
   if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 32
   if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 64
