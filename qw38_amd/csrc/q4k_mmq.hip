@@ -740,7 +740,7 @@ template <uint16_t Layout, bool Glu = false>
 hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const float* residual,
                         hipStream_t s, GluOut glu = {}) {
   // QW38_MMQ_TILE=32|64|128 pins the token tile (256: 256 rows x 128 tokens;
-  // 80: 80 x 128; 129: 128 x 128 with eight waves);
+  // 80: 80 x 128; 129: 128 x 128 and 192: 192 x 128 with eight waves);
   // QW38_MMQ_SPLIT=0 disables the tail split (tuning aids; every tile shape
   // and split gives bitwise-identical results).
   static const int forced = [] {
@@ -799,16 +799,22 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   // tiles leave CUs idle and the four-wave tiles lack the second wave per
   // SIMD, e.g. the 5120 x 6144 projection at M = 512 (114 against 133 us).
   const double c129 = q6 ? 1e30 : per_cu(128, 128) * 1.18;
+  // 192 x 128 on eight waves (Q4_K, unfused): 1.82 us per step; a 12288-row
+  // weight makes 64 row blocks, one full round at M = 512 (146 against 162 us).
+  const double c192 = (q6 || Glu) ? 1e30 : per_cu(192, 128) * 1.82;
   int bt = 32;
   double best = c32;
   if (x.m > 32 && c64 < best) bt = 64, best = c64;
   if (x.m > 64 && c_big < best) bt = 256, best = c_big;
   if (x.m > 64 && !Glu && c80 < best) bt = 80, best = c80;
   if (x.m > 64 && c129 < best) bt = 129, best = c129;
+  if (x.m > 64 && c192 < best) bt = 192, best = c192;
   if (forced) bt = forced;
   if (bt == 80) return launch_cfg<Layout, 1, 4, 5, 2>(w, x, out, residual, s, 0, pn);  // 80 x 128
   if constexpr (!q6)
     if (bt == 129) return launch_cfg<Layout, 2, 4, 4, 2, Glu>(w, x, out, residual, s, 0, pn / kv, glu);  // 128 x 128, 8 waves
+  if constexpr (!q6 && !Glu)
+    if (bt == 192) return launch_cfg<Layout, 4, 2, 3, 4>(w, x, out, residual, s, 0, pn);  // 192 x 128, 8 waves
   const uint32_t end = pn / kv;
   if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 32
   if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 64
