@@ -128,7 +128,8 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   // A staging: APT threads per (row, group), AW code words each. Tiles with
   // fewer (row, group) items than threads (80 rows) leave the last threads
   // out of A staging: they load a duplicate item and store nothing.
-  constexpr int APT = NT / (2 * BR) > 0 ? NT / (2 * BR) : 1, AW = 4 / APT;
+  constexpr int APT0 = NT / (2 * BR);
+  constexpr int APT = (APT0 == 1 || (APT0 == 2 && NT == 4 * BR && !kQ6)) ? APT0 : 1, AW = 4 / APT;
   static_assert((APT * 2 * BR == NT || (APT == 1 && 2 * BR < NT)) && (APT == 1 || (APT == 2 && !kQ6)),
                 "A staging share");
   constexpr int BB = BT * 64 / NT;  // B bytes staged per thread per step
@@ -740,7 +741,8 @@ template <uint16_t Layout, bool Glu = false>
 hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const float* residual,
                         hipStream_t s, GluOut glu = {}) {
   // QW38_MMQ_TILE=32|64|128 pins the token tile (256: 256 rows x 128 tokens;
-  // 80: 80 x 128; 129: 128 x 128 and 192: 192 x 128 with eight waves);
+  // 80: 80 x 128 on four waves; 81, 129, 192: 80 x 128, 128 x 128 and
+  // 192 x 128 on eight waves);
   // QW38_MMQ_SPLIT=0 disables the tail split (tuning aids; every tile shape
   // and split gives bitwise-identical results).
   static const int forced = [] {
@@ -790,10 +792,13 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   const double c_big = b_big * (q6 ? 1.77 : 1.9);
   const double c64 = q6 ? two(per_cu(128, 64), 1.33, 2.65) : two(per_cu(128, 64), 1.07, 1.39);
   const double c32 = q6 ? two(per_cu(128, 32), 1.0, 2.0) : two(per_cu(128, 32), 0.70, 0.89);
-  // 80 x 128 (one block per CU): 5120-row weights make 64 row blocks, so a
-  // 512-token chunk fills 256 CUs in one round where 128-row tiles leave 96
-  // idle. Step time about 0.7 of the 128 x 128 tile's.
-  const double c80 = per_cu(80, 128) * (q6 ? 1.77 : 1.9) * 0.7;
+  // 80 x 128 on eight waves (one block per CU, two waves per SIMD; the
+  // four-wave 80 x 128 tile, QW38_MMQ_TILE=80, is always slower): 5120-row
+  // weights make 64 row blocks, so a 512-token chunk fills 256 CUs in one
+  // round where 128-row tiles leave 96 idle. 1.16 us per step for Q6_K (the
+  // down projection at M = 512: 315 against 393 us on four waves), 1.12 for
+  // Q4_K.
+  const double c81 = Glu ? 1e30 : per_cu(80, 128) * (q6 ? 1.16 : 1.12);
   // 128 x 128 with eight waves (two per SIMD, like the 256 x 128 tile; Q4_K
   // only): 1.18 us per step at one block per CU. It wins where 256-row
   // tiles leave CUs idle and the four-wave tiles lack the second wave per
@@ -806,7 +811,7 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   double best = c32;
   if (x.m > 32 && c64 < best) bt = 64, best = c64;
   if (x.m > 64 && c_big < best) bt = 256, best = c_big;
-  if (x.m > 64 && !Glu && c80 < best) bt = 80, best = c80;
+  if (x.m > 64 && c81 < best) bt = 81, best = c81;
   if (x.m > 64 && c129 < best) bt = 129, best = c129;
   if (x.m > 64 && c192 < best) bt = 192, best = c192;
   if (forced) bt = forced;
@@ -815,6 +820,8 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
     if (bt == 129) return launch_cfg<Layout, 2, 4, 4, 2, Glu>(w, x, out, residual, s, 0, pn / kv, glu);  // 128 x 128, 8 waves
   if constexpr (!q6 && !Glu)
     if (bt == 192) return launch_cfg<Layout, 4, 2, 3, 4>(w, x, out, residual, s, 0, pn);  // 192 x 128, 8 waves
+  if constexpr (!Glu)
+    if (bt == 81) return launch_cfg<Layout, 1, 8, 5, 1>(w, x, out, residual, s, 0, pn);  // 80 x 128, 8 waves
   const uint32_t end = pn / kv;
   if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 32
   if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 64
