@@ -581,12 +581,24 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   // registers, load step s+2 into them, then compute step s. The stores of the
   // last step and the loads of the last two land in the buffer and
   // super-block slot that no remaining step reads.
+  // Between two barriers the store of step s+1 and the compute of step s touch
+  // different LDS buffers and super-block slots, so either order is valid. In
+  // eight-wave tiles with small wave tiles the second wave of each SIMD
+  // (waves 4..7) computes first and stages second, so the two waves sharing a
+  // SIMD overlap staging with matrix-core work instead of passing the phases
+  // together. Wave tiles of at most 8 MFMA tiles (80 x 16, 32 x 64); larger
+  // ones (the 192 x 128 and 256 x 128 tiles) no longer fit the registers in
+  // this order and their arrays go to scratch (the 256 x 128 tile ran 14x
+  // slower).
+  constexpr bool kPingPong = WR * WT == 8 && NI * NJ <= 8;
+  const bool compute_first = kPingPong && wave >= 4;
   auto step = [&](auto qc, uint32_t kb) {
     constexpr uint32_t q = decltype(qc)::value;
     __syncthreads();  // step s staged; step s-1 fully consumed
+    if (compute_first) compute(qc, kb);
     store(std::integral_constant<uint32_t, (q + 1) & 3u>{}, kb + (q == 3 ? 1u : 0u), F);
     fetch(std::integral_constant<uint32_t, (q + 2) & 3u>{}, kb + (q >= 2 ? 1u : 0u), F);
-    compute(qc, kb);
+    if (!compute_first) compute(qc, kb);
   };
 
   fetch(std::integral_constant<uint32_t, 0>{}, 0, F);
@@ -795,15 +807,15 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   // 80 x 128 on eight waves (one block per CU, two waves per SIMD; the
   // four-wave 80 x 128 tile, QW38_MMQ_TILE=80, is always slower): 5120-row
   // weights make 64 row blocks, so a 512-token chunk fills 256 CUs in one
-  // round where 128-row tiles leave 96 idle. 1.16 us per step for Q6_K (the
-  // down projection at M = 512: 315 against 393 us on four waves), 1.12 for
+  // round where 128-row tiles leave 96 idle. 1.07 us per step for Q6_K (the
+  // down projection at M = 512: 290 against 393 us on four waves), 1.02 for
   // Q4_K.
-  const double c81 = Glu ? 1e30 : per_cu(80, 128) * (q6 ? 1.16 : 1.12);
+  const double c81 = Glu ? 1e30 : per_cu(80, 128) * (q6 ? 1.07 : 1.02);
   // 128 x 128 with eight waves (two per SIMD, like the 256 x 128 tile; Q4_K
   // only): 1.18 us per step at one block per CU. It wins where 256-row
   // tiles leave CUs idle and the four-wave tiles lack the second wave per
-  // SIMD, e.g. the 5120 x 6144 projection at M = 512 (114 against 133 us).
-  const double c129 = q6 ? 1e30 : per_cu(128, 128) * 1.18;
+  // SIMD (1.15 us per step at one block per CU).
+  const double c129 = q6 ? 1e30 : per_cu(128, 128) * 1.15;
   // 192 x 128 on eight waves (Q4_K, unfused): 1.82 us per step; a 12288-row
   // weight makes 64 row blocks, one full round at M = 512 (146 against 162 us).
   const double c192 = (q6 || Glu) ? 1e30 : per_cu(192, 128) * 1.82;
