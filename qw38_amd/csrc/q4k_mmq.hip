@@ -170,7 +170,10 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   const uint32_t asel = kRowMajorA ? aslot / BR : aslot & 1u;
   const uint32_t arow = min(row0 + (Glu ? ar % HR : ar), pn - 1);
   if constexpr (Glu) {  // the tile's up half reads the up weight
-    if (ar >= uint32_t(HR)) {
+    // A wave's staging rows lie in one aligned run of 16..64 rows and the
+    // gate / up boundary HR is a multiple of 64, so the choice is the same in
+    // every lane: taken from the first lane, the pointers stay scalar.
+    if (__builtin_amdgcn_readfirstlane(ar >= uint32_t(HR) ? 1 : 0)) {
       codes = glu.codes2;
       meta = glu.meta2;
     }
