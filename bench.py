@@ -538,7 +538,8 @@ def main():
     ap.add_argument("--model-layout", default="0x020D", help="Q4_K layout of the model pass")
     ap.add_argument("--eager-leg", default=None, metavar="FMT:N:K:M:CALLS",
                     help="only run CALLS eager projections of one shape (q4k on --layout, q6k on "
-                         "0x0241) over 12 rotated weight copies, for rocprofv3 traces and counters")
+                         "0x0241, over 12 rotated weight copies; bf16: the BF16 prefill projection "
+                         "over Q4_K 0x020D), for rocprofv3 traces and counters")
     ap.add_argument("--mlp-leg", default=None, metavar="M:CALLS",
                     help="only run CALLS eager whole-MLP calls at M tokens (Q4_K gate/up on --layout "
                          "for M <= 8, else --mmq-layout; Q6_K down), for rocprofv3 traces")
@@ -568,6 +569,15 @@ def main():
     if args.eager_leg:
         fmt, n_, k_, m_, calls = args.eager_leg.split(":")
         n_, k_, m_, calls = int(n_), int(k_), int(m_), int(calls)
+        if fmt == "bf16":  # BF16 PrefillEngine projection over Q4_K 0x020D
+            w, _ = make_weight(torch, ops, n_, k_, 11, 0x020D)
+            x = torch.randn(m_, k_, device="cuda").to(torch.bfloat16).view(torch.int16)
+            out = torch.empty(m_, n_, device="cuda")
+            for i in range(calls):
+                ops.prefill_project(w, x, m_, out, ops.DECODE_STORE_FP32)
+            torch.cuda.synchronize()
+            log(f"eager leg {args.eager_leg}: done")
+            return
         w, _ = make_any_weight(torch, ops, fmt, n_, k_, 11, layout if fmt == "q4k" else 0x0241)
         ws = [w] + [clone_weight(ops, w) for _ in range(11)]
         q, _ = make_q8(torch, ops, m_, k_, 5, outliers=(fmt == "q4k"))

@@ -12,8 +12,9 @@
 // Block: 128 weight rows x 64 tokens, four waves as 2 x 2, each a 64 x 32
 // wave tile of 16x16 outputs. Per 64-wide K step every thread rebuilds one
 // (row, K32 group) of the weight tile (v_cvt_pk_bf16_f32 on pairs) and copies
-// a quarter of a (token, K32 group) activation row; operands for step s+1
+// a quarter of a (token, K32 group) activation row; operands for step s+2
 // are loaded into registers while step s runs on the matrix cores.
+#include <cmath>
 #include <cstdlib>
 
 #include "common.hpp"
@@ -68,7 +69,10 @@ __device__ __forceinline__ void store_w(const WFetch& f, uint32_t g, _Float16* d
   uint32_t o[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {  // code word i = codes 8i..8i+7 (byte b: codes 2b, 2b+1)
-    const uint32_t lo = f.c[i] & 0x0f0f0f0fu, hv = (f.c[i] >> 4) & 0x0f0f0f0fu;
+    uint32_t lo = f.c[i] & 0x0f0f0f0fu, hv = (f.c[i] >> 4) & 0x0f0f0f0fu;
+    // Opaque to the optimizer, so each byte converts with one
+    // v_cvt_f32_ubyte{0..3} instead of a bit-field extract and a convert.
+    asm volatile("" : "+v"(lo), "+v"(hv));
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const fl2 wv = {fmaf(ds, float((lo >> (8 * q)) & 0xffu), ndm),
@@ -82,20 +86,22 @@ __device__ __forceinline__ void store_w(const WFetch& f, uint32_t g, _Float16* d
 }
 
 
-template <bool Paired, bool Fast>
+template <bool Paired, bool Fast, int TT = kToks>
 __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(
     const uint8_t* __restrict__ codes_a, const uint8_t* __restrict__ meta_a,
     const uint8_t* __restrict__ codes_b, const uint8_t* __restrict__ meta_b, uint32_t n,
     uint32_t k, const uint16_t* __restrict__ x, uint32_t m, void* out,
-    const float* __restrict__ residual, int epi, uint32_t row_blocks, uint32_t tok_blocks) {
-  constexpr int NW = Paired ? 2 : 1;
+    const float* __restrict__ residual, int epi, uint32_t row_blocks, uint32_t tok_blocks,
+    uint32_t row_base) {
+  constexpr int NW = Paired ? 2 : 1, NJ = TT / 32, HPT = TT / 4;  // HPT: activation halfs per thread
+  static_assert(TT == 32 || TT == 64, "token tile");
   __shared__ __align__(16) _Float16 As[NW][kRows * kStride];
-  __shared__ __align__(16) _Float16 Bs[kToks * kStride];
+  __shared__ __align__(16) _Float16 Bs[TT * kStride];
 
   const uint32_t nblk = row_blocks * tok_blocks;
   const uint32_t b = blockIdx.x;
   const uint32_t tile = (nblk % 8 == 0) ? (b % 8) * (nblk / 8) + b / 8 : b;  // XCD-contiguous
-  const uint32_t row0 = (tile / tok_blocks) * kRows, tok0 = (tile % tok_blocks) * kToks;
+  const uint32_t row0 = row_base + (tile / tok_blocks) * kRows, tok0 = (tile % tok_blocks) * TT;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wr = wave >> 1, wt = wave & 1u, lr = lane & 15u, lk = lane >> 4;
   const uint32_t kbs = k / 256, steps = k / 64;
@@ -105,54 +111,59 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(
   const uint32_t ar = tid >> 1, asel = tid & 1u;
   const uint32_t arow = min(row0 + ar, pn8 - 1);
   const uint64_t trow0 = uint64_t(arow / 8) * kbs * 8 + arow % 8;
-  const uint32_t bt = tid >> 2, bp = tid & 3u;
-  const uint16_t* xrow = x + size_t(min(tok0 + bt, m - 1)) * k + bp * 16;
+  const uint32_t bt = tid / (256 / TT), bp = tid % (256 / TT);
+  const uint16_t* xrow = x + size_t(min(tok0 + bt, m - 1)) * k + bp * HPT;
 
-  f4 acc[NW][4][2];
+  f4 acc[NW][4][NJ];
 #pragma unroll
   for (int w = 0; w < NW; ++w)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[w][i][j] = f4{0, 0, 0, 0};
+      for (int j = 0; j < NJ; ++j) acc[w][i][j] = f4{0, 0, 0, 0};
 
-  WFetch fa, fb;
-  uint32_t xv[8];
-  auto fetch = [&](uint32_t s) {
+  // Two register sets: step s+2's operands are loaded while step s runs, so
+  // a step never waits on the loads issued by the one before it.
+  struct Stage {
+    WFetch fa, fb;
+    uint32_t xv[HPT / 2];
+  };
+  Stage st[2];
+  auto fetch = [&](uint32_t s, Stage& f) {
     const uint32_t kb = s >> 2, g = 2 * (s & 3u) + asel;
-    fetch_w<Fast>(codes_a, meta_a, trow0 + kb * 8, g, fa);
-    if constexpr (Paired) fetch_w<Fast>(codes_b, meta_b, trow0 + kb * 8, g, fb);
+    fetch_w<Fast>(codes_a, meta_a, trow0 + kb * 8, g, f.fa);
+    if constexpr (Paired) fetch_w<Fast>(codes_b, meta_b, trow0 + kb * 8, g, f.fb);
     const uint16_t* xp = xrow + s * 64;
     if constexpr (Fast) {
-      const uint4 v0 = reinterpret_cast<const uint4*>(xp)[0];
-      const uint4 v1 = reinterpret_cast<const uint4*>(xp)[1];
-      xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
-      xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+#pragma unroll
+      for (int q = 0; q < HPT / 8; ++q) {
+        const uint4 v = reinterpret_cast<const uint4*>(xp)[q];
+        f.xv[4 * q] = v.x; f.xv[4 * q + 1] = v.y; f.xv[4 * q + 2] = v.z; f.xv[4 * q + 3] = v.w;
+      }
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xv[i] = uint32_t(xp[2 * i]) | (uint32_t(xp[2 * i + 1]) << 16);
+      for (int i = 0; i < HPT / 2; ++i) f.xv[i] = uint32_t(xp[2 * i]) | (uint32_t(xp[2 * i + 1]) << 16);
     }
   };
-
-  fetch(0);
-  for (uint32_t s = 0; s < steps; ++s) {
+  auto step = [&](uint32_t s, Stage& f) {
     __syncthreads();  // previous step's tiles fully read
     const uint32_t g = 2 * (s & 3u) + asel;
-    store_w(fa, g, &As[0][ar * kStride + asel * 32]);
-    if constexpr (Paired) store_w(fb, g, &As[NW - 1][ar * kStride + asel * 32]);
+    store_w(f.fa, g, &As[0][ar * kStride + asel * 32]);
+    if constexpr (Paired) store_w(f.fb, g, &As[NW - 1][ar * kStride + asel * 32]);
     {
-      uint4* dst = reinterpret_cast<uint4*>(&Bs[bt * kStride + bp * 16]);
-      dst[0] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
-      dst[1] = make_uint4(xv[4], xv[5], xv[6], xv[7]);
+      uint4* dst = reinterpret_cast<uint4*>(&Bs[bt * kStride + bp * HPT]);
+#pragma unroll
+      for (int q = 0; q < HPT / 8; ++q)
+        dst[q] = make_uint4(f.xv[4 * q], f.xv[4 * q + 1], f.xv[4 * q + 2], f.xv[4 * q + 3]);
     }
     __syncthreads();
-    if (s + 1 < steps) fetch(s + 1);
+    if (s + 2 < steps) fetch(s + 2, f);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      bf8 bfr[2];
+      bf8 bfr[NJ];
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bfr[j] = *reinterpret_cast<const bf8*>(&Bs[(wt * 32 + j * 16 + lr) * kStride + ks * 32 + lk * 8]);
+      for (int j = 0; j < NJ; ++j)
+        bfr[j] = *reinterpret_cast<const bf8*>(&Bs[(wt * (TT / 2) + j * 16 + lr) * kStride + ks * 32 + lk * 8]);
 #pragma unroll
       for (int w = 0; w < NW; ++w)
 #pragma unroll
@@ -160,18 +171,26 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(
           const bf8 afr = *reinterpret_cast<const bf8*>(
               &As[w][(wr * 64 + i * 16 + lr) * kStride + ks * 32 + lk * 8]);
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
+          for (int j = 0; j < NJ; ++j)
             acc[w][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr, bfr[j], acc[w][i][j], 0, 0, 0);
         }
     }
+  };
+
+  // K is a whole number of 256-wide super-blocks, so steps is a multiple of 4.
+  fetch(0, st[0]);
+  fetch(1, st[1]);
+  for (uint32_t s = 0; s < steps; s += 2) {
+    step(s, st[0]);
+    step(s + 1, st[1]);
   }
 
   // ---- epilogue: lane holds rows 4 lk .. 4 lk + 3 of token lr in each tile ----
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t tok = tok0 + wt * 32 + j * 16 + lr;
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t tok = tok0 + wt * (TT / 2) + j * 16 + lr;
       if (tok >= m) continue;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -192,24 +211,29 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(
     }
 }
 
-// Large-M variant: 256 weight rows x 128 tokens per block, eight waves as
-// 4 x 2 with 64 x 64 wave tiles (sixteen independent accumulators each, so
-// the matrix core never waits on its own results). LDS is double-buffered:
-// one barrier per 64-wide K step separates the staging of step s+1 from the
-// last reads of that buffer at step s-1, and step s+2's operands are loaded
-// into registers while step s runs.
-template <bool Fast>
+// Large-M variants: 256 weight rows x BT tokens per block (BT = 128 or 256),
+// eight waves as 4 x 2 with 64 x BT/2 wave tiles (sixteen or thirty-two
+// independent accumulators each, so the matrix core never waits on its own
+// results). LDS is double-buffered: one barrier per 64-wide K step separates
+// the staging of step s+1 from the last reads of that buffer at step s-1,
+// and step s+2's operands are loaded into registers while step s runs. The
+// 256-token tile fills the 160 KB of LDS exactly; against the 128-token one
+// it reads a quarter fewer LDS bytes and rebuilds half the weight operands
+// per FLOP (gfx950 serves conflict-free b128 LDS reads at about 155 B per
+// clock per CU, close to what the 128-token tile's MFMAs need).
+template <int BT, bool Fast>
 __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n, uint32_t k,
     const uint16_t* __restrict__ x, uint32_t m, void* out, const float* __restrict__ residual,
-    int epi, uint32_t row_blocks, uint32_t tok_blocks) {
-  constexpr int BR = 256, BT = 128;
+    int epi, uint32_t row_blocks, uint32_t tok_blocks, uint32_t row_base) {
+  constexpr int BR = 256, NJ = BT / 32, XP = BT / 128;  // XP: 32-byte activation parts per thread
+  static_assert(BT == 128 || BT == 256, "token tile");
   __shared__ __align__(16) _Float16 As[2][BR * kStride];
   __shared__ __align__(16) _Float16 Bs[2][BT * kStride];
 
   const uint32_t nblk = row_blocks * tok_blocks, b = blockIdx.x;
   const uint32_t tile = (nblk % 8 == 0) ? (b % 8) * (nblk / 8) + b / 8 : b;
-  const uint32_t row0 = (tile / tok_blocks) * BR, tok0 = (tile % tok_blocks) * BT;
+  const uint32_t row0 = row_base + (tile / tok_blocks) * BR, tok0 = (tile % tok_blocks) * BT;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wr = wave >> 1, wt = wave & 1u, lr = lane & 15u, lk = lane >> 4;
   const uint32_t kbs = k / 256, steps = k / 64;
@@ -218,70 +242,96 @@ __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
   const uint32_t ar = tid >> 1, asel = tid & 1u;
   const uint32_t arow = min(row0 + ar, pn8 - 1);
   const uint64_t trow0 = uint64_t(arow / 8) * kbs * 8 + arow % 8;
-  const uint32_t bt = tid >> 2, bp = tid & 3u;
-  const uint16_t* xrow = x + size_t(min(tok0 + bt, m - 1)) * k + bp * 16;
+  // Activation role: token bt, 32-byte parts bp * XP .. bp * XP + XP - 1.
+  const uint32_t bt = tid * XP / 4, bp = tid & (4u / XP - 1u);
+  const uint16_t* xrow = x + size_t(min(tok0 + bt, m - 1)) * k + bp * XP * 16;
 
-  f4 acc[4][4];
+  f4 acc[4][NJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0, 0, 0, 0};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f4{0, 0, 0, 0};
 
   WFetch fa;
-  uint32_t xv[8];
+  uint32_t xv[8 * XP];
   auto fetch = [&](uint32_t s) {
     fetch_w<Fast>(codes, meta, trow0 + (s >> 2) * 8, 2 * (s & 3u) + asel, fa);
     const uint16_t* xp = xrow + s * 64;
     if constexpr (Fast) {
-      const uint4 v0 = reinterpret_cast<const uint4*>(xp)[0];
-      const uint4 v1 = reinterpret_cast<const uint4*>(xp)[1];
-      xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
-      xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+#pragma unroll
+      for (int q = 0; q < 2 * XP; ++q) {
+        const uint4 v = reinterpret_cast<const uint4*>(xp)[q];
+        xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
+      }
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xv[i] = uint32_t(xp[2 * i]) | (uint32_t(xp[2 * i + 1]) << 16);
+      for (int i = 0; i < 8 * XP; ++i) xv[i] = uint32_t(xp[2 * i]) | (uint32_t(xp[2 * i + 1]) << 16);
     }
   };
   auto store = [&](uint32_t s) {
     const uint32_t buf = s & 1u;
     store_w(fa, 2 * (s & 3u) + asel, &As[buf][ar * kStride + asel * 32]);
-    uint4* dst = reinterpret_cast<uint4*>(&Bs[buf][bt * kStride + bp * 16]);
-    dst[0] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
-    dst[1] = make_uint4(xv[4], xv[5], xv[6], xv[7]);
+    uint4* dst = reinterpret_cast<uint4*>(&Bs[buf][bt * kStride + bp * XP * 16]);
+#pragma unroll
+    for (int q = 0; q < 2 * XP; ++q) dst[q] = make_uint4(xv[4 * q], xv[4 * q + 1], xv[4 * q + 2], xv[4 * q + 3]);
   };
 
   // Fragment reads of a K step are issued before the staging work that
-  // follows the barrier (and those of its second half before the first
-  // half's MFMAs), so LDS latency hides behind VALU and matrix-core work.
-  bf8 af[2][4], bf[2][4];
+  // follows the barrier, so LDS latency hides behind VALU and matrix-core
+  // work. The 128-token tile holds both K halves' fragments at once; the
+  // 256-token tile reads the second half's after the first half's MFMAs
+  // (register budget: 128 accumulators of 256).
+  constexpr int KH = BT == 128 ? 2 : 1;
+  bf8 af[KH][4], bf[KH][NJ];
   auto read_frags = [&](uint32_t buf, int ks) {
+    const int h = KH == 2 ? ks : 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      bf[ks][j] = *reinterpret_cast<const bf8*>(&Bs[buf][(wt * 64 + j * 16 + lr) * kStride + ks * 32 + lk * 8]);
+    for (int j = 0; j < NJ; ++j)
+      bf[h][j] = *reinterpret_cast<const bf8*>(&Bs[buf][(wt * (BT / 2) + j * 16 + lr) * kStride + ks * 32 + lk * 8]);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      af[ks][i] = *reinterpret_cast<const bf8*>(&As[buf][(wr * 64 + i * 16 + lr) * kStride + ks * 32 + lk * 8]);
+      af[h][i] = *reinterpret_cast<const bf8*>(&As[buf][(wr * 64 + i * 16 + lr) * kStride + ks * 32 + lk * 8]);
   };
   auto mma = [&](int ks) {
+    const int h = KH == 2 ? ks : 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < NJ; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[h][i], bf[h][j], acc[i][j], 0, 0, 0);
   };
 
   fetch(0);
   store(0);
   if (steps > 1) fetch(1);
+  // The second wave on each SIMD (waves 4-7) runs its MFMAs before its
+  // staging work, so one wave's dequantization overlaps the other's matrix
+  // work instead of both SIMD waves moving through the phases in step.
+  const bool compute_first = wave >= 4;
   for (uint32_t s = 0; s < steps; ++s) {
     __syncthreads();
     const uint32_t buf = s & 1u;
     read_frags(buf, 0);
-    if (s + 1 < steps) store(s + 1);
-    if (s + 2 < steps) fetch(s + 2);
-    read_frags(buf, 1);
-    mma(0);
-    mma(1);
+    if (compute_first) {
+      if constexpr (KH == 2) {
+        read_frags(buf, 1);
+        mma(0);
+        mma(1);
+      } else {
+        mma(0);
+        read_frags(buf, 1);
+        mma(1);
+      }
+      if (s + 1 < steps) store(s + 1);
+      if (s + 2 < steps) fetch(s + 2);
+    } else {
+      if (s + 1 < steps) store(s + 1);
+      if (s + 2 < steps) fetch(s + 2);
+      if constexpr (KH == 2) read_frags(buf, 1);
+      mma(0);
+      if constexpr (KH == 1) read_frags(buf, 1);
+      mma(1);
+    }
   }
 
   const bool vec = (n % 4 == 0) &&
@@ -289,8 +339,8 @@ __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t tok = tok0 + wt * 64 + j * 16 + lr;
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t tok = tok0 + wt * (BT / 2) + j * 16 + lr;
       const uint32_t r4 = row0 + wr * 64 + i * 16 + lk * 4;
       if (tok >= m || r4 >= n) continue;
       const size_t o = size_t(tok) * n + r4;
@@ -323,34 +373,83 @@ hipError_t launch_prefill_bf16(const WeightView& a, const WeightView* b, const u
   auto al = [](const void* p, uintptr_t q) { return reinterpret_cast<uintptr_t>(p) % q == 0; };
   const bool fast = al(a.codes, 16) && al(a.scales, 16) && al(x, 16) && a.k % 8 == 0 &&
                     (!b || (al(b->codes, 16) && al(b->scales, 16)));
-  // QW38_PREFILL_TILE=64|128 pins the token tile (tuning aid).
+  // QW38_PREFILL_TILE=32|64|128|256 pins the token tile (tuning aid; every
+  // tile gives bitwise-identical results).
   static const int forced = [] {
     const char* e = std::getenv("QW38_PREFILL_TILE");
     return e ? std::atoi(e) : 0;
   }();
-  const bool big = !b && (forced ? forced == 128 : m > 64);
-  if (big) {
-    const uint32_t rb = (a.n + 255) / 256, tb = (m + 127) / 128;
-    if (fast)
-      hipLaunchKernelGGL((prefill_bf16_big_kernel<true>), dim3(rb * tb), dim3(512), 0, s, a.codes,
-                         a.scales, a.n, a.k, x, m, out, residual, epilogue, rb, tb);
-    else
-      hipLaunchKernelGGL((prefill_bf16_big_kernel<false>), dim3(rb * tb), dim3(512), 0, s, a.codes,
-                         a.scales, a.n, a.k, x, m, out, residual, epilogue, rb, tb);
-    return hipGetLastError();
+  const uint32_t cus = uint32_t(cu_count());
+  // 256 x BT tiles run one block per CU. When their last round would leave
+  // most CUs idle, they cover whole rounds of row blocks and the remaining
+  // rows run as 128-row tiles when those fit one round. All kernels chain
+  // the same MFMAs over K in the same order, so every split gives
+  // bitwise-identical results.
+  auto big_rows = [&](uint32_t bt) {
+    const uint32_t rb = (a.n + 255) / 256, tb = (m + bt - 1) / bt;
+    if (uint64_t(rb) * tb > cus) {
+      const uint32_t full_rb = uint32_t(uint64_t(rb) * tb / cus * cus / tb);
+      const uint64_t tail = uint64_t((a.n - full_rb * 256 + kRows - 1) / kRows) * ((m + kToks - 1) / kToks);
+      if (full_rb > 0 && full_rb < rb && tail <= 2ull * cus) return full_rb;
+    }
+    return rb;
+  };
+  // Tile choice by a cost model of the busiest CU, in microseconds per
+  // 64-wide K step measured on MI355X: 256 x 256 2.2, 256 x 128 1.2 (one
+  // block per CU); 128 x 64 0.79 alone, 0.86 for two co-resident blocks.
+  auto small_cost = [&](uint32_t rows) {
+    const double bl = double((uint64_t(rows + kRows - 1) / kRows * ((m + kToks - 1) / kToks) + cus - 1) / cus);
+    return std::floor(bl / 2) * 0.86 + std::fmod(bl, 2.0) * 0.79;
+  };
+  auto big_cost = [&](uint32_t bt, double t) {
+    const uint32_t rb = big_rows(bt), tb = (m + bt - 1) / bt;
+    const double rounds = double((uint64_t(rb) * tb + cus - 1) / cus);
+    return rounds * t + (rb * 256 < a.n ? small_cost(a.n - rb * 256) : 0.0);
+  };
+  int bt = 64;
+  if (forced) {
+    bt = b && forced > 64 ? 64 : forced;
+  } else if (!b && m > 64) {
+    double best = small_cost(a.n);
+    const double c128 = big_cost(128, 1.2), c256 = m > 128 ? big_cost(256, 2.2) : 1e30;
+    if (c128 < best) bt = 128, best = c128;
+    if (c256 < best) bt = 256;
   }
-  const uint32_t row_blocks = (a.n + kRows - 1) / kRows, tok_blocks = (m + kToks - 1) / kToks;
+  uint32_t row_base = 0;
+  if (bt == 128 || bt == 256) {
+    const uint32_t rb = big_rows(uint32_t(bt)), tb = (m + bt - 1) / bt;
+#define QW38_PF_BIG(T, F)                                                                            \
+  hipLaunchKernelGGL((prefill_bf16_big_kernel<T, F>), dim3(rb * tb), dim3(512), 0, s, a.codes, a.scales, \
+                     a.n, a.k, x, m, out, residual, epilogue, rb, tb, 0u)
+    if (bt == 256) {
+      if (fast) QW38_PF_BIG(256, true); else QW38_PF_BIG(256, false);
+    } else {
+      if (fast) QW38_PF_BIG(128, true); else QW38_PF_BIG(128, false);
+    }
+#undef QW38_PF_BIG
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || rb * 256 >= a.n) return e;
+    row_base = rb * 256;
+  }
+  // 128 x 32 tiles where 128 x 64 ones would leave CUs idle (a tail after
+  // the big tiles, or at most 32 tokens).
+  const uint32_t row_blocks = (a.n - row_base + kRows - 1) / kRows;
+  const bool t32 = bt == 32 || (forced != 64 && (m <= 32 || uint64_t(row_blocks) * ((m + 63) / 64) < cus));
+  const uint32_t tok_blocks = (m + (t32 ? 31 : 63)) / (t32 ? 32 : 64);
   const dim3 grid(row_blocks * tok_blocks);
   const uint8_t* cb = b ? b->codes : nullptr;
   const uint8_t* mb = b ? b->scales : nullptr;
-#define QW38_PF_LAUNCH(P, F)                                                                   \
-  hipLaunchKernelGGL((prefill_bf16_kernel<P, F>), grid, dim3(256), 0, s, a.codes, a.scales, cb, mb, \
-                     a.n, a.k, x, m, out, residual, epilogue, row_blocks, tok_blocks)
+#define QW38_PF_LAUNCH(P, F, T)                                                                      \
+  hipLaunchKernelGGL((prefill_bf16_kernel<P, F, T>), grid, dim3(256), 0, s, a.codes, a.scales, cb, mb, \
+                     a.n, a.k, x, m, out, residual, epilogue, row_blocks, tok_blocks, row_base)
+#define QW38_PF_T(P, F) \
+  if (t32) QW38_PF_LAUNCH(P, F, 32); else QW38_PF_LAUNCH(P, F, 64)
   if (b) {
-    if (fast) QW38_PF_LAUNCH(true, true); else QW38_PF_LAUNCH(true, false);
+    if (fast) { QW38_PF_T(true, true); } else { QW38_PF_T(true, false); }
   } else {
-    if (fast) QW38_PF_LAUNCH(false, true); else QW38_PF_LAUNCH(false, false);
+    if (fast) { QW38_PF_T(false, true); } else { QW38_PF_T(false, false); }
   }
+#undef QW38_PF_T
 #undef QW38_PF_LAUNCH
   return hipGetLastError();
 }

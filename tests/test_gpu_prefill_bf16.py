@@ -79,6 +79,28 @@ def test_epilogues_and_token_invariance(torch_gpu):
     assert np.array_equal(f32.cpu().numpy(), base)
 
 
+def test_tail_split_bitwise(torch_gpu):
+    """M=512 over 34816 rows makes 544 tiles of 256 x 128: whole rounds of
+    them and a 128 x 64 tail (rows 32768 on at 256 CUs). Every row, head or
+    tail, equals the 128 x 64 kernel's result for the same token bitwise, and
+    sampled rows match the oracle."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k, m = 34816, 256, 512
+    wl = random_q4k(n, k, 77)
+    w = _weight(ops, wl)
+    xb = oracle.fp32_to_bf16(normal((m, k), 78))
+    x = _dev(torch, xb.view(np.int16))
+    y = torch.full((m, n), float("nan"), device="cuda")
+    ops.prefill_project(w, x, m, y, ops.DECODE_STORE_FP32)
+    got = y.cpu().numpy()
+    small = torch.full((64, n), float("nan"), device="cuda")
+    ops.prefill_project(w, x[448:].contiguous(), 64, small, ops.DECODE_STORE_FP32)
+    assert np.array_equal(got[448:], small.cpu().numpy())
+    rows = np.concatenate([np.arange(0, 64), np.arange(32700, 32830), np.arange(n - 64, n)])
+    _check(got[::16][:, rows], _ref(wl, xb[::16], rows), "prefill split n=34816 m=512")
+
+
 def test_paired_swiglu(torch_gpu):
     torch = torch_gpu
     import qw38_amd.ops as ops
