@@ -83,8 +83,8 @@ __device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t nblk) {
 }
 
 // Global operands of one K step (two K32 groups), loaded into registers one
-// step ahead of their LDS store so the loads overlap the matrix-core work.
-// Loads of rows past the padded weight and of tokens past m read a clamped
+// or two steps ahead of their LDS store so the loads overlap the matrix-core
+// work. Loads of rows past the padded weight and of tokens past m read a clamped
 // (valid) row or token instead: every output element depends only on its own
 // row and token, and those rows and tokens are never stored.
 template <int ZW, int GPT, int AW>
@@ -579,11 +579,11 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     }
   };
 
-  Fetch<ZW, GPT, AW> F;
   // One step: wait for step (kb, q) to be staged, stage step s+1 from the
-  // registers, load step s+2 into them, then compute step s. The stores of the
-  // last step and the loads of the last two land in the buffer and
-  // super-block slot that no remaining step reads.
+  // registers, load a later step into them, then compute step s. The stores
+  // of the last step and the loads past the end land in the buffer and
+  // super-block slot that no remaining step reads (or re-read the last
+  // super-block).
   // Between two barriers the store of step s+1 and the compute of step s touch
   // different LDS buffers and super-block slots, so either order is valid. In
   // eight-wave tiles with small wave tiles the second wave of each SIMD
@@ -595,18 +595,27 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   // slower).
   constexpr bool kPingPong = WR * WT == 8 && NI * NJ <= 8;
   const bool compute_first = kPingPong && wave >= 4;
+  // Register sets: with two, step s+3 is loaded at step s (a load has two
+  // steps to arrive before its store); with one, step s+2 (one step).
+  // Small wave tiles have the registers for the second set.
+  constexpr int kSets = NI * NJ <= 8 ? 2 : 1;
+  Fetch<ZW, GPT, AW> F[kSets];
   auto step = [&](auto qc, uint32_t kb) {
-    constexpr uint32_t q = decltype(qc)::value;
+    constexpr uint32_t q = decltype(qc)::value, f = kSets == 2 ? (q + 1) & 1u : 0u;
     __syncthreads();  // step s staged; step s-1 fully consumed
     if (compute_first) compute(qc, kb);
-    store(std::integral_constant<uint32_t, (q + 1) & 3u>{}, kb + (q == 3 ? 1u : 0u), F);
-    fetch(std::integral_constant<uint32_t, (q + 2) & 3u>{}, kb + (q >= 2 ? 1u : 0u), F);
+    store(std::integral_constant<uint32_t, (q + 1) & 3u>{}, kb + (q == 3 ? 1u : 0u), F[f]);
+    if constexpr (kSets == 2)
+      fetch(std::integral_constant<uint32_t, (q + 3) & 3u>{}, kb + (q >= 1 ? 1u : 0u), F[f]);
+    else
+      fetch(std::integral_constant<uint32_t, (q + 2) & 3u>{}, kb + (q >= 2 ? 1u : 0u), F[f]);
     if (!compute_first) compute(qc, kb);
   };
 
-  fetch(std::integral_constant<uint32_t, 0>{}, 0, F);
-  store(std::integral_constant<uint32_t, 0>{}, 0, F);
-  fetch(std::integral_constant<uint32_t, 1>{}, 0, F);
+  fetch(std::integral_constant<uint32_t, 0>{}, 0, F[0]);
+  store(std::integral_constant<uint32_t, 0>{}, 0, F[0]);
+  fetch(std::integral_constant<uint32_t, 1>{}, 0, F[kSets - 1]);
+  if constexpr (kSets == 2) fetch(std::integral_constant<uint32_t, 2>{}, 0, F[0]);
   for (uint32_t kb = 0; kb < kbs; ++kb) {
     step(std::integral_constant<uint32_t, 0>{}, kb);
     step(std::integral_constant<uint32_t, 1>{}, kb);
