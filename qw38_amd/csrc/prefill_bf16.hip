@@ -221,26 +221,60 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(
 // it reads a quarter fewer LDS bytes and rebuilds half the weight operands
 // per FLOP (gfx950 serves conflict-free b128 LDS reads at about 155 B per
 // clock per CU, close to what the 128-token tile's MFMAs need).
-template <int BT, bool Fast>
+//
+// Paired (gate / up SwiGLU): a tile covers 128 features, its rows 0..127
+// from the gate weight and 128..255 from the up weight (threads 0..255 stage
+// gate rows, 256..511 up rows, so the weight choice is wave-uniform). Waves
+// 0..3 hold g and waves 4..7 u of the same features in the same register
+// positions; after K the gate waves park g in LDS and the up waves write
+// BF16(SiLU(g) * u). Each g and u is the same MFMA chain as in the
+// 128 x 64 paired kernel, so both give bitwise-identical outputs.
+template <int BT, bool Fast, bool Paired = false>
 __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
-    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n, uint32_t k,
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta,
+    const uint8_t* __restrict__ codes_b, const uint8_t* __restrict__ meta_b, uint32_t n, uint32_t k,
     const uint16_t* __restrict__ x, uint32_t m, void* out, const float* __restrict__ residual,
     int epi, uint32_t row_blocks, uint32_t tok_blocks, uint32_t row_base) {
   constexpr int BR = 256, NJ = BT / 32, XP = BT / 128;  // XP: 32-byte activation parts per thread
+  constexpr int HR = Paired ? BR / 2 : BR;              // output rows (features) per tile
   static_assert(BT == 128 || BT == 256, "token tile");
-  __shared__ __align__(16) _Float16 As[2][BR * kStride];
-  __shared__ __align__(16) _Float16 Bs[2][BT * kStride];
+  // LDS: the plain kernel indexes separate A and B arrays, the paired one
+  // offsets into a single array that also holds the parked gate tile after
+  // K. Each form is the one measured fastest for its kernel on one box (plain
+  // at N=34816, M=96: 96.7 against 113.6 us with per-buffer pointer
+  // arithmetic; paired at 17408 features, M=512: 313 against 382 us with
+  // two arrays), which the matrix-core issue order the compiler picks
+  // follows.
+  // (Each instantiation references only its own arrays.)
+  __shared__ __align__(16) _Float16 smem[2 * (BR + BT) * kStride];
+  __shared__ __align__(16) _Float16 a_lds[2][BR * kStride];
+  __shared__ __align__(16) _Float16 b_lds[2][BT * kStride];
+  static_assert(!Paired || sizeof(smem) >= size_t(HR) * BT * sizeof(float), "g tile fits");
+  auto As = [&](uint32_t buf, uint32_t o) -> _Float16* {
+    if constexpr (Paired) return smem + buf * (BR * kStride) + o;
+    else return &a_lds[buf][o];
+  };
+  auto Bs = [&](uint32_t buf, uint32_t o) -> _Float16* {
+    if constexpr (Paired) return smem + 2 * BR * kStride + buf * (BT * kStride) + o;
+    else return &b_lds[buf][o];
+  };
 
   const uint32_t nblk = row_blocks * tok_blocks, b = blockIdx.x;
   const uint32_t tile = (nblk % 8 == 0) ? (b % 8) * (nblk / 8) + b / 8 : b;
-  const uint32_t row0 = row_base + (tile / tok_blocks) * BR, tok0 = (tile % tok_blocks) * BT;
+  const uint32_t row0 = row_base + (tile / tok_blocks) * HR, tok0 = (tile % tok_blocks) * BT;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wr = wave >> 1, wt = wave & 1u, lr = lane & 15u, lk = lane >> 4;
   const uint32_t kbs = k / 256, steps = k / 64;
   const uint32_t pn8 = (n + 7) / 8 * 8;
 
   const uint32_t ar = tid >> 1, asel = tid & 1u;
-  const uint32_t arow = min(row0 + ar, pn8 - 1);
+  if constexpr (Paired) {
+    if (__builtin_amdgcn_readfirstlane(tid >= 256u ? 1 : 0)) {
+      codes = codes_b;
+      meta = meta_b;
+    }
+  }
+  const uint32_t arow = min(row0 + (Paired ? ar % HR : ar), pn8 - 1);
   const uint64_t trow0 = uint64_t(arow / 8) * kbs * 8 + arow % 8;
   // Activation role: token bt, 32-byte parts bp * XP .. bp * XP + XP - 1.
   const uint32_t bt = tid * XP / 4, bp = tid & (4u / XP - 1u);
@@ -270,8 +304,8 @@ __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
   };
   auto store = [&](uint32_t s) {
     const uint32_t buf = s & 1u;
-    store_w(fa, 2 * (s & 3u) + asel, &As[buf][ar * kStride + asel * 32]);
-    uint4* dst = reinterpret_cast<uint4*>(&Bs[buf][bt * kStride + bp * XP * 16]);
+    store_w(fa, 2 * (s & 3u) + asel, As(buf, ar * kStride + asel * 32));
+    uint4* dst = reinterpret_cast<uint4*>(Bs(buf, bt * kStride + bp * XP * 16));
 #pragma unroll
     for (int q = 0; q < 2 * XP; ++q) dst[q] = make_uint4(xv[4 * q], xv[4 * q + 1], xv[4 * q + 2], xv[4 * q + 3]);
   };
@@ -287,10 +321,10 @@ __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
     const int h = KH == 2 ? ks : 0;
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
-      bf[h][j] = *reinterpret_cast<const bf8*>(&Bs[buf][(wt * (BT / 2) + j * 16 + lr) * kStride + ks * 32 + lk * 8]);
+      bf[h][j] = *reinterpret_cast<const bf8*>(Bs(buf, (wt * (BT / 2) + j * 16 + lr) * kStride + ks * 32 + lk * 8));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      af[h][i] = *reinterpret_cast<const bf8*>(&As[buf][(wr * 64 + i * 16 + lr) * kStride + ks * 32 + lk * 8]);
+      af[h][i] = *reinterpret_cast<const bf8*>(As(buf, (wr * 64 + i * 16 + lr) * kStride + ks * 32 + lk * 8));
   };
   auto mma = [&](int ks) {
     const int h = KH == 2 ? ks : 0;
@@ -334,6 +368,38 @@ __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
     }
   }
 
+  if constexpr (Paired) {
+    __syncthreads();  // every wave is past its last fragment read
+    float* gl = reinterpret_cast<float*>(smem);
+    const bool gate_wave = wave < 4;
+    const uint32_t wq = wr & 1u;  // feature half of the tile
+    if (gate_wave) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            gl[(wq * 64 + i * 16 + lk * 4 + v) * BT + wt * (BT / 2) + j * 16 + lr] = acc[i][j][v];
+    }
+    __syncthreads();
+    if (gate_wave) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const uint32_t tl = wt * (BT / 2) + j * 16 + lr, tok = tok0 + tl;
+        if (tok >= m) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const uint32_t f = wq * 64 + i * 16 + lk * 4 + v, row = row0 + f;
+          if (row >= n) continue;
+          static_cast<uint16_t*>(out)[size_t(tok) * n + row] =
+              f32_to_bf16_rne(silu(gl[f * BT + tl]) * acc[i][j][v]);
+        }
+      }
+    return;
+  }
   const bool vec = (n % 4 == 0) &&
                    ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0;
 #pragma unroll
@@ -380,56 +446,65 @@ hipError_t launch_prefill_bf16(const WeightView& a, const WeightView* b, const u
     return e ? std::atoi(e) : 0;
   }();
   const uint32_t cus = uint32_t(cu_count());
-  // 256 x BT tiles run one block per CU. When their last round would leave
-  // most CUs idle, they cover whole rounds of row blocks and the remaining
-  // rows run as 128-row tiles when those fit one round. All kernels chain
-  // the same MFMAs over K in the same order, so every split gives
-  // bitwise-identical results.
+  // 256 x BT tiles run one block per CU; a paired tile's 256 rows are 128
+  // gate and 128 up rows of the same features. When their last round would
+  // leave most CUs idle, they cover whole rounds of row blocks and the
+  // remaining rows run as 128-row tiles when those fit one round. All
+  // kernels chain the same MFMAs over K in the same order, so every split
+  // gives bitwise-identical results.
+  const uint32_t hr = b ? 128 : 256;  // output rows per big tile
   auto big_rows = [&](uint32_t bt) {
-    const uint32_t rb = (a.n + 255) / 256, tb = (m + bt - 1) / bt;
+    const uint32_t rb = (a.n + hr - 1) / hr, tb = (m + bt - 1) / bt;
     if (uint64_t(rb) * tb > cus) {
       const uint32_t full_rb = uint32_t(uint64_t(rb) * tb / cus * cus / tb);
-      const uint64_t tail = uint64_t((a.n - full_rb * 256 + kRows - 1) / kRows) * ((m + kToks - 1) / kToks);
+      const uint64_t tail = uint64_t((a.n - full_rb * hr + kRows - 1) / kRows) * ((m + kToks - 1) / kToks);
       if (full_rb > 0 && full_rb < rb && tail <= 2ull * cus) return full_rb;
     }
     return rb;
   };
   // Tile choice by a cost model of the busiest CU, in microseconds per
   // 64-wide K step measured on MI355X: 256 x 256 2.2, 256 x 128 1.2 (one
-  // block per CU); 128 x 64 0.79 alone, 0.86 for two co-resident blocks.
+  // block per CU, paired or not); 128 x 64 0.79 alone, 0.86 for two
+  // co-resident blocks (paired: 1.0 and 2.0).
+  const double t1 = b ? 1.0 : 0.79, t2 = b ? 2.0 : 0.86;
   auto small_cost = [&](uint32_t rows) {
     const double bl = double((uint64_t(rows + kRows - 1) / kRows * ((m + kToks - 1) / kToks) + cus - 1) / cus);
-    return std::floor(bl / 2) * 0.86 + std::fmod(bl, 2.0) * 0.79;
+    return std::floor(bl / 2) * t2 + std::fmod(bl, 2.0) * t1;
   };
   auto big_cost = [&](uint32_t bt, double t) {
     const uint32_t rb = big_rows(bt), tb = (m + bt - 1) / bt;
     const double rounds = double((uint64_t(rb) * tb + cus - 1) / cus);
-    return rounds * t + (rb * 256 < a.n ? small_cost(a.n - rb * 256) : 0.0);
+    return rounds * t + (rb * hr < a.n ? small_cost(a.n - rb * hr) : 0.0);
   };
   int bt = 64;
   if (forced) {
-    bt = b && forced > 64 ? 64 : forced;
-  } else if (!b && m > 64) {
+    bt = forced;
+  } else if (m > 64) {
     double best = small_cost(a.n);
     const double c128 = big_cost(128, 1.2), c256 = m > 128 ? big_cost(256, 2.2) : 1e30;
     if (c128 < best) bt = 128, best = c128;
     if (c256 < best) bt = 256;
   }
+  const uint8_t* cb = b ? b->codes : nullptr;
+  const uint8_t* mb = b ? b->scales : nullptr;
   uint32_t row_base = 0;
   if (bt == 128 || bt == 256) {
     const uint32_t rb = big_rows(uint32_t(bt)), tb = (m + bt - 1) / bt;
-#define QW38_PF_BIG(T, F)                                                                            \
-  hipLaunchKernelGGL((prefill_bf16_big_kernel<T, F>), dim3(rb * tb), dim3(512), 0, s, a.codes, a.scales, \
-                     a.n, a.k, x, m, out, residual, epilogue, rb, tb, 0u)
-    if (bt == 256) {
-      if (fast) QW38_PF_BIG(256, true); else QW38_PF_BIG(256, false);
+#define QW38_PF_BIG(T, F, P)                                                                          \
+  hipLaunchKernelGGL((prefill_bf16_big_kernel<T, F, P>), dim3(rb * tb), dim3(512), 0, s, a.codes,      \
+                     a.scales, cb, mb, a.n, a.k, x, m, out, residual, epilogue, rb, tb, 0u)
+#define QW38_PF_BIG_F(T, P) \
+  if (fast) QW38_PF_BIG(T, true, P); else QW38_PF_BIG(T, false, P)
+    if (b) {
+      if (bt == 256) { QW38_PF_BIG_F(256, true); } else { QW38_PF_BIG_F(128, true); }
     } else {
-      if (fast) QW38_PF_BIG(128, true); else QW38_PF_BIG(128, false);
+      if (bt == 256) { QW38_PF_BIG_F(256, false); } else { QW38_PF_BIG_F(128, false); }
     }
+#undef QW38_PF_BIG_F
 #undef QW38_PF_BIG
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess || rb * 256 >= a.n) return e;
-    row_base = rb * 256;
+    if (e != hipSuccess || rb * hr >= a.n) return e;
+    row_base = rb * hr;
   }
   // 128 x 32 tiles where 128 x 64 ones would leave CUs idle (a tail after
   // the big tiles, or at most 32 tokens).
@@ -437,8 +512,6 @@ hipError_t launch_prefill_bf16(const WeightView& a, const WeightView* b, const u
   const bool t32 = bt == 32 || (forced != 64 && (m <= 32 || uint64_t(row_blocks) * ((m + 63) / 64) < cus));
   const uint32_t tok_blocks = (m + (t32 ? 31 : 63)) / (t32 ? 32 : 64);
   const dim3 grid(row_blocks * tok_blocks);
-  const uint8_t* cb = b ? b->codes : nullptr;
-  const uint8_t* mb = b ? b->scales : nullptr;
 #define QW38_PF_LAUNCH(P, F, T)                                                                      \
   hipLaunchKernelGGL((prefill_bf16_kernel<P, F, T>), grid, dim3(256), 0, s, a.codes, a.scales, cb, mb, \
                      a.n, a.k, x, m, out, residual, epilogue, row_blocks, tok_blocks, row_base)

@@ -120,6 +120,34 @@ def test_paired_swiglu(torch_gpu):
     assert np.all(ulp <= 65536)
 
 
+def test_paired_big_tile_bitwise(torch_gpu):
+    """17408 features at M=512 run the paired 256 x 256 tile (128 gate + 128
+    up rows per block) over whole rounds and a 128 x 64 paired tail: every
+    feature equals the 128 x 64 paired kernel's output for the same token
+    bitwise, and stays within 1 BF16 ulp of SiLU(g) * u from the separate
+    projections."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k, m = 17408, 256, 512
+    gl, ul = random_q4k(n, k, 31), random_q4k(n, k, 32)
+    g, u = _weight(ops, gl), _weight(ops, ul)
+    x = _dev(torch, oracle.fp32_to_bf16(normal((m, k), 33)).view(np.int16))
+    sw = torch.full((m, n), -1, dtype=torch.int16, device="cuda")
+    ops.prefill_paired_swiglu(g, u, x, sw, m)
+    small = torch.full((64, n), -1, dtype=torch.int16, device="cuda")
+    ops.prefill_paired_swiglu(g, u, x[448:].contiguous(), small, 64)
+    got = sw.cpu().numpy()
+    assert np.array_equal(got[448:], small.cpu().numpy())
+    ga, ua = torch.empty(m, n, device="cuda"), torch.empty(m, n, device="cuda")
+    ops.prefill_project(g, x, m, ga, ops.DECODE_STORE_FP32)
+    ops.prefill_project(u, x, m, ua, ops.DECODE_STORE_FP32)
+    gd, ud = ga.cpu().numpy().astype(np.float64), ua.cpu().numpy().astype(np.float64)
+    ref = oracle.bf16_to_fp32(oracle.fp32_to_bf16((gd / (1 + np.exp(-gd)) * ud).astype(np.float32)))
+    val = oracle.bf16_to_fp32(got.view(np.uint16))
+    ulp = np.abs(ref.view(np.int32).astype(np.int64) - val.view(np.int32).astype(np.int64))
+    assert np.all(ulp <= 65536)
+
+
 def test_hidden_rms_bf16_bit_exact(torch_gpu):
     torch = torch_gpu
     import qw38_amd.ops as ops
