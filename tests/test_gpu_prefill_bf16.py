@@ -80,10 +80,11 @@ def test_epilogues_and_token_invariance(torch_gpu):
 
 
 def test_tail_split_bitwise(torch_gpu):
-    """M=512 over 34816 rows makes 544 tiles of 256 x 128: whole rounds of
-    them and a 128 x 64 tail (rows 32768 on at 256 CUs). Every row, head or
-    tail, equals the 128 x 64 kernel's result for the same token bitwise, and
-    sampled rows match the oracle."""
+    """M=512 over 34816 rows makes 272 tiles of 256 x 256: one round of them
+    and a 128-row tail (rows 32768 on at 256 CUs). Every row, head or tail,
+    equals the 128 x 64 kernel's result for the same token bitwise, and
+    sampled rows match the oracle. The BF16 and residual epilogues and the
+    2-byte-aligned activation path of the same launch give the same values."""
     torch = torch_gpu
     import qw38_amd.ops as ops
     n, k, m = 34816, 256, 512
@@ -99,6 +100,18 @@ def test_tail_split_bitwise(torch_gpu):
     assert np.array_equal(got[448:], small.cpu().numpy())
     rows = np.concatenate([np.arange(0, 64), np.arange(32700, 32830), np.arange(n - 64, n)])
     _check(got[::16][:, rows], _ref(wl, xb[::16], rows), "prefill split n=34816 m=512")
+    # the 256 x 256 tile's other epilogues and its 2-byte-aligned load path
+    b16 = torch.empty(m, n, dtype=torch.int16, device="cuda")
+    ops.prefill_project(w, x, m, b16, ops.DECODE_STORE_BF16)
+    assert np.array_equal(b16.cpu().numpy().view(np.uint16), oracle.fp32_to_bf16(got))
+    res = normal((m, n), 79)
+    out = torch.empty(m, n, device="cuda")
+    ops.prefill_project(w, x, m, out, ops.DECODE_RESIDUAL_ADD_FP32, residual=_dev(torch, res))
+    assert np.array_equal(out.cpu().numpy(), (res + got).astype(np.float32))
+    xu = torch.empty(m * k + 1, dtype=torch.int16, device="cuda")
+    xu[1:] = x.flatten()
+    ops.prefill_project(w, xu[1:], m, y, ops.DECODE_STORE_FP32)
+    assert np.array_equal(y.cpu().numpy(), got)
 
 
 def test_paired_swiglu(torch_gpu):
