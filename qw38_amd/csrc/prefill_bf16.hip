@@ -32,6 +32,11 @@ constexpr int kRows = 128, kToks = 64;
 // multiple of 8) keeps the wave's b128 fragment reads free of bank conflicts on
 // the 64-bank LDS; 36 dwords (64 + 8 halfs) halves the read rate.
 constexpr int kStride = 80;
+// Half offset of the second K32 group in a weight-tile row: 40 (20 dwords, an
+// odd multiple of 4) instead of 32, so a store phase of lanes holding (row,
+// group) pairs of four rows hits eight distinct 4-bank groups; the fragment
+// reads stay conflict-free.
+constexpr int kG1 = 40;
 
 // Loads of one K step.
 struct WFetch {
@@ -148,8 +153,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(
   auto step = [&](uint32_t s, Stage& f) {
     __syncthreads();  // previous step's tiles fully read
     const uint32_t g = 2 * (s & 3u) + asel;
-    store_w(f.fa, g, &As[0][ar * kStride + asel * 32]);
-    if constexpr (Paired) store_w(f.fb, g, &As[NW - 1][ar * kStride + asel * 32]);
+    store_w(f.fa, g, &As[0][ar * kStride + asel * kG1]);
+    if constexpr (Paired) store_w(f.fb, g, &As[NW - 1][ar * kStride + asel * kG1]);
     {
       uint4* dst = reinterpret_cast<uint4*>(&Bs[bt * kStride + bp * HPT]);
 #pragma unroll
@@ -169,7 +174,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const bf8 afr = *reinterpret_cast<const bf8*>(
-              &As[w][(wr * 64 + i * 16 + lr) * kStride + ks * 32 + lk * 8]);
+              &As[w][(wr * 64 + i * 16 + lr) * kStride + ks * kG1 + lk * 8]);
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
             acc[w][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr, bfr[j], acc[w][i][j], 0, 0, 0);
@@ -304,7 +309,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
   };
   auto store = [&](uint32_t s) {
     const uint32_t buf = s & 1u;
-    store_w(fa, 2 * (s & 3u) + asel, As(buf, ar * kStride + asel * 32));
+    store_w(fa, 2 * (s & 3u) + asel, As(buf, ar * kStride + asel * kG1));
     uint4* dst = reinterpret_cast<uint4*>(Bs(buf, bt * kStride + bp * XP * 16));
 #pragma unroll
     for (int q = 0; q < 2 * XP; ++q) dst[q] = make_uint4(xv[4 * q], xv[4 * q + 1], xv[4 * q + 2], xv[4 * q + 3]);
@@ -324,7 +329,7 @@ __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
       bf[h][j] = *reinterpret_cast<const bf8*>(Bs(buf, (wt * (BT / 2) + j * 16 + lr) * kStride + ks * 32 + lk * 8));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      af[h][i] = *reinterpret_cast<const bf8*>(As(buf, (wr * 64 + i * 16 + lr) * kStride + ks * 32 + lk * 8));
+      af[h][i] = *reinterpret_cast<const bf8*>(As(buf, (wr * 64 + i * 16 + lr) * kStride + ks * kG1 + lk * 8));
   };
   auto mma = [&](int ks) {
     const int h = KH == 2 ? ks : 0;

@@ -44,6 +44,11 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // multiple of 8) keeps the b128 fragment reads free of bank conflicts on the
 // 64-bank LDS; a 36-dword stride (+8 pad) halves the read rate.
 constexpr int kStride = 80;
+// Half offset of the second K32 group in an A-tile row: 40 (20 dwords, an odd
+// multiple of 4) instead of 32, so a store phase of lanes holding (row, group)
+// pairs of four rows hits eight distinct 4-bank groups (with 32 the groups of
+// rows r and r + 2 coincide); the fragment reads stay conflict-free.
+constexpr int kG1 = 40;
 
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -318,7 +323,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
         o[2 * j] = as_u32(__builtin_elementwise_fma(lo_pair(v[j]), s2, b2));
         o[2 * j + 1] = as_u32(__builtin_elementwise_fma(hi_pair(v[j]), s2, b2));
       }
-      uint4* dst = reinterpret_cast<uint4*>(&As[buf][0][ar * kStride + asel * 32 + ah * 8 * AW]);
+      uint4* dst = reinterpret_cast<uint4*>(&As[buf][0][ar * kStride + asel * kG1 + ah * 8 * AW]);
       if (a_on) {
 #pragma unroll
         for (int i = 0; i < AW; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
@@ -343,8 +348,8 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
           ol[2 * j + e] = as_u32(lo);
         }
       }
-      uint4* dh = reinterpret_cast<uint4*>(&As[buf][0][ar * kStride + asel * 32]);
-      uint4* dl = reinterpret_cast<uint4*>(&As[buf][kPlanes - 1][ar * kStride + asel * 32]);
+      uint4* dh = reinterpret_cast<uint4*>(&As[buf][0][ar * kStride + asel * kG1]);
+      uint4* dl = reinterpret_cast<uint4*>(&As[buf][kPlanes - 1][ar * kStride + asel * kG1]);
       if (a_on) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -426,7 +431,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
 #pragma unroll
         for (int i = 0; i < NI; ++i)
           af[i] = *reinterpret_cast<const half8*>(
-              &As[buf][0][(wr * NI * 16 + i * 16 + lr) * kStride + gsel * 32 + lk * 8]);
+              &As[buf][0][(wr * NI * 16 + i * 16 + lr) * kStride + gsel * kG1 + lk * 8]);
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
@@ -436,7 +441,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
 #pragma unroll
           for (int i = 0; i < NI; ++i) {
             af[i] = *reinterpret_cast<const half8*>(
-                &As[buf][kPlanes - 1][(wr * NI * 16 + i * 16 + lr) * kStride + gsel * 32 + lk * 8]);
+                &As[buf][kPlanes - 1][(wr * NI * 16 + i * 16 + lr) * kStride + gsel * kG1 + lk * 8]);
 #pragma unroll
             for (int j = 0; j < NJ; ++j)  // hi + lo partial sums stay exact integers below 2^24
               P[gsel][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], P[gsel][i][j], 0, 0, 0);
@@ -473,7 +478,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
               bf[j] = *reinterpret_cast<const half8*>(&Bs[buf][t * kStride + gsel * 32 + lk * 8]);
             }
           }
-          const uint32_t ro = (wr * NI * 16 + i * 16 + lr) * kStride + gsel * 32 + lk * 8;
+          const uint32_t ro = (wr * NI * 16 + i * 16 + lr) * kStride + gsel * kG1 + lk * 8;
           const half8 af = *reinterpret_cast<const half8*>(&As[buf][0][ro]);
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
@@ -514,7 +519,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
         }
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-          const uint32_t ro = (wr * NI * 16 + i * 16 + lr) * kStride + gsel * 32 + lk * 8;
+          const uint32_t ro = (wr * NI * 16 + i * 16 + lr) * kStride + gsel * kG1 + lk * 8;
           const half8 af = *reinterpret_cast<const half8*>(&As[buf][0][ro]);
           f4 P[NJ];
 #pragma unroll
