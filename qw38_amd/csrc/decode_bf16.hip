@@ -76,7 +76,10 @@ __device__ __forceinline__ void consume(const Tile& t, uint32_t kb, uint32_t g0,
 #pragma unroll
     for (int i = 0; i < 4; ++i) {  // code word i: bytes 4i..4i+3 = codes 8i..8i+7
       const uint32_t w = t.c[4 * e + i];
-      const uint32_t lo = w & 0x0f0f0f0fu, hv = (w >> 4) & 0x0f0f0f0fu;
+      uint32_t lo = w & 0x0f0f0f0fu, hv = (w >> 4) & 0x0f0f0f0fu;
+      // Opaque to the optimizer, so each byte converts with one
+      // v_cvt_f32_ubyte{0..3} instead of a bit-field extract and a convert.
+      asm volatile("" : "+v"(lo), "+v"(hv));
       const uint4 xv = xp[i];
       const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
