@@ -227,7 +227,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   // Step s = 4 kb + q stages K groups 2q, 2q+1 of super-block kb. q is a
   // compile-time constant everywhere below, so a super-block is one branch-free
   // block the scheduler can interleave (staging VALU beside the MFMAs).
-  auto fetch = [&](auto qc, uint32_t kb_in, Fetch<ZW, GPT, AW>& F) {
+  auto fetch = [&](auto qc, uint32_t kb_in, Fetch<ZW, GPT, AW>& F) __attribute__((always_inline)) {
     constexpr uint32_t q = decltype(qc)::value;
     const uint32_t kb = min(kb_in, kbs - 1);  // past the end: a harmless re-read
     if constexpr (Layout == QW38_LAYOUT_Q4K_WAVE64) {
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   };
 
   // Stores step (kb, q) into LDS buffer q & 1 and super-block slot kb & 1.
-  auto store = [&](auto qc, uint32_t kb, const Fetch<ZW, GPT, AW>& F) {
+  auto store = [&](auto qc, uint32_t kb, const Fetch<ZW, GPT, AW>& F) __attribute__((always_inline)) {
     constexpr uint32_t q = decltype(qc)::value, buf = q & 1u;
     const uint32_t kp = kb & 1u, g = 2 * q + asel;
     // ---- A: 32 FP16 values of (row ar, group g) ----
@@ -408,7 +408,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     for (int v = 0; v < 4; ++v) x[v] = first ? at * P[v] : fmaf(at, P[v], x[v]);
   };
 
-  auto compute = [&](auto qc, uint32_t kb) {
+  auto compute = [&](auto qc, uint32_t kb) __attribute__((always_inline)) {
     constexpr uint32_t q = decltype(qc)::value, buf = q & 1u;
     const uint32_t kp = kb & 1u;
     // ---- one 16x16x32 MFMA per (row tile, token tile, group). Small wave
@@ -591,14 +591,13 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   // super-block).
   // Between two barriers the store of step s+1 and the compute of step s touch
   // different LDS buffers and super-block slots, so either order is valid. In
-  // eight-wave tiles with small wave tiles the second wave of each SIMD
-  // (waves 4..7) computes first and stages second, so the two waves sharing a
-  // SIMD overlap staging with matrix-core work instead of passing the phases
-  // together. Wave tiles of at most 8 MFMA tiles (80 x 16, 32 x 64); larger
-  // ones (the 192 x 128 and 256 x 128 tiles) no longer fit the registers in
-  // this order and their arrays go to scratch (the 256 x 128 tile ran 14x
-  // slower).
-  constexpr bool kPingPong = WR * WT == 8 && NI * NJ <= 8;
+  // eight-wave tiles the second wave of each SIMD (waves 4..7) computes
+  // first and stages second, so the two waves sharing a SIMD overlap staging
+  // with matrix-core work instead of passing the phases together. compute,
+  // store and fetch are then called from two places each; they are forced
+  // inline, because an out-of-line copy takes the accumulator arrays by
+  // reference and puts them in scratch (608 B per lane on the 256 x 128 tile).
+  constexpr bool kPingPong = WR * WT == 8 && NI * NJ <= 16;
   const bool compute_first = kPingPong && wave >= 4;
   // Register sets: with two, step s+3 is loaded at step s (a load has two
   // steps to arrive before its store); with one, step s+2 (one step).
