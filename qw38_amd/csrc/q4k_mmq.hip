@@ -138,10 +138,12 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   static_assert((APT * 2 * BR == NT || (APT == 1 && 2 * BR < NT)) && (APT == 1 || (APT == 2 && !kQ6)),
                 "A staging share");
   constexpr int BB = BT * 64 / NT;  // B bytes staged per thread per step
-  static_assert(BB == 8 || BB == 16 || BB == 32, "B staging share");
+  static_assert(BB == 4 || BB == 8 || BB == 16 || BB == 32, "B staging share");
   constexpr int ZW = BB / 4, PARTS = 32 / BB;
-  constexpr int TPT = NT / BT, GPT = 8 / TPT;  // super-block token data: threads per token
-  static_assert(TPT >= 1 && TPT <= 8 && GPT * TPT == 8, "token-data share");
+  // super-block token data: TPT threads per token (at most 8, one group each;
+  // threads past BT * TPT have no token-data role)
+  constexpr int TPT = NT / BT > 8 ? 8 : NT / BT, GPT = 8 / TPT;
+  static_assert(TPT >= 1 && GPT * TPT == 8, "token-data share");
   constexpr int kPlanes = kQ6 ? 2 : 1;  // Q6_K stages hi and lo FP16 planes
   constexpr int kMinR = kQ6 ? 1 : BR * 8, kMinT = kQ6 ? 1 : BT * 8;
   __shared__ __align__(16) _Float16 As[2][kPlanes][BR * kStride];
@@ -187,6 +189,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   const uint32_t bpart = tid % PARTS, bsel = (tid / PARTS) & 1u, bt = tid / (2 * PARTS);
   const uint32_t btok = min(tok0 + bt, m - 1);
   const uint32_t kt = tid / TPT, kg = (tid % TPT) * GPT;  // token kt, groups kg..kg+GPT-1
+  const bool k_on = kt < uint32_t(BT);
   const uint32_t ktok = min(tok0 + kt, m - 1);
   const bool xc_vec = (reinterpret_cast<uintptr_t>(xc) % BB) == 0;
 
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     const int ex = int(__float_as_uint(mx) >> 23);  // 0 for zero/subnormal, 255 for NaN/inf
     const int se = min(max(255 - ex, 1), 253);
     ts = __uint_as_float(uint32_t(se) << 23);
-    if (tid % TPT == 0) Ti[kt] = __uint_as_float(uint32_t(254 - se) << 23);
+    if (tid % TPT == 0 && k_on) Ti[kt] = __uint_as_float(uint32_t(254 - se) << 23);
   }
 
   // Step s = 4 kb + q stages K groups 2q, 2q+1 of super-block kb. q is a
@@ -279,7 +282,9 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     }
     const int8_t* zp = zrow + (kb * 8 + 2 * q) * 32;
     if (xc_vec) {
-      if constexpr (BB == 8) {
+      if constexpr (BB == 4) {
+        F.z[0] = *reinterpret_cast<const uint32_t*>(zp);
+      } else if constexpr (BB == 8) {
         const uint2 v = *reinterpret_cast<const uint2*>(zp);
         F.z[0] = v.x; F.z[1] = v.y;
       } else {
@@ -369,7 +374,9 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
         o[2 * j + 1] = as_u32(hi_pair(u) + off);
       }
       _Float16* dst = &Bs[buf][bt * kStride + bsel * 32 + bpart * BB];
-      if constexpr (BB == 8) {
+      if constexpr (BB == 4) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(o[0], o[1]);
+      } else if constexpr (BB == 8) {
         *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
       } else {
 #pragma unroll
@@ -379,7 +386,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     }
     // ---- super-block token data: a * ts per group; for Q4_K the min-term
     // operand u = a * ts * sum split into FP16 hi + lo ----
-    if constexpr (q == 0) {
+    if (q == 0 && k_on) {
 #pragma unroll
       for (int i = 0; i < GPT; ++i) {
         const float a = F.a[i] * ts;
@@ -769,8 +776,8 @@ template <uint16_t Layout, bool Glu = false>
 hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const float* residual,
                         hipStream_t s, GluOut glu = {}) {
   // QW38_MMQ_TILE=32|64|128 pins the token tile (256: 256 rows x 128 tokens;
-  // 80: 80 x 128 on four waves; 81, 129, 192: 80 x 128, 128 x 128 and
-  // 192 x 128 on eight waves);
+  // 80: 80 x 128 on four waves; 33, 81, 129, 192: 128 x 32, 80 x 128,
+  // 128 x 128 and 192 x 128 on eight waves);
   // QW38_MMQ_SPLIT=0 disables the tail split (tuning aids; every tile shape
   // and split gives bitwise-identical results).
   static const int forced = [] {
@@ -844,6 +851,13 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   if (x.m > 64 && c192 < best) bt = 192, best = c192;
   if (forced) bt = forced;
   if (bt == 80) return launch_cfg<Layout, 1, 4, 5, 2>(w, x, out, residual, s, 0, pn);  // 80 x 128
+  // Q6_K grids of at most one 128 x 32 block per CU (M <= 128 on 5120 rows)
+  // run it on eight waves (16 x 32 each, two per SIMD, ping-pong order):
+  // down projection at M=128 241 -> 219 us. Q4_K gained nothing this way.
+  if constexpr (q6)
+    if (bt == 32 && !forced && per_cu(128, 32) <= 1.0) bt = 33;
+  if constexpr (!Glu)
+    if (bt == 33) return launch_cfg<Layout, 8, 1, 1, 2>(w, x, out, residual, s, 0, pn);  // 128 x 32, 8 waves
   if constexpr (!q6)
     if (bt == 129) return launch_cfg<Layout, 2, 4, 4, 2, Glu>(w, x, out, residual, s, 0, pn / kv, glu);  // 128 x 128, 8 waves
   if constexpr (!q6 && !Glu)

@@ -159,8 +159,8 @@ def test_mmq_q4k_integer_exact(torch_gpu, layout, n, m):
 @pytest.mark.parametrize("n,k", [(264, 2048), (5120, 2048)])
 def test_q6k_integer_exact(torch_gpu, n, k):
     """Q6_K (layout 0x0241): streaming GEMV (M <= 2), int8-MFMA decode (M 3..8)
-    and the MMQ (M = 9, 40, 130, 512; on 5120 rows M = 130 and 512 run the
-    eight-wave 80x128 tile)."""
+    and the MMQ (M = 9, 40, 130, 512; M = 9 runs the eight-wave 128x32 tile,
+    and on 5120 rows M = 130 and 512 the eight-wave 80x128 tile)."""
     torch = torch_gpu
     import qw38_amd.ops as ops
     w, weff = integer_q6k(n, k, 3 * n, 16)
