@@ -173,6 +173,35 @@ def time_launches(torch, fn, copies, steps, warmup, use_graph=True, min_launches
     return start.elapsed_time(end) / n, n, rot, mode
 
 
+def time_both(torch, fn, copies, steps, warmup, min_launches=100):
+    """Times the same launch rotation twice: replayed from a hipGraph
+    (time_launches) and as eager stream launches (the same number of launches,
+    bracketed by events on the launch stream). Graph replay adds a gap of
+    about 2 us between kernel nodes on this ROCm, and eager launches are
+    host-bound when a call's host cost exceeds its kernel time, so the lower
+    of the two device times is reported, with both recorded. Returns
+    (ms per launch, launches, rotations, mode, {graph_us, eager_us})."""
+    g_ms, n, rot, g_mode = time_launches(torch, fn, copies, steps, warmup, min_launches=min_launches)
+    stream = torch.cuda.current_stream()
+    for _ in range(max(1, warmup)):
+        for i in range(copies):
+            fn(i)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(rot):
+        for i in range(copies):
+            fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    e_ms = start.elapsed_time(end) / n
+    extra = {"graph_us": round(g_ms * 1e3, 3), "eager_us": round(e_ms * 1e3, 3)}
+    if e_ms < g_ms:
+        return e_ms, n, rot, "eager", extra
+    return g_ms, n, rot, g_mode, extra
+
+
 def time_eager(torch, fn, copies, launches):
     """Eager (no graph) launches rotating over copies: device time per launch
     from events on the launch stream, and host wall time per call."""
@@ -240,10 +269,10 @@ def bench_decode(torch, ops, fmt, n, k, ms, steps, warmup, layout, seed, outlier
         q, _ = make_q8(torch, ops, m, k, seed + 100 + m, outliers=outliers)
         outs = [torch.empty(m, n, device="cuda") for _ in range(copies)]
         fn = lambda i: ops.q4k_q8_project(ws[i], q, outs[i])  # noqa: E731
-        ms_launch, launches, rot, mode = time_launches(torch, fn, copies, steps, warmup)
+        ms_launch, launches, rot, mode, both = time_both(torch, fn, copies, steps, warmup)
         algo = wbytes + m * k * 1.25 + m * n * 4  # weights + Q8 (1.25 B/elem) + fp32 out
         res[m] = hbm_roofline(algo, ms_launch, launches=launches, rotations=rot, copies=copies,
-                              timing=mode)
+                              timing=mode, **both)
         if eager_m1 and m == 1:
             dev_ms, host_ms = time_eager(torch, fn, copies, 600)
             res[m]["eager_us_per_launch"] = round(dev_ms * 1e3, 3)
@@ -315,8 +344,9 @@ def bench_mmq(torch, ops, shapes, steps, warmup, layout, peak_sclk, seed=21):
 def bench_mlp(torch, ops, layouts, steps, warmup, peak_sclk, seed=500):
     """The whole Q8 MLP (q4k_q8_mlp: RMS->Q8, gate+up, SwiGLU->Q8, down +
     residual; Q4_K gate/up 17408x5120, Q6_K down 5120x17408) at M=1 on the
-    decode layout and M=512 on the MMQ layout, captured in a hipGraph (with
-    the device failure flag, as a captured decode token runs it). Beside it
+    decode layout and M=512 on the MMQ layout, timed replayed from a hipGraph
+    (with the device failure flag, as a captured decode token runs it) and as
+    eager launches (time_both). Beside it
     the unfused chain of the same stages as separate launches (two FP32
     [m][17408] slabs and a standalone SwiGLU->Q8 pack); both end in the same
     bits."""
@@ -332,7 +362,7 @@ def bench_mlp(torch, ops, layouts, steps, warmup, peak_sclk, seed=500):
         ws = torch.zeros(ops.q8_mlp_workspace_bytes(m), dtype=torch.uint8, device="cuda")
         flag = torch.zeros(1, dtype=torch.int32, device="cuda")
         out = torch.empty(m, 5120, device="cuda")
-        ms_f, launches, _, mode = time_launches(
+        ms_f, launches, _, mode, both = time_both(
             torch, lambda i: ops.q4k_q8_mlp(gate, up, down, resid, gamma, 1e-6, out, m, ws,
                                             pending_failure=flag), 1, steps, warmup)
         fused_out = out.clone()
@@ -349,7 +379,7 @@ def bench_mlp(torch, ops, layouts, steps, warmup, peak_sclk, seed=500):
             ops.swiglu_q8(gs, us, m, 17408, qh, flag)
             ops.q4k_q8_project(down, qh, out2, residual=resid)
 
-        ms_c, _, _, _ = time_launches(torch, chain, 1, steps, warmup)
+        ms_c, _, _, _, _ = time_both(torch, chain, 1, steps, warmup)
         torch.cuda.synchronize()
         same = bool(torch.equal(fused_out, out2))
         nops = 2.0 * m * 5120 * (3 * 17408)
@@ -357,7 +387,7 @@ def bench_mlp(torch, ops, layouts, steps, warmup, peak_sclk, seed=500):
         key = f"mlp_m{m}"
         res[key] = {"us": round(ms_f * 1e3, 2), "unfused_chain_us": round(ms_c * 1e3, 2),
                     "layout": f"{layout:#06x}", "down": "q6k 0x0241", "launches": launches,
-                    "timing": mode, "equals_unfused": same}
+                    "timing": mode, **both, "equals_unfused": same}
         if m == 1:
             res[key]["weight_gbs"] = round(nbytes / (ms_f * 1e-3) / 1e9, 1)
         else:
@@ -379,8 +409,8 @@ def bench_model(torch, ops, layers, q4_layout, prefill_m, reps, peak_sclk, seed=
     (M=1, every projection of every layer once) and one prefill chunk
     (M=prefill_m). Each (layer, projection) has its own seeded ~N(0, 0.02)
     weights, quantized on the GPU, and its own fresh seeded ~N(0,1) Q8
-    activation rows. Each pass is captured in one hipGraph and timed with
-    events. After timing, the last layer's four projections are re-run eagerly
+    activation rows. Each pass is timed with events both replayed from one
+    hipGraph and as eager launches (time_both). After timing, the last layer's four projections are re-run eagerly
     and must equal the graph-replay outputs bitwise (the oracle parity of the
     same pass is a GPU test)."""
     t0 = time.perf_counter()
@@ -407,7 +437,7 @@ def bench_model(torch, ops, layers, q4_layout, prefill_m, reps, peak_sclk, seed=
                 for j in range(len(MODEL_LAYER)):
                     ops.q4k_q8_project(ws[l][j], qs[l][j], outs[j])
 
-        ms_pass, npass, _, mode = time_launches(torch, run_pass, 1, reps, 1, min_launches=1)
+        ms_pass, npass, _, mode, both = time_both(torch, run_pass, 1, reps, 1, min_launches=1)
         same = True
         for j, (_, n, _, _) in enumerate(MODEL_LAYER):
             again = torch.empty(m, n, device="cuda")
@@ -420,7 +450,8 @@ def bench_model(torch, ops, layers, q4_layout, prefill_m, reps, peak_sclk, seed=
         key = "decode_m1" if m == 1 else f"prefill_m{m}"
         entry = (hbm_roofline(nbytes, ms_pass) if m == 1 else mfma_roofline(nops, ms_pass, peak_sclk))
         entry.update({"ms": round(ms_pass, 4), "launches": layers * len(MODEL_LAYER),
-                      "passes": npass, "timing": mode, "replay_equals_eager": same})
+                      "passes": npass, "timing": mode, "replay_equals_eager": same,
+                      "graph_ms": round(both["graph_us"] / 1e3, 4), "eager_ms": round(both["eager_us"] / 1e3, 4)})
         res[key] = entry
         log(f"model pass M={m} ({layers} layers, {res['weight_bytes']/1e9:.2f} GB): "
             f"{ms_pass:.3f} ms, {entry['achieved']} {entry['unit']} ({mode}), replay==eager {same}")
