@@ -218,6 +218,66 @@ __device__ __forceinline__ void stream_quarter(const uint8_t* cstrip, const uint
   }
 }
 
+// A wave's whole K quarter (two or three tile pairs: even kbs, at most 12
+// pairs) loaded into registers before the block stages its activations, so
+// the first weight loads overlap the staging instead of following it: short
+// launches (few strips per CU) are otherwise a chain of three memory
+// latencies. Branch-free (a two-pair quarter re-reads its last pair), so the
+// loads stay countable for the waits that follow.
+struct QuarterPre {
+  Tile t[3];
+  uint32_t n = 0;   // pairs of the quarter
+  uint32_t q0 = 0;  // first pair of the quarter
+};
+
+typedef __attribute__((address_space(1))) const uint8_t g_u8;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4 g_u4;
+typedef __attribute__((address_space(1))) const uint32_t g_u32;
+
+// 16-byte aligned spans only. The strip pointers are global-memory pointers
+// whose provenance the caller hides from the optimizer (otherwise loads
+// through the read-only kernel arguments may be sunk past the barrier to their
+// first use).
+__device__ __forceinline__ void preload_quarter(g_u8* cstrip, g_u8* mstrip, uint32_t kbs, uint32_t qi,
+                                                uint32_t lane, QuarterPre& p) {
+  const uint32_t pairs = kbs / 2;
+  const uint32_t q0 = quarter_begin(pairs, qi), q1 = quarter_begin(pairs, qi + 1);
+  p.n = q1 - q0;
+  p.q0 = q0;
+#pragma unroll
+  for (uint32_t b = 0; b < 3; ++b) {
+    const uint32_t q = min(q0 + b, q1 - 1);
+    g_u4* c = reinterpret_cast<g_u4*>(cstrip + size_t(q) * 2048 + lane * 32);
+    const u32x4 a = c[0], d = c[1];
+    Tile& t = p.t[b];
+    t.c[0] = a.x; t.c[1] = a.y; t.c[2] = a.z; t.c[3] = a.w;
+    t.c[4] = d.x; t.c[5] = d.y; t.c[6] = d.z; t.c[7] = d.w;
+    t.m = *reinterpret_cast<g_u32*>(mstrip + size_t(q) * 256 + lane * 4);
+  }
+}
+
+// stream_quarter over preloaded pairs: the same consume sequence and lane
+// reduction, so the rows are bitwise those of stream_quarter.
+template <uint16_t Layout, int MT, bool Fast>
+__device__ __forceinline__ void consume_quarter(const QuarterPre& p, uint32_t lane, const int8_t* sz,
+                                                const float2* sau, uint32_t groups, float part[MT]) {
+  const uint32_t h = lane >> 5, j = lane & 3u, g0 = 2 * j;
+  const bool hi = j >= 2;
+  const uint32_t sh = 16u * (j & 1u);
+#pragma unroll
+  for (int t = 0; t < MT; ++t) part[t] = 0.f;
+#pragma unroll
+  for (uint32_t b = 0; b < 3; ++b)
+    if (b < p.n) consume<Layout, MT, Fast>(p.t[b], 2 * (p.q0 + b) + h, g0, hi, sh, sz, sau, groups, part);
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    part[t] += __shfl_xor(part[t], 1);
+    part[t] += __shfl_xor(part[t], 2);
+    part[t] += __shfl_xor(part[t], 32);
+  }
+}
+
 // Stages the Q8 activations of MT tokens in LDS: codes and (a, a*sum).
 template <int MT, bool Fast, int NT>
 __device__ __forceinline__ void stage_q8(const int8_t* __restrict__ xc, const float* __restrict__ xa,
@@ -239,7 +299,7 @@ __device__ __forceinline__ void stage_q8(const int8_t* __restrict__ xc, const fl
   }
 }
 
-template <uint16_t Layout, int MT, bool Fast, int WS>
+template <uint16_t Layout, int MT, bool Fast, int WS, bool Pre = false>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n,
     uint32_t strips, uint32_t kbs, const int8_t* __restrict__ xc,
@@ -251,28 +311,64 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
   int8_t* sz = reinterpret_cast<int8_t*>(smem);
   float2* sau = reinterpret_cast<float2*>(smem + MT * pk);
   float* red = reinterpret_cast<float*>(smem + MT * pk + MT * groups * 8);
-  stage_q8<MT, Fast, 256>(xc, xa, xs, pk, sz, sau);
-  __syncthreads();
-
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t r = (lane >> 2) & 7u;       // row in the strip
   const uint32_t ks = wave % WS;
+  // Pre (chosen by the launcher: WS = 4, M = 1, 16-byte spans, even kbs of
+  // at most 24, K <= 8192): the activations are read into registers first
+  // (two 16-byte code vectors and one group per thread, clamped reads), then
+  // the weight pairs, then the activations are written to LDS: loads complete
+  // in issue order, so those writes wait only for the activation loads.
+  QuarterPre pre;
+  if constexpr (Pre) {
+    const uint32_t nv = pk / 16;
+    const uint4* src = reinterpret_cast<const uint4*>(xc);
+    const uint32_t i0 = min(threadIdx.x, nv - 1), i1 = min(threadIdx.x + 256, nv - 1);
+    const uint32_t gi = min(threadIdx.x, groups - 1);
+    const uint4 v0 = src[i0], v1 = src[i1];
+    const float a = xa[gi];
+    const int32_t sm = xs[gi];
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+    const uint32_t strip0 = min(blockIdx.x, strips - 1);  // WS = 4: one strip per block
+    // Laundered pointers: loads through the read-only kernel arguments may
+    // otherwise be sunk past the barrier to their first use.
+    uintptr_t cp = reinterpret_cast<uintptr_t>(codes + size_t(strip0) * kbs * 1024);
+    uintptr_t mp = reinterpret_cast<uintptr_t>(meta + size_t(strip0) * kbs * 128);
+    asm volatile("" : "+s"(cp), "+s"(mp));
+    preload_quarter(reinterpret_cast<g_u8*>(cp), reinterpret_cast<g_u8*>(mp), kbs, ks, lane, pre);
+    asm volatile("" ::: "memory");  // nor the weight loads sunk below the LDS writes
+    // unconditional stores (threads past the end rewrite the last element
+    // with its own value), so no load is sunk below the weight loads
+    uint4* dst = reinterpret_cast<uint4*>(sz);
+    dst[i0] = v0;
+    dst[i1] = v1;
+    sau[gi] = make_float2(a, a * float(sm));
+  } else {
+  stage_q8<MT, Fast, 256>(xc, xa, xs, pk, sz, sau);
+  }
+  __syncthreads();
 
   // Blocks walk strip groups with a block-uniform stride (a persistent grid
   // when it is smaller than the strip groups); with WS > 1 every wave of the
   // block runs every iteration, since the K-split reduction synchronises.
   const uint32_t stride = persistent ? gridDim.x * SPB : SPB * gridDim.x + strips;
-  for (uint32_t base = blockIdx.x * SPB; base < strips; base += stride) {
+  // One strip group; the first one of the block consumes the preloaded
+  // quarter (peeled, so the preloaded pairs are dead in the loop after it).
+  auto strip_group = [&](uint32_t base, bool first) __attribute__((always_inline)) {
     const uint32_t strip = base + wave / WS;
     const bool live = strip < strips;
-    if (WS == 1 && !live) break;
+    if (WS == 1 && !live) return false;
     float part[QPW][MT];
     if (live) {
       const uint8_t* cstrip = codes + size_t(strip) * kbs * 1024;
       const uint8_t* mstrip = meta + size_t(strip) * kbs * 128;
+      if (Pre && first) {
+        consume_quarter<Layout, MT, Fast>(pre, lane, sz, sau, groups, part[0]);
+      } else {
 #pragma unroll
-      for (int u = 0; u < QPW; ++u)
-        stream_quarter<Layout, MT, Fast>(cstrip, mstrip, kbs, ks * QPW + u, lane, sz, sau, groups, part[u]);
+        for (int u = 0; u < QPW; ++u)
+          stream_quarter<Layout, MT, Fast>(cstrip, mstrip, kbs, ks * QPW + u, lane, sz, sau, groups, part[u]);
+      }
     }
     const uint32_t row = strip * 8 + r;
     const bool writer = (lane & 35u) == 0;
@@ -307,7 +403,15 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
       }
       if (base + stride < strips) __syncthreads();  // red is rewritten by the next strip group
     }
+    return true;
+  };
+  uint32_t base = blockIdx.x * SPB;
+  if (Pre && base < strips) {
+    strip_group(base, true);
+    base += stride;
   }
+  for (; base < strips; base += stride)
+    if (!strip_group(base, false)) break;
 }
 
 template <uint16_t Layout, int MT, bool Fast>
@@ -321,9 +425,13 @@ hipError_t stream_ws(const WeightView& w, const Q8View& x, float* out, const flo
     const uint32_t need = (strips + (4 / WSV) - 1) / (4 / WSV);                          \
     const uint32_t persistent = need > max_blocks ? 1u : 0u;                             \
     const uint32_t grid = persistent ? max_blocks : need;                                \
-    hipLaunchKernelGGL((gemv_stream_kernel<Layout, MT, Fast, WSV>), dim3(grid), dim3(256), \
-                       lds, s, w.codes, w.scales, w.n, strips, kbs, x.codes, x.scales,   \
-                       x.sums, x.pk, out, residual, persistent);                         \
+    auto kern = gemv_stream_kernel<Layout, MT, Fast, WSV>;                               \
+    if constexpr (WSV == 4 && MT == 1 && Fast)                                           \
+      if (kbs % 2 == 0 && kbs <= 24 && x.pk <= 8192)                                     \
+        kern = gemv_stream_kernel<Layout, MT, Fast, WSV, true>;                          \
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, s, w.codes, w.scales, w.n,      \
+                       strips, kbs, x.codes, x.scales, x.sums, x.pk, out, residual,      \
+                       persistent);                                                      \
   } while (0)
   if (ws == 4) QW38_STREAM_LAUNCH(4);
   else if (ws == 2) QW38_STREAM_LAUNCH(2);
