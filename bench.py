@@ -304,6 +304,31 @@ def bench_decode_bf16(torch, ops, n, k, steps, warmup, seed=31):
     return r
 
 
+def bench_decode_head(torch, ops, steps, warmup, seed=51):
+    """decode_mmv on the reference's vocabulary head geometry (Q8G32 dense
+    tiles 0x0202, N=248320, K=5120, M=1, BF16 input, StoreFp32;
+    cuda/decode_mmv.cu:548-553): 1.35 GB of seeded random codes and small
+    positive fp16 group scales, larger than the Infinity Cache, so one copy
+    streams from HBM on every launch. Timing only; the head's parity is a GPU
+    test at N=65536."""
+    n, k = 248320, 5120
+    pn, pk = ops.pad_n(n), ops.pad_k(k)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    codes = torch.randint(0, 256, (pn * pk,), generator=g, dtype=torch.uint8, device="cuda")
+    scales = (torch.rand(pn * pk // 32, generator=g, device="cuda") * 1e-3 + 1e-4).to(torch.float16)
+    w = ops.dense_weight(0x0202, codes, scales.view(torch.uint8), n, k)
+    x = torch.randn(k, generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
+    y = torch.empty(n, device="cuda")
+    d = ops.decode_desc(w, x, y, ops.DECODE_STORE_FP32)
+    ms_launch, launches, _, mode, both = time_both(torch, lambda i: ops.decode_mmv(d), 1, steps, warmup)
+    nbytes = codes.numel() + scales.numel() * 2 + k * 2 + n * 4
+    r = hbm_roofline(nbytes, ms_launch, launches=launches, layout="0x0202", timing=mode, **both)
+    log(f"decode head Q8G32 N={n} K={k}: {ms_launch*1e3:.2f} us/launch, {r['achieved']:.0f} GB/s ({mode})")
+    del codes, scales, w
+    return r
+
+
 def bench_prefill_bf16(torch, ops, n, k, m, steps, warmup, seed=41):
     """BF16 PrefillEngine::project (Q4_K 0x020D operands rebuilt as BF16,
     BF16 MFMA) on the config-4 shape."""
@@ -662,6 +687,7 @@ def main():
     if not args.no_bf16:
         rooflines["decode_bf16_config2_m1"] = bench_decode_bf16(torch, ops, n, k, args.steps,
                                                                 args.warmup)
+        rooflines["decode_q8g32_head_m1"] = bench_decode_head(torch, ops, args.steps, args.warmup)
         if not args.no_mmq:
             rooflines["prefill_bf16_config4_m512"] = bench_prefill_bf16(
                 torch, ops, n, k, 512, args.steps, args.warmup)
