@@ -351,7 +351,10 @@ __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
     __syncthreads();
     const uint32_t buf = s & 1u;
     read_frags(buf, 0);
+    // The wave in its matrix-core section issues ahead of the other wave of
+    // its SIMD (s_setprio).
     if (compute_first) {
+      __builtin_amdgcn_s_setprio(1);
       if constexpr (KH == 2) {
         read_frags(buf, 1);
         mma(0);
@@ -361,15 +364,18 @@ __global__ __launch_bounds__(512, 1) void prefill_bf16_big_kernel(
         read_frags(buf, 1);
         mma(1);
       }
+      __builtin_amdgcn_s_setprio(0);
       if (s + 1 < steps) store(s + 1);
       if (s + 2 < steps) fetch(s + 2);
     } else {
       if (s + 1 < steps) store(s + 1);
       if (s + 2 < steps) fetch(s + 2);
+      __builtin_amdgcn_s_setprio(1);
       if constexpr (KH == 2) read_frags(buf, 1);
       mma(0);
       if constexpr (KH == 1) read_frags(buf, 1);
       mma(1);
+      __builtin_amdgcn_s_setprio(0);
     }
   }
 
