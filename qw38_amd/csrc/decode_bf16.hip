@@ -340,16 +340,24 @@ __device__ __forceinline__ void consume_unit(const DUnit<K>& u, uint32_t k0, con
                                               __builtin_bit_cast(bf2, xw[q]), acc, false);
     }
   } else if constexpr (K == DKind::Q4) {
-    const float s = f16_to_f32(u.s);
+    // A signed nibble c is (c ^ 8) - 8 with c ^ 8 in 0..15, so every weight is
+    // fma(s, u, -8 s) with u = (nibble ^ 8): exact, as c * s is (4 + 11
+    // significant bits), hence the same BF16 after the RNE convert.
+    const float s = f16_to_f32(u.s), n8 = -8.f * s;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {  // word i: bytes 4i..4i+3 = weights 8i..8i+7 (low nibble first)
+      const uint32_t w = u.c[i] ^ 0x88888888u;
+      uint32_t lo = w & 0x0f0f0f0fu, hv = (w >> 4) & 0x0f0f0f0fu;
+      // Opaque to the optimizer, so each byte converts with one
+      // v_cvt_f32_ubyte{0..3} instead of a bit-field extract and a convert.
+      asm volatile("" : "+v"(lo), "+v"(hv));
       const uint4 xv = xp[i];
       const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int lo = __builtin_amdgcn_sbfe(int(u.c[i]), 8 * q, 4);
-        const int hi = __builtin_amdgcn_sbfe(int(u.c[i]), 8 * q + 4, 4);
-        const fl2 wv = {float(lo) * s, float(hi) * s};
+        const float c0 = float((lo >> (8 * q)) & 0xffu);
+        const float c1 = float((hv >> (8 * q)) & 0xffu);
+        const fl2 wv = {fmaf(s, c0, n8), fmaf(s, c1, n8)};
         acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_convertvector(wv, bf2),
                                               __builtin_bit_cast(bf2, xw[q]), acc, false);
       }
