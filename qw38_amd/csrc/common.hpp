@@ -182,7 +182,7 @@ constexpr uint32_t kRmsHidden = 5120;
 template <int NT>
 __device__ __forceinline__ void rms_q8_row(const float* __restrict__ x, const uint16_t* __restrict__ gamma,
                                            float eps, int8_t* codes, float* scales, int32_t* sums,
-                                           int* failure, float* sm) {
+                                           int* failure, float* sm, float* xs) {
   constexpr int kPer = kRmsHidden / 256, kGroups = kRmsHidden / 32, kHalves = NT / 32;
   constexpr int kSteps = kGroups / kHalves, kWaves = NT / 64;
   static_assert(kSteps * kHalves == kGroups && kWaves <= 16, "block shape");
@@ -194,6 +194,10 @@ __device__ __forceinline__ void rms_q8_row(const float* __restrict__ x, const ui
     xv[st] = x[i];
     gv[st] = bf16_to_f32(gamma[i]);
   }
+  // The row also goes to LDS (xs, kRmsHidden floats), so the sum of squares
+  // below reads its strided elements there instead of from memory again.
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) xs[(half + kHalves * st) * 32 + lane32] = xv[st];
   float s = 0.f;
 #pragma unroll
   for (int st = 0; st < kSteps; ++st) s = fmaxf(s, fabsf(xv[st]));
@@ -214,7 +218,7 @@ __device__ __forceinline__ void rms_q8_row(const float* __restrict__ x, const ui
     float sq = 0.f;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
-      const float q = x[tid + 256 * j] / safe;
+      const float q = xs[tid + 256 * j] / safe;
       sq = fmaf(q, q, sq);
     }
     sq = tree32_sum(sq);

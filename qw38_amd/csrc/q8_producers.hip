@@ -156,9 +156,10 @@ __global__ __launch_bounds__(1024) void rms_q8_wide_kernel(const float* __restri
                                                            int8_t* codes, float* scales, int32_t* sums,
                                                            int* failure) {
   __shared__ float sm[18];
+  __shared__ float xs[kRmsHidden];
   const size_t row = blockIdx.x;
   rms_q8_row<1024>(residual + row * kRmsHidden, gamma, eps, codes + row * kRmsHidden,
-                   scales + row * (kRmsHidden / 32), sums + row * (kRmsHidden / 32), failure, sm);
+                   scales + row * (kRmsHidden / 32), sums + row * (kRmsHidden / 32), failure, sm, xs);
 }
 
 // cuda/q4k_q8.cu:52-61: v = BF16(SiLU(g) * u); nonfinite g/u -> NaN -> flag.
