@@ -218,11 +218,11 @@ __device__ __forceinline__ void stream_quarter(const uint8_t* cstrip, const uint
   }
 }
 
-// A wave's whole K quarter (two or three tile pairs: even kbs, at most 12
-// pairs) loaded into registers before the block stages its activations, so
+// A wave's whole K quarter (one to three tile pairs: even kbs of 8 to 24, so
+// every quarter is non-empty) loaded into registers before the block stages its activations, so
 // the first weight loads overlap the staging instead of following it: short
 // launches (few strips per CU) are otherwise a chain of three memory
-// latencies. Branch-free (a two-pair quarter re-reads its last pair), so the
+// latencies. Branch-free (a shorter quarter re-reads its last pair), so the
 // loads stay countable for the waits that follow.
 struct QuarterPre {
   Tile t[3];
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
   const uint32_t r = (lane >> 2) & 7u;       // row in the strip
   const uint32_t ks = wave % WS;
   // Pre (chosen by the launcher: WS = 4, M = 1, 16-byte spans, even kbs of
-  // at most 24, K <= 8192): the activations are read into registers first
+  // 8 to 24, K <= 8192): the activations are read into registers first
   // (two 16-byte code vectors and one group per thread, clamped reads), then
   // the weight pairs, then the activations are written to LDS: loads complete
   // in issue order, so those writes wait only for the activation loads.
@@ -427,7 +427,7 @@ hipError_t stream_ws(const WeightView& w, const Q8View& x, float* out, const flo
     const uint32_t grid = persistent ? max_blocks : need;                                \
     auto kern = gemv_stream_kernel<Layout, MT, Fast, WSV>;                               \
     if constexpr (WSV == 4 && MT == 1 && Fast)                                           \
-      if (kbs % 2 == 0 && kbs <= 24 && x.pk <= 8192)                                     \
+      if (kbs % 2 == 0 && kbs >= 8 && kbs <= 24 && x.pk <= 8192)                         \
         kern = gemv_stream_kernel<Layout, MT, Fast, WSV, true>;                          \
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, s, w.codes, w.scales, w.n,      \
                        strips, kbs, x.codes, x.scales, x.sums, x.pk, out, residual,      \
