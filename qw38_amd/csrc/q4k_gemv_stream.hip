@@ -218,6 +218,44 @@ __device__ __forceinline__ void stream_quarter(const uint8_t* cstrip, const uint
   }
 }
 
+// A whole strip streamed by one wave into its four quarter partials: the
+// same consume sequence, lane reduction and partials as four stream_quarter
+// calls (so rows are bitwise theirs), with the next tile pair's loads in
+// flight across the quarter boundaries instead of restarting at each. The
+// odd tail tile (odd kbs) is left to the caller's stream_quarter semantics:
+// this is used only for even kbs.
+template <uint16_t Layout, int MT, bool Fast>
+__device__ __forceinline__ void stream_strip(const uint8_t* cstrip, const uint8_t* mstrip, uint32_t kbs,
+                                             uint32_t lane, const int8_t* sz, const float2* sau,
+                                             uint32_t groups, float part[4][MT]) {
+  const uint32_t h = lane >> 5, j = lane & 3u, g0 = 2 * j;
+  const bool hi = j >= 2;
+  const uint32_t sh = 16u * (j & 1u);
+  const uint32_t coff = lane * 32, moff = lane * 4;
+  const uint32_t pairs = kbs / 2;
+  Tile cur, nxt;
+  load_tile<Fast>(cstrip, mstrip, coff, moff, cur);
+  uint32_t q = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) part[u][t] = 0.f;
+    const uint32_t q1 = quarter_begin(pairs, uint32_t(u) + 1);
+    for (; q < q1; ++q) {
+      const uint32_t qn = min(q + 1, pairs - 1);  // past the end: a harmless re-read
+      load_tile<Fast>(cstrip + size_t(qn) * 2048, mstrip + size_t(qn) * 256, coff, moff, nxt);
+      consume<Layout, MT, Fast>(cur, 2 * q + h, g0, hi, sh, sz, sau, groups, part[u]);
+      cur = nxt;
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      part[u][t] += __shfl_xor(part[u][t], 1);
+      part[u][t] += __shfl_xor(part[u][t], 2);
+      part[u][t] += __shfl_xor(part[u][t], 32);
+    }
+  }
+}
+
 // A wave's whole K quarter (one to three tile pairs: even kbs of 8 to 24, so
 // every quarter is non-empty) loaded into registers before the block stages its activations, so
 // the first weight loads overlap the staging instead of following it: short
@@ -476,9 +514,13 @@ __global__ __launch_bounds__(512) void glu_stream_kernel(
   const uint8_t* cstrip = (up ? ucodes : gcodes) + size_t(strip) * kbs * 1024;
   const uint8_t* mstrip = (up ? umeta : gmeta) + size_t(strip) * kbs * 128;
   float part[4][MT];
+  if (kbs % 2 == 0 && kbs >= 8) {
+    stream_strip<Layout, MT, Fast>(cstrip, mstrip, kbs, lane, sz, sau, groups, part);
+  } else {
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
-    stream_quarter<Layout, MT, Fast>(cstrip, mstrip, kbs, u, lane, sz, sau, groups, part[u]);
+    for (int u = 0; u < 4; ++u)
+      stream_quarter<Layout, MT, Fast>(cstrip, mstrip, kbs, u, lane, sz, sau, groups, part[u]);
+  }
   if ((lane & 35u) == 0) {
     const uint32_t r = (lane >> 2) & 7u;
 #pragma unroll
