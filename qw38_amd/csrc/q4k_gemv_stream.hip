@@ -227,14 +227,13 @@ __device__ __forceinline__ void stream_quarter(const uint8_t* cstrip, const uint
 template <uint16_t Layout, int MT, bool Fast>
 __device__ __forceinline__ void stream_strip(const uint8_t* cstrip, const uint8_t* mstrip, uint32_t kbs,
                                              uint32_t lane, const int8_t* sz, const float2* sau,
-                                             uint32_t groups, float part[4][MT]) {
+                                             uint32_t groups, float part[4][MT], const Tile& first) {
   const uint32_t h = lane >> 5, j = lane & 3u, g0 = 2 * j;
   const bool hi = j >= 2;
   const uint32_t sh = 16u * (j & 1u);
   const uint32_t coff = lane * 32, moff = lane * 4;
   const uint32_t pairs = kbs / 2;
-  Tile cur, nxt;
-  load_tile<Fast>(cstrip, mstrip, coff, moff, cur);
+  Tile cur = first, nxt;  // pair 0, loaded by the caller
   uint32_t q = 0;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -493,7 +492,7 @@ hipError_t stream_m(const WeightView& w, const Q8View& x, float* out, const floa
 // gate / up values are those of gemv_stream_kernel (same quarter sums), so
 // the codes equal swiglu_q8 of two separate projections bit for bit; no FP32
 // slab is written.
-template <uint16_t Layout, int MT, bool Fast>
+template <uint16_t Layout, int MT, bool Fast, bool Pre = false>
 __global__ __launch_bounds__(512) void glu_stream_kernel(
     const uint8_t* __restrict__ gcodes, const uint8_t* __restrict__ gmeta,
     const uint8_t* __restrict__ ucodes, const uint8_t* __restrict__ umeta, uint32_t n, uint32_t kbs,
@@ -504,18 +503,50 @@ __global__ __launch_bounds__(512) void glu_stream_kernel(
   const uint32_t groups = pk / 32;
   int8_t* sz = reinterpret_cast<int8_t*>(smem);
   float2* sau = reinterpret_cast<float2*>(smem + MT * pk);
-  stage_q8<MT, Fast, 512>(xc, xa, xs, pk, sz, sau);
-  __syncthreads();
-
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t G = blockIdx.x;
   const uint32_t strip = G * 4 + (wave & 3u);
   const bool up = wave >= 4;
   const uint8_t* cstrip = (up ? ucodes : gcodes) + size_t(strip) * kbs * 1024;
   const uint8_t* mstrip = (up ? umeta : gmeta) + size_t(strip) * kbs * 128;
+  // Strip path (Pre: even kbs >= 8, M = 1, 16-byte spans, K <= 8192): the
+  // activations are read into registers, then the strip's first tile pair,
+  // then the activations are written to LDS, so the staging latency and the
+  // first weight latency overlap (as in gemv_stream_kernel's Pre path).
+  Tile first;
+  if constexpr (Pre) {
+    const uint32_t nv = pk / 16;
+    const uint4* src = reinterpret_cast<const uint4*>(xc);
+    const uint32_t i0 = min(threadIdx.x, nv - 1);
+    const uint32_t gi = min(threadIdx.x, groups - 1);
+    const uint4 v0 = src[i0];
+    const float a = xa[gi];
+    const int32_t sm = xs[gi];
+    __builtin_amdgcn_sched_barrier(0);
+    uintptr_t cp = reinterpret_cast<uintptr_t>(cstrip), mp = reinterpret_cast<uintptr_t>(mstrip);
+    asm volatile("" : "+v"(cp), "+v"(mp));
+    {
+      g_u4* c = reinterpret_cast<g_u4*>(reinterpret_cast<g_u8*>(cp) + lane * 32);
+      const u32x4 x0 = c[0], x1 = c[1];
+      first.c[0] = x0.x; first.c[1] = x0.y; first.c[2] = x0.z; first.c[3] = x0.w;
+      first.c[4] = x1.x; first.c[5] = x1.y; first.c[6] = x1.z; first.c[7] = x1.w;
+      first.m = *reinterpret_cast<g_u32*>(reinterpret_cast<g_u8*>(mp) + lane * 4);
+    }
+    asm volatile("" ::: "memory");
+    float a2 = a;
+    int32_t sm2 = sm;
+    asm volatile("" : "+v"(a2), "+v"(sm2));  // their arithmetic stays behind the weight loads
+    uint4* dst = reinterpret_cast<uint4*>(sz);
+    dst[i0] = v0;  // nv <= 512: one vector per thread (threads past the end rewrite the last)
+    sau[gi] = make_float2(a2, a2 * float(sm2));
+  } else {
+    stage_q8<MT, Fast, 512>(xc, xa, xs, pk, sz, sau);
+  }
+  __syncthreads();
+
   float part[4][MT];
-  if (kbs % 2 == 0 && kbs >= 8) {
-    stream_strip<Layout, MT, Fast>(cstrip, mstrip, kbs, lane, sz, sau, groups, part);
+  if constexpr (Pre) {
+    stream_strip<Layout, MT, Fast>(cstrip, mstrip, kbs, lane, sz, sau, groups, part, first);
   } else {
 #pragma unroll
     for (int u = 0; u < 4; ++u)
@@ -544,7 +575,10 @@ template <uint16_t Layout, int MT, bool Fast>
 hipError_t glu_launch(const WeightView& g, const WeightView& u, const Q8View& x, int8_t* qc, float* qa,
                       int32_t* qs, int* failure, hipStream_t s) {
   const size_t lds = size_t(MT) * g.pk + size_t(MT) * (g.pk / 32) * 8;
-  hipLaunchKernelGGL((glu_stream_kernel<Layout, MT, Fast>), dim3(g.n / 32), dim3(512), lds, s, g.codes,
+  auto kern = glu_stream_kernel<Layout, MT, Fast>;
+  if constexpr (MT == 1 && Fast)
+    if (g.pk % 512 == 0 && g.pk >= 2048 && g.pk <= 8192) kern = glu_stream_kernel<Layout, MT, Fast, true>;
+  hipLaunchKernelGGL(kern, dim3(g.n / 32), dim3(512), lds, s, g.codes,
                      g.scales, u.codes, u.scales, g.n, g.pk / 256, x.codes, x.scales, x.sums, x.pk, qc, qa,
                      qs, failure);
   return hipGetLastError();
