@@ -722,11 +722,17 @@ void orc_q6k_ggml_to_logical(const uint8_t* ggml, uint64_t blocks, uint8_t* q,
   }
 }
 
-/* Q6_K wave64 layout 0x0241. Per tile row (row, kb): 128 B of low nibbles
- * (per K32 group 16 B, nibble order as 0x0240) then 64 B of high bit pairs
- * (per group 8 B: word u, byte i, bits 2s..2s+1 hold code 16u+4s+i).
+/* Q6_K wave64 layout 0x0241. An 8-row x K256 tile (strip, kb) is 1536
+ * contiguous code bytes at (strip*kbs + kb)*1536: the 1024 B low-nibble plane
+ * (chunk c of 16 B per (row r, K32 group g), nibble order as 0x0240), then the
+ * 512 B high-pair plane (chunk c of 8 B: word u, byte i, bits 2s..2s+1 hold
+ * code 16u+4s+i), with c = (g/2)*16 + 2r + g%2, so the two groups of a pair
+ * are adjacent for each row and one chunk per lane covers a plane.
  * Metadata: 16 int8 scales at tile_row*16, then the fp16 d array at
  * padded_n*kbs*16 + tile_row*2. */
+static uint64_t q6_chunk(uint32_t r, uint32_t kb, uint32_t kbs, int g) {
+  return ((uint64_t)(r / 8) * kbs + kb) * 64 + (uint64_t)((g / 2) * 16 + 2 * (r % 8) + g % 2);
+}
 int orc_pack_q6k_layout(const uint8_t* q, const int8_t* sc, const uint16_t* d,
                         uint32_t n, uint32_t pk, uint8_t* co, uint8_t* mo) {
   if (pk % 256) return 1;
@@ -742,19 +748,20 @@ int orc_pack_q6k_layout(const uint8_t* q, const int8_t* sc, const uint16_t* d,
       mo[rows * 16 + tr * 2] = d[blk] & 255;
       mo[rows * 16 + tr * 2 + 1] = d[blk] >> 8;
       const uint8_t* c = q + (size_t)r * pk + kb * 256;
-      uint8_t* lo = co + tr * 192;
-      uint8_t* hi = lo + 128;
       for (int g = 0; g < 8; ++g) {
+        const uint64_t ch = q6_chunk(r, kb, kbs, g);
+        uint8_t* lo = co + (ch / 64) * 1536 + (ch % 64) * 16;
+        uint8_t* hi = co + (ch / 64) * 1536 + 1024 + (ch % 64) * 8;
         const uint8_t* cg = c + 32 * g;
         for (int j = 0; j < 16; ++j) {
           int t = j / 4, i = j % 4;
-          lo[16 * g + j] = (uint8_t)((cg[8 * t + i] & 15) | ((cg[8 * t + 4 + i] & 15) << 4));
+          lo[j] = (uint8_t)((cg[8 * t + i] & 15) | ((cg[8 * t + 4 + i] & 15) << 4));
         }
         for (int u = 0; u < 2; ++u)
           for (int i = 0; i < 4; ++i) {
             uint8_t b = 0;
             for (int s = 0; s < 4; ++s) b |= (uint8_t)(((cg[16 * u + 4 * s + i] >> 4) & 3) << (2 * s));
-            hi[8 * g + 4 * u + i] = b;
+            hi[4 * u + i] = b;
           }
       }
     }
@@ -773,19 +780,20 @@ int orc_unpack_q6k_layout(const uint8_t* ci, const uint8_t* mi, uint32_t n, uint
       memcpy(sc + blk * 16, mi + tr * 16, 16);
       d[blk] = (uint16_t)(mi[rows * 16 + tr * 2] | (mi[rows * 16 + tr * 2 + 1] << 8));
       uint8_t* c = q + (size_t)r * pk + kb * 256;
-      const uint8_t* lo = ci + tr * 192;
-      const uint8_t* hi = lo + 128;
       for (int g = 0; g < 8; ++g) {
+        const uint64_t ch = q6_chunk(r, kb, kbs, g);
+        const uint8_t* lo = ci + (ch / 64) * 1536 + (ch % 64) * 16;
+        const uint8_t* hi = ci + (ch / 64) * 1536 + 1024 + (ch % 64) * 8;
         uint8_t* cg = c + 32 * g;
         for (int j = 0; j < 16; ++j) {
           int t = j / 4, i = j % 4;
-          cg[8 * t + i] = lo[16 * g + j] & 15;
-          cg[8 * t + 4 + i] = lo[16 * g + j] >> 4;
+          cg[8 * t + i] = lo[j] & 15;
+          cg[8 * t + 4 + i] = lo[j] >> 4;
         }
         for (int u = 0; u < 2; ++u)
           for (int i = 0; i < 4; ++i)
             for (int s = 0; s < 4; ++s)
-              cg[16 * u + 4 * s + i] |= (uint8_t)(((hi[8 * g + 4 * u + i] >> (2 * s)) & 3) << 4);
+              cg[16 * u + 4 * s + i] |= (uint8_t)(((hi[4 * u + i] >> (2 * s)) & 3) << 4);
       }
     }
   return 0;

@@ -17,6 +17,16 @@ constexpr uint32_t kQ4CodeBytes = 128;  // per tile row
 constexpr uint32_t kQ4MetaBytes = 16;
 constexpr uint32_t kQ6CodeBytes = 192;  // 128 low-nibble + 64 high-pair bytes
 constexpr uint32_t kQ6ScaleBytes = 16;  // + 2 B fp16 d in a trailing array
+// Q6_K 0x0241 code planes: an 8-row tile (strip, kb) is 1536 contiguous bytes
+// at (strip * kbs + kb) * 1536, the 1024-byte low-nibble plane (16 B per
+// (row r, K32 group g)) followed by the 512-byte high-pair plane (8 B each),
+// both indexed by chunk q6_chunk(r, g): the two groups of a pair sit side by
+// side for each row, and one chunk per lane of a wave covers a whole plane.
+constexpr uint32_t kQ6TileBytes = 1536;
+constexpr uint32_t kQ6HiPlane = 1024;
+__host__ __device__ constexpr uint32_t q6_chunk(uint32_t r, uint32_t g) {
+  return (g >> 1) * 16 + 2 * r + (g & 1);
+}
 
 struct Q8View {
   const int8_t* codes;

@@ -191,9 +191,9 @@ __global__ __launch_bounds__(256, 2) void gemv_kernel(
           }
         } else {
           uint32_t w[4], h[2], v[8];
-          const uint8_t* row = cstrip + size_t(kb) * 1536 + r * 192;
-          load16<true>(row + g * 16, w);
-          const uint2 hv = *reinterpret_cast<const uint2*>(row + 128 + g * 8);
+          const uint8_t* tile = cstrip + size_t(kb) * kQ6TileBytes;
+          load16<true>(tile + q6_chunk(r, g) * 16, w);
+          const uint2 hv = *reinterpret_cast<const uint2*>(tile + kQ6HiPlane + q6_chunk(r, g) * 8);
           h[0] = hv.x; h[1] = hv.y;
           const uint16_t scw = *reinterpret_cast<const uint16_t*>(
               mstrip + size_t(kb) * 128 + r * 16 + g * 2);
@@ -267,9 +267,10 @@ __global__ void group_dots_kernel(const uint8_t* __restrict__ codes,
     dots[idx] = dot32(v, z);
   } else {
     uint32_t w[4], h[2];
-    load16<false>(codes + tr * 192 + g * 16, w);
-    h[0] = *reinterpret_cast<const uint32_t*>(codes + tr * 192 + 128 + g * 8);
-    h[1] = *reinterpret_cast<const uint32_t*>(codes + tr * 192 + 132 + g * 8);
+    const uint8_t* tile = codes + (tr - r % 8) * kQ6CodeBytes;
+    load16<false>(tile + q6_chunk(r % 8, g) * 16, w);
+    h[0] = *reinterpret_cast<const uint32_t*>(tile + kQ6HiPlane + q6_chunk(r % 8, g) * 8);
+    h[1] = *reinterpret_cast<const uint32_t*>(tile + kQ6HiPlane + q6_chunk(r % 8, g) * 8 + 4);
     q6_unpack(w, h, v);
     const uint16_t scw = *reinterpret_cast<const uint16_t*>(meta + tr * 16 + g * 2);
     const int sc0 = int(int8_t(scw & 0xffu)), sc1 = int(int8_t(scw >> 8));

@@ -272,9 +272,10 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     } else {
       const uint32_t g = 2 * q + asel;
       const uint64_t tr = a_base + kb * 8;
-      const uint8_t* rowp = codes + tr * 192;
-      const uint4 cw = *reinterpret_cast<const uint4*>(rowp + g * 16);
-      const uint2 hw = *reinterpret_cast<const uint2*>(rowp + 128 + g * 8);
+      const uint8_t* tp = codes + (tr - arow % 8) * kQ6CodeBytes;  // the tile's first byte
+      const uint32_t ch = q6_chunk(arow % 8, g);
+      const uint4 cw = *reinterpret_cast<const uint4*>(tp + ch * 16);
+      const uint2 hw = *reinterpret_cast<const uint2*>(tp + kQ6HiPlane + ch * 8);
       F.w[0] = cw.x; F.w[1] = cw.y; F.w[2] = cw.z; F.w[3] = cw.w;
       F.x[0] = hw.x; F.x[1] = hw.y;
       F.x[2] = *reinterpret_cast<const uint16_t*>(meta + tr * 16 + g * 2);

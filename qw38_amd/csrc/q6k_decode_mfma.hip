@@ -89,10 +89,12 @@ __global__ __launch_bounds__(W * 64, Occ) void q6k_mfma_decode_kernel(
     Slot ring[PD + 1];
     auto fetch = [&](uint32_t kb, Slot& sl) {
       const uint64_t tr = tr_base + uint64_t(kb) * 8;
-      const uint8_t* cp = codes + tr * 192;
-      sl.l0 = *reinterpret_cast<const uint4*>(cp + 32 * j);
-      sl.l1 = *reinterpret_cast<const uint4*>(cp + 32 * j + 16);
-      sl.hh = *reinterpret_cast<const uint4*>(cp + 128 + 16 * j);
+      // groups 2j and 2j+1 of the row: adjacent chunks in both planes
+      const uint8_t* cp = codes + (tr - row % 8) * kQ6CodeBytes;
+      const uint32_t c0 = q6_chunk(row % 8, 2 * j);
+      sl.l0 = *reinterpret_cast<const uint4*>(cp + c0 * 16);
+      sl.l1 = *reinterpret_cast<const uint4*>(cp + c0 * 16 + 16);
+      sl.hh = *reinterpret_cast<const uint4*>(cp + kQ6HiPlane + c0 * 8);
       sl.scw = *reinterpret_cast<const uint32_t*>(meta + tr * 16 + 4 * j);
       sl.dh = *reinterpret_cast<const uint16_t*>(meta + tiles_total * 16 + tr * 2);
 #pragma unroll

@@ -1,13 +1,13 @@
 // Linear-streaming Q6_K GEMV for M = 1..2 tokens (layout 0x0241; the down
 // projection of the Q4_K_M mixture at decode).
 //
-// In layout 0x0241 an 8-row x K256 tile is 1536 contiguous code bytes (per
-// row: 128 B of low nibbles, then 64 B of high bit pairs), 128 contiguous
-// bytes of int8 sub-block scales and 16 contiguous bytes of fp16 d, and the
-// tiles of an 8-row strip follow one another. One wave streams one tile per
-// step: lane l = 8 g + r owns row r, K32 group g (16 low-nibble bytes, 8
-// high-pair bytes, the group's two sub-block scales and the row's d), so each
-// wave load instruction reads whole contiguous runs. The activations of a
+// In layout 0x0241 an 8-row x K256 tile is 1536 contiguous code bytes (a
+// 1024-byte low-nibble plane and a 512-byte high-pair plane, 16 B and 8 B per
+// (row, K32 group) chunk), 128 contiguous bytes of int8 sub-block scales and
+// 16 contiguous bytes of fp16 d, and the tiles of an 8-row strip follow one
+// another. One wave streams one tile per step: lane l = 8 g + r owns row r,
+// K32 group g (its low-nibble and high-pair chunks, the group's two sub-block
+// scales and the row's d), so each plane is one contiguous wave load. The activations of a
 // tile (8 groups x 32 codes) are loaded once per wave, one dword per lane
 // (lane 8 g + i holds codes 4i..4i+3 of group g), and each lane gathers its
 // group's eight dwords with ds_swizzle broadcasts inside its 8-lane group, so
@@ -41,11 +41,11 @@ struct Q6Step {
 };
 
 template <int MT, bool Fast>
-__device__ __forceinline__ void load_q6(const uint8_t* crow, uint32_t g, const uint8_t* srow,
+__device__ __forceinline__ void load_q6(const uint8_t* ctile, uint32_t chunk, const uint8_t* srow,
                                         const uint8_t* drow, const int8_t* zp, const float* ap,
                                         uint32_t pk, uint32_t groups, Q6Step<MT>& t) {
-  const uint8_t* lp = crow + g * 16;
-  const uint8_t* hp = crow + 128 + g * 8;
+  const uint8_t* lp = ctile + chunk * 16;
+  const uint8_t* hp = ctile + kQ6HiPlane + chunk * 8;
   if constexpr (Fast) {
     const uint4 a = *reinterpret_cast<const uint4*>(lp);
     const uint2 b = *reinterpret_cast<const uint2*>(hp);
@@ -134,12 +134,13 @@ __global__ __launch_bounds__(256) void q6_stream_kernel(
     for (int t = 0; t < MT; ++t) acc[t] = 0.f;
     if (live && nkb > 0) {
       const uint64_t tr0 = (uint64_t(strip) * kbs + kb0) * 8 + r;  // tile row of (strip, kb0, r)
-      const uint8_t* cbase = codes + tr0 * 192;
+      const uint8_t* cbase = codes + (tr0 - r) * kQ6CodeBytes;  // the tile's first byte
+      const uint32_t chunk = q6_chunk(r, g);
       const uint8_t* sbase = meta + tr0 * 16 + g * 2;
       const uint8_t* dbase = meta + tiles * 16 + tr0 * 2;
       auto ld = [&](Q6Step<MT>& T, uint32_t i) {  // tile kb0 + i, clamped to the range
         const uint32_t j = min(i, nkb - 1);
-        load_q6<MT, Fast>(cbase + size_t(j) * 1536, g, sbase + size_t(j) * 128, dbase + size_t(j) * 16,
+        load_q6<MT, Fast>(cbase + size_t(j) * kQ6TileBytes, chunk, sbase + size_t(j) * 128, dbase + size_t(j) * 16,
                           zbase + size_t(j) * 256, abase + size_t(j) * 8, pk, groups, T);
       };
       Q6Step<MT> ring[D];

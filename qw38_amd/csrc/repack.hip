@@ -60,18 +60,21 @@ __global__ void repack_q6k_kernel(const uint8_t* __restrict__ blocks, uint32_t n
   const uint32_t row = wid / kbs, kb = wid % kbs;
   const uint8_t* y = blocks + size_t(wid) * 210;
   const uint64_t tr = (uint64_t(row / 8) * kbs + kb) * 8 + row % 8;
-  for (uint32_t byte = lane; byte < 192; byte += 64) {
-    uint32_t v = 0;
-    if (byte < 128) {
+  uint8_t* tile = codes + (tr - row % 8) * kQ6CodeBytes;
+  for (uint32_t byte = lane; byte < kQ6CodeBytes; byte += 64) {
+    uint32_t v = 0, dst;
+    if (byte < 128) {  // (group g, byte j) of the low-nibble chunk
       const uint32_t g = byte / 16, j = byte % 16, t = j / 4, i = j % 4;
       v = (q6_code(y, 32 * g + 8 * t + i) & 15u) | ((q6_code(y, 32 * g + 8 * t + 4 + i) & 15u) << 4);
-    } else {
+      dst = q6_chunk(row % 8, g) * 16 + j;
+    } else {  // (group g, byte b % 8) of the high-pair chunk
       const uint32_t b = byte - 128, g = b / 8, u = (b % 8) / 4, i = b % 4;
 #pragma unroll
       for (uint32_t s = 0; s < 4; ++s)
         v |= ((q6_code(y, 32 * g + 16 * u + 4 * s + i) >> 4) & 3u) << (2 * s);
+      dst = kQ6HiPlane + q6_chunk(row % 8, g) * 8 + b % 8;
     }
-    codes[tr * 192 + byte] = uint8_t(v);
+    tile[dst] = uint8_t(v);
   }
   if (lane < 16) meta[tr * 16 + lane] = y[192 + lane];
   if (lane < 2) meta[uint64_t(pn) * kbs * 16 + tr * 2 + lane] = y[208 + lane];
