@@ -112,9 +112,10 @@ __global__ __launch_bounds__(256) void q6_stream_kernel(
     uint32_t pk, float* __restrict__ out, const float* __restrict__ residual, uint32_t persistent) {
   constexpr int NW = 4;  // waves per block
   constexpr int SPB = NW / WS;
-  // tiles of loads in flight per wave (M=1, config 3: 2 tiles 16.5 us, 3 tiles
-  // 16.7, 4 tiles 17.5, 5 or 6 tiles 18.6)
-  constexpr int D = MT == 1 ? 2 : 3;
+  // tiles of loads in flight per wave (config 3, M=1: 1 tile 18.1 us, 2 tiles
+  // 16.2-16.5, 3 tiles 16.7, 4 tiles 17.5, 5 or 6 tiles 18.6; M=2: 2 tiles
+  // 18.1, 3 tiles 18.55)
+  constexpr int D = 2;
   __shared__ float red[WS > 1 ? NW * MT * 8 : 1];
   const uint32_t groups = pk / 32;
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
