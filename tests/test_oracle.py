@@ -186,6 +186,38 @@ def test_layout_0240_coordinates_and_roundtrip():
     assert np.array_equal(w2.codes, w.codes) and np.array_equal(w2.meta, w.meta)
 
 
+def test_layout_0241_chunk_planes():
+    """Q6_K 0x0241: an 8-row tile (strip, kb) is 1536 code bytes at
+    (strip*kbs + kb)*1536, a low-nibble plane of 16 B chunks then a high-pair
+    plane of 8 B chunks, chunk c = (g/2)*16 + 2r + g%2 for row r of the tile
+    and K32 group g; scales per tile row, then the fp16 d array."""
+    n, k = 20, 768  # three strips (the last padded), three super-blocks
+    q6 = random_q6k(n, k, 17)
+    co, mo = q6.physical()
+    kbs, pn = k // 256, oracle.pad8(n)
+    assert co.size == pn * kbs * 192 and mo.size == pn * kbs * 18
+    for row, kb, g in [(0, 0, 0), (13, 2, 5), (7, 1, 7), (19, 0, 3)]:
+        r, tile = row % 8, (row // 8) * kbs + kb
+        c = (g // 2) * 16 + 2 * r + g % 2
+        q = q6.q[row, kb * 256 + g * 32: kb * 256 + g * 32 + 32].astype(np.uint32)
+        lo = np.array([(q[8 * (j // 4) + j % 4] & 15) | ((q[8 * (j // 4) + 4 + j % 4] & 15) << 4)
+                       for j in range(16)], np.uint8)
+        assert np.array_equal(co[tile * 1536 + c * 16: tile * 1536 + c * 16 + 16], lo)
+        hi = np.array([sum(((q[16 * (b // 4) + 4 * s + b % 4] >> 4) & 3) << (2 * s) for s in range(4))
+                       for b in range(8)], np.uint8)
+        assert np.array_equal(co[tile * 1536 + 1024 + c * 8: tile * 1536 + 1024 + c * 8 + 8], hi)
+        tr = tile * 8 + r
+        assert np.array_equal(mo[tr * 16: tr * 16 + 16].view(np.int8), q6.sc[row, kb * 16: kb * 16 + 16])
+        d = int(mo[pn * kbs * 16 + tr * 2]) | (int(mo[pn * kbs * 16 + tr * 2 + 1]) << 8)
+        assert d == int(q6.d[row, kb])
+    # padding rows of the last strip stay zero
+    tile = 2 * kbs
+    for r in range(n % 8, 8):
+        for g in range(8):
+            c = (g // 2) * 16 + 2 * r + g % 2
+            assert not co[tile * 1536 + c * 16: tile * 1536 + c * 16 + 16].any()
+
+
 def test_ggml_roundtrips_and_pinned_dequant():
     w = random_q4k(9, 512, 11)
     assert np.array_equal(oracle.Q4K.from_ggml(w.ggml(), 9, 512).codes, w.codes)
