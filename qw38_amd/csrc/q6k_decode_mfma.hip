@@ -206,6 +206,12 @@ hipError_t launch_t(const WeightView& w, const Q8View& x, float* out, const floa
   const size_t lds = size_t(w.pk / 16) * T * 4 + size_t(w.pk / 32) * T * 4 + size_t(W) * 16 * T * 4;
   if (lds > 160 * 1024) return hipErrorNotSupported;
   uint32_t per_cu = std::max<uint32_t>(1, std::min<uint32_t>(uint32_t(160 * 1024 / lds), 32u / W));
+  // Fewer tiles than two per CU: one block per CU, looping over its tiles.
+  // Every block stages the whole activation operand in LDS first, and a
+  // second block on a CU only pays for that with a full round of its own
+  // (5120 rows = 320 tiles: M=3 26.1 -> 25.2 us, M=4 26.9 -> 25.8, M=8
+  // 36.3 -> 34.6).
+  if (tiles < 2 * uint32_t(cu_count())) per_cu = 1;
   if (per_cu_cap) per_cu = std::min(per_cu, per_cu_cap);
   const uint32_t grid = std::min<uint32_t>(tiles, uint32_t(cu_count()) * per_cu);
   auto kern = q6k_mfma_decode_kernel<TP, W, PD, Occ>;
@@ -239,10 +245,9 @@ hipError_t launch_q6k_mfma_decode(const WeightView& w, const Q8View& x, float* o
       reinterpret_cast<uintptr_t>(w.scales) % 4)
     return hipErrorNotSupported;
   // M 5..8 (two token passes): no load ring, bounded to four waves per SIMD
-  // (112 VGPRs), so all 320 tiles of the 5120-row down projection are
-  // resident at once; with the ring it needs 186 VGPRs, one block per CU and
-  // a second round (config 3, M=8: 38.2 against 43.1 us). M 3..4 keeps the
-  // ring (118 VGPRs either way).
+  // (112 VGPRs); with the ring it needs 186 VGPRs (config 3, M=8, both at
+  // 320 blocks: 38.2 against 43.1 us). M 3..4 keeps the ring (118 VGPRs
+  // either way).
   return x.m <= 4 ? launch_t<1, 8, 1>(w, x, out, residual, s, cap)
                   : launch_t<2, 8, 0, 4>(w, x, out, residual, s, cap);
 }
