@@ -130,8 +130,15 @@ int qw38_q4k_q8_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_w
  * (qw38_q8_mlp_static_scratch_bytes(), held on each GPU until the process
  * ends), so m <= QW38_Q8_MLP_STATIC_MAX_TOKENS; larger m is rejected with
  * QW38_INVALID_ARGUMENT before any launch. Every call on one GPU shares that
- * GPU's scratch: calls that overlap on one GPU (two streams, two threads)
- * race. The failure flag is cleared by a kernel on each call. */
+ * GPU's scratch, so calls must be serialized per device: a call made while
+ * another is running on the host, or while an earlier call's device work on
+ * another stream has not completed, is rejected with QW38_INVALID_ARGUMENT
+ * before any launch (calls on one stream are ordered by the stream and
+ * accepted). Work captured into a graph is not tracked: replays of captured
+ * calls on several streams must be serialized by the caller. Without
+ * pending_failure the internal failure flag is cleared by a kernel on each
+ * call; a caller-supplied pending_failure is never cleared (the caller zeroes
+ * it), as in qw38_q4k_q8_mlp. */
 #define QW38_Q8_MLP_STATIC_MAX_TOKENS 64u
 uint64_t qw38_q8_mlp_static_scratch_bytes(void);
 int qw38_q4k_q8_mlp_static(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* down,

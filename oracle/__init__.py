@@ -63,6 +63,7 @@ def lib():
             "orc_pack_q4k_layout": (I, [U16, V, V, U32, U32, V, V]),
             "orc_unpack_q4k_layout": (I, [U16, V, V, U32, U32, V, V]),
             "orc_quantize_q6k_block": (None, [V, V, V, V]),
+            "orc_q6k_fit_subblock": (C.c_float, [V, V]),
             "orc_quantize_q6k_rows": (I, [V, U64, U64, V, V, V, I]),
             "orc_q6k_logical_to_ggml": (None, [V, V, V, U64, V]),
             "orc_q6k_ggml_to_logical": (None, [V, U64, V, V, V]),

@@ -46,11 +46,18 @@
  *                         byte-exact; on random data every code is the clamped
  *                         round-half-even nearest of x/(d*sc) (restated in
  *                         numpy), the largest sub-block scale is -128, and the
- *                         error is <= d|sc|/2 off the clamp. The perturbed-
- *                         iscale least-squares search inside make_qx_quants is
- *                         pinned only where its result is exact.
- *   orc_q6k_*ggml*        ggml block_q6_K byte order (ggml-common.h). Pinned by
- *                         round trip only.
+ *                         error is <= d|sc|/2 off the clamp. The sub-block
+ *                         search (orc_q6k_fit_subblock: 19 iscales, x^2-
+ *                         weighted least squares) is pinned against an
+ *                         independent float64 brute force that maximises
+ *                         sumlx^2/suml2 over the candidates; unweighted and
+ *                         9-candidate variants are shown to disagree with it.
+ *   orc_q6k_*ggml*        ggml block_q6_K byte order (ggml-common.h:
+ *                         ql[128], qh[64], scales[16], d). Pinned: every
+ *                         source bit of a block is flipped alone and must move
+ *                         exactly the weight that ggml's dequantize_row_q6_K
+ *                         index expressions name (restated independently in
+ *                         the test), for both conversion directions.
  *   orc_q4k_q8_contract   tests/q4k_q8_test.cpp:121-131 (double closed form),
  *                         cuda/q4k_q8.cu:97,140 (FP32 K32 order). Pinned: brute
  *                         force integer dots, closed form on the reference
@@ -628,6 +635,10 @@ static float fit_qx(int n, int nmax, const float* x, uint8_t* L) {
   }
   return scale;
 }
+
+/* One 16-element sub-block's search, exposed so the tests can pin it against
+ * an independent brute force of the 19 candidates. */
+float orc_q6k_fit_subblock(const float* x, uint8_t* L) { return fit_qx(16, 32, x, L); }
 
 void orc_quantize_q6k_block(const float* x, uint8_t* q, int8_t* sc, uint16_t* d) {
   uint8_t L[256];

@@ -67,6 +67,7 @@ int orc_unpack_q4k_layout(uint16_t layout, const uint8_t* codes_in, const uint8_
 /* ---- Q6_K quantizer and layouts ----------------------------------------- */
 /* 256 floats -> q[256] in 0..63, sc[16] int8, d fp16 bits. */
 void orc_quantize_q6k_block(const float* x, uint8_t* q, int8_t* sc, uint16_t* d);
+float orc_q6k_fit_subblock(const float* x, uint8_t* L);
 int orc_quantize_q6k_rows(const float* x, uint64_t n, uint64_t k, uint8_t* q,
                           int8_t* sc, uint16_t* d, int threads);
 void orc_q6k_logical_to_ggml(const uint8_t* q, const int8_t* sc, const uint16_t* d,

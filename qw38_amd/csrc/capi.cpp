@@ -801,6 +801,19 @@ __device__ __align__(256) uint8_t scratch[kStaticMlpBytes];
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[64] = {};
 
+// Per-device record of the last call that used the scratch: a call still
+// running on the host (another thread) or a call whose device work was
+// enqueued on another stream and has not completed makes a new call reject
+// before any launch. `done` is created once per device at set-up and recorded
+// after each uncaptured submission; calls on one stream are ordered by it.
+struct StaticUse {
+  hipEvent_t done = nullptr;
+  hipStream_t stream = nullptr;
+  bool recorded = false;
+  bool busy = false;
+};
+StaticUse g_static_use[64];
+
 // Device address of this device's scratch (device must be current).
 int scratch_address(int device, void** out) {
   if (device < 0 || device >= 64) return fail(QW38_INVALID_ARGUMENT, "q8.mlp_static", "device index");
@@ -832,13 +845,48 @@ int qw38_q4k_q8_mlp_static(const qw38_weight* gate, const qw38_weight* up, const
   int device = 0;
   if (int st = stream_device(stream, &device, op)) return st;
   void* ws = nullptr;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  StaticUse& use = g_static_use[device];
   {
     DeviceScope scope(device);
     if (scope.status != hipSuccess) return hip_fail(scope.status, op);
     if (int st = scratch_address(device, &ws)) return st;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!use.done) {
+      hipError_t e = hipEventCreateWithFlags(&use.done, hipEventDisableTiming);
+      if (e != hipSuccess) {
+        use.done = nullptr;
+        return hip_fail(e, "q8.mlp_static.event");
+      }
+    }
+    if (use.busy)
+      return fail(QW38_INVALID_ARGUMENT, op,
+                  "the static scratch is in use by a concurrent call on this device");
+    if (use.recorded && use.stream != s) {
+      hipError_t q = hipEventQuery(use.done);
+      if (q == hipErrorNotReady)
+        return fail(QW38_INVALID_ARGUMENT, op,
+                    "the static scratch is in use by unfinished work on another stream");
+      if (q != hipSuccess) return hip_fail(q, "q8.mlp_static.event");
+    }
+    use.busy = true;
   }
-  return mlp_run(gate, up, down, residual, gamma, eps, output, m, ws,
-                 qw38_q8_mlp_workspace_bytes(m), stream, submitted, pending_failure, true);
+  int st = mlp_run(gate, up, down, residual, gamma, eps, output, m, ws,
+                   qw38_q8_mlp_workspace_bytes(m), stream, submitted, pending_failure, true);
+  DeviceScope scope(device);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  use.busy = false;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (*submitted && scope.status == hipSuccess && hipStreamIsCapturing(s, &cs) == hipSuccess &&
+      cs == hipStreamCaptureStatusNone) {
+    // Work left on the stream (a pending_failure call returns before it
+    // completes) is what a call on another stream must wait for.
+    if (hipEventRecord(use.done, s) == hipSuccess) {
+      use.recorded = true;
+      use.stream = s;
+    }
+  }
+  return st;
 }
 
 int qw38_hidden_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,

@@ -107,3 +107,37 @@ def quantized_q4k(n, k, seed) -> oracle.Q4K:
 
 def quantized_q6k(n, k, seed) -> oracle.Q6K:
     return oracle.quantize_q6k(normal((n, k), seed, 0.02))
+
+
+# ---- published GGML Q6_K block (ggml-common.h block_q6_K) -------------------
+# struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; ggml_half d; }
+# = 210 bytes. ggml's dequantize_row_q6_K walks the block in two halves of
+# 128 weights (ql += 64, qh += 32, sc += 8 per half) and, for l in 0..31 and
+# is = l/16, reads
+#   y[l +  0] = d*sc[is+0]*((ql[l   ] & 0xF) | ((qh[l] >> 0) & 3) << 4) - 32)
+#   y[l + 32] = d*sc[is+2]*((ql[l+32] & 0xF) | ((qh[l] >> 2) & 3) << 4) - 32)
+#   y[l + 64] = d*sc[is+4]*((ql[l   ] >>  4) | ((qh[l] >> 4) & 3) << 4) - 32)
+#   y[l + 96] = d*sc[is+6]*((ql[l+32] >>  4) | ((qh[l] >> 6) & 3) << 4) - 32)
+# The coordinates below are those expressions, written out per weight index.
+def ggml_q6k_coord(i: int):
+    """(ql byte, nibble shift 0/4, qh byte, qh shift, scale byte) that weight i
+    of a 256-weight block reads, as byte offsets into the 210-byte block."""
+    half, j = divmod(i, 128)
+    quarter, l = divmod(j, 32)
+    ql = 64 * half + l + (32 if quarter in (1, 3) else 0)
+    nib = 0 if quarter in (0, 1) else 4
+    qh = 128 + 32 * half + l
+    return ql, nib, qh, 2 * quarter, 192 + 8 * half + l // 16 + 2 * quarter
+
+
+def ggml_q6k_decode(blocks: np.ndarray):
+    """Unsigned 6-bit codes q [blocks][256], int8 scales [blocks][16] and fp16
+    d bits [blocks] of GGML Q6_K bytes, by the published index expressions."""
+    b = np.asarray(blocks, np.uint8).reshape(-1, 210)
+    q = np.zeros((b.shape[0], 256), np.uint8)
+    for i in range(256):
+        ql, nib, qh, sh, _ = ggml_q6k_coord(i)
+        q[:, i] = ((b[:, ql] >> nib) & 15) | (((b[:, qh] >> sh) & 3) << 4)
+    sc = b[:, 192:208].view(np.int8).copy()
+    d = (b[:, 208].astype(np.uint16) | (b[:, 209].astype(np.uint16) << 8))
+    return q, sc, d

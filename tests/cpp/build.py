@@ -18,9 +18,12 @@ def build_one(name: str) -> str:
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
            "-Wno-unused-command-line-argument",
            "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "qw38_amd", "cpp"),
+           "-I", os.path.join(ROOT, "oracle"),
            os.path.join(HERE, name + ".cpp"), "-o", out + ".tmp",
            "-L", os.path.join(ROOT, "qw38_amd"), "-lqw38_hip",
-           "-Wl,-rpath,$ORIGIN/../../qw38_amd"]
+           "-Wl,-rpath,$ORIGIN/../../qw38_amd",
+           # the oracle (test infrastructure) as the checker of the runtime test
+           "-L", os.path.join(ROOT, "oracle"), "-loracle", "-Wl,-rpath,$ORIGIN/../../oracle"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"C++ test build failed for {name}:\n{r.stderr}")

@@ -80,13 +80,21 @@ SHAPES = [(20, 192), (136, 768), (2048, 5120), (300, 17408)]
 def test_random_projection_vs_oracle(torch_gpu, layout, n, k):
     torch = torch_gpu
     import qw38_amd.ops as ops
-    if layout == 0x0203 and (n % 8 or k % 256):
-        pytest.skip("BF16 dense tile requires N%8==0 and K%256==0 (cuda/decode_mmv.cu:375-380)")
     print(f"dense decode layout={layout:#x} n={n} k={k}", flush=True)
-    co, so, wb = _random_dense(layout, n, k, n * 7 + k + layout)
-    w = _weight(torch, ops, layout, co, so, n, k)
     x = normal(k, n + 3 * k)
     y = torch.full((n,), float("nan"), device="cuda")
+    if layout == 0x0203 and (n % 8 or k % 256):
+        w = _weight(torch, ops, layout, np.zeros(oracle.pad8(n) * oracle.pad256(k) * 2, np.uint8), None, n, k)
+        # the reference rejects these shapes before any launch (cuda/decode_mmv.cu:375-380)
+        from qw38_amd._lib import QW38_INVALID_ARGUMENT, Qw38Error
+        with pytest.raises(Qw38Error) as e:
+            ops.decode_mmv(ops.decode_desc(w, _bf16(torch, x), y, ops.DECODE_STORE_FP32))
+        assert e.value.status == QW38_INVALID_ARGUMENT and "N%8==0 and K%256==0" in e.value.detail
+        torch.cuda.synchronize()
+        assert torch.isnan(y).all(), "nothing was written"
+        return
+    co, so, wb = _random_dense(layout, n, k, n * 7 + k + layout)
+    w = _weight(torch, ops, layout, co, so, n, k)
     ops.decode_mmv(ops.decode_desc(w, _bf16(torch, x), y, ops.DECODE_STORE_FP32))
     ref = oracle.bf16_gemv(wb, oracle.fp32_to_bf16(x))
     ok, ma, mr = _tol_ok(y.cpu().numpy(), ref)

@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 
 import oracle
-from _fix import normal
+from _fix import ggml_q6k_decode, normal
 
 pytestmark = pytest.mark.gpu
 
@@ -71,3 +71,23 @@ def test_repack_q6k(torch_gpu):
     co, mo = w.physical()
     assert np.array_equal(dw.codes.cpu().numpy(), co)
     assert np.array_equal(dw.scales.cpu().numpy(), mo)
+
+
+def test_repack_q6k_against_published_ggml_coordinates(torch_gpu):
+    """The device repack of arbitrary GGML Q6_K bytes, read back through the
+    coordinate-pinned 0x0241 unpacker, equals the weights that ggml's published
+    dequantize_row_q6_K index expressions read from those bytes
+    (tests/_fix.py ggml_q6k_decode), not the oracle's own GGML converter."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 13, 768
+    rng = np.random.Generator(np.random.PCG64(41))
+    blk = rng.integers(0, 256, size=(n * k // 256, 210), dtype=np.uint8)
+    blk[:, 209] &= 0x3B  # finite fp16 d
+    dw = ops.upload_q6k_blocks(torch.from_numpy(blk.reshape(-1)).cuda(), n, k)
+    torch.cuda.synchronize()
+    got = oracle.Q6K.from_physical(dw.codes.cpu().numpy(), dw.scales.cpu().numpy(), n, k)
+    q, sc, d = ggml_q6k_decode(blk)
+    assert np.array_equal(got.q.reshape(-1, 256), q)
+    assert np.array_equal(got.sc.reshape(-1, 16), sc)
+    assert np.array_equal(got.d.reshape(-1), d)
