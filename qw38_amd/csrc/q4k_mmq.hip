@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -124,7 +125,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     uint32_t pn, uint32_t kbs, const int8_t* __restrict__ xc, const float* __restrict__ xa,
     const int32_t* __restrict__ xs, uint32_t m, uint32_t pk, float* __restrict__ out,
     const float* __restrict__ residual, uint32_t row_begin, uint32_t row_blocks, uint32_t tok_blocks,
-    GluOut glu) {
+    GluOut glu, uint32_t seg_kb, uint32_t split, float* __restrict__ part) {
   constexpr bool kQ6 = Layout == QW38_LAYOUT_Q6K_WAVE64;
   using C = Cfg<WR, WT, NI, NJ>;
   constexpr int BR = C::BR, BT = C::BT, NT = WR * WT * 64;
@@ -155,7 +156,22 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   __shared__ float Aa[2][BT * 8];
   __shared__ float2 Dd[2][BR];                     // (d, -dmin) | (d, 0)
 
-  const uint32_t tile = xcd_tile(blockIdx.x, row_blocks * tok_blocks);
+  // Q6_K accumulates K in fixed segments of seg_kb super-blocks (a function
+  // of K alone): each segment's sum starts from zero and the segment sums are
+  // added in ascending order. With split > 1 each block runs one segment of
+  // one tile and writes its sum to part[segment]; mmq_seg_reduce_kernel adds
+  // them in the same order, so split and unsplit launches give the same bits.
+  // (Q4_K has neither: its accumulation order and registers are unchanged.)
+  const bool splitk = kQ6 && split > 1;
+  const uint32_t tiles_n = row_blocks * tok_blocks;
+  const uint32_t sseg = splitk ? blockIdx.x / tiles_n : 0u;
+  const uint32_t tile = xcd_tile(splitk ? blockIdx.x % tiles_n : blockIdx.x, tiles_n);
+  const uint32_t kb_lo = splitk ? sseg * seg_kb : 0u;
+  const uint32_t kb_hi = splitk ? min(kbs, kb_lo + seg_kb) : kbs;
+  if (splitk) {
+    out = part + size_t(sseg) * m * n;
+    residual = nullptr;
+  }
   const uint32_t row0 = row_begin + (tile / tok_blocks) * HR, tok0 = (tile % tok_blocks) * BT;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wr = wave / WT, wt = wave % WT;
@@ -232,7 +248,7 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   // block the scheduler can interleave (staging VALU beside the MFMAs).
   auto fetch = [&](auto qc, uint32_t kb_in, Fetch<ZW, GPT, AW>& F) __attribute__((always_inline)) {
     constexpr uint32_t q = decltype(qc)::value;
-    const uint32_t kb = min(kb_in, kbs - 1);  // past the end: a harmless re-read
+    const uint32_t kb = min(kb_in, kb_hi - 1);  // past the end: a harmless re-read
     if constexpr (Layout == QW38_LAYOUT_Q4K_WAVE64) {
       const uint32_t c = kb / 8, kq = kb % 8;
       const uint32_t nk = min(kbs - 8 * c, 8u);
@@ -403,6 +419,9 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   };
 
   float acc[NI][NJ][4], X[NI][NJ][4];
+  // Q6_K: sum of the completed K segments (see seg_kb)
+  float tot[kQ6 ? NI : 1][kQ6 ? NJ : 1][4];
+  bool have_tot = false;
 #pragma unroll
   for (int i = 0; i < NI; ++i)
 #pragma unroll
@@ -593,6 +612,20 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
           }
         }
       }
+      if constexpr (kQ6) {
+        if (seg_kb && (kb + 1) % seg_kb == 0 && kb + 1 < kb_hi) {  // a segment ends inside the range
+#pragma unroll
+          for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                tot[i][j][v] = have_tot ? tot[i][j][v] + acc[i][j][v] : acc[i][j][v];
+                acc[i][j][v] = 0.f;
+              }
+          have_tot = true;
+        }
+      }
     }
   };
 
@@ -628,17 +661,27 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
     if (!compute_first) compute(qc, kb);
   };
 
-  fetch(std::integral_constant<uint32_t, 0>{}, 0, F[0]);
-  store(std::integral_constant<uint32_t, 0>{}, 0, F[0]);
-  fetch(std::integral_constant<uint32_t, 1>{}, 0, F[kSets - 1]);
-  if constexpr (kSets == 2) fetch(std::integral_constant<uint32_t, 2>{}, 0, F[0]);
-  for (uint32_t kb = 0; kb < kbs; ++kb) {
+  fetch(std::integral_constant<uint32_t, 0>{}, kb_lo, F[0]);
+  store(std::integral_constant<uint32_t, 0>{}, kb_lo, F[0]);
+  fetch(std::integral_constant<uint32_t, 1>{}, kb_lo, F[kSets - 1]);
+  if constexpr (kSets == 2) fetch(std::integral_constant<uint32_t, 2>{}, kb_lo, F[0]);
+  for (uint32_t kb = kb_lo; kb < kb_hi; ++kb) {
     step(std::integral_constant<uint32_t, 0>{}, kb);
     step(std::integral_constant<uint32_t, 1>{}, kb);
     step(std::integral_constant<uint32_t, 2>{}, kb);
     step(std::integral_constant<uint32_t, 3>{}, kb);
   }
   __syncthreads();  // Ti visible (also when kbs is small)
+  if constexpr (kQ6) {
+    if (have_tot) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[i][j][v] = tot[i][j][v] + acc[i][j][v];
+    }
+  }
   if constexpr (Glu) {
     // ---- SwiGLU -> Q8 epilogue. Gate waves (wr < WR / 2) park g in LDS (the
     // A tiles are free now); up wave wr + WR / 2 holds u of the same features
@@ -752,15 +795,34 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
 // Launches one tile shape over weight rows [row_begin, row_end) (row_begin a
 // multiple of the tile height; row_end = pn or a multiple of it).
 // Glu: rows are features, glu carries the up weight and the Q8 outputs.
+// Fixed K segment of the Q6_K accumulation, in super-blocks (a function of K
+// only, so every M and every split sums the same segments in the same order):
+// four segments from 16 super-blocks on, one below.
+__host__ __device__ constexpr uint32_t q6_seg_kb(uint32_t kbs) { return kbs >= 16 ? (kbs + 3) / 4 : kbs; }
+
+// Sum of the split segments in ascending order (plus the residual), the
+// operation sequence of the unsplit kernel's segment sums and store.
+__global__ void mmq_seg_reduce_kernel(const float* __restrict__ part, uint32_t segs, uint64_t count,
+                                      const float* __restrict__ residual, float* __restrict__ out) {
+  const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+  for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+    float y = part[i];
+    for (uint32_t sgm = 1; sgm < segs; ++sgm) y = y + part[sgm * count + i];
+    out[i] = residual ? y + residual[i] : y;
+  }
+}
+
 template <uint16_t Layout, int WR, int WT, int NI, int NJ, bool Glu = false>
 hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const float* residual,
-                      hipStream_t s, uint32_t row_begin, uint32_t row_end, GluOut glu = {}) {
+                      hipStream_t s, uint32_t row_begin, uint32_t row_end, GluOut glu = {},
+                      uint32_t split = 1, float* part = nullptr) {
   using C = Cfg<WR, WT, NI, NJ>;
   constexpr uint32_t H = Glu ? C::BR / 2 : C::BR;
   const uint32_t row_blocks = (row_end - row_begin + H - 1) / H;
   const uint32_t tok_blocks = (x.m + C::BT - 1) / C::BT;
   if (row_blocks == 0) return hipSuccess;
-  const dim3 grid(row_blocks * tok_blocks);
+  const uint32_t seg_kb = Layout == QW38_LAYOUT_Q6K_WAVE64 ? q6_seg_kb(w.pk / 256) : 0u;
+  const dim3 grid(row_blocks * tok_blocks * (split > 1 ? split : 1));
   // 0x020D spans are 4-byte (codes) / 2-byte (metadata) aligned in general;
   // 16-byte aligned ones (every span this library allocates) load wide.
   const bool vec = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
@@ -771,8 +833,78 @@ hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const fl
     if (!vec) kern = mmq_kernel<Layout, false, WR, WT, NI, NJ, Glu>;
   hipLaunchKernelGGL(kern, grid, dim3(WR * WT * 64), 0, s, w.codes, w.scales,
                      w.n, w.pn, w.pk / 256, x.codes, x.scales, x.sums, x.m, x.pk, out, residual,
-                     row_begin, row_blocks, tok_blocks, glu);
+                     row_begin, row_blocks, tok_blocks, glu, seg_kb, split, part);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || split <= 1) return e;
+  const uint64_t count = uint64_t(x.m) * w.n;
+  const uint32_t rgrid = uint32_t(std::min<uint64_t>((count + 255) / 256, 4096));
+  hipLaunchKernelGGL(mmq_seg_reduce_kernel, dim3(rgrid), dim3(256), 0, s, part, split, count, residual, out);
   return hipGetLastError();
+}
+
+// ---- split-K scratch (Q6_K at small M) ---------------------------------------
+// The segment sums of a split launch live in this file-scope device array
+// (each GPU holds its own copy until the process ends); host code only ever
+// passes its device address from hipGetSymbolAddress. A per-device record
+// keeps calls on different streams apart: while an earlier split launch on
+// another stream has not completed, or another host thread holds the array,
+// a projection runs unsplit instead (the same bits, more time). Launches
+// captured into a graph are not tracked: replays of such graphs on several
+// streams at once must be serialized by the caller.
+constexpr uint64_t kSplitBytes = 32ull << 20;
+__device__ __align__(256) uint8_t split_scratch[kSplitBytes];
+
+struct SplitUse {
+  void* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t stream = nullptr;
+  bool recorded = false;
+  bool busy = false;
+  bool broken = false;
+};
+std::mutex g_split_mu;
+SplitUse g_split[64];
+
+// The device's split scratch for a launch on stream s, or null (use the
+// unsplit path). A non-null result must be released by split_release.
+float* split_acquire(hipStream_t s, uint64_t bytes, int* dev_out) {
+  if (bytes > kSplitBytes) return nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(g_split_mu);
+  SplitUse& u = g_split[dev];
+  if (u.broken || u.busy) return nullptr;
+  if (!u.ptr) {
+    if (hipGetSymbolAddress(&u.ptr, HIP_SYMBOL(split_scratch)) != hipSuccess ||
+        hipEventCreateWithFlags(&u.done, hipEventDisableTiming) != hipSuccess) {
+      (void)hipGetLastError();
+      u.ptr = nullptr;
+      u.broken = true;
+      return nullptr;
+    }
+  }
+  if (u.recorded && u.stream != s) {
+    const hipError_t q = hipEventQuery(u.done);
+    if (q != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+  }
+  u.busy = true;
+  *dev_out = dev;
+  return static_cast<float*>(u.ptr);
+}
+
+void split_release(int dev, hipStream_t s, bool launched) {
+  std::lock_guard<std::mutex> lock(g_split_mu);
+  SplitUse& u = g_split[dev];
+  u.busy = false;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (launched && hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone &&
+      hipEventRecord(u.done, s) == hipSuccess) {
+    u.recorded = true;
+    u.stream = s;
+  }
 }
 
 // Glu: the tile cost model runs over the 2 n virtual rows of gate and up, and
@@ -855,6 +987,31 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   if (x.m > 64 && c129 < best) bt = 129, best = c129;
   if (x.m > 64 && c192 < best) bt = 192, best = c192;
   if (forced) bt = forced;
+  // Q6_K split-K: the 80 x 128 eight-wave tile over the fixed K segments, one
+  // block per (tile, segment), then the ordered segment sum. Taken when the
+  // busiest CU's share (rounds x segment steps at 1.07 us, plus ~4 us for
+  // the sum) beats the unsplit pick, i.e. when the unsplit grid leaves CUs
+  // idle (down projection at M = 128: 64 tiles -> 256 blocks).
+  if constexpr (q6 && !Glu) {
+    const uint32_t kbs = w.pk / 256, seg = q6_seg_kb(kbs), segs = (kbs + seg - 1) / seg;
+    static const bool split_env = [] {
+      const char* e = std::getenv("QW38_MMQ_SPLITK");
+      return !(e && std::atoi(e) == 0);
+    }();
+    if (split_env && segs > 1 && (!forced || forced == 82)) {
+      const uint64_t blocks = uint64_t((pn + 79) / 80) * ((x.m + 127) / 128) * segs;
+      const double c_split = double((blocks + cus - 1) / cus) * seg * 4 * 1.07 + 4.0;
+      if (forced == 82 || c_split < best * kbs * 4) {
+        int dev = 0;
+        if (float* part = split_acquire(s, uint64_t(segs) * x.m * w.n * 4, &dev)) {
+          const hipError_t e = launch_cfg<Layout, 1, 8, 5, 1>(w, x, out, residual, s, 0, pn, {}, segs, part);
+          split_release(dev, s, e == hipSuccess);
+          return e;
+        }
+      }
+    }
+  }
+  if (bt == 82) bt = 81;
   if (bt == 80) return launch_cfg<Layout, 1, 4, 5, 2>(w, x, out, residual, s, 0, pn);  // 80 x 128
   // Q6_K grids of at most one 128 x 32 block per CU (M <= 128 on 5120 rows)
   // run it on eight waves (16 x 32 each, two per SIMD, ping-pong order):

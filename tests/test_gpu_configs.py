@@ -94,11 +94,46 @@ def test_config3_q6k_down(torch_gpu):
     import qw38_amd.ops as ops
     n, k = 5120, 17408
     w, wl = _fit_q6k(torch, ops, n, k, 301)
-    for m in (1, 2, 8, 40):
+    # M=3 runs the M 3..4 ring kernel whose blocks loop over several 16-row
+    # tiles at this K (320 tiles on the CUs)
+    for m in (1, 2, 3, 8, 40):
         q, ob = _q8(torch, ops, silu_rows(m, k, 302 + m))
         y = _project(torch, ops, w, q, m, n)
         ref, _, _ = oracle.q6k_q8_contract(wl, ob)
         _check(y, ref, f"config3 Q6_K M={m}")
+
+
+def test_q6k_split_k_rows_independent_of_m(torch_gpu):
+    """Q6_K MMQ sums K in fixed segments (four at K = 17408) whatever the
+    launch: small M splits the segments over blocks and adds them in a second
+    kernel (M = 40, 128, 256 on 5120 rows), M = 512 runs unsplit. Every token
+    row must be bitwise the same at every M, and M = 40 matches the oracle."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 5120, 17408
+    w, wl = _fit_q6k(torch, ops, n, k, 311)
+    xs = silu_rows(512, k, 312)
+    q, ob = _q8(torch, ops, xs)
+    full = None
+    for m in (512, 40, 128, 256, 9):
+        print(f"Q6_K split-K family M={m}", flush=True)
+        qm = ops.Q8Input.empty(m, k)
+        qm.codes.copy_(q.codes[:m]); qm.scales.copy_(q.scales[:m]); qm.sums.copy_(q.sums[:m])
+        res = torch.from_numpy(normal((m, n), 313 + m)).cuda() if m == 128 else None
+        y = torch.full((m, n), float("nan"), device="cuda")
+        ops.q4k_q8_project(w, qm, y, residual=res)
+        torch.cuda.synchronize()
+        yn = y.cpu().numpy()
+        if res is not None:
+            want = (full[:m] + res.cpu().numpy()).astype(np.float32)
+            assert np.array_equal(yn.view(np.uint32), want.view(np.uint32)), "residual epilogue of the split launch"
+        elif full is None:
+            full = yn
+        else:
+            assert np.array_equal(yn.view(np.uint32), full[:m].view(np.uint32)), f"M={m} rows differ from M=512"
+        if m == 40:
+            ref, _, _ = oracle.q6k_q8_contract(wl, oracle.Q8(ob.codes[:m], ob.scales[:m], ob.sums[:m], m, k, ob.pk))
+            _check(yn, ref, "Q6_K split-K M=40")
 
 
 def test_q6k_small_shapes_and_dots(torch_gpu):
