@@ -486,6 +486,37 @@ def bench_model(torch, ops, layers, q4_layout, prefill_m, reps, peak_sclk, seed=
     return res
 
 
+def read_probe(torch, nbytes, copies, steps, warmup):
+    """Pure-read ceiling (qw38_read_probe) for a launch that reads `nbytes`:
+    grid-stride and per-wave contiguous ranges (8 or 16 loads in flight), each
+    at 2 / 4 / 8 blocks of 256 threads per CU, rotating over `copies` buffers
+    (beyond the Infinity Cache) like the decode legs; >= 100 launches per
+    point, timed like the decode legs (the lower of hipGraph replay and eager
+    launches). Returns the best GB/s and every point."""
+    from qw38_amd._lib import lib
+    nb = nbytes // 1024 * 1024
+    buf = torch.empty(copies, nb, dtype=torch.uint8, device="cuda")
+    buf.random_(0, 256)
+    sink = torch.zeros(8 * 1024, dtype=torch.int32, device="cuda")
+    pts = {}
+    for mode, name in ((0, "grid_stride"), (1, "wave_ranges"), (2, "wave_ranges16")):
+        for bpc in (2, 4, 8):
+            def fn(i, mode=mode, bpc=bpc):  # on the current stream (the capture stream inside a graph)
+                st = lib().qw38_read_probe(buf[i].data_ptr(), nb, mode, bpc, sink.data_ptr(), sink.numel(),
+                                           torch.cuda.current_stream().cuda_stream)
+                assert st == 0
+            ms, n, _, how, extra = time_both(torch, fn, copies, steps, warmup)
+            pts[f"{name}_{bpc}"] = {"us": round(ms * 1e3, 3), "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
+                                    "launches": n, "timing": how, **extra}
+    best = max(pts, key=lambda k: pts[k]["GBps"])
+    del buf
+    torch.cuda.empty_cache()
+    r = {"bytes": nb, "copies": copies, "best": best, "best_GBps": pts[best]["GBps"],
+         "best_frac_of_8TBps": round(pts[best]["GBps"] / HBM_PEAK_GBS, 4), "points": pts}
+    log(f"read probe: {r}")
+    return r
+
+
 def clock_probe(torch, ops):
     """Shader clock under a full int8 MFMA load (qw38_mfma_clock_probe) and the
     int8 dense peak at that clock: CUs x 8192 ops/cycle x sclk."""
@@ -599,6 +630,9 @@ def main():
     ap.add_argument("--mlp-leg", default=None, metavar="M:CALLS",
                     help="only run CALLS eager whole-MLP calls at M tokens (Q4_K gate/up on --layout "
                          "for M <= 8, else --mmq-layout; Q6_K down), for rocprofv3 traces")
+    ap.add_argument("--no-read-probe", action="store_true", help="skip the pure-read ceiling leg")
+    ap.add_argument("--read-probe-only", action="store_true",
+                    help="only run the pure-read ceiling leg (for rocprofv3 traces)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (counter scale for rocprof --pmc)")
     args = ap.parse_args()
@@ -662,6 +696,10 @@ def main():
     ms_list = sorted({1, *[int(v) for v in args.decode_m.split(",")]})
     clock = clock_probe(torch, ops)
     peak_sclk = clock["int8_peak_tops_at_sclk"]
+    if args.read_probe_only:
+        read_probe(torch, 100_270_080, 12, args.steps, args.warmup)
+        return
+    probe = None if args.no_read_probe else read_probe(torch, 100_270_080, 12, args.steps, args.warmup)
     rooflines = {}
     dec = bench_decode(torch, ops, "q4k", n, k, ms_list, args.steps, args.warmup, layout, 11,
                        eager_m1=True)
@@ -729,7 +767,10 @@ def main():
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                                      "copy-calibrated)",
-                     "algorithmic_bytes": head["algorithmic_bytes"]},
+                     "algorithmic_bytes": head["algorithmic_bytes"],
+                     "read_ceiling_GBps": probe["best_GBps"] if probe else None,
+                     "frac_of_read_ceiling": round(head["achieved"] / probe["best_GBps"], 4) if probe else None},
+        "read_probe": probe,
         "rooflines": rooflines,
         "mfma_clock": clock,
         "config5_model_pass": model,

@@ -419,6 +419,17 @@ int qw38_prefill_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_
  * bench to recompute the int8 MFMA dense peak at the measured sclk. */
 int qw38_mfma_clock_probe(uint32_t iterations, uint64_t* ticks, uint32_t* blocks, void* stream);
 
+/* No counterpart in the reference: a measurement aid. Reads `bytes` (a
+ * multiple of 1024, 16-byte aligned device memory) once with no arithmetic
+ * beyond an XOR fold: mode 0 grid-stride 16-byte loads, modes 1 / 2 one
+ * contiguous range per wave streamed 1 KB per load instruction with 8 / 16
+ * loads in flight; blocks_per_cu x CUs
+ * blocks of 256 threads. `sink` (>= that many uint32) is written only by a
+ * block whose fold hits a fixed 32-bit value. The pure-read ceiling the
+ * decode GEMVs are compared against. */
+int qw38_read_probe(const void* buf, uint64_t bytes, uint32_t mode, uint32_t blocks_per_cu,
+                    uint32_t* sink, uint64_t sink_len, void* stream);
+
 /* Replaces qw38::runtime::profiling::enabled (src/runtime/profiling.hpp:9-10):
  * turns the calling thread's roctx ranges ("qw38:op name=q4k_project ...",
  * the reference's NVTX strings) on or off. QW38_PROFILE=1 in the environment

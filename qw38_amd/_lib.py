@@ -121,6 +121,7 @@ SIGNATURES = {
     "qw38_prefill_mlp": (_I, [_P(Weight), _P(Weight), _P(Weight), _V, _V, _F, _V, _U32, _V, _U64,
                               _V]),
     "qw38_mfma_clock_probe": (_I, [_U32, _V, _P(_U32), _V]),
+    "qw38_read_probe": (_I, [_V, _U64, _U32, _U32, _V, _U64, _V]),
     "qw38_set_profiling": (None, [_I]),
     "qw38_code_bytes": (_U64, [_U16, _U32, _U32]),
     "qw38_scale_bytes": (_U64, [_U16, _U32, _U32]),

@@ -6,6 +6,14 @@
 // cycles / (realtime / 100 MHz) is the sclk the matrix cores actually ran at.
 // The int8 dense peak at that clock is CUs x 8192 ops x sclk. The host also
 // times the launch, which gives the achieved int8 rate of this pure-MFMA loop.
+//
+// Second aid: a pure HBM read of a buffer (no arithmetic beyond an XOR fold
+// that keeps the loads live), the ceiling a bandwidth-bound decode kernel of
+// the same byte count is measured against. Mode 0 reads grid-stride (thread
+// i of the grid reads 16 B at 16 (i + j grid_threads)); modes 1 and 2 give
+// each wave one contiguous range and stream it 1 KB per load instruction,
+// eight (mode 1) or sixteen (mode 2) loads in flight, the access pattern of
+// the streaming GEMV.
 #include "common.hpp"
 
 namespace qw38hip {
@@ -46,8 +54,63 @@ __global__ __launch_bounds__(256) void mfma_clock_kernel(uint32_t iters, uint64_
   if (acc == 0x7fffffff) ticks[2] = uint64_t(acc);  // keeps the chains live
 }
 
+template <int Mode>
+__global__ __launch_bounds__(256) void read_probe_kernel(const uint4* __restrict__ buf, uint64_t n16,
+                                                         uint32_t* __restrict__ sink) {
+  uint32_t acc = 0;
+  if constexpr (Mode == 0) {
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    for (; i + 7 * stride < n16; i += 8 * stride) {
+      uint4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = buf[i + u * stride];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += stride) {
+      const uint4 v = buf[i];
+      acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+  } else {
+    constexpr int U = Mode == 1 ? 8 : 16;  // 1 KB wave loads in flight
+    const uint64_t waves = uint64_t(gridDim.x) * (blockDim.x / 64);
+    const uint64_t wave = uint64_t(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64;
+    const uint64_t chunks = n16 / 64;  // 1 KB wave loads
+    const uint64_t c0 = chunks * wave / waves, c1 = chunks * (wave + 1) / waves;
+    const uint32_t lane = threadIdx.x & 63u;
+    uint64_t c = c0;
+    for (; c + U <= c1; c += U) {
+      uint4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = buf[(c + u) * 64 + lane];
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; c < c1; ++c) {
+      const uint4 v = buf[c * 64 + lane];
+      acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+  }
+  if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;  // keeps the loads live; practically never stored
+}
+
 }  // namespace
 }  // namespace qw38hip
+
+extern "C" int qw38_read_probe(const void* buf, uint64_t bytes, uint32_t mode, uint32_t blocks_per_cu,
+                               uint32_t* sink, uint64_t sink_len, void* stream) {
+  using namespace qw38hip;
+  if (buf == nullptr || sink == nullptr || bytes == 0 || bytes % 1024 || mode > 2 ||
+      blocks_per_cu == 0 || blocks_per_cu > 32 || reinterpret_cast<uintptr_t>(buf) % 16)
+    return QW38_INVALID_ARGUMENT;
+  const uint32_t grid = uint32_t(cu_count()) * blocks_per_cu;
+  if (sink_len < grid) return QW38_INVALID_ARGUMENT;
+  auto kern = mode == 0 ? read_probe_kernel<0> : mode == 1 ? read_probe_kernel<1> : read_probe_kernel<2>;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint4*>(buf), bytes / 16, sink);
+  return hipGetLastError() == hipSuccess ? QW38_OK : QW38_STATUS;
+}
 
 extern "C" int qw38_mfma_clock_probe(uint32_t iterations, uint64_t* ticks, uint32_t* blocks,
                                      void* stream) {

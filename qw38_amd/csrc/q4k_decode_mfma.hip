@@ -70,7 +70,8 @@ __global__ __launch_bounds__(kWaves * 64) void q4k_mfma_decode_kernel(
     const float* __restrict__ residual, uint32_t tiles) {
   extern __shared__ __align__(16) uint8_t lds[];
   // [chunk][t] 16-byte operand rows (pk/16 chunks), then a zero row, then
-  // a [g][t] and u = a*sum [g][t] (fp32), then the wave partials [w][16][T].
+  // a [g][t] and u = a*sum [g][t] (fp32), then the wave partials
+  // [slot][w][16][T] of up to six tiles.
   const uint32_t chunks = pk / 16, groups = pk / 32;
   uint4* zs = reinterpret_cast<uint4*>(lds);
   uint4* zero = zs + chunks * T;
@@ -115,27 +116,90 @@ __global__ __launch_bounds__(kWaves * 64) void q4k_mfma_decode_kernel(
   const uint32_t kb_per = (kbs + kWaves - 1) / kWaves;
   const uint32_t kb0 = min(kbs, wave * kb_per), kb1 = min(kbs, kb0 + kb_per);
 
-  for (uint32_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    const uint32_t row = min(tile * 16 + r, pn - 1);  // rows past pn: clamped, never stored
-    const uint64_t tr_base = uint64_t(row / 8) * kbs * 8 + row % 8;
-    // Partials per group class c = g % 4 (groups c and c + 4 of a super-block,
-    // in that order), summed at the end as ((c0 + c1) + (c2 + c3)): the same
-    // operation sequence for T = 4 and T = 8, so every M in 3..8 gives
-    // bitwise-identical rows for the same token. A T = 8 lane of slot gs owns
-    // classes gs and gs + 2, a T = 4 lane of slot j class j.
-    constexpr int NX = T == 8 ? 2 : 1;
-    float acc[NX][4] = {};
-    // One super-block per step: its five loads are issued together right
-    // before its arithmetic. Deeper per-wave prefetch (a ring of 2 to 4
-    // super-blocks) measured slower (34.6 to 48 us at config 2, M=8): the
-    // grid's waves already keep enough weight bytes in flight.
-    for (uint32_t kb = kb0; kb < kb1; ++kb) {
-      const uint64_t tr = tr_base + uint64_t(kb) * 8;
-      const uint4 mw = *reinterpret_cast<const uint4*>(meta + tr * 16);
-      uint2 wq[4];
+  // Partials per group class c = g % 4 (groups c and c + 4 of a super-block,
+  // in that order), summed at the end as ((c0 + c1) + (c2 + c3)): the same
+  // operation sequence for T = 4 and T = 8, so every M in 3..8 gives
+  // bitwise-identical rows for the same token. A T = 8 lane of slot gs owns
+  // classes gs and gs + 2, a T = 4 lane of slot j class j.
+  constexpr int NX = T == 8 ? 2 : 1;
+  // The block's tiles (blockIdx.x + i gridDim.x) and the wave's K range form
+  // one stream of (tile, super-block) items; the next item's five loads are
+  // issued before the current one's arithmetic, across tile boundaries, so a
+  // wave never waits a full memory latency at the start of a tile. Each
+  // tile's row partial goes to an LDS slot; every kRing tiles (and at the
+  // end) the block sums the waves' partials of those tiles in wave order.
+  constexpr uint32_t kRing = 6;
+  const uint32_t nkb = kb1 - kb0;
+  const uint32_t ntl = blockIdx.x < tiles ? (tiles - blockIdx.x + gridDim.x - 1) / gridDim.x : 0u;
+  struct Item {
+    uint4 mw;
+    uint2 wq[4];
+  };
+  auto load = [&](uint32_t ti, uint32_t kb, Item& L) __attribute__((always_inline)) {
+    const uint32_t row = min((blockIdx.x + ti * gridDim.x) * 16 + r, pn - 1);  // clamped, never stored
+    const uint64_t tr = uint64_t(row / 8) * kbs * 8 + row % 8 + uint64_t(kb) * 8;
+    L.mw = *reinterpret_cast<const uint4*>(meta + tr * 16);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        wq[i] = *reinterpret_cast<const uint2*>(codes + tr * 128 + chunk_of<T>(i, j) * 8);
+    for (int i = 0; i < 4; ++i)
+      L.wq[i] = *reinterpret_cast<const uint2*>(codes + tr * 128 + chunk_of<T>(i, j) * 8);
+  };
+  // Sums the wave partials of tiles [t_lo, t_hi) of this block (slots ti % kRing).
+  auto flush = [&](uint32_t t_lo, uint32_t t_hi) __attribute__((always_inline)) {
+    __syncthreads();
+    const uint32_t cnt = t_hi - t_lo;
+    for (uint32_t e = tid; e < cnt * 16 * T; e += blockDim.x) {
+      const uint32_t ti = t_lo + e / (16 * T), rem = e % (16 * T);
+      const uint32_t rr = rem % 16, t = rem / 16, slot = ti % kRing;
+      const uint32_t orow = (blockIdx.x + ti * gridDim.x) * 16 + rr;
+      float y = red[((slot * kWaves + 0) * 16 + rr) * T + t];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) y += red[((slot * kWaves + w) * 16 + rr) * T + t];
+      if (t < m && orow < n) {
+        const size_t o = size_t(t) * n + orow;
+        out[o] = residual ? y + residual[o] : y;
+      }
+    }
+    __syncthreads();
+  };
+  // Writes this wave's partial of tile ti (zeros for a wave without K range).
+  auto park = [&](uint32_t ti, const float (&acc)[NX][4]) __attribute__((always_inline)) {
+    float tot[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if constexpr (T == 8) {  // lanes j, j + 2 hold classes (0, 2) and (1, 3)
+        const float c01 = acc[0][v] + __shfl_xor(acc[0][v], 32);
+        const float c23 = acc[1][v] + __shfl_xor(acc[1][v], 32);
+        tot[v] = c01 + c23;
+      } else {  // lane j holds class j
+        const float c01 = acc[0][v] + __shfl_xor(acc[0][v], 16);
+        tot[v] = c01 + __shfl_xor(c01, 32);
+      }
+    }
+    if (j < (T == 8 ? 2u : 1u)) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[(((ti % kRing) * kWaves + wave) * 16 + r) * T + t0 + v] = tot[v];
+    }
+  };
+
+  float acc[NX][4] = {};
+  Item cur, nxt;
+  if (nkb && ntl) load(0, kb0, cur);
+  uint32_t t_done = 0;  // tiles already summed
+  for (uint32_t ti = 0; ti < ntl; ++ti) {
+    for (uint32_t kq = 0; kq < nkb; ++kq) {
+      const uint32_t kb = kb0 + kq;
+      // T = 8: the next item (the following super-block, or the next tile's
+      // first) is loaded now. T = 4 loads each item right before its use:
+      // a second item in registers would leave fewer than four eight-wave
+      // blocks per CU (72 VGPRs; M = 2 / 4 took 25.8 / 26.8 against 21 /
+      // 22.5 us), and its four blocks per CU keep enough loads in flight.
+      if constexpr (T == 8) {
+        if (kq + 1 < nkb) load(ti, kb + 1, nxt);
+        else if (ti + 1 < ntl) load(ti + 1, kb0, nxt);
+      } else if (kq > 0 || ti > 0) {
+        load(ti, kb, cur);
+      }
+      const uint4 mw = cur.mw;
       float X[NX][4], Y[NX][4];
       constexpr int P = T == 8 ? 4 : 2;  // epilogues per super-block
 #pragma unroll
@@ -146,7 +210,7 @@ __global__ __launch_bounds__(kWaves * 64) void q4k_mfma_decode_kernel(
         for (int h = 0; h < CH; ++h) {
           const uint32_t mp = uint32_t(p * CH + h);
           const uint32_t c = chunk_of<T>(mp, j);
-          const v4i B = unpack8(wq[mp].x, wq[mp].y);
+          const v4i B = unpack8(cur.wq[mp].x, cur.wq[mp].y);
           const bool on = slot_of<T>(j) == a_slot;
           const uint4 av = on ? zs[(kb * 16 + c) * T + a_tok] : *zero;
           const v4i A = {int(av.x), int(av.y), int(av.z), int(av.w)};
@@ -178,37 +242,19 @@ __global__ __launch_bounds__(kWaves * 64) void q4k_mfma_decode_kernel(
       for (int c = 0; c < NX; ++c)
 #pragma unroll
         for (int v = 0; v < 4; ++v) acc[c][v] = fmaf(-dmin, Y[c][v], fmaf(d, X[c][v], acc[c][v]));
+      if constexpr (T == 8) cur = nxt;
     }
-    float tot[4];
+    park(ti, acc);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      if constexpr (T == 8) {  // lanes j, j + 2 hold classes (0, 2) and (1, 3)
-        const float c01 = acc[0][v] + __shfl_xor(acc[0][v], 32);
-        const float c23 = acc[1][v] + __shfl_xor(acc[1][v], 32);
-        tot[v] = c01 + c23;
-      } else {  // lane j holds class j
-        const float c01 = acc[0][v] + __shfl_xor(acc[0][v], 16);
-        tot[v] = c01 + __shfl_xor(c01, 32);
-      }
-    }
-    if (j < (T == 8 ? 2u : 1u)) {
+    for (int c = 0; c < NX; ++c)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) red[(wave * 16 + r) * T + t0 + v] = tot[v];
+      for (int v = 0; v < 4; ++v) acc[c][v] = 0.f;
+    if (ti + 1 - t_done == kRing) {
+      flush(t_done, ti + 1);
+      t_done = ti + 1;
     }
-    __syncthreads();
-    for (uint32_t e = tid; e < 16 * T; e += blockDim.x) {
-      const uint32_t rr = e % 16, t = e / 16;
-      const uint32_t orow = tile * 16 + rr;
-      float y = red[rr * T + t];
-#pragma unroll
-      for (int w = 1; w < kWaves; ++w) y += red[(w * 16 + rr) * T + t];
-      if (t < m && orow < n) {
-        const size_t o = size_t(t) * n + orow;
-        out[o] = residual ? y + residual[o] : y;
-      }
-    }
-    __syncthreads();
   }
+  if (t_done < ntl) flush(t_done, ntl);
 }
 
 template <int T, int W>
@@ -216,7 +262,7 @@ hipError_t launch_t(const WeightView& w, const Q8View& x, float* out, const floa
                     hipStream_t s, uint32_t per_cu_cap) {
   const uint32_t kbs = w.pk / 256, tiles = (w.pn + 15) / 16;
   const size_t lds = size_t(w.pk / 16) * T * 16 + 16 + size_t(w.pk / 32) * T * 8 +
-                     size_t(W) * 16 * T * 4;
+                     6 * size_t(W) * 16 * T * 4;  // partial slots of six tiles
   if (lds > 160 * 1024) return hipErrorNotSupported;
   uint32_t per_cu = uint32_t(160 * 1024 / lds);
   per_cu = std::max(1u, std::min(per_cu, 32u / W));
