@@ -283,6 +283,23 @@ __host__ __device__ __forceinline__ uint64_t q4k_meta_row(uint16_t layout, uint3
   return uint64_t(strips) * 1024 * c + uint64_t(row / 8) * nk * 128 + (kq * 8 + row % 8) * 16;
 }
 
+// Fixed K segment of the Q6_K accumulation, in super-blocks (a function of K
+// only, so every M, tiling and split sums the same segments in the same
+// order): four segments from 16 super-blocks on, one below. The Q6_K MMQ and
+// the Q6_K batched decode both accumulate each segment from zero and add the
+// segment sums in ascending order.
+__host__ __device__ constexpr uint32_t q6_seg_kb(uint32_t kbs) { return kbs >= 16 ? (kbs + 3) / 4 : kbs; }
+
+// Library-owned device scratch (scratch.hip) for cross-block partial sums:
+// the device address of this device's array for a launch on stream s, or
+// null when `bytes` exceed it, another host thread holds it, or an earlier
+// launch on another stream that used it has not completed (callers then take
+// a path that needs no scratch and gives the same bits). A non-null result is
+// handed back with scratch_release after the launches that use it.
+constexpr uint64_t kScratchBytes = 32ull << 20;
+void* scratch_acquire(hipStream_t s, uint64_t bytes, int* device);
+void scratch_release(int device, hipStream_t s, bool launched);
+
 // ---- launchers (defined in the .hip files) ---------------------------------
 hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t pk,
                           int8_t* codes, float* scales, int32_t* sums, int* failure,

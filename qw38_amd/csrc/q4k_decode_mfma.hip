@@ -128,7 +128,7 @@ __global__ __launch_bounds__(kWaves * 64) void q4k_mfma_decode_kernel(
   // wave never waits a full memory latency at the start of a tile. Each
   // tile's row partial goes to an LDS slot; every kRing tiles (and at the
   // end) the block sums the waves' partials of those tiles in wave order.
-  constexpr uint32_t kRing = 6;
+  constexpr uint32_t kRing = 48 / kWaves;
   const uint32_t nkb = kb1 - kb0;
   const uint32_t ntl = blockIdx.x < tiles ? (tiles - blockIdx.x + gridDim.x - 1) / gridDim.x : 0u;
   struct Item {
@@ -262,7 +262,7 @@ hipError_t launch_t(const WeightView& w, const Q8View& x, float* out, const floa
                     hipStream_t s, uint32_t per_cu_cap) {
   const uint32_t kbs = w.pk / 256, tiles = (w.pn + 15) / 16;
   const size_t lds = size_t(w.pk / 16) * T * 16 + 16 + size_t(w.pk / 32) * T * 8 +
-                     6 * size_t(W) * 16 * T * 4;  // partial slots of six tiles
+                     size_t(48 / W) * W * 16 * T * 4;  // partial slots of 48 / W tiles
   if (lds > 160 * 1024) return hipErrorNotSupported;
   uint32_t per_cu = uint32_t(160 * 1024 / lds);
   per_cu = std::max(1u, std::min(per_cu, 32u / W));
@@ -299,7 +299,8 @@ hipError_t launch_q4k_mfma_decode(const WeightView& w, const Q8View& x, float* o
     const char* e = std::getenv("QW38_DECODE_MFMA_BLOCKS");
     return e ? uint32_t(std::atoi(e)) : 0u;
   }();
-  return x.m <= 4 ? launch_t<4, 8>(w, x, out, residual, s, cap) : launch_t<8, 8>(w, x, out, residual, s, cap);
+  if (x.m <= 4) return launch_t<4, 8>(w, x, out, residual, s, cap);
+  return launch_t<8, 8>(w, x, out, residual, s, cap);
 }
 
 }  // namespace qw38hip

@@ -28,7 +28,6 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
-#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -795,11 +794,6 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
 // Launches one tile shape over weight rows [row_begin, row_end) (row_begin a
 // multiple of the tile height; row_end = pn or a multiple of it).
 // Glu: rows are features, glu carries the up weight and the Q8 outputs.
-// Fixed K segment of the Q6_K accumulation, in super-blocks (a function of K
-// only, so every M and every split sums the same segments in the same order):
-// four segments from 16 super-blocks on, one below.
-__host__ __device__ constexpr uint32_t q6_seg_kb(uint32_t kbs) { return kbs >= 16 ? (kbs + 3) / 4 : kbs; }
-
 // Sum of the split segments in ascending order (plus the residual), the
 // operation sequence of the unsplit kernel's segment sums and store.
 __global__ void mmq_seg_reduce_kernel(const float* __restrict__ part, uint32_t segs, uint64_t count,
@@ -840,71 +834,6 @@ hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const fl
   const uint32_t rgrid = uint32_t(std::min<uint64_t>((count + 255) / 256, 4096));
   hipLaunchKernelGGL(mmq_seg_reduce_kernel, dim3(rgrid), dim3(256), 0, s, part, split, count, residual, out);
   return hipGetLastError();
-}
-
-// ---- split-K scratch (Q6_K at small M) ---------------------------------------
-// The segment sums of a split launch live in this file-scope device array
-// (each GPU holds its own copy until the process ends); host code only ever
-// passes its device address from hipGetSymbolAddress. A per-device record
-// keeps calls on different streams apart: while an earlier split launch on
-// another stream has not completed, or another host thread holds the array,
-// a projection runs unsplit instead (the same bits, more time). Launches
-// captured into a graph are not tracked: replays of such graphs on several
-// streams at once must be serialized by the caller.
-constexpr uint64_t kSplitBytes = 32ull << 20;
-__device__ __align__(256) uint8_t split_scratch[kSplitBytes];
-
-struct SplitUse {
-  void* ptr = nullptr;
-  hipEvent_t done = nullptr;
-  hipStream_t stream = nullptr;
-  bool recorded = false;
-  bool busy = false;
-  bool broken = false;
-};
-std::mutex g_split_mu;
-SplitUse g_split[64];
-
-// The device's split scratch for a launch on stream s, or null (use the
-// unsplit path). A non-null result must be released by split_release.
-float* split_acquire(hipStream_t s, uint64_t bytes, int* dev_out) {
-  if (bytes > kSplitBytes) return nullptr;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(g_split_mu);
-  SplitUse& u = g_split[dev];
-  if (u.broken || u.busy) return nullptr;
-  if (!u.ptr) {
-    if (hipGetSymbolAddress(&u.ptr, HIP_SYMBOL(split_scratch)) != hipSuccess ||
-        hipEventCreateWithFlags(&u.done, hipEventDisableTiming) != hipSuccess) {
-      (void)hipGetLastError();
-      u.ptr = nullptr;
-      u.broken = true;
-      return nullptr;
-    }
-  }
-  if (u.recorded && u.stream != s) {
-    const hipError_t q = hipEventQuery(u.done);
-    if (q != hipSuccess) {
-      (void)hipGetLastError();
-      return nullptr;
-    }
-  }
-  u.busy = true;
-  *dev_out = dev;
-  return static_cast<float*>(u.ptr);
-}
-
-void split_release(int dev, hipStream_t s, bool launched) {
-  std::lock_guard<std::mutex> lock(g_split_mu);
-  SplitUse& u = g_split[dev];
-  u.busy = false;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (launched && hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone &&
-      hipEventRecord(u.done, s) == hipSuccess) {
-    u.recorded = true;
-    u.stream = s;
-  }
 }
 
 // Glu: the tile cost model runs over the 2 n virtual rows of gate and up, and
@@ -1003,9 +932,10 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
       const double c_split = double((blocks + cus - 1) / cus) * seg * 4 * 1.07 + 4.0;
       if (forced == 82 || c_split < best * kbs * 4) {
         int dev = 0;
-        if (float* part = split_acquire(s, uint64_t(segs) * x.m * w.n * 4, &dev)) {
-          const hipError_t e = launch_cfg<Layout, 1, 8, 5, 1>(w, x, out, residual, s, 0, pn, {}, segs, part);
-          split_release(dev, s, e == hipSuccess);
+        if (void* part = scratch_acquire(s, uint64_t(segs) * x.m * w.n * 4, &dev)) {
+          const hipError_t e = launch_cfg<Layout, 1, 8, 5, 1>(w, x, out, residual, s, 0, pn, {}, segs,
+                                                              static_cast<float*>(part));
+          scratch_release(dev, s, e == hipSuccess);
           return e;
         }
       }

@@ -1,0 +1,74 @@
+// Library-owned device scratch for cross-block partial sums (the Q6_K MMQ
+// split-K segments and the Q6_K batched decode's segment partials).
+//
+// The array is file-scope device memory: each GPU holds its own copy until
+// the process ends. Host code only ever passes its device
+// address, looked up with hipGetSymbolAddress once per device. A per-device
+// record keeps calls on different streams apart: while an earlier launch on
+// another stream that used the array has not completed, or another host
+// thread holds it, scratch_acquire returns null and the caller takes its
+// no-scratch path (the same bits, more time). Launches captured into a graph
+// are not tracked: replays of such graphs on several streams at once must be
+// serialized by the caller.
+#include <mutex>
+
+#include "common.hpp"
+
+namespace qw38hip {
+namespace {
+
+__device__ __align__(256) uint8_t device_scratch[kScratchBytes];
+
+struct ScratchUse {
+  void* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t stream = nullptr;
+  bool recorded = false;
+  bool busy = false;
+  bool broken = false;
+};
+std::mutex g_mu;
+ScratchUse g_use[64];
+
+}  // namespace
+
+void* scratch_acquire(hipStream_t s, uint64_t bytes, int* device) {
+  if (bytes > kScratchBytes) return nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(g_mu);
+  ScratchUse& u = g_use[dev];
+  if (u.broken || u.busy) return nullptr;
+  if (!u.ptr) {
+    if (hipGetSymbolAddress(&u.ptr, HIP_SYMBOL(device_scratch)) != hipSuccess ||
+        hipEventCreateWithFlags(&u.done, hipEventDisableTiming) != hipSuccess) {
+      (void)hipGetLastError();
+      u.ptr = nullptr;
+      u.broken = true;
+      return nullptr;
+    }
+  }
+  if (u.recorded && u.stream != s) {
+    if (hipEventQuery(u.done) != hipSuccess) {  // not ready (or failed): leave it alone
+      (void)hipGetLastError();
+      return nullptr;
+    }
+  }
+  u.busy = true;
+  *device = dev;
+  return u.ptr;
+}
+
+void scratch_release(int device, hipStream_t s, bool launched) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  ScratchUse& u = g_use[device];
+  u.busy = false;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (launched && hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone &&
+      hipEventRecord(u.done, s) == hipSuccess) {
+    u.recorded = true;
+    u.stream = s;
+  }
+}
+
+}  // namespace qw38hip

@@ -136,6 +136,71 @@ def test_q6k_split_k_rows_independent_of_m(torch_gpu):
             _check(yn, ref, "Q6_K split-K M=40")
 
 
+_OWN_SCRIPT = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
+import oracle, qw38_amd.ops as ops
+from _fix import silu_rows
+n, k, m = 5120, 17408, 8
+g = torch.Generator(device="cuda"); g.manual_seed(321)
+x = torch.randn(n, k, generator=g, device="cuda") * 0.02
+w = ops.upload_q6k_blocks(ops.quantize_q6k_blocks(x, n, k), n, k)
+bf = oracle.fp32_to_bf16(silu_rows(m, k, 322))
+q = ops.Q8Input.empty(m, k)
+flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+ops.pack_q8(torch.from_numpy(bf.view(np.int16)).cuda(), q, flag)
+y = torch.empty(m, n, device="cuda")
+ops.q4k_q8_project(w, q, y)
+torch.cuda.synchronize()
+np.save(sys.argv[2], y.cpu().numpy())
+"""
+
+
+def test_q6k_decode_segments_rows_independent_of_m_and_mode(torch_gpu, tmp_path):
+    """Q6_K batched decode (M 3..8): fixed K segments, two half-waves each,
+    partials added in order. Rows are bitwise the same at every M in 3..8,
+    and the whole-tile mode (no scratch; QW38_Q6_DECODE_OWN=1, run in a child
+    process since the switch is read once) gives the same bits as the
+    spread mode with the cross-block counters."""
+    import os
+    import subprocess
+    import sys
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 5120, 17408
+    g = torch.Generator(device="cuda")
+    g.manual_seed(321)
+    x = torch.randn(n, k, generator=g, device="cuda") * 0.02
+    w = ops.upload_q6k_blocks(ops.quantize_q6k_blocks(x, n, k), n, k)
+    wl = oracle.Q6K.from_ggml(ops.quantize_q6k_blocks(x, n, k).cpu().numpy(), n, k)
+    del x
+    q, ob = _q8(torch, ops, silu_rows(8, k, 322))
+    ys = {}
+    for m in (8, 3, 4, 5, 6, 7):
+        print(f"Q6_K decode segments M={m}", flush=True)
+        qm = ops.Q8Input.empty(m, k)
+        qm.codes.copy_(q.codes[:m]); qm.scales.copy_(q.scales[:m]); qm.sums.copy_(q.sums[:m])
+        for rep in range(2):  # the second call reuses the counters the first one reset
+            y = torch.full((m, n), float("nan"), device="cuda")
+            ops.q4k_q8_project(w, qm, y)
+            torch.cuda.synchronize()
+            yn = y.cpu().numpy()
+            if rep:
+                assert np.array_equal(yn.view(np.uint32), ys[m].view(np.uint32)), f"M={m} repeat differs"
+            ys[m] = yn
+        assert np.array_equal(ys[m].view(np.uint32), ys[8][:m].view(np.uint32)), f"M={m} rows differ from M=8"
+    ref, _, _ = oracle.q6k_q8_contract(wl, ob)
+    _check(ys[8], ref, "Q6_K decode M=8")
+    out = str(tmp_path / "own.npy")
+    env = dict(os.environ, QW38_Q6_DECODE_OWN="1")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _OWN_SCRIPT, root, out], env=env, timeout=110,
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    own = np.load(out)
+    assert np.array_equal(own.view(np.uint32), ys[8].view(np.uint32)), "whole-tile mode differs from spread mode"
+
+
 def test_q6k_small_shapes_and_dots(torch_gpu):
     torch = torch_gpu
     import qw38_amd.ops as ops
