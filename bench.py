@@ -486,7 +486,7 @@ def bench_model(torch, ops, layers, q4_layout, prefill_m, reps, peak_sclk, seed=
     return res
 
 
-def read_probe(torch, nbytes, copies, steps, warmup):
+def read_probe(torch, nbytes, copies, steps, warmup, points=None):
     """Pure-read ceiling (qw38_read_probe) for a launch that reads `nbytes`:
     grid-stride and per-wave contiguous ranges (8 or 16 loads in flight), each
     at 2 / 4 / 8 blocks of 256 threads per CU, rotating over `copies` buffers
@@ -501,6 +501,8 @@ def read_probe(torch, nbytes, copies, steps, warmup):
     pts = {}
     for mode, name in ((0, "grid_stride"), (1, "wave_ranges"), (2, "wave_ranges16")):
         for bpc in (2, 4, 8):
+            if points is not None and (mode, bpc) not in points:
+                continue
             def fn(i, mode=mode, bpc=bpc):  # on the current stream (the capture stream inside a graph)
                 st = lib().qw38_read_probe(buf[i].data_ptr(), nb, mode, bpc, sink.data_ptr(), sink.numel(),
                                            torch.cuda.current_stream().cuda_stream)
@@ -700,6 +702,10 @@ def main():
         read_probe(torch, 100_270_080, 12, args.steps, args.warmup)
         return
     probe = None if args.no_read_probe else read_probe(torch, 100_270_080, 12, args.steps, args.warmup)
+    if probe:  # the same ceiling at the config-1 and config-3 weight sizes
+        few = {(0, 4), (1, 8), (2, 8)}
+        probe["config1_weights"] = read_probe(torch, 14_745_600, 82, args.steps, args.warmup, few)
+        probe["config3_weights"] = read_probe(torch, 73_113_600, 17, args.steps, args.warmup, few)
     rooflines = {}
     dec = bench_decode(torch, ops, "q4k", n, k, ms_list, args.steps, args.warmup, layout, 11,
                        eager_m1=True)

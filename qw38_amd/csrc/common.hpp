@@ -300,6 +300,10 @@ constexpr uint64_t kScratchBytes = 32ull << 20;
 void* scratch_acquire(hipStream_t s, uint64_t bytes, int* device);
 void scratch_release(int device, hipStream_t s, bool launched);
 
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per (kernel, device)
+// and size: the runtime call costs host time on every launch otherwise.
+hipError_t set_max_lds(const void* kernel, int bytes);
+
 // ---- launchers (defined in the .hip files) ---------------------------------
 hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t pk,
                           int8_t* codes, float* scales, int32_t* sums, int* failure,

@@ -270,8 +270,7 @@ hipError_t launch_t(const WeightView& w, const Q8View& x, float* out, const floa
   const uint32_t grid = std::min<uint32_t>(tiles, uint32_t(cu_count()) * per_cu);
   auto kern = q4k_mfma_decode_kernel<T, W>;
   if (lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    const hipError_t e = set_max_lds(reinterpret_cast<const void*>(kern), int(lds));
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(W * 64), lds, s, w.codes, w.scales, w.n, w.pn,

@@ -401,8 +401,7 @@ hipError_t launch_t(const WeightView& w, const Q8View& x, float* out, const floa
     if (lds_own > 160 * 1024 || segs > kIPB) return hipErrorNotSupported;
     auto kern = q6k_decode_own_kernel<TP, PDO>;
     if (lds_own > 64 * 1024) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_own));
+      const hipError_t e = set_max_lds(reinterpret_cast<const void*>(kern), int(lds_own));
       if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(kern, dim3(std::min<uint32_t>(tiles, uint32_t(cu_count()))), dim3(kW * 64), lds_own, s,
@@ -412,8 +411,7 @@ hipError_t launch_t(const WeightView& w, const Q8View& x, float* out, const floa
   auto kern = q6k_decode_spread_kernel<TP, PDS>;
   hipError_t e = hipSuccess;
   if (lds_spread > 64 * 1024)
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            int(lds_spread));
+    e = set_max_lds(reinterpret_cast<const void*>(kern), int(lds_spread));
   float* part = static_cast<float*>(sc);
   if (e == hipSuccess) {
     hipLaunchKernelGGL(kern, dim3(uint32_t((items + kIPB - 1) / kIPB)), dim3(kW * 64), lds_spread, s, w.codes,

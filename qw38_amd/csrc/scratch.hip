@@ -11,6 +11,8 @@
 // are not tracked: replays of such graphs on several streams at once must be
 // serialized by the caller.
 #include <mutex>
+#include <tuple>
+#include <vector>
 
 #include "common.hpp"
 
@@ -69,6 +71,20 @@ void scratch_release(int device, hipStream_t s, bool launched) {
     u.recorded = true;
     u.stream = s;
   }
+}
+
+hipError_t set_max_lds(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::vector<std::tuple<const void*, int, int>> done;  // (kernel, device, bytes)
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  for (auto const& d : done)
+    if (std::get<0>(d) == kernel && std::get<1>(d) == dev && std::get<2>(d) >= bytes) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.emplace_back(kernel, dev, bytes);
+  return e;
 }
 
 }  // namespace qw38hip
