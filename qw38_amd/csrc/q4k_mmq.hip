@@ -157,18 +157,23 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
 
   // Q6_K accumulates K in fixed segments of seg_kb super-blocks (a function
   // of K alone): each segment's sum starts from zero and the segment sums are
-  // added in ascending order. With split > 1 each block runs one segment of
-  // one tile and writes its sum to part[segment]; mmq_seg_reduce_kernel adds
-  // them in the same order, so split and unsplit launches give the same bits.
-  // (Q4_K has neither: its accumulation order and registers are unchanged.)
+  // added in ascending order. With split > 1 each block runs one or two
+  // consecutive segments (split = segments or segments / 2 runs) of one tile
+  // and, after its loop, writes each segment's sum to part[segment];
+  // mmq_seg_reduce_kernel adds them in the same order, so split and unsplit
+  // launches give the same bits. (Q4_K has neither: its accumulation order and
+  // registers are unchanged.)
   const bool splitk = kQ6 && split > 1;
   const uint32_t tiles_n = row_blocks * tok_blocks;
-  const uint32_t sseg = splitk ? blockIdx.x / tiles_n : 0u;
+  const uint32_t run = splitk ? blockIdx.x / tiles_n : 0u;
   const uint32_t tile = xcd_tile(splitk ? blockIdx.x % tiles_n : blockIdx.x, tiles_n);
-  const uint32_t kb_lo = splitk ? sseg * seg_kb : 0u;
-  const uint32_t kb_hi = splitk ? min(kbs, kb_lo + seg_kb) : kbs;
+  const uint32_t spr = splitk ? ((kbs + seg_kb - 1) / seg_kb) / split : 0u;  // segments per run
+  const uint32_t kb_lo = splitk ? run * spr * seg_kb : 0u;
+  const uint32_t kb_hi = splitk ? min(kbs, kb_lo + spr * seg_kb) : kbs;
+  float* part_first = nullptr;  // split runs of two segments: the first one's sum
   if (splitk) {
-    out = part + size_t(sseg) * m * n;
+    part_first = part + size_t(kb_lo / seg_kb) * m * n;
+    out = part + size_t((kb_hi - 1) / seg_kb) * m * n;
     residual = nullptr;
   }
   const uint32_t row0 = row_begin + (tile / tok_blocks) * HR, tok0 = (tile % tok_blocks) * BT;
@@ -672,7 +677,19 @@ __global__ __launch_bounds__(WR * WT * 64, (WR * WT * NI * NJ >= 64) ? 1 : 2) vo
   }
   __syncthreads();  // Ti visible (also when kbs is small)
   if constexpr (kQ6) {
-    if (have_tot) {
+    if (have_tot && splitk) {  // the run's first segment: its own partial
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const uint32_t tok = tok0 + wt * NJ * 16 + j * 16 + lr;
+          const uint32_t r4 = row0 + wr * NI * 16 + i * 16 + lk * 4;
+          if (tok >= m || r4 >= n) continue;
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (r4 + v < n) part_first[size_t(tok) * n + r4 + v] = tot[i][j][v];
+        }
+    } else if (have_tot) {
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll
@@ -816,6 +833,7 @@ hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const fl
   const uint32_t tok_blocks = (x.m + C::BT - 1) / C::BT;
   if (row_blocks == 0) return hipSuccess;
   const uint32_t seg_kb = Layout == QW38_LAYOUT_Q6K_WAVE64 ? q6_seg_kb(w.pk / 256) : 0u;
+  const uint32_t segs = seg_kb ? (w.pk / 256 + seg_kb - 1) / seg_kb : 1u;
   const dim3 grid(row_blocks * tok_blocks * (split > 1 ? split : 1));
   // 0x020D spans are 4-byte (codes) / 2-byte (metadata) aligned in general;
   // 16-byte aligned ones (every span this library allocates) load wide.
@@ -832,9 +850,13 @@ hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const fl
   if (e != hipSuccess || split <= 1) return e;
   const uint64_t count = uint64_t(x.m) * w.n;
   const uint32_t rgrid = uint32_t(std::min<uint64_t>((count + 255) / 256, 4096));
-  hipLaunchKernelGGL(mmq_seg_reduce_kernel, dim3(rgrid), dim3(256), 0, s, part, split, count, residual, out);
+  hipLaunchKernelGGL(mmq_seg_reduce_kernel, dim3(rgrid), dim3(256), 0, s, part, segs, count, residual, out);
   return hipGetLastError();
 }
+
+// Q6_K 160 x 128 eight-wave tile: microseconds per two-group K step at one
+// block per CU (measured).
+constexpr double kQ6Step160 = 1.71;
 
 // Glu: the tile cost model runs over the 2 n virtual rows of gate and up, and
 // the launches get feature ranges (virtual rows / 2).
@@ -916,32 +938,52 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   if (x.m > 64 && c129 < best) bt = 129, best = c129;
   if (x.m > 64 && c192 < best) bt = 192, best = c192;
   if (forced) bt = forced;
-  // Q6_K split-K: the 80 x 128 eight-wave tile over the fixed K segments, one
-  // block per (tile, segment), then the ordered segment sum. Taken when the
-  // busiest CU's share (rounds x segment steps at 1.07 us, plus ~4 us for
-  // the sum) beats the unsplit pick, i.e. when the unsplit grid leaves CUs
-  // idle (down projection at M = 128: 64 tiles -> 256 blocks).
+  // Q6_K: two more shapes, each unsplit or with the fixed K segments split
+  // over blocks (one segment of one tile per block, then the ordered segment
+  // sum, ~4 us):
+  //   80 x 128 eight-wave tile (1.07 us per step): split, the down projection
+  //     at M = 128 makes 64 tiles x 4 segments = 256 blocks;
+  //   160 x 128 eight-wave tile (wave tile 80 x 32: half the LDS fragment
+  //     reads per MFMA of 80 x 16; 1.71 us per step).
+  // Each cost is the busiest CU's share, rounds x steps x step time; taken
+  // when below the unsplit pick (split launches only with the library scratch).
   if constexpr (q6 && !Glu) {
     const uint32_t kbs = w.pk / 256, seg = q6_seg_kb(kbs), segs = (kbs + seg - 1) / seg;
     static const bool split_env = [] {
       const char* e = std::getenv("QW38_MMQ_SPLITK");
       return !(e && std::atoi(e) == 0);
     }();
-    if (split_env && segs > 1 && (!forced || forced == 82)) {
-      const uint64_t blocks = uint64_t((pn + 79) / 80) * ((x.m + 127) / 128) * segs;
-      const double c_split = double((blocks + cus - 1) / cus) * seg * 4 * 1.07 + 4.0;
-      if (forced == 82 || c_split < best * kbs * 4) {
-        int dev = 0;
-        if (void* part = scratch_acquire(s, uint64_t(segs) * x.m * w.n * 4, &dev)) {
-          const hipError_t e = launch_cfg<Layout, 1, 8, 5, 1>(w, x, out, residual, s, 0, pn, {}, segs,
-                                                              static_cast<float*>(part));
-          scratch_release(dev, s, e == hipSuccess);
-          return e;
-        }
+    auto rounds = [&](uint32_t rows, uint32_t runs) {
+      const uint64_t blocks = uint64_t((pn + rows - 1) / rows) * ((x.m + 127) / 128) * runs;
+      return double((blocks + cus - 1) / cus);
+    };
+    double c_best = forced ? 1e30 : best * kbs * 4;  // unsplit pick, whole launch
+    int pick = 0;                                    // 81 / 160 unsplit, 82 / 162 split
+    auto consider = [&](int id, double c) {
+      if ((!forced && c < c_best) || forced == id) c_best = c, pick = id;
+    };
+    consider(160, rounds(160, 1) * kbs * 4 * kQ6Step160);
+    if (split_env && segs > 1) {
+      consider(82, rounds(80, segs) * seg * 4 * 1.07 + 4.0);
+      consider(162, rounds(160, segs) * seg * 4 * kQ6Step160 + 4.0);
+      if (segs % 2 == 0)  // runs of two segments
+        consider(163, rounds(160, segs / 2) * 2 * seg * 4 * kQ6Step160 + 4.0);
+    }
+    if (pick == 160) return launch_cfg<Layout, 2, 4, 5, 2>(w, x, out, residual, s, 0, pn);  // 160 x 128
+    if (pick == 82 || pick == 162 || pick == 163) {
+      int dev = 0;
+      if (void* part = scratch_acquire(s, uint64_t(segs) * x.m * w.n * 4, &dev)) {
+        float* pp = static_cast<float*>(part);
+        const uint32_t runs = pick == 163 ? segs / 2 : segs;
+        const hipError_t e = pick == 82
+                                 ? launch_cfg<Layout, 1, 8, 5, 1>(w, x, out, residual, s, 0, pn, {}, runs, pp)
+                                 : launch_cfg<Layout, 2, 4, 5, 2>(w, x, out, residual, s, 0, pn, {}, runs, pp);
+        scratch_release(dev, s, e == hipSuccess);
+        return e;
       }
     }
   }
-  if (bt == 82) bt = 81;
+  if (bt == 82 || bt > 160) bt = 81;
   if (bt == 80) return launch_cfg<Layout, 1, 4, 5, 2>(w, x, out, residual, s, 0, pn);  // 80 x 128
   // Q6_K grids of at most one 128 x 32 block per CU (M <= 128 on 5120 rows)
   // run it on eight waves (16 x 32 each, two per SIMD, ping-pong order):
