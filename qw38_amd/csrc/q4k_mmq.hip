@@ -983,7 +983,7 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
       }
     }
   }
-  if (bt == 82 || bt > 160) bt = 81;
+  if (bt == 82 || (bt > 160 && bt < 192)) bt = 81;  // Q6_K split ids without the scratch
   if (bt == 80) return launch_cfg<Layout, 1, 4, 5, 2>(w, x, out, residual, s, 0, pn);  // 80 x 128
   // Q6_K grids of at most one 128 x 32 block per CU (M <= 128 on 5120 rows)
   // run it on eight waves (16 x 32 each, two per SIMD, ping-pong order):
