@@ -446,8 +446,12 @@ hipError_t launch_q6k_mfma_decode(const WeightView& w, const Q8View& x, float* o
   if ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(x.codes)) % 16 ||
       reinterpret_cast<uintptr_t>(w.scales) % 4)
     return hipErrorNotSupported;
-  return x.m <= 4 ? launch_t<1, 1, 3>(w, x, out, residual, s, own_env)
-                  : launch_t<2, 0, 3>(w, x, out, residual, s, own_env);
+  // Spread-mode weight ring: one super-block ahead (config 3 M=3 / M=8 with
+  // 1, 2, 3, 4, 5 ahead: 20.4 / 22.3, 20.6 / 22.8, 20.8 / 23.5, 21.6 / 24.4,
+  // 22.1 / 29.1 us; the staging and the LDS operand reads, not the weight
+  // latency, set the pace). Own mode at M 5..8 keeps no ring (144 VGPRs).
+  return x.m <= 4 ? launch_t<1, 1, 1>(w, x, out, residual, s, own_env)
+                  : launch_t<2, 0, 1>(w, x, out, residual, s, own_env);
 }
 
 }  // namespace qw38hip
