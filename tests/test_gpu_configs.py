@@ -106,16 +106,19 @@ def test_config3_q6k_down(torch_gpu):
 def test_q6k_split_k_rows_independent_of_m(torch_gpu):
     """Q6_K MMQ sums K in fixed segments (four at K = 17408) whatever the
     launch: small M splits the segments over blocks and adds them in a second
-    kernel (M = 40, 128, 256 on 5120 rows), M = 512 runs unsplit. Every token
-    row must be bitwise the same at every M, and M = 40 matches the oracle."""
+    kernel (M = 40, 128, 256 on 5120 rows), M = 512 and 2048 run unsplit on
+    different tiles. Every token row must be bitwise the same at every M, and
+    M = 40 matches the oracle."""
     torch = torch_gpu
     import qw38_amd.ops as ops
     n, k = 5120, 17408
     w, wl = _fit_q6k(torch, ops, n, k, 311)
-    xs = silu_rows(512, k, 312)
+    xs = silu_rows(2048, k, 312)
     q, ob = _q8(torch, ops, xs)
     full = None
-    for m in (512, 40, 128, 256, 9):
+    # 2048: the unsplit 160 x 128 tile; 512: unsplit 80 x 128; 40 / 128 / 256:
+    # split launches; 9: the smallest MMQ
+    for m in (2048, 512, 40, 128, 256, 9):
         print(f"Q6_K split-K family M={m}", flush=True)
         qm = ops.Q8Input.empty(m, k)
         qm.codes.copy_(q.codes[:m]); qm.scales.copy_(q.scales[:m]); qm.sums.copy_(q.sums[:m])
