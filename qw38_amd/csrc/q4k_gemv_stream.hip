@@ -255,6 +255,44 @@ __device__ __forceinline__ void stream_strip(const uint8_t* cstrip, const uint8_
   }
 }
 
+// stream_quarter with the quarter's first pair already in registers (`t`, in)
+// and, while the quarter's last pair is consumed, the first pair of the same
+// quarter of the next strip loaded into `t` (out) when there is one: a wave
+// of the persistent grid then never starts a strip with a full memory latency.
+// The consume sequence and lane reduction are stream_quarter's (bitwise the
+// same partials). Even kbs only (no odd tail tile).
+template <uint16_t Layout, int MT, bool Fast>
+__device__ __forceinline__ void stream_quarter_chain(const uint8_t* cstrip, const uint8_t* mstrip,
+                                                     const uint8_t* ncstrip, const uint8_t* nmstrip,
+                                                     bool have_next, uint32_t kbs, uint32_t qi, uint32_t lane,
+                                                     const int8_t* sz, const float2* sau, uint32_t groups,
+                                                     float part[MT], Tile& t) {
+  const uint32_t h = lane >> 5, j = lane & 3u, g0 = 2 * j;
+  const bool hi = j >= 2;
+  const uint32_t sh = 16u * (j & 1u);
+  const uint32_t coff = lane * 32, moff = lane * 4;
+  const uint32_t pairs = kbs / 2;
+  const uint32_t q0 = quarter_begin(pairs, qi), q1 = quarter_begin(pairs, qi + 1);
+#pragma unroll
+  for (int u = 0; u < MT; ++u) part[u] = 0.f;
+  Tile cur = t, nxt;
+  for (uint32_t q = q0; q < q1; ++q) {
+    if (q + 1 < q1)
+      load_tile<Fast>(cstrip + size_t(q + 1) * 2048, mstrip + size_t(q + 1) * 256, coff, moff, nxt);
+    else if (have_next)
+      load_tile<Fast>(ncstrip + size_t(q0) * 2048, nmstrip + size_t(q0) * 256, coff, moff, nxt);
+    consume<Layout, MT, Fast>(cur, 2 * q + h, g0, hi, sh, sz, sau, groups, part);
+    cur = nxt;
+  }
+  t = cur;
+#pragma unroll
+  for (int u = 0; u < MT; ++u) {
+    part[u] += __shfl_xor(part[u], 1);
+    part[u] += __shfl_xor(part[u], 2);
+    part[u] += __shfl_xor(part[u], 32);
+  }
+}
+
 // A wave's whole K quarter (one to three tile pairs: even kbs of 8 to 24, so
 // every quarter is non-empty) loaded into registers before the block stages its activations, so
 // the first weight loads overlap the staging instead of following it: short
@@ -341,7 +379,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n,
     uint32_t strips, uint32_t kbs, const int8_t* __restrict__ xc,
     const float* __restrict__ xa, const int32_t* __restrict__ xs, uint32_t pk,
-    float* __restrict__ out, const float* __restrict__ residual, uint32_t persistent) {
+    float* __restrict__ out, const float* __restrict__ residual, uint32_t persistent, uint32_t chain) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int SPB = 4 / WS, QPW = 4 / WS;  // strips per block, quarters per wave
   const uint32_t groups = pk / 32;
@@ -443,12 +481,70 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
     return true;
   };
   uint32_t base = blockIdx.x * SPB;
-  if (Pre && base < strips) {
-    strip_group(base, true);
-    base += stride;
+  if constexpr (WS == 4 && Fast) {
+    // Persistent K-split grid with even kbs: strips chained, the next strip's
+    // first pair in flight while the current strip's last pair is consumed.
+    if (Pre || chain) {  // (the Pre launch is always chained)
+      const uint32_t lane_off = lane * 32, moff = lane * 4;
+      const uint32_t pairs = kbs / 2, q0 = quarter_begin(pairs, ks);
+      Tile t;
+      auto strip_ptrs = [&](uint32_t st, const uint8_t*& c, const uint8_t*& mm) __attribute__((always_inline)) {
+        c = codes + size_t(min(st, strips - 1)) * kbs * 1024;
+        mm = meta + size_t(min(st, strips - 1)) * kbs * 128;
+      };
+      // the K-split reduction of one strip (as strip_group's)
+      auto finish = [&](uint32_t strip, const float (&part)[MT], bool more) __attribute__((always_inline)) {
+        const uint32_t row = strip * 8 + r;
+        const bool writer = (lane & 35u) == 0;
+        if (writer) {
+#pragma unroll
+          for (int u = 0; u < MT; ++u) red[((wave * QPW + 0) * MT + u) * 8 + r] = part[u];
+        }
+        __syncthreads();
+        if (ks == 0 && writer && row < n) {
+#pragma unroll
+          for (int u = 0; u < MT; ++u) {
+            float total = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) total += red[((wave * QPW + q) * MT + u) * 8 + r];
+            const size_t i = size_t(u) * n + row;
+            out[i] = total + (residual ? residual[i] : 0.f);
+          }
+        }
+        if (more) __syncthreads();  // red is rewritten by the next strip
+      };
+      if (base < strips) {
+        const uint8_t *c, *mm;
+        strip_ptrs(Pre ? base + stride : base, c, mm);
+        if (!Pre || base + stride < strips)
+          load_tile<Fast>(c + size_t(q0) * 2048, mm + size_t(q0) * 256, lane_off, moff, t);
+      }
+      if (Pre && base < strips) {  // the first strip from the preloaded quarter
+        float part[MT];
+        consume_quarter<Layout, MT, Fast>(pre, lane, sz, sau, groups, part);
+        finish(base, part, base + stride < strips);
+        base += stride;
+      }
+      for (; base < strips; base += stride) {
+        const bool have_next = base + stride < strips;
+        const uint8_t *cs, *ms, *nc, *nm;
+        strip_ptrs(base, cs, ms);
+        strip_ptrs(base + stride, nc, nm);
+        float part[MT];
+        stream_quarter_chain<Layout, MT, Fast>(cs, ms, nc, nm, have_next, kbs, ks, lane, sz, sau, groups, part, t);
+        finish(base, part, have_next);
+      }
+      return;
+    }
   }
-  for (; base < strips; base += stride)
-    if (!strip_group(base, false)) break;
+  if constexpr (!(WS == 4 && Fast && Pre)) {
+    if (Pre && base < strips) {
+      strip_group(base, true);
+      base += stride;
+    }
+    for (; base < strips; base += stride)
+      if (!strip_group(base, false)) break;
+  }
 }
 
 template <uint16_t Layout, int MT, bool Fast>
@@ -457,6 +553,13 @@ hipError_t stream_ws(const WeightView& w, const Q8View& x, float* out, const flo
   const uint32_t strips = w.pn / 8, kbs = w.pk / 256;
   const uint32_t groups = w.pk / 32;
   const size_t lds = size_t(MT) * w.pk + size_t(MT) * groups * 8 + 8 * MT * 8 * 4;
+  // Chained strips (persistent K-split grid, even kbs >= 8); QW38_GEMV_CHAIN=0
+  // turns it off (same bits).
+  static const bool chain_env = [] {
+    const char* e = std::getenv("QW38_GEMV_CHAIN");
+    return !(e && std::atoi(e) == 0);
+  }();
+  const uint32_t chain = (chain_env && ws == 4 && Fast && kbs % 2 == 0 && kbs >= 8) ? 1u : 0u;
 #define QW38_STREAM_LAUNCH(WSV)                                                          \
   do {                                                                                   \
     const uint32_t need = (strips + (4 / WSV) - 1) / (4 / WSV);                          \
@@ -468,7 +571,7 @@ hipError_t stream_ws(const WeightView& w, const Q8View& x, float* out, const flo
         kern = gemv_stream_kernel<Layout, MT, Fast, WSV, true>;                          \
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, s, w.codes, w.scales, w.n,      \
                        strips, kbs, x.codes, x.scales, x.sums, x.pk, out, residual,      \
-                       persistent);                                                      \
+                       persistent, chain);                                               \
   } while (0)
   if (ws == 4) QW38_STREAM_LAUNCH(4);
   else if (ws == 2) QW38_STREAM_LAUNCH(2);
