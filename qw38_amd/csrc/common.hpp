@@ -296,7 +296,8 @@ __host__ __device__ constexpr uint32_t q6_seg_kb(uint32_t kbs) { return kbs >= 1
 // launch on another stream that used it has not completed (callers then take
 // a path that needs no scratch and gives the same bits). A non-null result is
 // handed back with scratch_release after the launches that use it.
-constexpr uint64_t kScratchBytes = 32ull << 20;
+// 64 MB: four Q6_K segment partials of a 5120-row weight up to M = 800.
+constexpr uint64_t kScratchBytes = 64ull << 20;
 void* scratch_acquire(hipStream_t s, uint64_t bytes, int* device);
 void scratch_release(int device, hipStream_t s, bool launched);
 

@@ -940,7 +940,7 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   if (forced) bt = forced;
   // Q6_K: two more shapes, each unsplit or with the fixed K segments split
   // over blocks (one segment of one tile per block, then the ordered segment
-  // sum, ~4 us):
+  // sum, c_sum):
   //   80 x 128 eight-wave tile (1.07 us per step): split, the down projection
   //     at M = 128 makes 64 tiles x 4 segments = 256 blocks;
   //   160 x 128 eight-wave tile (wave tile 80 x 32: half the LDS fragment
@@ -957,6 +957,9 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
       const uint64_t blocks = uint64_t((pn + rows - 1) / rows) * ((x.m + 127) / 128) * runs;
       return double((blocks + cus - 1) / cus);
     };
+    // the ordered segment sum reads every partial once: about 1.5 us plus the
+    // partial bytes at 5 TB/s (3 us at M = 128, 9 us at M = 512 on 5120 rows)
+    const double c_sum = 1.5 + double(segs) * x.m * w.n * 4 / 5e6;
     double c_best = forced ? 1e30 : best * kbs * 4;  // unsplit pick, whole launch
     int pick = 0;                                    // 81 / 160 unsplit, 82 / 162 split
     auto consider = [&](int id, double c) {
@@ -964,10 +967,10 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
     };
     consider(160, rounds(160, 1) * kbs * 4 * kQ6Step160);
     if (split_env && segs > 1) {
-      consider(82, rounds(80, segs) * seg * 4 * 1.07 + 4.0);
-      consider(162, rounds(160, segs) * seg * 4 * kQ6Step160 + 4.0);
+      consider(82, rounds(80, segs) * seg * 4 * 1.07 + c_sum);
+      consider(162, rounds(160, segs) * seg * 4 * kQ6Step160 + c_sum);
       if (segs % 2 == 0)  // runs of two segments
-        consider(163, rounds(160, segs / 2) * 2 * seg * 4 * kQ6Step160 + 4.0);
+        consider(163, rounds(160, segs / 2) * 2 * seg * 4 * kQ6Step160 + c_sum);
     }
     if (pick == 160) return launch_cfg<Layout, 2, 4, 5, 2>(w, x, out, residual, s, 0, pn);  // 160 x 128
     if (pick == 82 || pick == 162 || pick == 163) {
