@@ -419,6 +419,14 @@ int qw38_prefill_mlp(const qw38_weight* gate, const qw38_weight* up, const qw38_
  * bench to recompute the int8 MFMA dense peak at the measured sclk. */
 int qw38_mfma_clock_probe(uint32_t iterations, uint64_t* ticks, uint32_t* blocks, void* stream);
 
+/* No counterpart in the reference: a diagnostic. Writes the library scratch
+ * requests on the current device since the process started: stats[0]
+ * granted, stats[1] refused because the request exceeded the 64 MB array,
+ * stats[2] refused because the array was in use (another thread, or earlier
+ * work on another stream). Refused requests run the path without scratch
+ * (same bits, more time); tests use the counts to confirm which path ran. */
+int qw38_scratch_stats(uint64_t* stats);
+
 /* No counterpart in the reference: a measurement aid. Reads `bytes` (a
  * multiple of 1024, 16-byte aligned device memory) once with no arithmetic
  * beyond an XOR fold: mode 0 grid-stride 16-byte loads, modes 1 / 2 one

@@ -28,6 +28,7 @@ struct ScratchUse {
   bool recorded = false;
   bool busy = false;
   bool broken = false;
+  uint64_t granted = 0, refused_size = 0, refused_busy = 0;  // qw38_scratch_stats
 };
 std::mutex g_mu;
 ScratchUse g_use[64];
@@ -35,12 +36,18 @@ ScratchUse g_use[64];
 }  // namespace
 
 void* scratch_acquire(hipStream_t s, uint64_t bytes, int* device) {
-  if (bytes > kScratchBytes) return nullptr;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
   std::lock_guard<std::mutex> lock(g_mu);
   ScratchUse& u = g_use[dev];
-  if (u.broken || u.busy) return nullptr;
+  if (bytes > kScratchBytes) {
+    ++u.refused_size;
+    return nullptr;
+  }
+  if (u.broken || u.busy) {
+    ++u.refused_busy;
+    return nullptr;
+  }
   if (!u.ptr) {
     if (hipGetSymbolAddress(&u.ptr, HIP_SYMBOL(device_scratch)) != hipSuccess ||
         hipEventCreateWithFlags(&u.done, hipEventDisableTiming) != hipSuccess) {
@@ -53,10 +60,12 @@ void* scratch_acquire(hipStream_t s, uint64_t bytes, int* device) {
   if (u.recorded && u.stream != s) {
     if (hipEventQuery(u.done) != hipSuccess) {  // not ready (or failed): leave it alone
       (void)hipGetLastError();
+      ++u.refused_busy;
       return nullptr;
     }
   }
   u.busy = true;
+  ++u.granted;
   *device = dev;
   return u.ptr;
 }
@@ -88,3 +97,22 @@ hipError_t set_max_lds(const void* kernel, int bytes) {
 }
 
 }  // namespace qw38hip
+
+// Scratch requests on the current device since the process started:
+// stats[0] granted, stats[1] refused for size (larger than the array),
+// stats[2] refused because the array was in use (another thread, or earlier
+// work on another stream). A refused request runs the no-scratch path.
+extern "C" int qw38_scratch_stats(uint64_t* stats) {
+  if (!stats) return QW38_INVALID_ARGUMENT;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return QW38_STATUS;
+  }
+  std::lock_guard<std::mutex> lock(qw38hip::g_mu);
+  const qw38hip::ScratchUse& u = qw38hip::g_use[dev];
+  stats[0] = u.granted;
+  stats[1] = u.refused_size;
+  stats[2] = u.refused_busy;
+  return QW38_OK;
+}

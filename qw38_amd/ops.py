@@ -140,6 +140,14 @@ def q4k_q8_gate_up_swiglu(gate: PrefillWeight, up: PrefillWeight, x: Q8Input, ou
                                            _ptr(failure), failure.numel(), _stream(stream)))
 
 
+def scratch_stats() -> tuple[int, int, int]:
+    """Library scratch requests on the current device since the process
+    started: (granted, refused for size, refused because in use)."""
+    st = (C.c_uint64 * 3)()
+    check(lib().qw38_scratch_stats(st))
+    return int(st[0]), int(st[1]), int(st[2])
+
+
 def q8_mlp_workspace_bytes(m: int) -> int:
     return int(lib().qw38_q8_mlp_workspace_bytes(m))
 

@@ -106,9 +106,11 @@ def test_config3_q6k_down(torch_gpu):
 def test_q6k_split_k_rows_independent_of_m(torch_gpu):
     """Q6_K MMQ sums K in fixed segments (four at K = 17408) whatever the
     launch: small M splits the segments over blocks and adds them in a second
-    kernel (M = 40, 128, 256 on 5120 rows), M = 512 and 2048 run unsplit on
-    different tiles. Every token row must be bitwise the same at every M, and
-    M = 40 matches the oracle."""
+    kernel (M = 9, 40, 128, 256, 512 on 5120 rows), M = 2048 runs unsplit on
+    the 160 x 128 tile. Every token row must be bitwise the same at every M,
+    M = 40 matches the oracle, and the split launches must really have run
+    split: the library scratch counters show each of them granted (a refused
+    request silently takes the no-scratch path, which gives the same bits)."""
     torch = torch_gpu
     import qw38_amd.ops as ops
     n, k = 5120, 17408
@@ -116,16 +118,23 @@ def test_q6k_split_k_rows_independent_of_m(torch_gpu):
     xs = silu_rows(2048, k, 312)
     q, ob = _q8(torch, ops, xs)
     full = None
-    # 2048: the unsplit 160 x 128 tile; 512: unsplit 80 x 128; 40 / 128 / 256:
-    # split launches; 9: the smallest MMQ
+    # 2048: the unsplit 160 x 128 tile; 512: 160 x 128 split per segment (42 MB
+    # of partials); 40 / 128 / 256: 80 x 128 or 160 x 128 split; 9: the
+    # smallest MMQ
     for m in (2048, 512, 40, 128, 256, 9):
         print(f"Q6_K split-K family M={m}", flush=True)
         qm = ops.Q8Input.empty(m, k)
         qm.codes.copy_(q.codes[:m]); qm.scales.copy_(q.scales[:m]); qm.sums.copy_(q.sums[:m])
         res = torch.from_numpy(normal((m, n), 313 + m)).cuda() if m == 128 else None
         y = torch.full((m, n), float("nan"), device="cuda")
+        torch.cuda.synchronize()
+        before = ops.scratch_stats()
         ops.q4k_q8_project(w, qm, y, residual=res)
         torch.cuda.synchronize()
+        after = ops.scratch_stats()
+        if m != 2048:
+            assert after[0] == before[0] + 1 and after[1:] == before[1:], \
+                f"M={m}: split launch did not get the scratch ({before} -> {after})"
         yn = y.cpu().numpy()
         if res is not None:
             want = (full[:m] + res.cpu().numpy()).astype(np.float32)
@@ -183,10 +192,15 @@ def test_q6k_decode_segments_rows_independent_of_m_and_mode(torch_gpu, tmp_path)
         print(f"Q6_K decode segments M={m}", flush=True)
         qm = ops.Q8Input.empty(m, k)
         qm.codes.copy_(q.codes[:m]); qm.scales.copy_(q.scales[:m]); qm.sums.copy_(q.sums[:m])
-        for rep in range(2):  # the second call reuses the counters the first one reset
+        for rep in range(2):  # the second call reuses the partials of the first one
             y = torch.full((m, n), float("nan"), device="cuda")
+            torch.cuda.synchronize()
+            before = ops.scratch_stats()
             ops.q4k_q8_project(w, qm, y)
             torch.cuda.synchronize()
+            after = ops.scratch_stats()
+            assert after[0] == before[0] + 1 and after[1:] == before[1:], \
+                f"M={m}: the spread decode did not get the scratch ({before} -> {after})"
             yn = y.cpu().numpy()
             if rep:
                 assert np.array_equal(yn.view(np.uint32), ys[m].view(np.uint32)), f"M={m} repeat differs"
