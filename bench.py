@@ -499,7 +499,7 @@ def read_probe(torch, nbytes, copies, steps, warmup, points=None):
     buf.random_(0, 256)
     sink = torch.zeros(8 * 1024, dtype=torch.int32, device="cuda")
     pts = {}
-    for mode, name in ((0, "grid_stride"), (1, "wave_ranges"), (2, "wave_ranges16")):
+    for mode, name in ((0, "grid_stride"), (1, "wave_ranges"), (2, "wave_ranges16"), (3, "wave_ranges_nt")):
         for bpc in (2, 4, 8):
             if points is not None and (mode, bpc) not in points:
                 continue

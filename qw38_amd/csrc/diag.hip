@@ -73,7 +73,7 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const uint4* __restrict
       acc ^= v.x ^ v.y ^ v.z ^ v.w;
     }
   } else {
-    constexpr int U = Mode == 1 ? 8 : 16;  // 1 KB wave loads in flight
+    constexpr int U = Mode == 2 ? 16 : 8;  // 1 KB wave loads in flight
     const uint64_t waves = uint64_t(gridDim.x) * (blockDim.x / 64);
     const uint64_t wave = uint64_t(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64;
     const uint64_t chunks = n16 / 64;  // 1 KB wave loads
@@ -83,7 +83,16 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const uint4* __restrict
     for (; c + U <= c1; c += U) {
       uint4 v[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = buf[(c + u) * 64 + lane];
+      for (int u = 0; u < U; ++u) {
+        if constexpr (Mode == 3)  // non-temporal hint on the streamed lines
+        {
+          typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+          const u4v t = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(&buf[(c + u) * 64 + lane]));
+          v[u] = make_uint4(t.x, t.y, t.z, t.w);
+        }
+        else
+          v[u] = buf[(c + u) * 64 + lane];
+      }
 #pragma unroll
       for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
@@ -101,12 +110,15 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const uint4* __restrict
 extern "C" int qw38_read_probe(const void* buf, uint64_t bytes, uint32_t mode, uint32_t blocks_per_cu,
                                uint32_t* sink, uint64_t sink_len, void* stream) {
   using namespace qw38hip;
-  if (buf == nullptr || sink == nullptr || bytes == 0 || bytes % 1024 || mode > 2 ||
+  if (buf == nullptr || sink == nullptr || bytes == 0 || bytes % 1024 || mode > 3 ||
       blocks_per_cu == 0 || blocks_per_cu > 32 || reinterpret_cast<uintptr_t>(buf) % 16)
     return QW38_INVALID_ARGUMENT;
   const uint32_t grid = uint32_t(cu_count()) * blocks_per_cu;
   if (sink_len < grid) return QW38_INVALID_ARGUMENT;
-  auto kern = mode == 0 ? read_probe_kernel<0> : mode == 1 ? read_probe_kernel<1> : read_probe_kernel<2>;
+  auto kern = mode == 0   ? read_probe_kernel<0>
+              : mode == 1 ? read_probe_kernel<1>
+              : mode == 2 ? read_probe_kernel<2>
+                          : read_probe_kernel<3>;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint4*>(buf), bytes / 16, sink);
   return hipGetLastError() == hipSuccess ? QW38_OK : QW38_STATUS;
