@@ -33,6 +33,9 @@
 #include "common.hpp"
 
 namespace qw38hip {
+uint64_t mmq_dma_scratch_bytes(uint32_t m, uint32_t pk);
+hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
+                          hipStream_t s, uint32_t rows, void* scratch);
 namespace {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -1009,7 +1012,26 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   } else {
     if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 128
     if (forced) big_rows = pn;
-    hipError_t e = launch_cfg<Layout, 4, 2, 4, 4, Glu>(w, x, out, residual, s, 0, big_rows / kv, glu);
+    hipError_t e = hipErrorNotReady;
+    // 0x020D with 16-byte aligned spans: the direct-copy form of the same
+    // tile (q4k_mmq_dma.hip, bitwise-equal outputs) when the library scratch
+    // holds its pre-pass; QW38_MMQ_DMA=0 turns it off.
+    static const bool dma_env = [] {
+      const char* v = std::getenv("QW38_MMQ_DMA");
+      return !(v && std::atoi(v) == 0);
+    }();
+    if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2 && !Glu) {
+      const bool aligned = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
+                             reinterpret_cast<uintptr_t>(x.codes)) % 16) == 0;
+      if (dma_env && aligned && x.pk == w.pk) {
+        int dev = 0;
+        if (void* sc = scratch_acquire(s, mmq_dma_scratch_bytes(x.m, x.pk), &dev)) {
+          e = launch_mmq_dma(w, x, out, residual, s, big_rows, sc);
+          scratch_release(dev, s, e == hipSuccess);
+        }
+      }
+    }
+    if (e == hipErrorNotReady) e = launch_cfg<Layout, 4, 2, 4, 4, Glu>(w, x, out, residual, s, 0, big_rows / kv, glu);
     if (e != hipSuccess || big_rows == pn) return e;
     return launch_cfg<Layout, 4, 1, 2, 2, Glu>(w, x, out, residual, s, big_rows / kv, end, glu);
   }

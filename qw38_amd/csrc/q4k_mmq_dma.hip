@@ -1,0 +1,519 @@
+// Prefill MMQ for Q4_K layout 0x020D with direct global->LDS staging: the
+// 256 x 128 tile of mmq_kernel (q4k_mmq.hip), restructured so that no VALU
+// work and no VGPRs go into moving operands.
+//
+// Per-(row, token) arithmetic is that of mmq_kernel, operation for operation
+// (cuda/q4k_q8.cu:140,245 reassociated as described there): one
+// v_mfma_f32_16x16x32_f16 per K32 group gives P = s * dot exactly (A = s * w
+// <= 945, B = z, every partial sum an integer below 2^24), X = a' P0 then
+// X = fma(a', P, X) over the super-block's groups in order, the min term Y
+// from two 16x16x16 MFMAs on the same hi / lo operands, acc = fma(-dmin, Y,
+// fma(d, X, acc)), and out = acc * (1 / ts) (+ residual). The outputs are
+// therefore bitwise equal to every mmq_kernel tile shape.
+//
+// What differs is the data movement:
+// - A pre-pass (mmq_dma_prep_kernel) writes the activations once per call as
+//   FP16 codes in the B-fragment order of the tile (chunk-major per K step, so
+//   each 1 KB wave copy is one contiguous run), plus per (token, super-block)
+//   the scaled a' = a * ts, the min-term operand hi / lo and 1 / ts. The
+//   per-token scale ts is computed once there instead of in every block.
+// - The block's 256 weight rows arrive as raw 0x020D bytes (1 KB per 8-row
+//   tile and super-block, 16-byte chunks XOR-swizzled within a row so the
+//   fragment reads are conflict-free) and each wave owns 32 rows x all 128 tokens: it
+//   dequantizes its own A fragments straight from the raw bytes, so A never
+//   makes an FP16 round trip through LDS.
+// - All staging is global_load_lds_dwordx4 (no VGPRs, no VALU). A ring of four
+//   K-step slots for B and two super-block slots for A and the token data is
+//   filled two steps ahead; one barrier per pair of K steps, with explicit
+//   vmcnt waits (each wave waits for its own copies, the barrier publishes
+//   them).
+#include <algorithm>
+#include <cstdlib>
+
+#include "common.hpp"
+
+namespace qw38hip {
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kBR = 256, kBT = 128;
+// LDS: B ring (4 K steps x 16 KB), A (2 super-blocks x 256 rows x 128 B raw
+// codes), metadata (2 x 256 rows x 16 B), token data (2 x 8 KB)
+constexpr uint32_t kBSlot = 16384, kASlot = 32768, kMSlot = 4096, kTSlot = 8192;
+// metadata and token data of one super-block share a region (the compiler
+// tracks at most eight regions of copies in flight)
+constexpr uint32_t kOffA = 4 * kBSlot, kOffM = kOffA + 2 * kASlot;  // then slot 1 at + kMSlot + kTSlot
+constexpr uint32_t kLds = kOffM + 2 * (kMSlot + kTSlot);  // 155648 B
+// token data block per (token block, super-block): a' as [8 groups][128
+// tokens] fp32, then per token 32 B of min-term operands: hi of groups 0-3,
+// lo of groups 0-3, hi of groups 4-7, lo of groups 4-7 (FP16), so a lane
+// reads its hi and lo K-quarter with one 16-byte read
+constexpr uint32_t kTokA = 0, kTokU = 4096;
+
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// One 16-byte direct global->LDS copy per active lane: lane l's bytes land at
+// lds + 16 l (lds wave-uniform).
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// Wait until at most N of this wave's vector memory operations are
+// outstanding, then the workgroup barrier. The memory clobber keeps the
+// compiler from moving LDS reads of the next step above it.
+template <int N>
+__device__ __forceinline__ void wait_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Calls f with the eight LDS regions of the tile (B step slots 0-3, A code
+// super-block slots 0-1, metadata + token-data super-block slots 0-1) as pairwise disjoint
+// __restrict__ pointers. Every LDS access of the main loop goes through them:
+// that is what lets the compiler see that a copy in flight into one slot does
+// not write the slot being read, so it adds no wait for the copies before
+// each LDS read (the ring's waits are explicit, see wait_barrier).
+template <class F>
+__device__ __attribute__((always_inline)) inline void regions(
+    uint8_t* __restrict__ b0, uint8_t* __restrict__ b1, uint8_t* __restrict__ b2, uint8_t* __restrict__ b3,
+    uint8_t* __restrict__ a0, uint8_t* __restrict__ a1, uint8_t* __restrict__ mt0, uint8_t* __restrict__ mt1,
+    F&& f) {
+  f(b0, b1, b2, b3, a0, a1, mt0, mt1);
+}
+
+// A 16-byte LDS read that completes inside the asm statement (its own
+// lgkmcnt wait), for reads the compiler would otherwise order behind every
+// copy in flight.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  const auto* lp = (__attribute__((address_space(3))) const uint8_t*)(p);
+  return uint32_t(reinterpret_cast<uintptr_t>(lp));
+}
+__device__ __forceinline__ uint4 lds_read16_sync(const uint8_t* p) {
+  uint4 v;
+  const uint32_t a = lds_addr(p);
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+
+// ---- pre-pass ----
+// bq: [tb][step][chunk 8][token 128] 16-byte entries; chunk c = gsel * 4 + lk
+//     holds the codes 32 g + 8 lk + {0, 2, 4, 6, 1, 3, 5, 7} of group
+//     g = 2 step + gsel as FP16 (the slot order the A fragments unpack to).
+// tq: [tb][kb] token data blocks (kTokA / kTokUh / kTokUl).
+// ti: [mp] 1 / ts. Tokens m .. mp - 1 get zero codes and data, ti = 1.
+// Block (x, y) covers tokens 64 x .. 64 x + 63. y < kbs: the codes of
+// super-block y, transposed through LDS (row reads of 256 B per token, then
+// each wave store one contiguous 1 KB run: 64 tokens x 16 B of one chunk).
+// y = kbs .. kbs + 15: the token data, one wave per token.
+__global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restrict__ xc,
+                                                           const float* __restrict__ xa,
+                                                           const int32_t* __restrict__ xs, uint32_t m,
+                                                           uint32_t pk, uint8_t* __restrict__ bq,
+                                                           uint8_t* __restrict__ tq, float* __restrict__ ti) {
+  const uint32_t groups = pk / 32, kbs = pk / 256, steps = kbs * 4;
+  const uint32_t t0 = blockIdx.x * 64, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
+  if (blockIdx.y < kbs) {
+    const uint32_t kb = blockIdx.y;
+    __shared__ uint32_t rows[64][65];  // 64 tokens x 256 codes (+1 dword pad)
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) {  // 16 tokens per pass: 16 threads x 16 B per token
+      const uint32_t tl = r * 16 + tid / 16, part = tid % 16, t = t0 + tl;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (t < m) v = *reinterpret_cast<const uint4*>(xc + size_t(t) * pk + kb * 256 + part * 16);
+      rows[tl][part * 4] = v.x;
+      rows[tl][part * 4 + 1] = v.y;
+      rows[tl][part * 4 + 2] = v.z;
+      rows[tl][part * 4 + 3] = v.w;
+    }
+    __syncthreads();
+    const h2 off = {_Float16(-1152.f), _Float16(-1152.f)};
+    const uint32_t t = t0 + lane, tb = t / kBT, tl = t % kBT;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      const uint32_t ch = w * 8 + i;  // 8-code chunk of the super-block (0..31)
+      const uint32_t g = kb * 8 + ch / 4, lk = ch % 4, st = g / 2, c = (g % 2) * 4 + lk;
+      const uint32_t u0 = rows[lane][ch * 2] ^ 0x80808080u, u1 = rows[lane][ch * 2 + 1] ^ 0x80808080u;
+      uint4 o;
+      o.x = as_u32(as_h2(perm(0x64646464u, u0, 0x04020400u)) + off);  // z0, z2
+      o.y = as_u32(as_h2(perm(0x64646464u, u1, 0x04020400u)) + off);  // z4, z6
+      o.z = as_u32(as_h2(perm(0x64646464u, u0, 0x04030401u)) + off);  // z1, z3
+      o.w = as_u32(as_h2(perm(0x64646464u, u1, 0x04030401u)) + off);  // z5, z7
+      *reinterpret_cast<uint4*>(bq + ((size_t(tb) * steps + st) * 8 + c) * (kBT * 16) + tl * 16) = o;
+    }
+    return;
+  }
+  // token data: ts = 2^e by mmq_kernel's rule (max_g |a| 2^12 ts in [2^13, 2^14))
+  {
+    const uint32_t t = t0 + (blockIdx.y - kbs) * 4 + w, tb = t / kBT, tl = t % kBT;
+    const bool real = t < m;
+    float mx = 0.f;
+    if (real)
+      for (uint32_t g = lane; g < groups; g += 64) mx = fmaxf(mx, fabsf(xa[size_t(t) * groups + g]));
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh /= 2) mx = fmaxf(mx, __shfl_xor(mx, sh));
+    const int ex = int(__float_as_uint(mx) >> 23);
+    const int se = min(max(255 - ex, 1), 253);
+    const float ts = __uint_as_float(uint32_t(se) << 23);
+    if (lane == 0) ti[t] = real ? __uint_as_float(uint32_t(254 - se) << 23) : 1.f;
+    for (uint32_t g = lane; g < groups; g += 64) {
+      uint8_t* base = tq + (size_t(tb) * kbs + g / 8) * kTSlot;
+      const uint32_t g8 = g % 8;
+      float a = 0.f;
+      _Float16 h = 0, l = 0;
+      if (real) {
+        a = xa[size_t(t) * groups + g] * ts;
+        const float v = a * float(xs[size_t(t) * groups + g]);
+        h = _Float16(v);
+        l = _Float16(v - float(h));
+      }
+      *reinterpret_cast<float*>(base + kTokA + (g8 * kBT + tl) * 4) = a;
+      // per token: hi of groups 0-3, lo of 0-3, hi of 4-7, lo of 4-7
+      const uint32_t hpos = (g8 / 4) * 16 + (g8 % 4) * 2;
+      *reinterpret_cast<_Float16*>(base + kTokU + tl * 32 + hpos) = h;
+      *reinterpret_cast<_Float16*>(base + kTokU + tl * 32 + hpos + 8) = l;
+    }
+  }
+}
+
+// ---- main kernel: one 256 x 128 tile per block, 8 waves of 32 rows x 128 tokens ----
+__global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n, uint32_t pn,
+    uint32_t kbs, const uint8_t* __restrict__ bq, const uint8_t* __restrict__ tq,
+    const float* __restrict__ ti, uint32_t m, float* __restrict__ out, const float* __restrict__ residual,
+    uint32_t row_blocks, uint32_t tok_blocks) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const uint32_t tiles_n = row_blocks * tok_blocks;
+  const uint32_t tile = (tiles_n % 8 == 0) ? (blockIdx.x % 8) * (tiles_n / 8) + blockIdx.x / 8 : blockIdx.x;
+  const uint32_t rb = tile / tok_blocks, tb = tile % tok_blocks;
+  const uint32_t row0 = rb * kBR;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
+  const uint32_t lr = lane & 15u, lk = lane >> 4;
+  const uint32_t steps = kbs * 4;
+  const uint32_t last8 = pn / 8 - 1;
+
+  // ---- copy issue (every wave issues 6 copies per super-block and 2 per K
+  // step; past the end they re-read the last data into a slot
+  // nobody reads, so the vmcnt arithmetic never changes) ----
+  // A codes: block-local row R is 128 LDS bytes; within it, chunk position p
+  // holds the row's chunk p ^ ((R / 2) % 8), so the fragment reads of 16
+  // consecutive rows hit distinct banks. Copy u (0..3) of wave w is 8-row
+  // tile T = 4 w + u: 1 KB contiguous in 0x020D, with lane l reading row
+  // l / 8, chunk (l % 8) ^ (4 (T % 2) + l / 16) % 8 -- two lane offsets.
+  // Metadata: rows 32 w .. 32 w + 31, 16 B each, half a wave copy (lane l:
+  // row l / 8 of 8-row tile 4 w + l / 8 ... in steps of kbs * 128 B).
+  const uint32_t a_off0 = (lane >> 3) * 128 + (((lane & 7u) ^ ((lane >> 4) & 7u)) * 16);
+  const uint32_t a_off1 = (lane >> 3) * 128 + (((lane & 7u) ^ ((4u + (lane >> 4)) & 7u)) * 16);
+  auto issue_super = [&](uint32_t kb_in, uint8_t* wA, uint8_t* wM, uint8_t* wT) __attribute__((always_inline)) {
+    const uint32_t kb = min(kb_in, kbs - 1);
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+      const uint32_t T = wave * 4 + u;
+      const uint32_t r8 = min(row0 / 8 + T, last8);
+      dma16(codes + ((r8 * kbs + kb) * 1024 + (u % 2 ? a_off1 : a_off0)), wA + T * 1024);
+    }
+    {
+      const uint32_t r8 = min(row0 / 8 + wave * 4 + ((lane & 31u) >> 3), last8);
+      if (lane < 32) dma16(meta + ((r8 * kbs + kb) * 128 + (lane & 7u) * 16), wM + wave * 512);
+    }
+    dma16(tq + (uint64_t(tb) * kbs + kb) * kTSlot + wave * 1024 + lane * 16, wT + wave * 1024);
+  };
+  auto issue_step = [&](uint32_t s_in, uint8_t* wB) __attribute__((always_inline)) {
+    const uint32_t s = min(s_in, steps - 1);
+    const uint8_t* src = bq + ((uint64_t(tb) * steps + s) * 8 + wave) * (kBT * 16) + lane * 16;
+    uint8_t* dst = wB + wave * (kBT * 16);
+    dma16(src, dst);
+    dma16(src + 1024, dst + 1024);
+  };
+
+  float acc[2][8][4], X[2][8][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
+
+  // all ones in lanes lk < 2 (K 0..7 of the min-term MFMA), zero in the
+  // padding lanes; opaque, so the compiler keeps an AND instead of branching
+  uint32_t ymask = lk < 2 ? ~0u : 0u;
+  asm volatile("" : "+v"(ymask));
+  // per super-block row data of this lane's A rows (32 wave + 16 i + lr)
+  uint32_t S[2][2];  // scale bytes of groups 0-3 and 4-7
+  half4 mf[2];       // min-term A operand (m of groups 4 lk .. 4 lk + 3; zero for lk >= 2)
+
+  auto compute = [&](auto qc, const uint8_t* Bs, const uint8_t* As, const uint8_t* Ms, const uint8_t* Ts) __attribute__((always_inline)) {
+    constexpr uint32_t q = decltype(qc)::value;
+    if constexpr (q == 0) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint4 mw = lds_read16_sync(Ms + (wave * 32 + i * 16 + lr) * 16);
+        S[i][0] = mw.y & 0x3f3f3f3fu;
+        S[i][1] = (mw.w & 0x0f0f0f0fu) | ((mw.y >> 2) & 0x30303030u);
+        const uint32_t mlo = mw.z & 0x3f3f3f3fu;
+        const uint32_t mhi = ((mw.w >> 4) & 0x0f0f0f0fu) | ((mw.z >> 2) & 0x30303030u);
+        const uint32_t mm = lk == 0 ? mlo : mhi;
+        const h2 k1024 = {_Float16(-1024.f), _Float16(-1024.f)};
+        const h2 m01 = as_h2(perm(0x64646464u, mm, 0x04010400u)) + k1024;
+        const h2 m23 = as_h2(perm(0x64646464u, mm, 0x04030402u)) + k1024;
+        mf[i] = lk < 2 ? half4{m01.x, m01.y, m23.x, m23.y} : half4{0, 0, 0, 0};
+      }
+    }
+    // A fragments of row tiles 0, 1 for group g = 2 q + gsel: codes
+    // 8 lk .. 8 lk + 7 in slot order {0, 2, 4, 6, 1, 3, 5, 7}, scaled by s
+    // exactly ((1024 + c) s - 1024 s = c s <= 945).
+    uint32_t wraw[2][2];
+#pragma unroll
+    for (uint32_t gsel = 0; gsel < 2; ++gsel)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t g = 2 * q + gsel, R = wave * 32 + i * 16 + lr;
+        wraw[gsel][i] = *reinterpret_cast<const uint32_t*>(As + R * 128 + ((g ^ (lr >> 1)) * 16) + lk * 4);
+      }
+    auto dequant = [&](uint32_t gsel, int i) __attribute__((always_inline)) {
+      const uint32_t g = 2 * q + gsel, w = wraw[gsel][i];
+      const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+      const uint32_t sel = 0x04000400u | ((g & 3u) << 16) | (g & 3u);
+      const h2 s2 = as_h2(perm(0x64646464u, S[i][g >> 2], sel)) + h2{_Float16(-1024.f), _Float16(-1024.f)};
+      const h2 b2 = s2 * h2{_Float16(-1024.f), _Float16(-1024.f)};
+      const h2 p0 = __builtin_elementwise_fma(as_h2(perm(0x64646464u, lo, 0x04010400u)), s2, b2);
+      const h2 p1 = __builtin_elementwise_fma(as_h2(perm(0x64646464u, lo, 0x04030402u)), s2, b2);
+      const h2 p2 = __builtin_elementwise_fma(as_h2(perm(0x64646464u, hi, 0x04010400u)), s2, b2);
+      const h2 p3 = __builtin_elementwise_fma(as_h2(perm(0x64646464u, hi, 0x04030402u)), s2, b2);
+      return half8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+    };
+    // Software pipeline over the step's 16 items u = (group gsel = u / 8,
+    // token tile j = u % 8): item u's MFMAs are issued after the B fragment
+    // and a' of item u + kPF are requested and before item u - 1's results
+    // are scaled; sched_barrier keeps the compiler from hoisting further
+    // (the register budget is two waves per SIMD).
+    constexpr int kPF = 2;
+    auto bfrag = [&](int u) __attribute__((always_inline)) {
+      return *reinterpret_cast<const half8*>(Bs + (((u >> 3) * 4 + lk) * kBT + (u & 7) * 16 + lr) * 16);
+    };
+    auto afac = [&](int u) __attribute__((always_inline)) {
+      return *reinterpret_cast<const float*>(Ts + kTokA + ((2 * q + (u >> 3)) * kBT + (u & 7) * 16 + lr) * 4);
+    };
+    half8 bq_[kPF + 1];
+    float aq_[kPF + 1];
+#pragma unroll
+    for (int u = 0; u < kPF; ++u) {
+      bq_[u] = bfrag(u);
+      aq_[u] = afac(u);
+    }
+    half8 af[2][2];
+    af[0][0] = dequant(0, 0);
+    af[0][1] = dequant(0, 1);
+    f4 Pp[2];
+    float ap = 0.f;
+#pragma unroll
+    for (int u = 0; u <= 16; ++u) {
+      f4 Pc[2];
+      float ac = 0.f;
+      if (u < 16) {
+        if (u + kPF < 16) {
+          bq_[(u + kPF) % (kPF + 1)] = bfrag(u + kPF);
+          aq_[(u + kPF) % (kPF + 1)] = afac(u + kPF);
+        }
+        if (u == 6) af[1][0] = dequant(1, 0);
+        if (u == 7) af[1][1] = dequant(1, 1);
+        const half8 bf = bq_[u % (kPF + 1)];
+        ac = aq_[u % (kPF + 1)];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) Pc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[u >> 3][i], bf, f4{0, 0, 0, 0}, 0, 0, 0);
+      }
+      if (u > 0) {
+        const int pu = u - 1, pj = pu & 7;
+        const bool first = q == 0 && pu < 8;  // the super-block's first group
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) X[i][pj][v] = first ? ap * Pp[i][v] : fmaf(ap, Pp[i][v], X[i][pj][v]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      Pp[0] = Pc[0];
+      Pp[1] = Pc[1];
+      ap = ac;
+    }
+    // Pin X: otherwise the compiler defers the scaling FMAs and keeps
+    // (spills) the MFMA results.
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(X[i][j][v]));
+    // ---- end of super-block: acc += d X - dmin Y ----
+    // The epilogue's LDS operands come through completing asm reads (the
+    // compiler would otherwise order them behind every copy in flight).
+    if constexpr (q == 3) {
+      // d, -dmin of output rows 32 wave + 16 i + 4 lk + v
+      uint32_t dw[8];
+      {
+        const uint32_t a0 = lds_addr(Ms + (wave * 32 + lk * 4) * 16);
+        asm volatile(
+            "ds_read_b32 %0, %8\n\tds_read_b32 %1, %8 offset:16\n\tds_read_b32 %2, %8 offset:32\n\t"
+            "ds_read_b32 %3, %8 offset:48\n\tds_read_b32 %4, %8 offset:256\n\tds_read_b32 %5, %8 offset:272\n\t"
+            "ds_read_b32 %6, %8 offset:288\n\tds_read_b32 %7, %8 offset:304\n\ts_waitcnt lgkmcnt(0)"
+            : "=&v"(dw[0]), "=&v"(dw[1]), "=&v"(dw[2]), "=&v"(dw[3]), "=&v"(dw[4]), "=&v"(dw[5]), "=&v"(dw[6]),
+              "=&v"(dw[7])
+            : "v"(a0)
+            : "memory");
+      }
+#pragma unroll
+      for (int jh = 0; jh < 2; ++jh) {
+        // min-term operands of token tiles 4 jh .. 4 jh + 3; lanes lk >= 2
+        // (K 8..15, the zero padding) read a valid address and are masked
+        uint4 r[4];
+        const uint32_t a0 = lds_addr(Ts + kTokU + (jh * 64 + lr) * 32 + (lk & 1u) * 16);
+        asm volatile(
+            "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:512\n\tds_read_b128 %2, %4 offset:1024\n\t"
+            "ds_read_b128 %3, %4 offset:1536\n\ts_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+            : "v"(a0)
+            : "memory");
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = jh * 4 + jj;
+          const half4 uh = __builtin_bit_cast(half4, make_uint2(r[jj].x & ymask, r[jj].y & ymask));
+          const half4 ul = __builtin_bit_cast(half4, make_uint2(r[jj].z & ymask, r[jj].w & ymask));
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            f4 Y = __builtin_amdgcn_mfma_f32_16x16x16f16(mf[i], uh, f4{0, 0, 0, 0}, 0, 0, 0);
+            Y = __builtin_amdgcn_mfma_f32_16x16x16f16(mf[i], ul, Y, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const uint32_t w0 = dw[i * 4 + v];
+              acc[i][j][v] = fmaf(-f16_to_f32(w0 >> 16), Y[v], fmaf(f16_to_f32(w0 & 0xffffu), X[i][j][v], acc[i][j][v]));
+            }
+          }
+        }
+      }
+      // Pin acc: the super-block's epilogue completes here, so X is dead
+      // before the next super-block starts it again.
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(acc[i][j][v]));
+    }
+  };
+
+  using C0 = std::integral_constant<uint32_t, 0>;
+  using C1 = std::integral_constant<uint32_t, 1>;
+  using C2 = std::integral_constant<uint32_t, 2>;
+  using C3 = std::integral_constant<uint32_t, 3>;
+  // Step 4 kb + q of super-block kb in LDS slot SB = kb % 2. Steps run in
+  // pairs (q = 0, 1 and q = 2, 3) with one barrier per pair: at q = 0 and
+  // q = 2 each wave waits for all of its copies (the pair's B slots, issued
+  // one pair earlier, and at q = 0 the super-block's data, issued one
+  // super-block earlier), the barrier publishes them and retires the previous
+  // pair's slots, which are refilled with the next pair (at q = 0 also
+  // super-block kb + 1 into slot SB ^ 1).
+  auto run = [&](uint8_t* B0, uint8_t* B1, uint8_t* B2, uint8_t* B3, uint8_t* A0, uint8_t* A1, uint8_t* MT0,
+                 uint8_t* MT1) __attribute__((always_inline)) {
+  uint8_t* const Bsl[4] = {B0, B1, B2, B3};
+  uint8_t* const Asl[2] = {A0, A1};
+  uint8_t* const Msl[2] = {MT0, MT1};
+  uint8_t* const Tsl[2] = {MT0 + kMSlot, MT1 + kMSlot};
+  auto step = [&](auto qc, auto sbc, uint32_t kb) __attribute__((always_inline)) {
+    constexpr uint32_t q = decltype(qc)::value, SB = decltype(sbc)::value;
+    if constexpr (q % 2 == 0) {
+      wait_barrier<0>();
+      if constexpr (q == 0) issue_super(kb + 1, Asl[SB ^ 1u], Msl[SB ^ 1u], Tsl[SB ^ 1u]);
+      issue_step(4 * kb + q + 2, Bsl[(q + 2) & 3u]);
+      issue_step(4 * kb + q + 3, Bsl[(q + 3) & 3u]);
+    }
+    compute(qc, Bsl[q], Asl[SB], Msl[SB], Tsl[SB]);
+  };
+  auto super_block = [&](uint32_t kb, auto sbc) __attribute__((always_inline)) {
+    step(C0{}, sbc, kb);
+    step(C1{}, sbc, kb);
+    step(C2{}, sbc, kb);
+    step(C3{}, sbc, kb);
+  };
+  // Prologue: super-block 0 and K steps 0, 1 in flight. kbs is even.
+  issue_super(0, A0, Msl[0], Tsl[0]);
+  issue_step(0, B0);
+  issue_step(1, B1);
+  for (uint32_t kb = 0; kb < kbs; kb += 2) {
+    super_block(kb, C0{});
+    super_block(kb + 1, C1{});
+  }
+  };
+  regions(lds, lds + kBSlot, lds + 2 * kBSlot, lds + 3 * kBSlot, lds + kOffA, lds + kOffA + kASlot, lds + kOffM,
+          lds + kOffM + kMSlot + kTSlot, run);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy outlives the block
+
+  // ---- store: lane holds rows 4 lk .. 4 lk + 3 of token lr in each tile ----
+  const bool vec = (n % 4 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t tok = tb * kBT + j * 16 + lr;
+    if (tok >= m) continue;
+    const float inv = ti[tok];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t r4 = row0 + wave * 32 + i * 16 + lk * 4;
+      if (r4 >= n) continue;
+      const size_t o = size_t(tok) * n + r4;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[i][j][v] *= inv;
+      if (vec) {
+        float4 y = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        if (residual) {
+          const float4 rv = *reinterpret_cast<const float4*>(residual + o);
+          y.x += rv.x; y.y += rv.y; y.z += rv.z; y.w += rv.w;
+        }
+        *reinterpret_cast<float4*>(out + o) = y;
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (r4 + v < n) out[o + v] = acc[i][j][v] + (residual ? residual[o + v] : 0.f);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// Scratch bytes the pre-pass needs for m tokens of padded width pk.
+uint64_t mmq_dma_scratch_bytes(uint32_t m, uint32_t pk) {
+  const uint64_t mp = (uint64_t(m) + kBT - 1) / kBT * kBT;
+  return mp * pk * 2 + mp / kBT * (pk / 256) * kTSlot + mp * 4;
+}
+
+// Rows [0, rows) of a Q4_K 0x020D weight (rows a multiple of 256 or pn) for
+// all m tokens; scratch holds mmq_dma_scratch_bytes(m, pk). Codes and
+// metadata must be 16-byte aligned.
+hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
+                          hipStream_t s, uint32_t rows, void* scratch) {
+  if (w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2 || rows == 0 || x.pk != w.pk ||
+      ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
+        reinterpret_cast<uintptr_t>(x.codes)) % 16) != 0)
+    return hipErrorInvalidValue;
+  if ((w.pk / 256) % 2 != 0) return hipErrorNotReady;  // the main loop runs super-block pairs
+  const uint32_t mp = (x.m + kBT - 1) / kBT * kBT;
+  uint8_t* bq = static_cast<uint8_t*>(scratch);
+  uint8_t* tq = bq + uint64_t(mp) * w.pk * 2;
+  float* ti = reinterpret_cast<float*>(tq + uint64_t(mp / kBT) * (w.pk / 256) * kTSlot);
+  hipLaunchKernelGGL(mmq_dma_prep_kernel, dim3(mp / 64, w.pk / 256 + 16), dim3(256), 0, s, x.codes, x.scales,
+                     x.sums, x.m, x.pk, bq, tq, ti);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  e = set_max_lds(reinterpret_cast<const void*>(mmq_dma_kernel), int(kLds));
+  if (e != hipSuccess) return e;
+  const uint32_t row_blocks = (rows + kBR - 1) / kBR, tok_blocks = mp / kBT;
+  hipLaunchKernelGGL(mmq_dma_kernel, dim3(row_blocks * tok_blocks), dim3(512), kLds, s, w.codes, w.scales,
+                     w.n, w.pn, w.pk / 256, bq, tq, ti, x.m, out, residual, row_blocks, tok_blocks);
+  return hipGetLastError();
+}
+
+}  // namespace qw38hip

@@ -237,6 +237,82 @@ def test_q6k_small_shapes_and_dots(torch_gpu):
                 assert np.array_equal(d.cpu().numpy().reshape(dots.shape), dots)
 
 
+_DMA_OFF_SCRIPT = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
+import oracle, qw38_amd.ops as ops
+from _fix import normal
+n, k, m = 34816, 5120, 512
+g = torch.Generator(device="cuda"); g.manual_seed(331)
+x = torch.randn(n, k, generator=g, device="cuda") * 0.02
+fail = torch.zeros(1, dtype=torch.int32, device="cuda")
+w = ops.upload_q4k_blocks(ops.quantize_q4k_blocks(x, n, k, fail), n, k, layout=oracle.LAYOUT_Q4K_SEQ)
+bf = oracle.fp32_to_bf16(normal((m, k), 332))
+q = ops.Q8Input.empty(m, k)
+flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+ops.pack_q8(torch.from_numpy(bf.view(np.int16)).cuda(), q, flag)
+y = torch.empty(m, n, device="cuda")
+ops.q4k_q8_project(w, q, y)
+torch.cuda.synchronize()
+np.save(sys.argv[2], y.cpu().numpy())
+"""
+
+
+def test_q4k_mmq_direct_copy_rows_independent_of_m(torch_gpu, tmp_path):
+    """Q4_K 0x020D MMQ at config 2's N: the 256 x 128 tiles run the
+    direct-copy kernel (q4k_mmq_dma.hip: pre-pass plus global->LDS copies)
+    when the library scratch holds its pre-pass, next to the 128 x 32 tail
+    split and the smaller tiles of the other M. Every token row must be
+    bitwise the same at every M (the reference's schedule invariance,
+    tests/q4k_q8_test.cpp:118-120), the launches that take the direct-copy
+    kernel must have got the scratch, M = 40 matches the oracle, and the
+    same M = 512 call with the kernel switched off (QW38_MMQ_DMA=0, a child
+    process since the switch is read once) must give the same bits."""
+    import os
+    import subprocess
+    import sys
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    n, k = 34816, 5120
+    w, wl = _fit_q4k(torch, ops, n, k, 331, oracle.LAYOUT_Q4K_SEQ)
+    q, ob = _q8(torch, ops, normal((512, k), 332))
+    full = None
+    # 512: direct-copy 256 x 128 tiles + 128 x 32 tail split; 130: 256 x 128
+    # tiles over two token blocks; 9 / 40 / 64: mmq_kernel's 128 x 32 and
+    # 128 x 64 tiles
+    for m in (512, 130, 9, 40, 64):
+        print(f"Q4_K MMQ family M={m}", flush=True)
+        qm = ops.Q8Input.empty(m, k)
+        qm.codes.copy_(q.codes[:m]); qm.scales.copy_(q.scales[:m]); qm.sums.copy_(q.sums[:m])
+        y = torch.full((m, n), float("nan"), device="cuda")
+        torch.cuda.synchronize()
+        before = ops.scratch_stats()
+        ops.q4k_q8_project(w, qm, y)
+        torch.cuda.synchronize()
+        after = ops.scratch_stats()
+        if m == 512:
+            assert after[0] == before[0] + 1 and after[1:] == before[1:], \
+                f"M={m}: the direct-copy kernel did not get the scratch ({before} -> {after})"
+        yn = y.cpu().numpy()
+        if full is None:
+            full = yn
+        else:
+            assert np.array_equal(yn.view(np.uint32), full[:m].view(np.uint32)), f"M={m} rows differ from M=512"
+        if m == 40:
+            rows = np.sort(np.random.Generator(np.random.PCG64(40)).choice(n, 512, replace=False))
+            sub = oracle.Q4K(wl.codes[rows], wl.meta[rows], len(rows), k)
+            ref, _, _ = oracle.q4k_q8_contract(sub, oracle.Q8(ob.codes[:m], ob.scales[:m], ob.sums[:m], m, k, ob.pk))
+            _check(yn[:, rows], ref, "Q4_K MMQ M=40")
+    out = str(tmp_path / "dma_off.npy")
+    env = dict(os.environ, QW38_MMQ_DMA="0")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _DMA_OFF_SCRIPT, root, out], env=env, timeout=110,
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    off = np.load(out)
+    assert np.array_equal(off.view(np.uint32), full.view(np.uint32)), "QW38_MMQ_DMA=0 differs from the direct-copy kernel"
+
+
 @pytest.mark.parametrize("layout", [oracle.LAYOUT_Q4K_SEQ, oracle.LAYOUT_Q4K_W64], ids=["020D", "0240"])
 @pytest.mark.parametrize("n,k,m", [(12288, 5120, 128), (12288, 5120, 512), (12288, 5120, 2048),
                                    (34816, 5120, 128), (34816, 5120, 512), (34816, 5120, 2048)])
