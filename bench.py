@@ -549,6 +549,42 @@ def clock_probe(torch, ops):
     return r
 
 
+def issue_probe(torch):
+    """VALU / matrix-core overlap on one SIMD (qw38_issue_probe, two waves per
+    SIMD), timed with events: nanoseconds per loop iteration of 32 FP16
+    16x16x32 MFMAs alone, 128 FP32 FMAs alone, both interleaved 1:4, and 16
+    MFMAs with 128 FMAs interleaved 1:8; 'overlap' is the fraction of the
+    shorter unit's time hidden under the other's (1 = fully hidden, 0 =
+    serialized)."""
+    from qw38_amd._lib import lib
+    ticks = torch.zeros(2, dtype=torch.int64, device="cuda")
+    sink = torch.zeros(1, dtype=torch.float32, device="cuda")
+    iters = 20000
+    ns = {}
+    stream = torch.cuda.current_stream()
+    for mode in range(4):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for rep in range(2):  # the second launch is the one timed
+            if rep:
+                start.record(stream)
+            st = lib().qw38_issue_probe(mode, iters, ticks.data_ptr(), sink.data_ptr(), stream.cuda_stream)
+            assert st == 0
+        end.record(stream)
+        torch.cuda.synchronize()
+        ns[mode] = start.elapsed_time(end) * 1e6 / iters
+    mf, va = ns[0], ns[1]  # 32 MFMAs, 128 FMAs per SIMD and iteration
+
+    def ov(t, m, v):
+        return round((m + v - t) / min(m, v), 3)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    r = {"ns_per_iter": {"mfma32": round(mf, 1), "fma128": round(va, 1), "mix_1to4": round(ns[2], 1),
+                         "mix_1to8_16mfma": round(ns[3], 1)},
+         "overlap_1to4": ov(ns[2], mf, va), "overlap_1to8": ov(ns[3], mf / 2, va),
+         "mfma_only_fp16_tflops": round(cus * 4 * 32 * 16384 / mf / 1e3, 1)}
+    log(f"issue probe: {r}")
+    return r
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -633,6 +669,8 @@ def main():
                     help="only run CALLS eager whole-MLP calls at M tokens (Q4_K gate/up on --layout "
                          "for M <= 8, else --mmq-layout; Q6_K down), for rocprofv3 traces")
     ap.add_argument("--no-read-probe", action="store_true", help="skip the pure-read ceiling leg")
+    ap.add_argument("--issue-probe-only", action="store_true",
+                    help="only the VALU / matrix-core overlap probe")
     ap.add_argument("--read-probe-only", action="store_true",
                     help="only run the pure-read ceiling leg (for rocprofv3 traces)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -700,6 +738,9 @@ def main():
     peak_sclk = clock["int8_peak_tops_at_sclk"]
     if args.read_probe_only:
         read_probe(torch, 100_270_080, 12, args.steps, args.warmup)
+        return
+    issue = issue_probe(torch)
+    if args.issue_probe_only:
         return
     probe = None if args.no_read_probe else read_probe(torch, 100_270_080, 12, args.steps, args.warmup)
     if probe:  # the same ceiling at the config-1 and config-3 weight sizes
@@ -779,6 +820,7 @@ def main():
         "read_probe": probe,
         "rooflines": rooflines,
         "mfma_clock": clock,
+        "issue_probe": issue,
         "config5_model_pass": model,
         "mlp": mlp,
         "cpu_baseline": cpu,

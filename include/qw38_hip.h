@@ -438,6 +438,16 @@ int qw38_scratch_stats(uint64_t* stats);
 int qw38_read_probe(const void* buf, uint64_t bytes, uint32_t mode, uint32_t blocks_per_cu,
                     uint32_t* sink, uint64_t sink_len, void* stream);
 
+/* No counterpart in the reference: a measurement aid. Eight waves per CU
+ * (two per SIMD) run `iterations` of a register-only loop: mode 0 sixteen
+ * independent v_mfma_f32_16x16x32_f16, mode 1 sixty-four independent FP32
+ * FMAs, mode 2 both interleaved one MFMA to four FMAs, mode 3 eight MFMAs
+ * interleaved one to eight FMAs. ticks[0] (device memory) receives the
+ * s_memtime ticks wave 0 spent in its loop; `sink` (device, >= 1 float)
+ * is written only on a value the loop never produces. Shows how far the
+ * VALU and the matrix core overlap on one SIMD. */
+int qw38_issue_probe(uint32_t mode, uint32_t iterations, uint64_t* ticks, float* sink, void* stream);
+
 /* Replaces qw38::runtime::profiling::enabled (src/runtime/profiling.hpp:9-10):
  * turns the calling thread's roctx ranges ("qw38:op name=q4k_project ...",
  * the reference's NVTX strings) on or off. QW38_PROFILE=1 in the environment

@@ -122,6 +122,7 @@ SIGNATURES = {
                               _V]),
     "qw38_mfma_clock_probe": (_I, [_U32, _V, _P(_U32), _V]),
     "qw38_read_probe": (_I, [_V, _U64, _U32, _U32, _V, _U64, _V]),
+    "qw38_issue_probe": (_I, [_U32, _U32, _V, _V, _V]),
     "qw38_scratch_stats": (_I, [_V]),
     "qw38_set_profiling": (None, [_I]),
     "qw38_code_bytes": (_U64, [_U16, _U32, _U32]),

@@ -14,6 +14,14 @@
 // each wave one contiguous range and stream it 1 KB per load instruction,
 // eight (mode 1) or sixteen (mode 2) loads in flight, the access pattern of
 // the streaming GEMV.
+//
+// Third aid: how far FP32 VALU work and FP16 matrix-core work overlap on one
+// SIMD (two waves per SIMD, eight per CU, register operands only): mode 0
+// issues 16 independent v_mfma_f32_16x16x32_f16 per iteration, mode 1 64
+// independent FP32 FMAs, mode 2 both interleaved one MFMA to four FMAs (the
+// MMQ's per-group scale ratio), mode 3 eight MFMAs interleaved one to eight
+// FMAs. Time per iteration against the single-unit modes gives the overlap
+// (the bench times the launches with events).
 #include "common.hpp"
 
 namespace qw38hip {
@@ -52,6 +60,55 @@ __global__ __launch_bounds__(256) void mfma_clock_kernel(uint32_t iters, uint64_
     ticks[1] = r1 - r0;
   }
   if (acc == 0x7fffffff) ticks[2] = uint64_t(acc);  // keeps the chains live
+}
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <int Mode>
+__global__ __launch_bounds__(512, 1) void issue_probe_kernel(uint32_t iters, float s, uint64_t* ticks,
+                                                             float* sink) {
+  half8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = _Float16(float(threadIdx.x & 7u) + i);
+    b[i] = _Float16(0.5f * i);
+  }
+  f4 acc[16];
+  float x[64];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = f4{0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < 64; ++j) x[j] = float(threadIdx.x + j);
+  const bool rec = blockIdx.x == 0 && threadIdx.x == 0;
+  uint64_t t0 = 0;
+  if (rec) t0 = __builtin_amdgcn_s_memtime();
+  for (uint32_t it = 0; it < iters; ++it) {
+    if constexpr (Mode == 0) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
+    } else if constexpr (Mode == 1) {
+#pragma unroll
+      for (int j = 0; j < 64; ++j) x[j] = fmaf(x[j], s, 1.0f);
+    } else {
+      constexpr int kM = Mode == 2 ? 16 : 8, kF = 64 / kM;
+#pragma unroll
+      for (int j = 0; j < kM; ++j) {
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < kF; ++u) x[kF * j + u] = fmaf(x[kF * j + u], s, 1.0f);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, kF, 0);  // then kF VALU
+      }
+    }
+  }
+  if (rec) ticks[0] = __builtin_amdgcn_s_memtime() - t0;
+  float r = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) r += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+#pragma unroll
+  for (int j = 0; j < 64; ++j) r += x[j];
+  if (r == 1234.5f) sink[0] = r;  // keeps the chains live
 }
 
 template <int Mode>
@@ -133,5 +190,18 @@ extern "C" int qw38_mfma_clock_probe(uint32_t iterations, uint64_t* ticks, uint3
   *blocks = uint32_t(cus);  // 4 waves per block = one wave per SIMD
   hipLaunchKernelGGL(mfma_clock_kernel, dim3(cus), dim3(256), 0, static_cast<hipStream_t>(stream),
                      iterations, ticks, int(iterations & 0x7f));
+  return hipGetLastError() == hipSuccess ? QW38_OK : QW38_STATUS;
+}
+
+extern "C" int qw38_issue_probe(uint32_t mode, uint32_t iterations, uint64_t* ticks, float* sink, void* stream) {
+  using namespace qw38hip;
+  if (ticks == nullptr || sink == nullptr || mode > 3 || iterations == 0 || iterations > (1u << 24))
+    return QW38_INVALID_ARGUMENT;
+  auto kern = mode == 0   ? issue_probe_kernel<0>
+              : mode == 1 ? issue_probe_kernel<1>
+              : mode == 2 ? issue_probe_kernel<2>
+                          : issue_probe_kernel<3>;
+  hipLaunchKernelGGL(kern, dim3(cu_count()), dim3(512), 0, static_cast<hipStream_t>(stream), iterations, 0.999f,
+                     ticks, sink);
   return hipGetLastError() == hipSuccess ? QW38_OK : QW38_STATUS;
 }
