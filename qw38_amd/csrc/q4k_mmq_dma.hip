@@ -104,7 +104,7 @@ __device__ __forceinline__ uint4 lds_read16_sync(const uint8_t* p) {
 // bq: [tb][step][chunk 8][token 128] 16-byte entries; chunk c = gsel * 4 + lk
 //     holds the codes 32 g + 8 lk + {0, 2, 4, 6, 1, 3, 5, 7} of group
 //     g = 2 step + gsel as FP16 (the slot order the A fragments unpack to).
-// tq: [tb][kb] token data blocks (kTokA / kTokUh / kTokUl).
+// tq: [tb][kb] token data blocks (kTokA, kTokU).
 // ti: [mp] 1 / ts. Tokens m .. mp - 1 get zero codes and data, ti = 1.
 // Block (x, y) covers tokens 64 x .. 64 x + 63. y < kbs: the codes of
 // super-block y, transposed through LDS (row reads of 256 B per token, then
