@@ -35,7 +35,9 @@
 namespace qw38hip {
 uint64_t mmq_dma_scratch_bytes(uint32_t m, uint32_t pk);
 hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
-                          hipStream_t s, uint32_t rows, void* scratch);
+                          hipStream_t s, uint32_t rows, void* scratch, const WeightView* up = nullptr,
+                          int8_t* qc = nullptr, float* qa = nullptr, int32_t* qs = nullptr,
+                          int* failure = nullptr);
 namespace {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -1020,13 +1022,20 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
       const char* v = std::getenv("QW38_MMQ_DMA");
       return !(v && std::atoi(v) == 0);
     }();
-    if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2 && !Glu) {
+    if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2) {
       const bool aligned = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
-                             reinterpret_cast<uintptr_t>(x.codes)) % 16) == 0;
+                             reinterpret_cast<uintptr_t>(x.codes) | reinterpret_cast<uintptr_t>(glu.codes2) |
+                             reinterpret_cast<uintptr_t>(glu.meta2)) % 16) == 0;
       if (dma_env && aligned && x.pk == w.pk) {
         int dev = 0;
         if (void* sc = scratch_acquire(s, mmq_dma_scratch_bytes(x.m, x.pk), &dev)) {
-          e = launch_mmq_dma(w, x, out, residual, s, big_rows, sc);
+          if constexpr (Glu) {
+            const WeightView up{glu.codes2, glu.meta2, w.layout, w.n, w.k, w.pn, w.pk};
+            e = launch_mmq_dma(w, x, nullptr, nullptr, s, big_rows / kv, sc, &up, glu.qc, glu.qa, glu.qs,
+                               glu.failure);
+          } else {
+            e = launch_mmq_dma(w, x, out, residual, s, big_rows, sc);
+          }
           scratch_release(dev, s, e == hipSuccess);
         }
       }

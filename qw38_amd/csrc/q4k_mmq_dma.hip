@@ -181,18 +181,38 @@ __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restr
 }
 
 // ---- main kernel: one 256 x 128 tile per block, 8 waves of 32 rows x 128 tokens ----
+// Glu (fused gate + up, features [row0, row0 + 128) per tile): waves 0-3
+// hold the gate rows of the tile's 128 features, waves 4-7 the up rows of the
+// same features (codes2 / meta2); the epilogue applies SwiGLU -> BF16 -> Q8
+// per K32 feature group with mmq_kernel's Glu arithmetic, so the codes equal
+// swiglu_q8 of the two separate projections bit for bit.
+struct GluDma {
+  const uint8_t* codes2;
+  const uint8_t* meta2;
+  int8_t* qc;
+  float* qa;
+  int32_t* qs;
+  int* failure;
+};
+
+template <bool Glu>
 __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n, uint32_t pn,
     uint32_t kbs, const uint8_t* __restrict__ bq, const uint8_t* __restrict__ tq,
     const float* __restrict__ ti, uint32_t m, float* __restrict__ out, const float* __restrict__ residual,
-    uint32_t row_blocks, uint32_t tok_blocks) {
+    uint32_t row_blocks, uint32_t tok_blocks, GluDma glu) {
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t tiles_n = row_blocks * tok_blocks;
   const uint32_t tile = (tiles_n % 8 == 0) ? (blockIdx.x % 8) * (tiles_n / 8) + blockIdx.x / 8 : blockIdx.x;
   const uint32_t rb = tile / tok_blocks, tb = tile % tok_blocks;
-  const uint32_t row0 = rb * kBR;
+  constexpr uint32_t HR = Glu ? kBR / 2 : kBR;  // output rows (features) per tile
+  const uint32_t row0 = rb * HR;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
+  // the wave's 32 weight rows: first row and source arrays (wave-uniform)
+  const uint32_t wrow0 = Glu ? row0 + (wave & 3u) * 32 : row0 + wave * 32;
+  const uint8_t* const wcodes = (Glu && wave >= 4) ? glu.codes2 : codes;
+  const uint8_t* const wmeta = (Glu && wave >= 4) ? glu.meta2 : meta;
   const uint32_t lr = lane & 15u, lk = lane >> 4;
   const uint32_t steps = kbs * 4;
   const uint32_t last8 = pn / 8 - 1;
@@ -214,12 +234,12 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
 #pragma unroll
     for (uint32_t u = 0; u < 4; ++u) {
       const uint32_t T = wave * 4 + u;
-      const uint32_t r8 = min(row0 / 8 + T, last8);
-      dma16(codes + ((r8 * kbs + kb) * 1024 + (u % 2 ? a_off1 : a_off0)), wA + T * 1024);
+      const uint32_t r8 = min(wrow0 / 8 + u, last8);
+      dma16(wcodes + ((r8 * kbs + kb) * 1024 + (u % 2 ? a_off1 : a_off0)), wA + T * 1024);
     }
     {
-      const uint32_t r8 = min(row0 / 8 + wave * 4 + ((lane & 31u) >> 3), last8);
-      if (lane < 32) dma16(meta + ((r8 * kbs + kb) * 128 + (lane & 7u) * 16), wM + wave * 512);
+      const uint32_t r8 = min(wrow0 / 8 + ((lane & 31u) >> 3), last8);
+      if (lane < 32) dma16(wmeta + ((r8 * kbs + kb) * 128 + (lane & 7u) * 16), wM + wave * 512);
     }
     dma16(tq + (uint64_t(tb) * kbs + kb) * kTSlot + wave * 1024 + lane * 16, wT + wave * 1024);
   };
@@ -451,6 +471,83 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
           lds + kOffM + kMSlot + kTSlot, run);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy outlives the block
 
+  if constexpr (Glu) {
+    // ---- SwiGLU -> Q8 epilogue (mmq_kernel's Glu arithmetic). Gate waves
+    // 0-3 park their unscaled g in LDS (the ring is free once every wave is
+    // past its loop); up wave w holds u of the same features in the same
+    // register positions. The wave's K32 feature group of token lr is row
+    // tiles 0, 1 of lanes lr + 16 lk: eight values in each of 4 lanes. ----
+    __syncthreads();
+    float* gl = reinterpret_cast<float*>(lds);  // [128 features][128 tokens]
+    const bool gate_wave = wave < 4;
+    const uint32_t wq = wave & 3u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t tok = min(tb * kBT + j * 16 + lr, m - 1);
+      const float inv = ti[tok];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[i][j][v] *= inv;
+    }
+    if (gate_wave) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) gl[(wq * 32 + i * 16 + lk * 4 + v) * kBT + j * 16 + lr] = acc[i][j][v];
+    }
+    __syncthreads();
+    if (gate_wave) return;
+    const uint32_t groups_out = n / 32;
+    const uint32_t f0 = row0 + wq * 32;  // first feature of the group
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t tl = j * 16 + lr, tok = tb * kBT + tl;
+      float x[8];
+      float peak = 0.f;
+      int finite = 1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float g = gl[(wq * 32 + h * 16 + lk * 4 + v) * kBT + tl];
+          const float y = swiglu_q8_value(g, acc[h][j][v]);
+          x[4 * h + v] = y;
+          const bool f = isfinite(y);
+          finite &= int(f);
+          peak = fmaxf(peak, f ? fabsf(y) : 0.f);
+        }
+      peak = fmaxf(peak, __shfl_xor(peak, 16));
+      peak = fmaxf(peak, __shfl_xor(peak, 32));
+      finite &= __shfl_xor(finite, 16);
+      finite &= __shfl_xor(finite, 32);
+      const float a = peak == 0.f ? 1.f : peak / 127.f;
+      const bool valid = finite && isfinite(a) && a > 0.f;
+      uint32_t word[2] = {0u, 0u};
+      int sum = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int z = valid ? max(-127, min(127, int(rintf(x[e] / a)))) : 0;
+        sum += z;
+        word[e / 4] |= uint32_t(uint8_t(int8_t(z))) << (8 * (e % 4));
+      }
+      sum += __shfl_xor(sum, 16);
+      sum += __shfl_xor(sum, 32);
+      if (tok >= m || f0 >= n) continue;
+      int8_t* cp = glu.qc + size_t(tok) * n + f0 + lk * 4;
+      *reinterpret_cast<uint32_t*>(cp) = word[0];
+      *reinterpret_cast<uint32_t*>(cp + 16) = word[1];
+      if (lk == 0) {
+        const size_t gi = size_t(tok) * groups_out + f0 / 32;
+        glu.qa[gi] = valid ? a : __uint_as_float(0x7fc00000u);
+        glu.qs[gi] = sum;
+        if (!valid) *glu.failure = 1;  // sticky flag, plain vector store
+      }
+    }
+    return;
+  }
   // ---- store: lane holds rows 4 lk .. 4 lk + 3 of token lr in each tile ----
   const bool vec = (n % 4 == 0) &&
                    ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0;
@@ -461,7 +558,7 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
     const float inv = ti[tok];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const uint32_t r4 = row0 + wave * 32 + i * 16 + lk * 4;
+      const uint32_t r4 = wrow0 + i * 16 + lk * 4;
       if (r4 >= n) continue;
       const size_t o = size_t(tok) * n + r4;
 #pragma unroll
@@ -490,14 +587,22 @@ uint64_t mmq_dma_scratch_bytes(uint32_t m, uint32_t pk) {
   return mp * pk * 2 + mp / kBT * (pk / 256) * kTSlot + mp * 4;
 }
 
-// Rows [0, rows) of a Q4_K 0x020D weight (rows a multiple of 256 or pn) for
-// all m tokens; scratch holds mmq_dma_scratch_bytes(m, pk). Codes and
-// metadata must be 16-byte aligned.
+// Output rows [0, rows) of a Q4_K 0x020D weight (rows a multiple of the tile
+// height or all of pn) for all m tokens; scratch holds
+// mmq_dma_scratch_bytes(m, pk). Codes and metadata must be 16-byte aligned.
+// up != nullptr: fused gate + up over features [0, rows) (w is the gate, up
+// the same geometry), writing the down projection's Q8 operand.
 hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
-                          hipStream_t s, uint32_t rows, void* scratch) {
+                          hipStream_t s, uint32_t rows, void* scratch, const WeightView* up, int8_t* qc,
+                          float* qa, int32_t* qs, int* failure) {
+  const bool glu = up != nullptr;
   if (w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2 || rows == 0 || x.pk != w.pk ||
       ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
-        reinterpret_cast<uintptr_t>(x.codes)) % 16) != 0)
+        reinterpret_cast<uintptr_t>(x.codes) | reinterpret_cast<uintptr_t>(glu ? up->codes : nullptr) |
+        reinterpret_cast<uintptr_t>(glu ? up->scales : nullptr)) % 16) != 0)
+    return hipErrorInvalidValue;
+  if (glu && (up->layout != w.layout || up->pn != w.pn || up->pk != w.pk || w.n % 32 != 0 || !qc || !qa ||
+              !qs || !failure))
     return hipErrorInvalidValue;
   if ((w.pk / 256) % 2 != 0) return hipErrorNotReady;  // the main loop runs super-block pairs
   const uint32_t mp = (x.m + kBT - 1) / kBT * kBT;
@@ -508,11 +613,14 @@ hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, cons
                      x.sums, x.m, x.pk, bq, tq, ti);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  e = set_max_lds(reinterpret_cast<const void*>(mmq_dma_kernel), int(kLds));
+  auto kern = glu ? mmq_dma_kernel<true> : mmq_dma_kernel<false>;
+  e = set_max_lds(reinterpret_cast<const void*>(kern), int(kLds));
   if (e != hipSuccess) return e;
-  const uint32_t row_blocks = (rows + kBR - 1) / kBR, tok_blocks = mp / kBT;
-  hipLaunchKernelGGL(mmq_dma_kernel, dim3(row_blocks * tok_blocks), dim3(512), kLds, s, w.codes, w.scales,
-                     w.n, w.pn, w.pk / 256, bq, tq, ti, x.m, out, residual, row_blocks, tok_blocks);
+  const uint32_t hr = glu ? kBR / 2 : kBR;
+  const uint32_t row_blocks = (rows + hr - 1) / hr, tok_blocks = mp / kBT;
+  const GluDma g{glu ? up->codes : nullptr, glu ? up->scales : nullptr, qc, qa, qs, failure};
+  hipLaunchKernelGGL(kern, dim3(row_blocks * tok_blocks), dim3(512), kLds, s, w.codes, w.scales, w.n, w.pn,
+                     w.pk / 256, bq, tq, ti, x.m, out, residual, row_blocks, tok_blocks, g);
   return hipGetLastError();
 }
 
