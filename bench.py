@@ -552,8 +552,9 @@ def clock_probe(torch, ops):
 def issue_probe(torch):
     """VALU / matrix-core overlap on one SIMD (qw38_issue_probe, two waves per
     SIMD), timed with events: nanoseconds per loop iteration of 32 FP16
-    16x16x32 MFMAs alone, 128 FP32 FMAs alone, both interleaved 1:4, and 16
-    MFMAs with 128 FMAs interleaved 1:8; 'overlap' is the fraction of the
+    16x16x32 MFMAs alone, 128 FP32 FMAs alone, both interleaved 1:4, 16
+    MFMAs with 128 FMAs interleaved 1:8, and one MFMA-only wave (16) beside
+    one FMA-only wave (64) per SIMD; 'overlap' is the fraction of the
     shorter unit's time hidden under the other's (1 = fully hidden, 0 =
     serialized)."""
     from qw38_amd._lib import lib
@@ -562,7 +563,7 @@ def issue_probe(torch):
     iters = 20000
     ns = {}
     stream = torch.cuda.current_stream()
-    for mode in range(4):
+    for mode in range(5):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         for rep in range(2):  # the second launch is the one timed
             if rep:
@@ -578,8 +579,9 @@ def issue_probe(torch):
         return round((m + v - t) / min(m, v), 3)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     r = {"ns_per_iter": {"mfma32": round(mf, 1), "fma128": round(va, 1), "mix_1to4": round(ns[2], 1),
-                         "mix_1to8_16mfma": round(ns[3], 1)},
+                         "mix_1to8_16mfma": round(ns[3], 1), "split_waves_16mfma_64fma": round(ns[4], 1)},
          "overlap_1to4": ov(ns[2], mf, va), "overlap_1to8": ov(ns[3], mf / 2, va),
+         "overlap_split_waves": ov(ns[4], mf / 2, va / 2),
          "mfma_only_fp16_tflops": round(cus * 4 * 32 * 16384 / mf / 1e3, 1)}
     log(f"issue probe: {r}")
     return r

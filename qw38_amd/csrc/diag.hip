@@ -20,8 +20,9 @@
 // issues 16 independent v_mfma_f32_16x16x32_f16 per iteration, mode 1 64
 // independent FP32 FMAs, mode 2 both interleaved one MFMA to four FMAs (the
 // MMQ's per-group scale ratio), mode 3 eight MFMAs interleaved one to eight
-// FMAs. Time per iteration against the single-unit modes gives the overlap
-// (the bench times the launches with events).
+// FMAs, mode 4 one MFMA-only and one FMA-only wave per SIMD (16 MFMAs, 64
+// FMAs per SIMD and iteration). Time per iteration against the single-unit
+// modes gives the overlap (the bench times the launches with events).
 #include "common.hpp"
 
 namespace qw38hip {
@@ -90,6 +91,14 @@ __global__ __launch_bounds__(512, 1) void issue_probe_kernel(uint32_t iters, flo
     } else if constexpr (Mode == 1) {
 #pragma unroll
       for (int j = 0; j < 64; ++j) x[j] = fmaf(x[j], s, 1.0f);
+    } else if constexpr (Mode == 4) {  // waves 0-3 MFMAs only, waves 4-7 FMAs only: one of each per SIMD
+      if (threadIdx.x < 256) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 64; ++j) x[j] = fmaf(x[j], s, 1.0f);
+      }
     } else {
       constexpr int kM = Mode == 2 ? 16 : 8, kF = 64 / kM;
 #pragma unroll
@@ -195,12 +204,13 @@ extern "C" int qw38_mfma_clock_probe(uint32_t iterations, uint64_t* ticks, uint3
 
 extern "C" int qw38_issue_probe(uint32_t mode, uint32_t iterations, uint64_t* ticks, float* sink, void* stream) {
   using namespace qw38hip;
-  if (ticks == nullptr || sink == nullptr || mode > 3 || iterations == 0 || iterations > (1u << 24))
+  if (ticks == nullptr || sink == nullptr || mode > 4 || iterations == 0 || iterations > (1u << 24))
     return QW38_INVALID_ARGUMENT;
   auto kern = mode == 0   ? issue_probe_kernel<0>
               : mode == 1 ? issue_probe_kernel<1>
               : mode == 2 ? issue_probe_kernel<2>
-                          : issue_probe_kernel<3>;
+              : mode == 3 ? issue_probe_kernel<3>
+                          : issue_probe_kernel<4>;
   hipLaunchKernelGGL(kern, dim3(cu_count()), dim3(512), 0, static_cast<hipStream_t>(stream), iterations, 0.999f,
                      ticks, sink);
   return hipGetLastError() == hipSuccess ? QW38_OK : QW38_STATUS;
