@@ -277,24 +277,27 @@ def test_q4k_mmq_direct_copy_rows_independent_of_m(torch_gpu, tmp_path):
     w, wl = _fit_q4k(torch, ops, n, k, 331, oracle.LAYOUT_Q4K_SEQ)
     q, ob = _q8(torch, ops, normal((512, k), 332))
     full = None
-    # 512: direct-copy 256 x 128 tiles + 128 x 32 tail split; 130: 256 x 128
-    # tiles over two token blocks; 9 / 40 / 64: mmq_kernel's 128 x 32 and
-    # 128 x 64 tiles
-    for m in (512, 130, 9, 40, 64):
+    # 512: direct-copy 256 x 128 tiles + 128 x 32 tail split (the second time
+    # with a residual); 130 / 9 / 40 / 64: mmq_kernel's other tile picks
+    for m in (512, 512, 130, 9, 40, 64):
         print(f"Q4_K MMQ family M={m}", flush=True)
         qm = ops.Q8Input.empty(m, k)
         qm.codes.copy_(q.codes[:m]); qm.scales.copy_(q.scales[:m]); qm.sums.copy_(q.sums[:m])
         y = torch.full((m, n), float("nan"), device="cuda")
+        res = torch.from_numpy(normal((m, n), 333)).cuda() if full is not None and m == 512 else None
         torch.cuda.synchronize()
         before = ops.scratch_stats()
-        ops.q4k_q8_project(w, qm, y)
+        ops.q4k_q8_project(w, qm, y, residual=res)
         torch.cuda.synchronize()
         after = ops.scratch_stats()
         if m == 512:
             assert after[0] == before[0] + 1 and after[1:] == before[1:], \
                 f"M={m}: the direct-copy kernel did not get the scratch ({before} -> {after})"
         yn = y.cpu().numpy()
-        if full is None:
+        if res is not None:  # the residual epilogue adds exactly
+            want = (full[:m] + res.cpu().numpy()).astype(np.float32)
+            assert np.array_equal(yn.view(np.uint32), want.view(np.uint32)), "residual epilogue, M=512"
+        elif full is None:
             full = yn
         else:
             assert np.array_equal(yn.view(np.uint32), full[:m].view(np.uint32)), f"M={m} rows differ from M=512"
