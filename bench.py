@@ -554,7 +554,8 @@ def issue_probe(torch):
     SIMD), timed with events: nanoseconds per loop iteration of 32 FP16
     16x16x32 MFMAs alone, 128 FP32 FMAs alone, both interleaved 1:4, 16
     MFMAs with 128 FMAs interleaved 1:8, and one MFMA-only wave (16) beside
-    one FMA-only wave (64) per SIMD; 'overlap' is the fraction of the
+    one FMA-only wave (64) per SIMD; and 32 int8 16x16x32 / 16x16x64 MFMAs
+    alone; 'overlap' is the fraction of the
     shorter unit's time hidden under the other's (1 = fully hidden, 0 =
     serialized)."""
     from qw38_amd._lib import lib
@@ -563,7 +564,7 @@ def issue_probe(torch):
     iters = 20000
     ns = {}
     stream = torch.cuda.current_stream()
-    for mode in range(5):
+    for mode in range(7):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         for rep in range(2):  # the second launch is the one timed
             if rep:
@@ -579,7 +580,8 @@ def issue_probe(torch):
         return round((m + v - t) / min(m, v), 3)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     r = {"ns_per_iter": {"mfma32": round(mf, 1), "fma128": round(va, 1), "mix_1to4": round(ns[2], 1),
-                         "mix_1to8_16mfma": round(ns[3], 1), "split_waves_16mfma_64fma": round(ns[4], 1)},
+                         "mix_1to8_16mfma": round(ns[3], 1), "split_waves_16mfma_64fma": round(ns[4], 1),
+                         "i8_16x16x32_32": round(ns[5], 1), "i8_16x16x64_32": round(ns[6], 1)},
          "overlap_1to4": ov(ns[2], mf, va), "overlap_1to8": ov(ns[3], mf / 2, va),
          "overlap_split_waves": ov(ns[4], mf / 2, va / 2),
          "mfma_only_fp16_tflops": round(cus * 4 * 32 * 16384 / mf / 1e3, 1)}

@@ -443,7 +443,8 @@ int qw38_read_probe(const void* buf, uint64_t bytes, uint32_t mode, uint32_t blo
  * independent v_mfma_f32_16x16x32_f16, mode 1 sixty-four independent FP32
  * FMAs, mode 2 both interleaved one MFMA to four FMAs, mode 3 eight MFMAs
  * interleaved one to eight FMAs, mode 4 one MFMA-only and one FMA-only wave
- * per SIMD (16 MFMAs and 64 FMAs per SIMD and iteration). ticks[0] (device memory) receives the
+ * per SIMD (16 MFMAs and 64 FMAs per SIMD and iteration), modes 5 / 6
+ * sixteen independent v_mfma_i32_16x16x32_i8 / 16x16x64_i8 alone. ticks[0] (device memory) receives the
  * s_memtime ticks wave 0 spent in its loop; `sink` (device, >= 1 float)
  * is written only on a value the loop never produces. Shows how far the
  * VALU and the matrix core overlap on one SIMD. */

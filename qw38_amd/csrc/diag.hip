@@ -22,7 +22,8 @@
 // MMQ's per-group scale ratio), mode 3 eight MFMAs interleaved one to eight
 // FMAs, mode 4 one MFMA-only and one FMA-only wave per SIMD (16 MFMAs, 64
 // FMAs per SIMD and iteration). Time per iteration against the single-unit
-// modes gives the overlap (the bench times the launches with events).
+// modes gives the overlap (the bench times the launches with events). Modes 5
+// and 6 time 16 independent int8 MFMAs alone (16x16x32 and 16x16x64).
 #include "common.hpp"
 
 namespace qw38hip {
@@ -91,6 +92,16 @@ __global__ __launch_bounds__(512, 1) void issue_probe_kernel(uint32_t iters, flo
     } else if constexpr (Mode == 1) {
 #pragma unroll
       for (int j = 0; j < 64; ++j) x[j] = fmaf(x[j], s, 1.0f);
+    } else if constexpr (Mode == 5 || Mode == 6) {  // int8 MFMAs alone: 16x16x32 / 16x16x64
+      const v4i ia = {int(threadIdx.x), 3, 5, 7}, ib = {1, 2, 3, int(threadIdx.x)};
+      const long la = long(threadIdx.x) * 77, lb = long(threadIdx.x) * 13 + 5;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        v4i c = __builtin_bit_cast(v4i, acc[j]);
+        if constexpr (Mode == 5) c = __builtin_amdgcn_mfma_i32_16x16x32_i8(la, lb, c, 0, 0, 0);
+        else c = __builtin_amdgcn_mfma_i32_16x16x64_i8(ia, ib, c, 0, 0, 0);
+        acc[j] = __builtin_bit_cast(f4, c);
+      }
     } else if constexpr (Mode == 4) {  // waves 0-3 MFMAs only, waves 4-7 FMAs only: one of each per SIMD
       if (threadIdx.x < 256) {
 #pragma unroll
@@ -204,13 +215,15 @@ extern "C" int qw38_mfma_clock_probe(uint32_t iterations, uint64_t* ticks, uint3
 
 extern "C" int qw38_issue_probe(uint32_t mode, uint32_t iterations, uint64_t* ticks, float* sink, void* stream) {
   using namespace qw38hip;
-  if (ticks == nullptr || sink == nullptr || mode > 4 || iterations == 0 || iterations > (1u << 24))
+  if (ticks == nullptr || sink == nullptr || mode > 6 || iterations == 0 || iterations > (1u << 24))
     return QW38_INVALID_ARGUMENT;
   auto kern = mode == 0   ? issue_probe_kernel<0>
               : mode == 1 ? issue_probe_kernel<1>
               : mode == 2 ? issue_probe_kernel<2>
               : mode == 3 ? issue_probe_kernel<3>
-                          : issue_probe_kernel<4>;
+              : mode == 4 ? issue_probe_kernel<4>
+              : mode == 5 ? issue_probe_kernel<5>
+                          : issue_probe_kernel<6>;
   hipLaunchKernelGGL(kern, dim3(cu_count()), dim3(512), 0, static_cast<hipStream_t>(stream), iterations, 0.999f,
                      ticks, sink);
   return hipGetLastError() == hipSuccess ? QW38_OK : QW38_STATUS;
