@@ -225,8 +225,8 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
   // consecutive rows hit distinct banks. Copy u (0..3) of wave w is 8-row
   // tile T = 4 w + u: 1 KB contiguous in 0x020D, with lane l reading row
   // l / 8, chunk (l % 8) ^ (4 (T % 2) + l / 16) % 8 -- two lane offsets.
-  // Metadata: rows 32 w .. 32 w + 31, 16 B each, half a wave copy (lane l:
-  // row l / 8 of 8-row tile 4 w + l / 8 ... in steps of kbs * 128 B).
+  // Metadata: the wave's 32 rows, 16 B each, half a wave copy (lane l < 32:
+  // row l % 8 of the wave's 8-row tile l / 8).
   const uint32_t a_off0 = (lane >> 3) * 128 + (((lane & 7u) ^ ((lane >> 4) & 7u)) * 16);
   const uint32_t a_off1 = (lane >> 3) * 128 + (((lane & 7u) ^ ((4u + (lane >> 4)) & 7u)) * 16);
   auto issue_super = [&](uint32_t kb_in, uint8_t* wA, uint8_t* wM, uint8_t* wT) __attribute__((always_inline)) {
