@@ -35,7 +35,7 @@
 namespace qw38hip {
 uint64_t mmq_dma_scratch_bytes(uint32_t m, uint32_t pk);
 hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
-                          hipStream_t s, uint32_t rows, void* scratch, const WeightView* up = nullptr,
+                          hipStream_t s, uint32_t rows, uint32_t tail_end, void* scratch, const WeightView* up = nullptr,
                           int8_t* qc = nullptr, float* qa = nullptr, int32_t* qs = nullptr,
                           int* failure = nullptr);
 namespace {
@@ -865,12 +865,22 @@ constexpr double kQ6Step160 = 1.71;
 
 // Glu: the tile cost model runs over the 2 n virtual rows of gate and up, and
 // the launches get feature ranges (virtual rows / 2).
+// QW38_MMQ_DMA: 0 turns the direct-copy tiles off, 2 keeps them off the
+// 128 x 32 tiles (tuning aids: every setting gives the same bits).
+static int mmq_dma_env() {
+  static const int v = [] {
+    const char* e = std::getenv("QW38_MMQ_DMA");
+    return e ? std::atoi(e) : 1;
+  }();
+  return v;
+}
+
 template <uint16_t Layout, bool Glu = false>
 hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const float* residual,
                         hipStream_t s, GluOut glu = {}) {
   // QW38_MMQ_TILE=32|64|128 pins the token tile (256: 256 rows x 128 tokens;
   // 80: 80 x 128 on four waves; 33, 81, 129, 192: 128 x 32, 80 x 128,
-  // 128 x 128 and 192 x 128 on eight waves);
+  // 128 x 128 and 192 x 128 on eight waves; 34: 128 x 32 direct-copy);
   // QW38_MMQ_SPLIT=0 disables the tail split (tuning aids; every tile shape
   // and split gives bitwise-identical results).
   static const int forced = [] {
@@ -919,7 +929,12 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   }
   const double c_big = b_big * (q6 ? 1.77 : 1.9);
   const double c64 = q6 ? two(per_cu(128, 64), 1.33, 2.65) : two(per_cu(128, 64), 1.07, 1.39);
-  const double c32 = q6 ? two(per_cu(128, 32), 1.0, 2.0) : two(per_cu(128, 32), 0.70, 0.89);
+  // The direct-copy 128 x 32 tile (Q4_K 0x020D with the library scratch)
+  // takes 0.86 of mmq_kernel's time at every grid size measured (5120 to
+  // 34816 rows, M = 16 to 512).
+  const bool dma32 = Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2 && mmq_dma_env() == 1 && x.pk == w.pk &&
+                      (w.pk / 256) % 2 == 0;
+  const double c32 = q6 ? two(per_cu(128, 32), 1.0, 2.0) : two(per_cu(128, 32), 0.70, 0.89) * (dma32 ? 0.86 : 1.0);
   // 80 x 128 on eight waves (one block per CU, two waves per SIMD; the
   // four-wave 80 x 128 tile, QW38_MMQ_TILE=80, is always slower): 5120-row
   // weights make 64 row blocks, so a 512-token chunk fills 256 CUs in one
@@ -1007,6 +1022,41 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   if constexpr (!Glu)
     if (bt == 81) return launch_cfg<Layout, 1, 8, 5, 1>(w, x, out, residual, s, 0, pn);  // 80 x 128, 8 waves
   const uint32_t end = pn / kv;
+  // 0x020D with 16-byte aligned spans: the direct-copy form of the 256 x 128
+  // and 128 x 32 tiles (q4k_mmq_dma.hip, bitwise-equal outputs) when the
+  // library scratch holds its pre-pass: rows [0, big) on the big tile, [big,
+  // end) on the small one. hipErrorNotReady when it does not apply.
+  const int dma_env = mmq_dma_env();
+  auto try_dma = [&](uint32_t big, uint32_t tail_end) -> hipError_t {
+    if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2) {
+      const bool aligned = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
+                             reinterpret_cast<uintptr_t>(x.codes) | reinterpret_cast<uintptr_t>(glu.codes2) |
+                             reinterpret_cast<uintptr_t>(glu.meta2)) % 16) == 0;
+      if (!dma_env || !aligned || x.pk != w.pk || (w.pk / 256) % 2 != 0) return hipErrorNotReady;
+      if (dma_env == 2) tail_end = big;
+      if (tail_end == 0) return hipErrorNotReady;
+      int dev = 0;
+      void* sc = scratch_acquire(s, mmq_dma_scratch_bytes(x.m, x.pk), &dev);
+      if (!sc) return hipErrorNotReady;
+      hipError_t e;
+      if constexpr (Glu) {
+        const WeightView up{glu.codes2, glu.meta2, w.layout, w.n, w.k, w.pn, w.pk};
+        e = launch_mmq_dma(w, x, nullptr, nullptr, s, big, tail_end, sc, &up, glu.qc, glu.qa, glu.qs,
+                           glu.failure);
+      } else {
+        e = launch_mmq_dma(w, x, out, residual, s, big, tail_end, sc);
+      }
+      scratch_release(dev, s, e == hipSuccess);
+      return e;
+    }
+    return hipErrorNotReady;
+  };
+  if (bt == 32 && !forced && dma32) bt = 34;
+  if (bt == 34) {  // 128 x 32 direct-copy over all rows
+    const hipError_t e = try_dma(0, end);
+    if (e != hipErrorNotReady) return e;
+    bt = 32;
+  }
   if (bt == 32) return launch_cfg<Layout, 4, 1, 2, 2, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 32
   if (bt == 64) return launch_cfg<Layout, 4, 1, 2, 4, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 64
   if constexpr (q6) {  // Q6_K's two A planes: 128 x 128 at most
@@ -1014,32 +1064,9 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   } else {
     if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 128
     if (forced) big_rows = pn;
-    hipError_t e = hipErrorNotReady;
-    // 0x020D with 16-byte aligned spans: the direct-copy form of the same
-    // tile (q4k_mmq_dma.hip, bitwise-equal outputs) when the library scratch
-    // holds its pre-pass; QW38_MMQ_DMA=0 turns it off.
-    static const bool dma_env = [] {
-      const char* v = std::getenv("QW38_MMQ_DMA");
-      return !(v && std::atoi(v) == 0);
-    }();
-    if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2) {
-      const bool aligned = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
-                             reinterpret_cast<uintptr_t>(x.codes) | reinterpret_cast<uintptr_t>(glu.codes2) |
-                             reinterpret_cast<uintptr_t>(glu.meta2)) % 16) == 0;
-      if (dma_env && aligned && x.pk == w.pk) {
-        int dev = 0;
-        if (void* sc = scratch_acquire(s, mmq_dma_scratch_bytes(x.m, x.pk), &dev)) {
-          if constexpr (Glu) {
-            const WeightView up{glu.codes2, glu.meta2, w.layout, w.n, w.k, w.pn, w.pk};
-            e = launch_mmq_dma(w, x, nullptr, nullptr, s, big_rows / kv, sc, &up, glu.qc, glu.qa, glu.qs,
-                               glu.failure);
-          } else {
-            e = launch_mmq_dma(w, x, out, residual, s, big_rows, sc);
-          }
-          scratch_release(dev, s, e == hipSuccess);
-        }
-      }
-    }
+    const uint32_t dma_end = dma_env == 2 ? big_rows / kv : end;
+    hipError_t e = try_dma(big_rows / kv, dma_end);
+    if (e == hipSuccess && dma_end == end) return e;
     if (e == hipErrorNotReady) e = launch_cfg<Layout, 4, 2, 4, 4, Glu>(w, x, out, residual, s, 0, big_rows / kv, glu);
     if (e != hipSuccess || big_rows == pn) return e;
     return launch_cfg<Layout, 4, 1, 2, 2, Glu>(w, x, out, residual, s, big_rows / kv, end, glu);

@@ -40,19 +40,28 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kBR = 256, kBT = 128;
-// LDS: B ring (4 K steps x 16 KB), A (2 super-blocks x 256 rows x 128 B raw
-// codes), metadata (2 x 256 rows x 16 B), token data (2 x 8 KB)
-constexpr uint32_t kBSlot = 16384, kASlot = 32768, kMSlot = 4096, kTSlot = 8192;
-// metadata and token data of one super-block share a region (the compiler
-// tracks at most eight regions of copies in flight)
-constexpr uint32_t kOffA = 4 * kBSlot, kOffM = kOffA + 2 * kASlot;  // then slot 1 at + kMSlot + kTSlot
-constexpr uint32_t kLds = kOffM + 2 * (kMSlot + kTSlot);  // 155648 B
-// token data block per (token block, super-block): a' as [8 groups][128
-// tokens] fp32, then per token 32 B of min-term operands: hi of groups 0-3,
-// lo of groups 0-3, hi of groups 4-7, lo of groups 4-7 (FP16), so a lane
-// reads its hi and lo K-quarter with one 16-byte read
-constexpr uint32_t kTokA = 0, kTokU = 4096;
+// The pre-pass writes the activations in blocks of kPB = 128 tokens. Its token
+// data block per (token block, super-block) is a' as [8 groups][128 tokens]
+// fp32, then per token 32 B of min-term operands: hi of groups 0-3, lo of
+// groups 0-3, hi of groups 4-7, lo of groups 4-7 (FP16), so a lane reads its
+// hi and lo K-quarter with one 16-byte read.
+constexpr uint32_t kPB = 128, kTSlot = 8192, kTokU = 4096;
+
+// Tile geometry of the main kernel: NW waves of 32 rows x NJ 16-token tiles;
+// 256 x 128 (NW = 8, NJ = 8) for the large grids, 128 x 32 (NW = 4, NJ = 2)
+// for the tail rows and small M. LDS: a B ring of 4 K steps (BT tokens x
+// 64 K, FP16), two super-block slots of raw codes (BR x 128 B), and two of
+// metadata (BR x 16 B) + token data (a' [8][BT] fp32, min-term operands
+// [BT][32 B]); metadata and token data of one super-block share a region
+// (the compiler tracks at most eight regions of copies in flight).
+template <int NW, int NJ>
+struct Geo {
+  static constexpr uint32_t BR = 32 * NW, BT = 16 * NJ;
+  static constexpr uint32_t BSL = BT * 128, ASL = BR * 128, MSL = BR * 16, TSL = BT * 64;
+  static constexpr uint32_t OffA = 4 * BSL, OffM = OffA + 2 * ASL, MTS = MSL + TSL;
+  static constexpr uint32_t Lds = OffM + 2 * MTS;  // 155648 B for 256 x 128, 57344 B for 128 x 32
+  static constexpr uint32_t TokU = 32 * BT;         // min-term operands in the tile's token data
+};
 
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -104,7 +113,7 @@ __device__ __forceinline__ uint4 lds_read16_sync(const uint8_t* p) {
 // bq: [tb][step][chunk 8][token 128] 16-byte entries; chunk c = gsel * 4 + lk
 //     holds the codes 32 g + 8 lk + {0, 2, 4, 6, 1, 3, 5, 7} of group
 //     g = 2 step + gsel as FP16 (the slot order the A fragments unpack to).
-// tq: [tb][kb] token data blocks (kTokA, kTokU).
+// tq: [tb][kb] token data blocks (a' at 0, min-term operands at kTokU).
 // ti: [mp] 1 / ts. Tokens m .. mp - 1 get zero codes and data, ti = 1.
 // Block (x, y) covers tokens 64 x .. 64 x + 63. y < kbs: the codes of
 // super-block y, transposed through LDS (row reads of 256 B per token, then
@@ -132,7 +141,7 @@ __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restr
     }
     __syncthreads();
     const h2 off = {_Float16(-1152.f), _Float16(-1152.f)};
-    const uint32_t t = t0 + lane, tb = t / kBT, tl = t % kBT;
+    const uint32_t t = t0 + lane, tb = t / kPB, tl = t % kPB;
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
       const uint32_t ch = w * 8 + i;  // 8-code chunk of the super-block (0..31)
@@ -143,13 +152,13 @@ __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restr
       o.y = as_u32(as_h2(perm(0x64646464u, u1, 0x04020400u)) + off);  // z4, z6
       o.z = as_u32(as_h2(perm(0x64646464u, u0, 0x04030401u)) + off);  // z1, z3
       o.w = as_u32(as_h2(perm(0x64646464u, u1, 0x04030401u)) + off);  // z5, z7
-      *reinterpret_cast<uint4*>(bq + ((size_t(tb) * steps + st) * 8 + c) * (kBT * 16) + tl * 16) = o;
+      *reinterpret_cast<uint4*>(bq + ((size_t(tb) * steps + st) * 8 + c) * (kPB * 16) + tl * 16) = o;
     }
     return;
   }
   // token data: ts = 2^e by mmq_kernel's rule (max_g |a| 2^12 ts in [2^13, 2^14))
   {
-    const uint32_t t = t0 + (blockIdx.y - kbs) * 4 + w, tb = t / kBT, tl = t % kBT;
+    const uint32_t t = t0 + (blockIdx.y - kbs) * 4 + w, tb = t / kPB, tl = t % kPB;
     const bool real = t < m;
     float mx = 0.f;
     if (real)
@@ -171,7 +180,7 @@ __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restr
         h = _Float16(v);
         l = _Float16(v - float(h));
       }
-      *reinterpret_cast<float*>(base + kTokA + (g8 * kBT + tl) * 4) = a;
+      *reinterpret_cast<float*>(base + (g8 * kPB + tl) * 4) = a;
       // per token: hi of groups 0-3, lo of 0-3, hi of 4-7, lo of 4-7
       const uint32_t hpos = (g8 / 4) * 16 + (g8 % 4) * 2;
       *reinterpret_cast<_Float16*>(base + kTokU + tl * 32 + hpos) = h;
@@ -195,24 +204,27 @@ struct GluDma {
   int* failure;
 };
 
-template <bool Glu>
-__global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
+template <int NW, int NJ, bool Glu>
+__global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n, uint32_t pn,
     uint32_t kbs, const uint8_t* __restrict__ bq, const uint8_t* __restrict__ tq,
     const float* __restrict__ ti, uint32_t m, float* __restrict__ out, const float* __restrict__ residual,
-    uint32_t row_blocks, uint32_t tok_blocks, GluDma glu) {
+    uint32_t row_begin, uint32_t row_blocks, uint32_t tok_blocks, GluDma glu) {
+  using G = Geo<NW, NJ>;
+  constexpr uint32_t BR = G::BR, BT = G::BT, NH = NW / 2;
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t tiles_n = row_blocks * tok_blocks;
   const uint32_t tile = (tiles_n % 8 == 0) ? (blockIdx.x % 8) * (tiles_n / 8) + blockIdx.x / 8 : blockIdx.x;
   const uint32_t rb = tile / tok_blocks, tb = tile % tok_blocks;
-  constexpr uint32_t HR = Glu ? kBR / 2 : kBR;  // output rows (features) per tile
-  const uint32_t row0 = rb * HR;
+  constexpr uint32_t HR = Glu ? BR / 2 : BR;  // output rows (features) per tile
+  const uint32_t row0 = row_begin + rb * HR;
+  const uint32_t pb = tb * BT / kPB, toff = tb * BT % kPB;  // pre-pass token block and offset
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
   // the wave's 32 weight rows: first row and source arrays (wave-uniform)
-  const uint32_t wrow0 = Glu ? row0 + (wave & 3u) * 32 : row0 + wave * 32;
-  const uint8_t* const wcodes = (Glu && wave >= 4) ? glu.codes2 : codes;
-  const uint8_t* const wmeta = (Glu && wave >= 4) ? glu.meta2 : meta;
+  const uint32_t wrow0 = Glu ? row0 + (wave % NH) * 32 : row0 + wave * 32;
+  const uint8_t* const wcodes = (Glu && wave >= NH) ? glu.codes2 : codes;
+  const uint8_t* const wmeta = (Glu && wave >= NH) ? glu.meta2 : meta;
   const uint32_t lr = lane & 15u, lk = lane >> 4;
   const uint32_t steps = kbs * 4;
   const uint32_t last8 = pn / 8 - 1;
@@ -241,21 +253,37 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
       const uint32_t r8 = min(wrow0 / 8 + ((lane & 31u) >> 3), last8);
       if (lane < 32) dma16(wmeta + ((r8 * kbs + kb) * 128 + (lane & 7u) * 16), wM + wave * 512);
     }
-    dma16(tq + (uint64_t(tb) * kbs + kb) * kTSlot + wave * 1024 + lane * 16, wT + wave * 1024);
+    {  // token data: 16-byte LDS positions p = P wave + lane of the tile's
+       // a' [8][BT] then min-term operands [BT][32 B], gathered from the
+       // pre-pass block at token offset toff
+      constexpr uint32_t P = 4 * BT / NW;  // positions per wave (<= 64)
+      const uint32_t pos = P * wave + lane;
+      const uint8_t* blk = tq + (uint64_t(pb) * kbs + kb) * kTSlot;
+      const uint8_t* src = pos < 2 * BT ? blk + (pos / (BT / 4)) * (kPB * 4) + (toff + (pos % (BT / 4)) * 4) * 4
+                                        : blk + kTokU + (toff + (pos - 2 * BT) / 2) * 32 + ((pos - 2 * BT) % 2) * 16;
+      if (P == 64 || lane < P) dma16(src, wT + P * wave * 16);
+    }
   };
+  // B of K step s: LDS [8 chunks][BT tokens][16 B]; wave w copies 1 KB runs
+  // kc = CPW w .. CPW w + CPW - 1 of the slot (lane l: position 64 kc + l =
+  // chunk, token), gathered from the pre-pass block's chunk rows.
   auto issue_step = [&](uint32_t s_in, uint8_t* wB) __attribute__((always_inline)) {
+    constexpr uint32_t CPW = BT / 8 / NW;  // 1 KB copies per wave and step
+    static_assert(CPW >= 1, "B copy share");
     const uint32_t s = min(s_in, steps - 1);
-    const uint8_t* src = bq + ((uint64_t(tb) * steps + s) * 8 + wave) * (kBT * 16) + lane * 16;
-    uint8_t* dst = wB + wave * (kBT * 16);
-    dma16(src, dst);
-    dma16(src + 1024, dst + 1024);
+    const uint8_t* row = bq + (uint64_t(pb) * steps + s) * 8 * (kPB * 16);
+#pragma unroll
+    for (uint32_t k = 0; k < CPW; ++k) {
+      const uint32_t pos = (CPW * wave + k) * 64 + lane, c = pos / BT, t = pos % BT;
+      dma16(row + c * (kPB * 16) + (toff + t) * 16, wB + (CPW * wave + k) * 1024);
+    }
   };
 
-  float acc[2][8][4], X[2][8][4];
+  float acc[2][NJ][4], X[2][NJ][4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
 
@@ -307,17 +335,17 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
       const h2 p3 = __builtin_elementwise_fma(as_h2(perm(0x64646464u, hi, 0x04030402u)), s2, b2);
       return half8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
     };
-    // Software pipeline over the step's 16 items u = (group gsel = u / 8,
-    // token tile j = u % 8): item u's MFMAs are issued after the B fragment
+    // Software pipeline over the step's 2 NJ items u = (group gsel = u / NJ,
+    // token tile j = u % NJ): item u's MFMAs are issued after the B fragment
     // and a' of item u + kPF are requested and before item u - 1's results
     // are scaled; sched_barrier keeps the compiler from hoisting further
     // (the register budget is two waves per SIMD).
     constexpr int kPF = 2;
     auto bfrag = [&](int u) __attribute__((always_inline)) {
-      return *reinterpret_cast<const half8*>(Bs + (((u >> 3) * 4 + lk) * kBT + (u & 7) * 16 + lr) * 16);
+      return *reinterpret_cast<const half8*>(Bs + (((u / NJ) * 4 + lk) * BT + (u % NJ) * 16 + lr) * 16);
     };
     auto afac = [&](int u) __attribute__((always_inline)) {
-      return *reinterpret_cast<const float*>(Ts + kTokA + ((2 * q + (u >> 3)) * kBT + (u & 7) * 16 + lr) * 4);
+      return *reinterpret_cast<const float*>(Ts + ((2 * q + u / NJ) * BT + (u % NJ) * 16 + lr) * 4);
     };
     half8 bq_[kPF + 1];
     float aq_[kPF + 1];
@@ -332,24 +360,24 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
     f4 Pp[2];
     float ap = 0.f;
 #pragma unroll
-    for (int u = 0; u <= 16; ++u) {
+    for (int u = 0; u <= 2 * NJ; ++u) {
       f4 Pc[2];
       float ac = 0.f;
-      if (u < 16) {
-        if (u + kPF < 16) {
+      if (u < 2 * NJ) {
+        if (u + kPF < 2 * NJ) {
           bq_[(u + kPF) % (kPF + 1)] = bfrag(u + kPF);
           aq_[(u + kPF) % (kPF + 1)] = afac(u + kPF);
         }
-        if (u == 6) af[1][0] = dequant(1, 0);
-        if (u == 7) af[1][1] = dequant(1, 1);
+        if (u == (NJ >= 2 ? NJ - 2 : 0)) af[1][0] = dequant(1, 0);  // the second group's fragments,
+        if (u == NJ - 1) af[1][1] = dequant(1, 1);                  // ready before its first item
         const half8 bf = bq_[u % (kPF + 1)];
         ac = aq_[u % (kPF + 1)];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) Pc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[u >> 3][i], bf, f4{0, 0, 0, 0}, 0, 0, 0);
+        for (int i = 0; i < 2; ++i) Pc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[u / NJ][i], bf, f4{0, 0, 0, 0}, 0, 0, 0);
       }
       if (u > 0) {
-        const int pu = u - 1, pj = pu & 7;
-        const bool first = q == 0 && pu < 8;  // the super-block's first group
+        const int pu = u - 1, pj = pu % NJ;
+        const bool first = q == 0 && pu < NJ;  // the super-block's first group
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -365,7 +393,7 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(X[i][j][v]));
     // ---- end of super-block: acc += d X - dmin Y ----
@@ -386,19 +414,27 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
             : "memory");
       }
 #pragma unroll
-      for (int jh = 0; jh < 2; ++jh) {
+      for (int jh = 0; jh < (NJ + 3) / 4; ++jh) {
         // min-term operands of token tiles 4 jh .. 4 jh + 3; lanes lk >= 2
         // (K 8..15, the zero padding) read a valid address and are masked
         uint4 r[4];
-        const uint32_t a0 = lds_addr(Ts + kTokU + (jh * 64 + lr) * 32 + (lk & 1u) * 16);
-        asm volatile(
-            "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:512\n\tds_read_b128 %2, %4 offset:1024\n\t"
-            "ds_read_b128 %3, %4 offset:1536\n\ts_waitcnt lgkmcnt(0)"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-            : "v"(a0)
-            : "memory");
+        const uint32_t a0 = lds_addr(Ts + G::TokU + (jh * 64 + lr) * 32 + (lk & 1u) * 16);
+        if constexpr (NJ % 4 == 0) {
+          asm volatile(
+              "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:512\n\tds_read_b128 %2, %4 offset:1024\n\t"
+              "ds_read_b128 %3, %4 offset:1536\n\ts_waitcnt lgkmcnt(0)"
+              : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+              : "v"(a0)
+              : "memory");
+        } else {
+          static_assert(NJ == 2, "token tiles per wave: 2 or a multiple of 4");
+          asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:512\n\ts_waitcnt lgkmcnt(0)"
+                       : "=&v"(r[0]), "=&v"(r[1])
+                       : "v"(a0)
+                       : "memory");
+        }
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
+        for (int jj = 0; jj < (NJ < 4 ? NJ : 4); ++jj) {
           const int j = jh * 4 + jj;
           const half4 uh = __builtin_bit_cast(half4, make_uint2(r[jj].x & ymask, r[jj].y & ymask));
           const half4 ul = __builtin_bit_cast(half4, make_uint2(r[jj].z & ymask, r[jj].w & ymask));
@@ -419,7 +455,7 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
           for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(acc[i][j][v]));
     }
@@ -441,7 +477,7 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
   uint8_t* const Bsl[4] = {B0, B1, B2, B3};
   uint8_t* const Asl[2] = {A0, A1};
   uint8_t* const Msl[2] = {MT0, MT1};
-  uint8_t* const Tsl[2] = {MT0 + kMSlot, MT1 + kMSlot};
+  uint8_t* const Tsl[2] = {MT0 + G::MSL, MT1 + G::MSL};
   auto step = [&](auto qc, auto sbc, uint32_t kb) __attribute__((always_inline)) {
     constexpr uint32_t q = decltype(qc)::value, SB = decltype(sbc)::value;
     if constexpr (q % 2 == 0) {
@@ -467,23 +503,23 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
     super_block(kb + 1, C1{});
   }
   };
-  regions(lds, lds + kBSlot, lds + 2 * kBSlot, lds + 3 * kBSlot, lds + kOffA, lds + kOffA + kASlot, lds + kOffM,
-          lds + kOffM + kMSlot + kTSlot, run);
+  regions(lds, lds + G::BSL, lds + 2 * G::BSL, lds + 3 * G::BSL, lds + G::OffA, lds + G::OffA + G::ASL,
+          lds + G::OffM, lds + G::OffM + G::MTS, run);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy outlives the block
 
   if constexpr (Glu) {
-    // ---- SwiGLU -> Q8 epilogue (mmq_kernel's Glu arithmetic). Gate waves
-    // 0-3 park their unscaled g in LDS (the ring is free once every wave is
+    // ---- SwiGLU -> Q8 epilogue (mmq_kernel's Glu arithmetic). The gate
+    // waves (the first NW / 2) park their unscaled g in LDS (the ring is free once every wave is
     // past its loop); up wave w holds u of the same features in the same
     // register positions. The wave's K32 feature group of token lr is row
     // tiles 0, 1 of lanes lr + 16 lk: eight values in each of 4 lanes. ----
     __syncthreads();
-    float* gl = reinterpret_cast<float*>(lds);  // [128 features][128 tokens]
-    const bool gate_wave = wave < 4;
-    const uint32_t wq = wave & 3u;
+    float* gl = reinterpret_cast<float*>(lds);  // [HR features][BT tokens]
+    const bool gate_wave = wave < NH;
+    const uint32_t wq = wave % NH;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t tok = min(tb * kBT + j * 16 + lr, m - 1);
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t tok = min(tb * BT + j * 16 + lr, m - 1);
       const float inv = ti[tok];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -494,17 +530,17 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) gl[(wq * 32 + i * 16 + lk * 4 + v) * kBT + j * 16 + lr] = acc[i][j][v];
+          for (int v = 0; v < 4; ++v) gl[(wq * 32 + i * 16 + lk * 4 + v) * BT + j * 16 + lr] = acc[i][j][v];
     }
     __syncthreads();
     if (gate_wave) return;
     const uint32_t groups_out = n / 32;
     const uint32_t f0 = row0 + wq * 32;  // first feature of the group
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t tl = j * 16 + lr, tok = tb * kBT + tl;
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t tl = j * 16 + lr, tok = tb * BT + tl;
       float x[8];
       float peak = 0.f;
       int finite = 1;
@@ -512,7 +548,7 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float g = gl[(wq * 32 + h * 16 + lk * 4 + v) * kBT + tl];
+          const float g = gl[(wq * 32 + h * 16 + lk * 4 + v) * BT + tl];
           const float y = swiglu_q8_value(g, acc[h][j][v]);
           x[4 * h + v] = y;
           const bool f = isfinite(y);
@@ -552,8 +588,8 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
   const bool vec = (n % 4 == 0) &&
                    ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t tok = tb * kBT + j * 16 + lr;
+  for (int j = 0; j < NJ; ++j) {
+    const uint32_t tok = tb * BT + j * 16 + lr;
     if (tok >= m) continue;
     const float inv = ti[tok];
 #pragma unroll
@@ -583,20 +619,45 @@ __global__ __launch_bounds__(512, 1) void mmq_dma_kernel(
 
 // Scratch bytes the pre-pass needs for m tokens of padded width pk.
 uint64_t mmq_dma_scratch_bytes(uint32_t m, uint32_t pk) {
-  const uint64_t mp = (uint64_t(m) + kBT - 1) / kBT * kBT;
-  return mp * pk * 2 + mp / kBT * (pk / 256) * kTSlot + mp * 4;
+  const uint64_t mp = (uint64_t(m) + kPB - 1) / kPB * kPB;
+  return mp * pk * 2 + mp / kPB * (pk / 256) * kTSlot + mp * 4;
 }
 
-// Output rows [0, rows) of a Q4_K 0x020D weight (rows a multiple of the tile
-// height or all of pn) for all m tokens; scratch holds
-// mmq_dma_scratch_bytes(m, pk). Codes and metadata must be 16-byte aligned.
-// up != nullptr: fused gate + up over features [0, rows) (w is the gate, up
-// the same geometry), writing the down projection's Q8 operand.
-hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
-                          hipStream_t s, uint32_t rows, void* scratch, const WeightView* up, int8_t* qc,
-                          float* qa, int32_t* qs, int* failure) {
+namespace {
+
+template <int NW, int NJ>
+hipError_t launch_dma_tiles(const WeightView& w, const Q8View& x, float* out, const float* residual, hipStream_t s,
+                            uint32_t row_begin, uint32_t rows, const uint8_t* bq, const uint8_t* tq,
+                            const float* ti, const WeightView* up, const GluDma& g) {
+  using G = Geo<NW, NJ>;
   const bool glu = up != nullptr;
-  if (w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2 || rows == 0 || x.pk != w.pk ||
+  auto kern = glu ? mmq_dma_kernel<NW, NJ, true> : mmq_dma_kernel<NW, NJ, false>;
+  if (G::Lds > 64 * 1024) {
+    const hipError_t e = set_max_lds(reinterpret_cast<const void*>(kern), int(G::Lds));
+    if (e != hipSuccess) return e;
+  }
+  const uint32_t hr = glu ? G::BR / 2 : G::BR;
+  const uint32_t row_blocks = (rows + hr - 1) / hr, tok_blocks = (x.m + G::BT - 1) / G::BT;
+  hipLaunchKernelGGL(kern, dim3(row_blocks * tok_blocks), dim3(NW * 64), G::Lds, s, w.codes, w.scales, w.n, w.pn,
+                     w.pk / 256, bq, tq, ti, x.m, out, residual, row_begin, row_blocks, tok_blocks, g);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Output rows [0, rows) on 256 x 128 tiles and [rows, tail_end) on 128 x 32
+// tiles (tail_end = rows: none) of a Q4_K 0x020D weight for all m tokens,
+// after one activation pre-pass; rows a multiple of the big tile height (in
+// features for the fused form), tail_end a multiple of the small one or the
+// whole weight. scratch holds mmq_dma_scratch_bytes(m, pk). Codes and
+// metadata must be 16-byte aligned. up != nullptr: fused gate + up over
+// features (w is the gate, up the same geometry), writing the down
+// projection's Q8 operand.
+hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
+                          hipStream_t s, uint32_t rows, uint32_t tail_end, void* scratch, const WeightView* up,
+                          int8_t* qc, float* qa, int32_t* qs, int* failure) {
+  const bool glu = up != nullptr;
+  if (w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2 || tail_end < rows || tail_end == 0 || x.pk != w.pk ||
       ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
         reinterpret_cast<uintptr_t>(x.codes) | reinterpret_cast<uintptr_t>(glu ? up->codes : nullptr) |
         reinterpret_cast<uintptr_t>(glu ? up->scales : nullptr)) % 16) != 0)
@@ -605,23 +666,19 @@ hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, cons
               !qs || !failure))
     return hipErrorInvalidValue;
   if ((w.pk / 256) % 2 != 0) return hipErrorNotReady;  // the main loop runs super-block pairs
-  const uint32_t mp = (x.m + kBT - 1) / kBT * kBT;
+  const uint32_t mp = (x.m + kPB - 1) / kPB * kPB;
   uint8_t* bq = static_cast<uint8_t*>(scratch);
   uint8_t* tq = bq + uint64_t(mp) * w.pk * 2;
-  float* ti = reinterpret_cast<float*>(tq + uint64_t(mp / kBT) * (w.pk / 256) * kTSlot);
+  float* ti = reinterpret_cast<float*>(tq + uint64_t(mp / kPB) * (w.pk / 256) * kTSlot);
   hipLaunchKernelGGL(mmq_dma_prep_kernel, dim3(mp / 64, w.pk / 256 + 16), dim3(256), 0, s, x.codes, x.scales,
                      x.sums, x.m, x.pk, bq, tq, ti);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  auto kern = glu ? mmq_dma_kernel<true> : mmq_dma_kernel<false>;
-  e = set_max_lds(reinterpret_cast<const void*>(kern), int(kLds));
-  if (e != hipSuccess) return e;
-  const uint32_t hr = glu ? kBR / 2 : kBR;
-  const uint32_t row_blocks = (rows + hr - 1) / hr, tok_blocks = mp / kBT;
   const GluDma g{glu ? up->codes : nullptr, glu ? up->scales : nullptr, qc, qa, qs, failure};
-  hipLaunchKernelGGL(kern, dim3(row_blocks * tok_blocks), dim3(512), kLds, s, w.codes, w.scales, w.n, w.pn,
-                     w.pk / 256, bq, tq, ti, x.m, out, residual, row_blocks, tok_blocks, g);
-  return hipGetLastError();
+  if (rows > 0) e = launch_dma_tiles<8, 8>(w, x, out, residual, s, 0, rows, bq, tq, ti, up, g);
+  if (e == hipSuccess && tail_end > rows)
+    e = launch_dma_tiles<4, 2>(w, x, out, residual, s, rows, tail_end - rows, bq, tq, ti, up, g);
+  return e;
 }
 
 }  // namespace qw38hip
