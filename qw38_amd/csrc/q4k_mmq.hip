@@ -859,6 +859,15 @@ hipError_t launch_cfg(const WeightView& w, const Q8View& x, float* out, const fl
   return hipGetLastError();
 }
 
+// The direct-copy Q6_K path's segment sum (mmq_seg_reduce_kernel).
+hipError_t q6_seg_reduce(const float* part, uint32_t segs, uint32_t m, uint32_t n, const float* residual,
+                         float* out, hipStream_t s) {
+  const uint64_t count = uint64_t(m) * n;
+  const uint32_t rgrid = uint32_t(std::min<uint64_t>((count + 255) / 256, 4096));
+  hipLaunchKernelGGL(mmq_seg_reduce_kernel, dim3(rgrid), dim3(256), 0, s, part, segs, count, residual, out);
+  return hipGetLastError();
+}
+
 // Q6_K 160 x 128 eight-wave tile: microseconds per two-group K step at one
 // block per CU (measured).
 constexpr double kQ6Step160 = 1.71;
@@ -986,11 +995,33 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
       if ((!forced && c < c_best) || forced == id) c_best = c, pick = id;
     };
     consider(160, rounds(160, 1) * kbs * 4 * kQ6Step160);
+    // The direct-copy 160 x 128 tile (q4k_mmq_dma.hip; one fixed segment per
+    // block, tokens in chunks the scratch holds) measured faster than every
+    // tile above for all M > 128 at 5120 x 17408 (M = 160: 132 against
+    // 146 us; 512: 230 / 260; 1536: 668 / 853; 2048: 887 / 924) and slower
+    // at M = 128 (126 / 95), where one token tile leaves half the CUs idle.
+    // 171 (80 x 128) is a tuning id only.
+    if (mmq_dma_env() != 0 && x.pk == w.pk && w.pn % 8 == 0) {
+      consider(170, x.m > 128 ? 0.0 : 1e30);
+      consider(171, 1e30);
+    }
     if (split_env && segs > 1) {
       consider(82, rounds(80, segs) * seg * 4 * 1.07 + c_sum);
       consider(162, rounds(160, segs) * seg * 4 * kQ6Step160 + c_sum);
       if (segs % 2 == 0)  // runs of two segments
         consider(163, rounds(160, segs / 2) * 2 * seg * 4 * kQ6Step160 + c_sum);
+    }
+    if (pick == 170 || pick == 171) {  // direct-copy 160 x 128 / 80 x 128, one segment per block
+      const uint32_t cap = (x.m + 127) / 128 * 128;
+      uint32_t mc = 0;
+      for (uint32_t c = 128; c <= cap; c += 128)
+        if (q6_mmq_dma_scratch_bytes(c, w.n, w.pk) <= kScratchBytes) mc = c;
+      int dev = 0;
+      if (void* sc = mc ? scratch_acquire(s, q6_mmq_dma_scratch_bytes(mc, w.n, w.pk), &dev) : nullptr) {
+        const hipError_t e = launch_q6_mmq_dma(w, x, out, residual, s, sc, pick == 170 ? 10 : 5, mc, q6_seg_reduce);
+        scratch_release(dev, s, e == hipSuccess);
+        return e;
+      }
     }
     if (pick == 160) return launch_cfg<Layout, 2, 4, 5, 2>(w, x, out, residual, s, 0, pn);  // 160 x 128
     if (pick == 82 || pick == 162 || pick == 163) {

@@ -123,7 +123,8 @@ __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restr
                                                            const float* __restrict__ xa,
                                                            const int32_t* __restrict__ xs, uint32_t m,
                                                            uint32_t pk, uint8_t* __restrict__ bq,
-                                                           uint8_t* __restrict__ tq, float* __restrict__ ti) {
+                                                           uint8_t* __restrict__ tq, float* __restrict__ ti,
+                                                           bool unit_scale) {
   const uint32_t groups = pk / 32, kbs = pk / 256, steps = kbs * 4;
   const uint32_t t0 = blockIdx.x * 64, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
   if (blockIdx.y < kbs) {
@@ -156,7 +157,8 @@ __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restr
     }
     return;
   }
-  // token data: ts = 2^e by mmq_kernel's rule (max_g |a| 2^12 ts in [2^13, 2^14))
+  // token data: ts = 2^e by mmq_kernel's rule (max_g |a| 2^12 ts in [2^13, 2^14));
+  // unit_scale (the Q6_K form, which has no min term): ts = 1, a' = a
   {
     const uint32_t t = t0 + (blockIdx.y - kbs) * 4 + w, tb = t / kPB, tl = t % kPB;
     const bool real = t < m;
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restr
 #pragma unroll
     for (int sh = 32; sh >= 1; sh /= 2) mx = fmaxf(mx, __shfl_xor(mx, sh));
     const int ex = int(__float_as_uint(mx) >> 23);
-    const int se = min(max(255 - ex, 1), 253);
+    const int se = unit_scale ? 127 : min(max(255 - ex, 1), 253);  // Q6_K: ts = 1
     const float ts = __uint_as_float(uint32_t(se) << 23);
     if (lane == 0) ti[t] = real ? __uint_as_float(uint32_t(254 - se) << 23) : 1.f;
     for (uint32_t g = lane; g < groups; g += 64) {
@@ -615,6 +617,279 @@ __global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
   }
 }
 
+// ---- Q6_K (0x0241) direct-copy MMQ ----
+// mmq_kernel's Q6_K arithmetic per (row, token), operation for operation:
+// P = sum over the K32 group of sc (q - 32) z, exact (A split into FP16
+// hi + lo, two chained 16x16x32 MFMAs, every partial sum an integer below
+// 2^24), X = a P0 then X = fma(a, P, X) over the super-block's groups,
+// acc = fma(d, X, acc), the fixed K segments of q6_seg_kb (a segment's sum
+// starts from zero; the caller adds the sums in ascending order), and out =
+// acc (+ residual). Each block runs one segment of one tile, so the outputs
+// are bitwise equal to mmq_kernel's Q6_K tiles, split or not.
+//
+// NW waves of 16 rows x 128 tokens (160 x 128 for NW = 10, 80 x 128 for 5).
+// Each wave dequantizes its own A fragments from the raw code planes: the
+// 0x0241 tile of 8 rows stores a K step's two groups contiguously (256 B of
+// low nibbles, 128 B of high pairs), so a wave's codes of one step are one
+// 768 B copy. The step ring holds B (16 KB) and the NW waves' codes; a
+// super-block slot holds the waves' scales and d and the tokens' a (fp32).
+template <int NW>
+struct Geo6 {
+  static constexpr uint32_t BR = 16 * NW, BT = 128;
+  static constexpr uint32_t BSL = BT * 128, AW = 768, SSL = BSL + NW * AW;  // one K step
+  static constexpr uint32_t MW = 288, TSL = 8 * BT * 4, MTS = NW * MW + TSL;  // one super-block
+  static constexpr uint32_t OffM = 4 * SSL, Lds = OffM + 2 * MTS;
+};
+
+template <class F>
+__device__ __attribute__((always_inline)) inline void q6_regions(uint8_t* __restrict__ b0, uint8_t* __restrict__ b1,
+                                                                   uint8_t* __restrict__ b2, uint8_t* __restrict__ b3,
+                                                                   uint8_t* __restrict__ mt0,
+                                                                   uint8_t* __restrict__ mt1, F&& f) {
+  f(b0, b1, b2, b3, mt0, mt1);
+}
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void q6_mmq_dma_kernel(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n, uint32_t pn,
+    uint32_t kbs, const uint8_t* __restrict__ bq, const uint8_t* __restrict__ tq, uint32_t m,
+    float* __restrict__ out, const float* __restrict__ residual, uint32_t row_blocks, uint32_t tok_blocks,
+    uint32_t seg_kb, uint32_t segs, float* __restrict__ part) {
+  using G = Geo6<NW>;
+  constexpr uint32_t BT = G::BT, NJ = 8;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const uint32_t tiles_n = row_blocks * tok_blocks;
+  // segs > 1: block b runs segment b / tiles_n and writes its sum to part
+  const uint32_t sgm = blockIdx.x / tiles_n, bx = blockIdx.x % tiles_n;
+  const uint32_t tile = (tiles_n % 8 == 0) ? (bx % 8) * (tiles_n / 8) + bx / 8 : bx;
+  const uint32_t rb = tile / tok_blocks, tb = tile % tok_blocks;
+  const uint32_t kb_lo = sgm * seg_kb, kb_hi = min(kbs, kb_lo + seg_kb);
+  if (segs > 1) {
+    out = part + size_t(sgm) * m * n;
+    residual = nullptr;
+  }
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wrow0 = rb * G::BR + wave * 16;
+  const uint32_t lr = lane & 15u, lk = lane >> 4;
+  const uint32_t steps = kbs * 4, last8 = pn / 8 - 1;
+  const uint64_t trows = uint64_t(pn) * kbs;  // tile rows: d follows the 16-byte scale rows
+
+  // ---- copy issue ----
+  // Super-block: lanes 0..15 the scale rows of the wave's two 8-row tiles,
+  // lanes 16, 17 their d (8 x fp16 each); waves 0..3 also 1 KB each of the
+  // tokens' a [8 groups][128 tokens] (pre-pass block tb, super-block kb).
+  auto issue_super = [&](uint32_t kb_in, uint8_t* MT) __attribute__((always_inline)) {
+    const uint32_t kb = min(kb_in, kbs - 1);
+    if (lane < 18) {
+      const uint32_t t = lane < 16 ? lane >> 3 : lane - 16;
+      const uint64_t tr = (uint64_t(min(wrow0 / 8 + t, last8)) * kbs + kb) * 8;
+      const uint8_t* src = lane < 16 ? meta + (tr + (lane & 7u)) * 16 : meta + trows * 16 + tr * 2;
+      dma16(src, MT + wave * G::MW);
+    }
+    if (wave < 4) dma16(tq + (uint64_t(tb) * kbs + kb) * kTSlot + wave * 1024 + lane * 16, MT + NW * G::MW + wave * 1024);
+  };
+  // K step s: the wave's codes (lanes 0..31 low nibbles of tiles 0, 1 -- the
+  // second tile's 16-byte chunks in the order p ^ 1, so the two tiles'
+  // fragment reads use different banks -- lanes 32..47 the high pairs) and B
+  // units k = wave, wave + NW, ... of 1 KB (the pre-pass block's K step is
+  // one contiguous 16 KB run: [8 chunks][128 tokens][16 B]).
+  auto issue_step = [&](uint32_t s_in, uint8_t* SL) __attribute__((always_inline)) {
+    const uint32_t s = min(s_in, steps - 1), kb = s / 4, q = s % 4;
+    if (lane < 48) {
+      const uint32_t t = lane < 32 ? lane >> 4 : (lane - 32) >> 3;
+      const uint8_t* base = codes + (uint64_t(min(wrow0 / 8 + t, last8)) * kbs + kb) * kQ6TileBytes;
+      const uint8_t* src = lane < 32 ? base + q * 256 + (((lane & 15u) ^ t) * 16)
+                                     : base + kQ6HiPlane + q * 128 + ((lane - 32) & 7u) * 16;
+      dma16(src, SL + G::BSL + wave * G::AW);
+    }
+    const uint8_t* row = bq + (uint64_t(tb) * steps + s) * G::BSL;
+#pragma unroll
+    for (uint32_t k0 = 0; k0 < 16; k0 += NW) {
+      const uint32_t k = k0 + wave;
+      if (k < 16) dma16(row + k * 1024 + lane * 16, SL + k * 1024);
+    }
+  };
+
+  float acc[NJ][4], X[NJ][4];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[j][v] = 0.f;
+  uint32_t S[4];  // this lane's row: the super-block's 16 scale bytes, each + 128 (xor 0x80)
+  // perm selectors of the lane's scale byte 2 gsel + lk / 2 of a step's dword
+  const uint32_t sb0 = lk >> 1, sb1 = 2u + (lk >> 1);
+  const uint32_t ssel0 = 0x04000400u | (sb0 << 16) | sb0, ssel1 = 0x04000400u | (sb1 << 16) | sb1;
+  const uint32_t hsh = (lk & 1u) * 4;  // the lane's 2-bit fields within its high-pair bytes
+
+  auto compute = [&](auto qc, const uint8_t* SL, const uint8_t* MT) __attribute__((always_inline)) {
+    constexpr uint32_t q = decltype(qc)::value;
+    const uint8_t* Bs = SL;
+    const uint8_t* As = SL + G::BSL + wave * G::AW;
+    const uint8_t* Ts = MT + NW * G::MW;
+    if constexpr (q == 0) {
+      const uint4 sw = lds_read16_sync(MT + wave * G::MW + (lr >> 3) * 128 + (lr & 7u) * 16);
+      S[0] = sw.x ^ 0x80808080u;
+      S[1] = sw.y ^ 0x80808080u;
+      S[2] = sw.z ^ 0x80808080u;
+      S[3] = sw.w ^ 0x80808080u;
+    }
+    // A fragments (hi, lo) of group g = 2 q + gsel: codes 8 lk .. 8 lk + 7 of
+    // row lr in slot order {0, 2, 4, 6, 1, 3, 5, 7}
+    const uint32_t t = lr >> 3, r = lr & 7u;
+    uint32_t nib[2], hp[2];
+#pragma unroll
+    for (uint32_t gsel = 0; gsel < 2; ++gsel) {
+      nib[gsel] = *reinterpret_cast<const uint32_t*>(As + t * 256 + (((2 * r + gsel) ^ t) * 16) + lk * 4);
+      hp[gsel] = *reinterpret_cast<const uint32_t*>(As + 512 + t * 128 + (2 * r + gsel) * 8 + (lk >> 1) * 4);
+    }
+    auto dequant = [&](uint32_t gsel, half8& hi, half8& lo) __attribute__((always_inline)) {
+      const uint32_t w = nib[gsel], xs = hp[gsel] >> hsh;
+      const uint32_t q0 = (w & 0x0f0f0f0fu) | ((xs & 0x03030303u) << 4);         // codes 8 lk + 0..3
+      const uint32_t q1 = ((w >> 4) & 0x0f0f0f0fu) | ((xs & 0x0c0c0c0cu) << 2);  // codes 8 lk + 4..7
+      const h2 s2 = as_h2(perm(0x64646464u, S[q], gsel ? ssel1 : ssel0)) - h2{_Float16(1152.f), _Float16(1152.f)};
+      const h2 k = {_Float16(1056.f), _Float16(1056.f)};  // 1024 + q -> q - 32, exact
+      const h2 c0 = as_h2(perm(0x64646464u, q0, 0x04020400u)) - k;  // codes 0, 2
+      const h2 c1 = as_h2(perm(0x64646464u, q1, 0x04020400u)) - k;  // 4, 6
+      const h2 c2 = as_h2(perm(0x64646464u, q0, 0x04030401u)) - k;  // 1, 3
+      const h2 c3 = as_h2(perm(0x64646464u, q1, 0x04030401u)) - k;  // 5, 7
+      const h2 h0 = c0 * s2, h1 = c1 * s2, h2_ = c2 * s2, h3 = c3 * s2;  // RN(sc (q - 32))
+      const h2 l0 = __builtin_elementwise_fma(c0, s2, -h0), l1 = __builtin_elementwise_fma(c1, s2, -h1);
+      const h2 l2 = __builtin_elementwise_fma(c2, s2, -h2_), l3 = __builtin_elementwise_fma(c3, s2, -h3);
+      hi = half8{h0.x, h0.y, h1.x, h1.y, h2_.x, h2_.y, h3.x, h3.y};
+      lo = half8{l0.x, l0.y, l1.x, l1.y, l2.x, l2.y, l3.x, l3.y};
+    };
+    constexpr int kPF = 2;
+    auto bfrag = [&](int u) __attribute__((always_inline)) {
+      return *reinterpret_cast<const half8*>(Bs + (((u / NJ) * 4 + lk) * BT + (u % NJ) * 16 + lr) * 16);
+    };
+    auto afac = [&](int u) __attribute__((always_inline)) {
+      return *reinterpret_cast<const float*>(Ts + ((2 * q + u / NJ) * BT + (u % NJ) * 16 + lr) * 4);
+    };
+    half8 bq_[kPF + 1];
+    float aq_[kPF + 1];
+#pragma unroll
+    for (int u = 0; u < kPF; ++u) {
+      bq_[u] = bfrag(u);
+      aq_[u] = afac(u);
+    }
+    half8 ah[2], al[2];
+    dequant(0, ah[0], al[0]);
+    f4 Pp;
+    float ap = 0.f;
+#pragma unroll
+    for (int u = 0; u <= int(2 * NJ); ++u) {
+      f4 Pc;
+      float ac = 0.f;
+      if (u < int(2 * NJ)) {
+        if (u + kPF < int(2 * NJ)) {
+          bq_[(u + kPF) % (kPF + 1)] = bfrag(u + kPF);
+          aq_[(u + kPF) % (kPF + 1)] = afac(u + kPF);
+        }
+        if (u == int(NJ) - 2) dequant(1, ah[1], al[1]);  // the second group's fragments
+        const half8 bf = bq_[u % (kPF + 1)];
+        ac = aq_[u % (kPF + 1)];
+        Pc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u / NJ], bf, f4{0, 0, 0, 0}, 0, 0, 0);
+        Pc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[u / NJ], bf, Pc, 0, 0, 0);
+      }
+      if (u > 0) {
+        const int pu = u - 1, pj = pu % NJ;
+        const bool first = q == 0 && pu < int(NJ);  // the super-block's first group
+#pragma unroll
+        for (int v = 0; v < 4; ++v) X[pj][v] = first ? ap * Pp[v] : fmaf(ap, Pp[v], X[pj][v]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      Pp = Pc;
+      ap = ac;
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(X[j][v]));
+    if constexpr (q == 3) {  // ---- end of super-block: acc += d X ----
+      uint2 dw;
+      {
+        const uint32_t a0 = lds_addr(MT + wave * G::MW + 256 + lk * 8);
+        asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(dw) : "v"(a0) : "memory");
+      }
+      const float d[4] = {f16_to_f32(dw.x & 0xffffu), f16_to_f32(dw.x >> 16), f16_to_f32(dw.y & 0xffffu),
+                          f16_to_f32(dw.y >> 16)};
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[j][v] = fmaf(d[v], X[j][v], acc[j][v]);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) asm volatile("" : "+v"(acc[j][v]));
+    }
+  };
+
+  using C0 = std::integral_constant<uint32_t, 0>;
+  using C1 = std::integral_constant<uint32_t, 1>;
+  using C2 = std::integral_constant<uint32_t, 2>;
+  using C3 = std::integral_constant<uint32_t, 3>;
+  // The ring discipline of mmq_dma_kernel: steps in pairs, one barrier per
+  // pair after each wave's copies have landed, the next pair's steps (and at
+  // q = 0 the next super-block) issued into the slots the barrier retired.
+  // Super-block slots alternate from kb_lo; an odd range ends with one
+  // super-block in slot 0.
+  auto body = [&](uint8_t* B0, uint8_t* B1, uint8_t* B2, uint8_t* B3, uint8_t* MT0, uint8_t* MT1)
+                 __attribute__((always_inline)) {
+    uint8_t* const Ssl[4] = {B0, B1, B2, B3};
+    uint8_t* const Msl[2] = {MT0, MT1};
+    auto step = [&](auto qc, auto sbc, uint32_t kb) __attribute__((always_inline)) {
+      constexpr uint32_t q = decltype(qc)::value, SB = decltype(sbc)::value;
+      if constexpr (q % 2 == 0) {
+        wait_barrier<0>();
+        if constexpr (q == 0) issue_super(kb + 1, Msl[SB ^ 1u]);
+        issue_step(4 * kb + q + 2, Ssl[(q + 2) & 3u]);
+        issue_step(4 * kb + q + 3, Ssl[(q + 3) & 3u]);
+      }
+      compute(qc, Ssl[q], Msl[SB]);
+    };
+    auto super_block = [&](uint32_t kb, auto sbc) __attribute__((always_inline)) {
+      step(C0{}, sbc, kb);
+      step(C1{}, sbc, kb);
+      step(C2{}, sbc, kb);
+      step(C3{}, sbc, kb);
+    };
+    issue_super(kb_lo, MT0);
+    issue_step(4 * kb_lo, B0);
+    issue_step(4 * kb_lo + 1, B1);
+    uint32_t kb = kb_lo;
+    for (; kb + 1 < kb_hi; kb += 2) {
+      super_block(kb, C0{});
+      super_block(kb + 1, C1{});
+    }
+    if (kb < kb_hi) super_block(kb, C0{});
+  };
+  q6_regions(lds, lds + G::SSL, lds + 2 * G::SSL, lds + 3 * G::SSL, lds + G::OffM, lds + G::OffM + G::MTS, body);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy outlives the block
+
+  // ---- store: lane holds rows 4 lk .. 4 lk + 3 of token lr in each tile ----
+  const bool vec = (n % 4 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const uint32_t tok = tb * BT + j * 16 + lr, r4 = wrow0 + lk * 4;
+    if (tok >= m || r4 >= n) continue;
+    const size_t o = size_t(tok) * n + r4;
+    if (vec) {
+      float4 y = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+      if (residual) {
+        const float4 rv = *reinterpret_cast<const float4*>(residual + o);
+        y.x += rv.x; y.y += rv.y; y.z += rv.z; y.w += rv.w;
+      }
+      *reinterpret_cast<float4*>(out + o) = y;
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (r4 + v < n) out[o + v] = acc[j][v] + (residual ? residual[o + v] : 0.f);
+    }
+  }
+}
+
 }  // namespace
 
 // Scratch bytes the pre-pass needs for m tokens of padded width pk.
@@ -671,13 +946,64 @@ hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, cons
   uint8_t* tq = bq + uint64_t(mp) * w.pk * 2;
   float* ti = reinterpret_cast<float*>(tq + uint64_t(mp / kPB) * (w.pk / 256) * kTSlot);
   hipLaunchKernelGGL(mmq_dma_prep_kernel, dim3(mp / 64, w.pk / 256 + 16), dim3(256), 0, s, x.codes, x.scales,
-                     x.sums, x.m, x.pk, bq, tq, ti);
+                     x.sums, x.m, x.pk, bq, tq, ti, false);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const GluDma g{glu ? up->codes : nullptr, glu ? up->scales : nullptr, qc, qa, qs, failure};
   if (rows > 0) e = launch_dma_tiles<8, 8>(w, x, out, residual, s, 0, rows, bq, tq, ti, up, g);
   if (e == hipSuccess && tail_end > rows)
     e = launch_dma_tiles<4, 2>(w, x, out, residual, s, rows, tail_end - rows, bq, tq, ti, up, g);
+  return e;
+}
+
+}  // namespace qw38hip
+
+namespace qw38hip {
+
+// Q6_K 0x0241 on the direct-copy tiles, NW = 10 (160 x 128) or 5 (80 x 128):
+// one block per (tile, fixed K segment). With several segments the tokens run
+// in chunks of mc (a multiple of 128): the chunk's pre-pass and segment sums
+// (one mc x n array per segment) share the scratch, and reduce(part, segs,
+// mc, residual, out) adds them in ascending order (+ residual). scratch holds
+// q6_mmq_dma_scratch_bytes(mc, n, pk).
+uint64_t q6_mmq_dma_scratch_bytes(uint32_t mc, uint32_t n, uint32_t pk) {
+  const uint32_t kbs = pk / 256, seg_kb = q6_seg_kb(kbs), segs = (kbs + seg_kb - 1) / seg_kb;
+  const uint64_t prep = (mmq_dma_scratch_bytes(mc, pk) + 255) / 256 * 256;
+  return prep + (segs > 1 ? uint64_t(segs) * mc * n * 4 : 0);
+}
+
+hipError_t launch_q6_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
+                             hipStream_t s, void* scratch, int nw, uint32_t mc, Q6SegReduce reduce) {
+  const uint32_t kbs = w.pk / 256, seg_kb = q6_seg_kb(kbs), segs = (kbs + seg_kb - 1) / seg_kb;
+  if (w.layout != QW38_LAYOUT_Q6K_WAVE64 || x.pk != w.pk || w.pn % 8 != 0 || (nw != 10 && nw != 5) ||
+      mc == 0 || mc % kPB != 0 || x.m == 0 ||
+      ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
+        reinterpret_cast<uintptr_t>(x.codes)) % 16) != 0 ||
+      (segs > 1 && !reduce))
+    return hipErrorInvalidValue;
+  const uint32_t groups = x.pk / 32;
+  uint8_t* bq = static_cast<uint8_t*>(scratch);
+  float* part = reinterpret_cast<float*>(bq + (mmq_dma_scratch_bytes(mc, w.pk) + 255) / 256 * 256);
+  auto kern = nw == 10 ? q6_mmq_dma_kernel<10> : q6_mmq_dma_kernel<5>;
+  const uint32_t br = nw == 10 ? Geo6<10>::BR : Geo6<5>::BR;
+  const uint32_t lds_bytes = nw == 10 ? Geo6<10>::Lds : Geo6<5>::Lds;
+  hipError_t e = set_max_lds(reinterpret_cast<const void*>(kern), int(lds_bytes));
+  for (uint32_t t0 = 0; e == hipSuccess && t0 < x.m; t0 += mc) {
+    const uint32_t m = std::min(mc, x.m - t0), mp = (m + kPB - 1) / kPB * kPB;
+    uint8_t* tq = bq + uint64_t(mp) * w.pk * 2;
+    float* ti = reinterpret_cast<float*>(tq + uint64_t(mp / kPB) * kbs * kTSlot);
+    hipLaunchKernelGGL(mmq_dma_prep_kernel, dim3(mp / 64, kbs + 16), dim3(256), 0, s, x.codes + size_t(t0) * x.pk,
+                       x.scales + size_t(t0) * groups, x.sums + size_t(t0) * groups, m, x.pk, bq, tq, ti, true);
+    e = hipGetLastError();
+    if (e != hipSuccess) break;
+    float* o = out + size_t(t0) * w.n;
+    const float* res = residual ? residual + size_t(t0) * w.n : nullptr;
+    const uint32_t row_blocks = (w.pn + br - 1) / br, tok_blocks = mp / kPB;
+    hipLaunchKernelGGL(kern, dim3(row_blocks * tok_blocks * segs), dim3(nw * 64), lds_bytes, s, w.codes, w.scales,
+                       w.n, w.pn, kbs, bq, tq, m, o, res, row_blocks, tok_blocks, seg_kb, segs, part);
+    e = hipGetLastError();
+    if (e == hipSuccess && segs > 1) e = reduce(part, segs, m, w.n, res, o, s);
+  }
   return e;
 }
 

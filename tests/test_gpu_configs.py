@@ -148,6 +148,39 @@ def test_q6k_split_k_rows_independent_of_m(torch_gpu):
             _check(yn, ref, "Q6_K split-K M=40")
 
 
+@pytest.mark.parametrize("n", [5120, 776])
+def test_q6k_mmq_direct_copy_matches_tiles(torch_gpu, n):
+    """Q6_K MMQ for M > 128 runs the direct-copy 160 x 128 tile
+    (q4k_mmq_dma.hip: one fixed K segment per block, tokens in chunks of at
+    most what the scratch holds, here 512 + 188 at M = 700). Its rows, with a
+    residual, must equal bitwise the rows of mmq_kernel's split tiles (M = 96
+    calls on token windows of the first and the second chunk) plus the same
+    residual. n = 776: a partial last row tile (776 = 4 x 160 + 136)."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    k = 17408
+    w, _ = _fit_q6k(torch, ops, n, k, 341)
+    m = 700 if n == 5120 else 130
+    q, _ = _q8(torch, ops, silu_rows(m, k, 342))
+    res = torch.from_numpy(normal((m, n), 343)).cuda()
+    y = torch.full((m, n), float("nan"), device="cuda")
+    torch.cuda.synchronize()
+    before = ops.scratch_stats()
+    print(f"Q6_K direct-copy n={n} M={m}", flush=True)
+    ops.q4k_q8_project(w, q, y, residual=res)
+    torch.cuda.synchronize()
+    after = ops.scratch_stats()
+    assert after[0] == before[0] + 1 and after[1:] == before[1:], f"scratch not granted ({before} -> {after})"
+    yn, rn = y.cpu().numpy(), res.cpu().numpy()
+    for t0 in ((0, 560) if m == 700 else (0, 34)):
+        print(f"Q6_K split tiles n={n} tokens {t0}..{t0 + 95}", flush=True)
+        qm = ops.Q8Input.empty(96, k)
+        qm.codes.copy_(q.codes[t0:t0 + 96]); qm.scales.copy_(q.scales[t0:t0 + 96]); qm.sums.copy_(q.sums[t0:t0 + 96])
+        ym = _project(torch, ops, w, qm, 96, n)
+        want = (ym + rn[t0:t0 + 96]).astype(np.float32)
+        assert np.array_equal(yn[t0:t0 + 96].view(np.uint32), want.view(np.uint32)), f"tokens {t0}.. differ"
+
+
 _OWN_SCRIPT = r"""
 import sys, numpy as np, torch
 sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
