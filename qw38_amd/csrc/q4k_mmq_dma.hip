@@ -118,7 +118,7 @@ __device__ __forceinline__ uint4 lds_read16_sync(const uint8_t* p) {
 // Block (x, y) covers tokens 64 x .. 64 x + 63. y < kbs: the codes of
 // super-block y, transposed through LDS (row reads of 256 B per token, then
 // each wave store one contiguous 1 KB run: 64 tokens x 16 B of one chunk).
-// y = kbs .. kbs + 15: the token data, one wave per token.
+// y = kbs .. kbs + 15: the token data.
 __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restrict__ xc,
                                                            const float* __restrict__ xa,
                                                            const int32_t* __restrict__ xs, uint32_t m,
@@ -158,35 +158,55 @@ __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restr
     return;
   }
   // token data: ts = 2^e by mmq_kernel's rule (max_g |a| 2^12 ts in [2^13, 2^14));
-  // unit_scale (the Q6_K form, which has no min term): ts = 1, a' = a
+  // unit_scale (the Q6_K form, which has no min term): ts = 1, a' = a.
+  // Block y = kbs + j: the block's 64 tokens' scale exponents first (four
+  // threads per token), then wave w writes super-blocks kb = 4 j + w,
+  // 4 j + w + 64, ..., lane = token: a' coalesced per group, the 32-byte
+  // min-term operands as two 16-byte stores.
   {
-    const uint32_t t = t0 + (blockIdx.y - kbs) * 4 + w, tb = t / kPB, tl = t % kPB;
+    __shared__ int se_s[64];
+    const uint32_t j = blockIdx.y - kbs;
+    {
+      const uint32_t tl = tid >> 2, part = tid & 3u, t = t0 + tl;
+      float mx = 0.f;
+      if (!unit_scale && t < m)
+        for (uint32_t g = part; g < groups; g += 4) mx = fmaxf(mx, fabsf(xa[size_t(t) * groups + g]));
+      mx = fmaxf(mx, __shfl_xor(mx, 1));
+      mx = fmaxf(mx, __shfl_xor(mx, 2));
+      const int ex = int(__float_as_uint(mx) >> 23);  // 0 for zero/subnormal, 255 for NaN/inf
+      if (part == 0) se_s[tl] = unit_scale ? 127 : min(max(255 - ex, 1), 253);
+    }
+    __syncthreads();
+    const uint32_t t = t0 + lane, tb = t / kPB, tl = t % kPB;
     const bool real = t < m;
-    float mx = 0.f;
-    if (real)
-      for (uint32_t g = lane; g < groups; g += 64) mx = fmaxf(mx, fabsf(xa[size_t(t) * groups + g]));
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh /= 2) mx = fmaxf(mx, __shfl_xor(mx, sh));
-    const int ex = int(__float_as_uint(mx) >> 23);
-    const int se = unit_scale ? 127 : min(max(255 - ex, 1), 253);  // Q6_K: ts = 1
+    const int se = se_s[lane];
     const float ts = __uint_as_float(uint32_t(se) << 23);
-    if (lane == 0) ti[t] = real ? __uint_as_float(uint32_t(254 - se) << 23) : 1.f;
-    for (uint32_t g = lane; g < groups; g += 64) {
-      uint8_t* base = tq + (size_t(tb) * kbs + g / 8) * kTSlot;
-      const uint32_t g8 = g % 8;
-      float a = 0.f;
-      _Float16 h = 0, l = 0;
-      if (real) {
-        a = xa[size_t(t) * groups + g] * ts;
-        const float v = a * float(xs[size_t(t) * groups + g]);
-        h = _Float16(v);
-        l = _Float16(v - float(h));
+    if (j == 0 && w == 0) ti[t] = real ? __uint_as_float(uint32_t(254 - se) << 23) : 1.f;
+    for (uint32_t kb = 4 * j + w; kb < kbs; kb += 64) {
+      uint8_t* base = tq + (size_t(tb) * kbs + kb) * kTSlot;
+      uint32_t hl[8];  // per token: hi of groups 0-3, lo of 0-3, hi of 4-7, lo of 4-7 (FP16)
+#pragma unroll
+      for (uint32_t g8 = 0; g8 < 8; g8 += 2) {
+        float a[2] = {0.f, 0.f};
+        _Float16 h[2] = {0, 0}, l[2] = {0, 0};
+#pragma unroll
+        for (uint32_t e = 0; e < 2; ++e) {
+          if (real) {
+            const size_t gi = size_t(t) * groups + kb * 8 + g8 + e;
+            a[e] = xa[gi] * ts;
+            const float v = a[e] * float(xs[gi]);
+            h[e] = _Float16(v);
+            l[e] = _Float16(v - float(h[e]));
+          }
+          reinterpret_cast<float*>(base)[(g8 + e) * kPB + tl] = a[e];
+        }
+        const uint32_t q = (g8 / 4) * 2, r = (g8 % 4) / 2;  // dword of the hi pair; the lo pair is 2 dwords on
+        hl[q * 2 + r] = as_u32(h2{h[0], h[1]});
+        hl[q * 2 + r + 2] = as_u32(h2{l[0], l[1]});
       }
-      *reinterpret_cast<float*>(base + (g8 * kPB + tl) * 4) = a;
-      // per token: hi of groups 0-3, lo of 0-3, hi of 4-7, lo of 4-7
-      const uint32_t hpos = (g8 / 4) * 16 + (g8 % 4) * 2;
-      *reinterpret_cast<_Float16*>(base + kTokU + tl * 32 + hpos) = h;
-      *reinterpret_cast<_Float16*>(base + kTokU + tl * 32 + hpos + 8) = l;
+      uint4* dst = reinterpret_cast<uint4*>(base + kTokU + tl * 32);
+      dst[0] = make_uint4(hl[0], hl[1], hl[2], hl[3]);
+      dst[1] = make_uint4(hl[4], hl[5], hl[6], hl[7]);
     }
   }
 }
