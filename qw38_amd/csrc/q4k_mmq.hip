@@ -37,7 +37,7 @@ uint64_t mmq_dma_scratch_bytes(uint32_t m, uint32_t pk);
 hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
                           hipStream_t s, uint32_t rows, uint32_t tail_end, void* scratch, const WeightView* up = nullptr,
                           int8_t* qc = nullptr, float* qa = nullptr, int32_t* qs = nullptr,
-                          int* failure = nullptr);
+                          int* failure = nullptr, int tail_nj = 2);
 namespace {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -944,6 +944,11 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   const bool dma32 = Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2 && mmq_dma_env() == 1 && x.pk == w.pk &&
                       (w.pk / 256) % 2 == 0;
   const double c32 = q6 ? two(per_cu(128, 32), 1.0, 2.0) : two(per_cu(128, 32), 0.70, 0.89) * (dma32 ? 0.86 : 1.0);
+  // 128 x 16 direct-copy tiles (the same kernel with one 16-token tile per
+  // wave): a block step takes about 0.8 of the 128 x 32 direct-copy one
+  // (5120 rows at M = 16: 41 against 50 us; 34816 rows at M = 16: 57 / 73,
+  // M = 40: 94 / 106); no half-empty token tiles at M <= 16.
+  const double c16 = dma32 ? two(per_cu(128, 16), 0.70, 0.89) * 0.86 * 0.8 : 1e30;
   // 80 x 128 on eight waves (one block per CU, two waves per SIMD; the
   // four-wave 80 x 128 tile, QW38_MMQ_TILE=80, is always slower): 5120-row
   // weights make 64 row blocks, so a 512-token chunk fills 256 CUs in one
@@ -961,6 +966,7 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   const double c192 = (q6 || Glu) ? 1e30 : per_cu(192, 128) * 1.82;
   int bt = 32;
   double best = c32;
+  if (c16 < best) bt = 35, best = c16;
   if (x.m > 32 && c64 < best) bt = 64, best = c64;
   if (x.m > 64 && c_big < best) bt = 256, best = c_big;
   if (x.m > 64 && c81 < best) bt = 81, best = c81;
@@ -1058,7 +1064,7 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   // library scratch holds its pre-pass: rows [0, big) on the big tile, [big,
   // end) on the small one. hipErrorNotReady when it does not apply.
   const int dma_env = mmq_dma_env();
-  auto try_dma = [&](uint32_t big, uint32_t tail_end) -> hipError_t {
+  auto try_dma = [&](uint32_t big, uint32_t tail_end, int tail_nj = 2) -> hipError_t {
     if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2) {
       const bool aligned = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
                              reinterpret_cast<uintptr_t>(x.codes) | reinterpret_cast<uintptr_t>(glu.codes2) |
@@ -1073,9 +1079,10 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
       if constexpr (Glu) {
         const WeightView up{glu.codes2, glu.meta2, w.layout, w.n, w.k, w.pn, w.pk};
         e = launch_mmq_dma(w, x, nullptr, nullptr, s, big, tail_end, sc, &up, glu.qc, glu.qa, glu.qs,
-                           glu.failure);
+                           glu.failure, tail_nj);
       } else {
-        e = launch_mmq_dma(w, x, out, residual, s, big, tail_end, sc);
+        e = launch_mmq_dma(w, x, out, residual, s, big, tail_end, sc, nullptr, nullptr, nullptr, nullptr, nullptr,
+                           tail_nj);
       }
       scratch_release(dev, s, e == hipSuccess);
       return e;
@@ -1083,8 +1090,8 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
     return hipErrorNotReady;
   };
   if (bt == 32 && !forced && dma32) bt = 34;
-  if (bt == 34) {  // 128 x 32 direct-copy over all rows
-    const hipError_t e = try_dma(0, end);
+  if (bt == 34 || bt == 35) {  // 128 x 32 / 128 x 16 direct-copy over all rows
+    const hipError_t e = try_dma(0, end, bt == 35 ? 1 : 2);
     if (e != hipErrorNotReady) return e;
     bt = 32;
   }
@@ -1096,7 +1103,7 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
     if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 128
     if (forced) big_rows = pn;
     const uint32_t dma_end = dma_env == 2 ? big_rows / kv : end;
-    hipError_t e = try_dma(big_rows / kv, dma_end);
+    hipError_t e = try_dma(big_rows / kv, dma_end, dma_env == 3 ? 1 : 2);
     if (e == hipSuccess && dma_end == end) return e;
     if (e == hipErrorNotReady) e = launch_cfg<Layout, 4, 2, 4, 4, Glu>(w, x, out, residual, s, 0, big_rows / kv, glu);
     if (e != hipSuccess || big_rows == pn) return e;

@@ -290,14 +290,18 @@ __global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
   // kc = CPW w .. CPW w + CPW - 1 of the slot (lane l: position 64 kc + l =
   // chunk, token), gathered from the pre-pass block's chunk rows.
   auto issue_step = [&](uint32_t s_in, uint8_t* wB) __attribute__((always_inline)) {
-    constexpr uint32_t CPW = BT / 8 / NW;  // 1 KB copies per wave and step
-    static_assert(CPW >= 1, "B copy share");
+    constexpr uint32_t units = BT / 8, CPW = units / NW;  // 1 KB copies per step; per wave
     const uint32_t s = min(s_in, steps - 1);
     const uint8_t* row = bq + (uint64_t(pb) * steps + s) * 8 * (kPB * 16);
+    if constexpr (CPW >= 1) {
 #pragma unroll
-    for (uint32_t k = 0; k < CPW; ++k) {
-      const uint32_t pos = (CPW * wave + k) * 64 + lane, c = pos / BT, t = pos % BT;
-      dma16(row + c * (kPB * 16) + (toff + t) * 16, wB + (CPW * wave + k) * 1024);
+      for (uint32_t k = 0; k < CPW; ++k) {
+        const uint32_t pos = (CPW * wave + k) * 64 + lane, c = pos / BT, t = pos % BT;
+        dma16(row + c * (kPB * 16) + (toff + t) * 16, wB + (CPW * wave + k) * 1024);
+      }
+    } else if (wave < units) {  // fewer units than waves (16-token tiles)
+      const uint32_t pos = wave * 64 + lane, c = pos / BT, t = pos % BT;
+      dma16(row + c * (kPB * 16) + (toff + t) * 16, wB + wave * 1024);
     }
   };
 
@@ -448,12 +452,14 @@ __global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
               : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
               : "v"(a0)
               : "memory");
-        } else {
-          static_assert(NJ == 2, "token tiles per wave: 2 or a multiple of 4");
+        } else if constexpr (NJ == 2) {
           asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:512\n\ts_waitcnt lgkmcnt(0)"
                        : "=&v"(r[0]), "=&v"(r[1])
                        : "v"(a0)
                        : "memory");
+        } else {
+          static_assert(NJ == 1, "token tiles per wave: 1, 2 or a multiple of 4");
+          asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(r[0]) : "v"(a0) : "memory");
         }
 #pragma unroll
         for (int jj = 0; jj < (NJ < 4 ? NJ : 4); ++jj) {
@@ -941,7 +947,7 @@ hipError_t launch_dma_tiles(const WeightView& w, const Q8View& x, float* out, co
 }  // namespace
 
 // Output rows [0, rows) on 256 x 128 tiles and [rows, tail_end) on 128 x 32
-// tiles (tail_end = rows: none) of a Q4_K 0x020D weight for all m tokens,
+// tiles (tail_nj = 2) or 128 x 16 tiles (tail_nj = 1; tail_end = rows: none) of a Q4_K 0x020D weight for all m tokens,
 // after one activation pre-pass; rows a multiple of the big tile height (in
 // features for the fused form), tail_end a multiple of the small one or the
 // whole weight. scratch holds mmq_dma_scratch_bytes(m, pk). Codes and
@@ -950,7 +956,7 @@ hipError_t launch_dma_tiles(const WeightView& w, const Q8View& x, float* out, co
 // projection's Q8 operand.
 hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
                           hipStream_t s, uint32_t rows, uint32_t tail_end, void* scratch, const WeightView* up,
-                          int8_t* qc, float* qa, int32_t* qs, int* failure) {
+                          int8_t* qc, float* qa, int32_t* qs, int* failure, int tail_nj) {
   const bool glu = up != nullptr;
   if (w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2 || tail_end < rows || tail_end == 0 || x.pk != w.pk ||
       ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
@@ -972,7 +978,8 @@ hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, cons
   const GluDma g{glu ? up->codes : nullptr, glu ? up->scales : nullptr, qc, qa, qs, failure};
   if (rows > 0) e = launch_dma_tiles<8, 8>(w, x, out, residual, s, 0, rows, bq, tq, ti, up, g);
   if (e == hipSuccess && tail_end > rows)
-    e = launch_dma_tiles<4, 2>(w, x, out, residual, s, rows, tail_end - rows, bq, tq, ti, up, g);
+    e = tail_nj == 1 ? launch_dma_tiles<4, 1>(w, x, out, residual, s, rows, tail_end - rows, bq, tq, ti, up, g)
+                     : launch_dma_tiles<4, 2>(w, x, out, residual, s, rows, tail_end - rows, bq, tq, ti, up, g);
   return e;
 }
 
