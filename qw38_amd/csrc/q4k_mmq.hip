@@ -884,6 +884,44 @@ static int mmq_dma_env() {
   return v;
 }
 
+// Batched-decode passes for M = 9..24 (unfused projections): ceil(M / 8)
+// token slices of 4..8 tokens through launch_gemv. Its kernels at M 2..8
+// (Q4_K 0x020D) and 3..8 (Q6_K) compute each token's rows independently of
+// the call's other tokens, so every token gets that family's bits. The
+// estimate per pass is those kernels' time at M = 8 (about 8 us plus the
+// weight bytes at 4.5 TB/s: 5120 x 5120 11.7 us, 12288 x 5120 15, 34816 x
+// 5120 29, Q6_K 5120 x 17408 21 with its segment sum); the caller compares it
+// with its MMQ estimate. QW38_DECODE_PASSES=0 turns it off.
+static double decode_passes_us(const WeightView& w, const Q8View& x) {
+  static const int env = [] {
+    const char* e = std::getenv("QW38_DECODE_PASSES");
+    return e ? std::atoi(e) : 1;
+  }();
+  const bool q6 = w.layout == QW38_LAYOUT_Q6K_WAVE64;
+  if (!env || x.m < 9 || x.m > 24 || (!q6 && w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2)) return 1e30;
+  // the batched-decode kernels' alignment (other spans take other kernels)
+  if ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
+       reinterpret_cast<uintptr_t>(x.codes)) % 16)
+    return 1e30;
+  const double bytes = double(w.pn) * w.pk * (q6 ? 210.0 / 256 : 144.0 / 256);
+  return double((x.m + 7) / 8) * (8.0 + bytes / 4.5e6);
+}
+
+static hipError_t run_decode_passes(const WeightView& w, const Q8View& x, float* out, const float* residual,
+                                    hipStream_t s) {
+  const uint32_t p = (x.m + 7) / 8, base = x.m / p, extra = x.m % p, groups = x.pk / 32;
+  uint32_t t0 = 0;
+  for (uint32_t i = 0; i < p; ++i) {
+    const uint32_t mi = base + (i < extra ? 1u : 0u);
+    const Q8View xi{x.codes + size_t(t0) * x.pk, x.scales + size_t(t0) * groups, x.sums + size_t(t0) * groups,
+                    mi, x.k, x.pk};
+    const hipError_t e = launch_gemv(w, xi, out + size_t(t0) * w.n, residual ? residual + size_t(t0) * w.n : nullptr, s);
+    if (e != hipSuccess) return e;
+    t0 += mi;
+  }
+  return hipSuccess;
+}
+
 template <uint16_t Layout, bool Glu = false>
 hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const float* residual,
                         hipStream_t s, GluOut glu = {}) {
@@ -973,6 +1011,9 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   if (x.m > 64 && c129 < best) bt = 129, best = c129;
   if (x.m > 64 && c192 < best) bt = 192, best = c192;
   if (forced) bt = forced;
+  if constexpr (!q6 && !Glu)  // MMQ estimate: the pick's steps + the direct-copy pre-pass
+    if (!forced && decode_passes_us(w, x) < best * (w.pk / 256) * 4 + 7.0)
+      return run_decode_passes(w, x, out, residual, s);
   // Q6_K: two more shapes, each unsplit or with the fixed K segments split
   // over blocks (one segment of one tile per block, then the ordered segment
   // sum, c_sum):
@@ -1017,6 +1058,7 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
       if (segs % 2 == 0)  // runs of two segments
         consider(163, rounds(160, segs / 2) * 2 * seg * 4 * kQ6Step160 + c_sum);
     }
+    if (!forced && decode_passes_us(w, x) < c_best) return run_decode_passes(w, x, out, residual, s);
     if (pick == 170 || pick == 171) {  // direct-copy 160 x 128 / 80 x 128, one segment per block
       const uint32_t cap = (x.m + 127) / 128 * 128;
       uint32_t mc = 0;

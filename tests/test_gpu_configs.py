@@ -105,9 +105,10 @@ def test_config3_q6k_down(torch_gpu):
 
 def test_q6k_split_k_rows_independent_of_m(torch_gpu):
     """Q6_K MMQ sums K in fixed segments (four at K = 17408) whatever the
-    launch: small M splits the segments over blocks and adds them in a second
-    kernel (M = 9, 40, 128, 256, 512 on 5120 rows), M = 2048 runs unsplit on
-    the 160 x 128 tile. Every token row must be bitwise the same at every M,
+    launch: M <= 128 splits the segments over mmq_kernel blocks and adds them
+    in a second kernel (M = 25, 40, 128), M > 128 runs the direct-copy
+    160 x 128 tile, one segment per block (M = 256, 512, and 2048 in four
+    token chunks). Every token row must be bitwise the same at every M,
     M = 40 matches the oracle, and the split launches must really have run
     split: the library scratch counters show each of them granted (a refused
     request silently takes the no-scratch path, which gives the same bits)."""
@@ -118,10 +119,9 @@ def test_q6k_split_k_rows_independent_of_m(torch_gpu):
     xs = silu_rows(2048, k, 312)
     q, ob = _q8(torch, ops, xs)
     full = None
-    # 2048: the unsplit 160 x 128 tile; 512: 160 x 128 split per segment (42 MB
-    # of partials); 40 / 128 / 256: 80 x 128 or 160 x 128 split; 9: the
-    # smallest MMQ
-    for m in (2048, 512, 40, 128, 256, 9):
+    # 2048 / 512 / 256: direct-copy tile; 40 / 128: 80 x 128 split; 25: the
+    # smallest M above the batched-decode passes
+    for m in (2048, 512, 40, 128, 256, 25):
         print(f"Q6_K split-K family M={m}", flush=True)
         qm = ops.Q8Input.empty(m, k)
         qm.codes.copy_(q.codes[:m]); qm.scales.copy_(q.scales[:m]); qm.sums.copy_(q.sums[:m])
@@ -132,9 +132,8 @@ def test_q6k_split_k_rows_independent_of_m(torch_gpu):
         ops.q4k_q8_project(w, qm, y, residual=res)
         torch.cuda.synchronize()
         after = ops.scratch_stats()
-        if m != 2048:
-            assert after[0] == before[0] + 1 and after[1:] == before[1:], \
-                f"M={m}: split launch did not get the scratch ({before} -> {after})"
+        assert after[0] == before[0] + 1 and after[1:] == before[1:], \
+            f"M={m}: split launch did not get the scratch ({before} -> {after})"
         yn = y.cpu().numpy()
         if res is not None:
             want = (full[:m] + res.cpu().numpy()).astype(np.float32)
@@ -179,6 +178,48 @@ def test_q6k_mmq_direct_copy_matches_tiles(torch_gpu, n):
         ym = _project(torch, ops, w, qm, 96, n)
         want = (ym + rn[t0:t0 + 96]).astype(np.float32)
         assert np.array_equal(yn[t0:t0 + 96].view(np.uint32), want.view(np.uint32)), f"tokens {t0}.. differ"
+
+
+@pytest.mark.parametrize("fmt,n,k", [("q4k", 5120, 5120), ("q6k", 5120, 17408)])
+def test_decode_passes_rows_match_decode(torch_gpu, fmt, n, k):
+    """M = 9..24 on small weights runs ceil(M / 8) batched-decode passes of
+    4..8 tokens instead of the MMQ (the cost model's pick here). The decode
+    kernels' rows for a token do not depend on the call's other tokens, so
+    the rows of the M = 9 / 16 / 24 call must equal bitwise those of M = 8
+    calls on the same tokens; M = 9 also matches the oracle."""
+    torch = torch_gpu
+    import qw38_amd.ops as ops
+    if fmt == "q4k":
+        w, wl = _fit_q4k(torch, ops, n, k, 351, oracle.LAYOUT_Q4K_SEQ)
+        x = normal((24, k), 352)
+    else:
+        w, wl = _fit_q6k(torch, ops, n, k, 353)
+        x = silu_rows(24, k, 354)
+    q, ob = _q8(torch, ops, x)
+
+    def sub(t0, m):
+        qm = ops.Q8Input.empty(m, k)
+        qm.codes.copy_(q.codes[t0:t0 + m]); qm.scales.copy_(q.scales[t0:t0 + m]); qm.sums.copy_(q.sums[t0:t0 + m])
+        return qm
+
+    eights = {t0: _project(torch, ops, w, sub(t0, 8), 8, n) for t0 in (0, 8, 16)}
+    for m in (9, 16, 24):
+        print(f"{fmt} decode passes M={m}", flush=True)
+        y = _project(torch, ops, w, sub(0, m), m, n)
+        for t0, y8 in eights.items():
+            hi = min(m, t0 + 8)
+            if hi > t0:
+                assert np.array_equal(y[t0:hi].view(np.uint32), y8[:hi - t0].view(np.uint32)), \
+                    f"{fmt} M={m}: tokens {t0}..{hi - 1} differ from the M=8 call"
+        if m == 9:
+            q9 = oracle.Q8(ob.codes[:9], ob.scales[:9], ob.sums[:9], 9, k, ob.pk)
+            if fmt == "q4k":
+                rows = np.sort(np.random.Generator(np.random.PCG64(9)).choice(n, 512, replace=False))
+                ref, _, _ = oracle.q4k_q8_contract(oracle.Q4K(wl.codes[rows], wl.meta[rows], len(rows), k), q9)
+                _check(y[:, rows], ref, "Q4_K decode passes M=9")
+            else:
+                ref, _, _ = oracle.q6k_q8_contract(wl, q9)
+                _check(y, ref, "Q6_K decode passes M=9")
 
 
 _OWN_SCRIPT = r"""
@@ -311,8 +352,9 @@ def test_q4k_mmq_direct_copy_rows_independent_of_m(torch_gpu, tmp_path):
     q, ob = _q8(torch, ops, normal((512, k), 332))
     full = None
     # 512: direct-copy 256 x 128 tiles + 128 x 32 tail split (the second time
-    # with a residual); 130 / 9 / 40 / 64: mmq_kernel's other tile picks
-    for m in (512, 512, 130, 9, 40, 64):
+    # with a residual); 130 / 25 / 40 / 64: the other tile picks (25 is the
+    # smallest M above the batched-decode passes)
+    for m in (512, 512, 130, 25, 40, 64):
         print(f"Q4_K MMQ family M={m}", flush=True)
         qm = ops.Q8Input.empty(m, k)
         qm.codes.copy_(q.codes[:m]); qm.scales.copy_(q.scales[:m]); qm.sums.copy_(q.sums[:m])

@@ -137,10 +137,12 @@ def test_gemv_q4k_integer_exact(torch_gpu, layout, n, k):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("layout", [oracle.LAYOUT_Q4K_SEQ, oracle.LAYOUT_Q4K_W64], ids=["020D", "0240"])
-@pytest.mark.parametrize("n,m", [(4104, 9), (4104, 40), (34816, 64), (4104, 130), (34816, 512), (5120, 512),
+@pytest.mark.parametrize("n,m", [(4104, 25), (4104, 40), (34816, 64), (4104, 130), (34816, 512), (5120, 512),
                                  (12288, 512), (8192, 512)])
 def test_mmq_q4k_integer_exact(torch_gpu, layout, n, m):
-    """MMQ tile shapes: 128x32 (M=9, 40 on 4104 rows), 128x64 (M=64 on 34816
+    """MMQ tile shapes: direct-copy 128x16 / 128x32 on 0x020D, mmq_kernel's
+    128x32 on 0x0240 (M=25, 40 on 4104 rows; M = 9..24 on small weights runs
+    batched-decode passes instead), 128x64 (M=64 on 34816
     rows), 256x128 (M=130), 256x128 plus the 128x32 tail split (M=512 on
     34816 rows, config 2's N) and the eight-wave 80x128, 192x128 and 128x128
     tiles (M=512 on 5120, 12288 and 8192 rows)."""
@@ -158,9 +160,10 @@ def test_mmq_q4k_integer_exact(torch_gpu, layout, n, m):
 @pytest.mark.gpu
 @pytest.mark.parametrize("n,k", [(264, 2048), (5120, 2048)])
 def test_q6k_integer_exact(torch_gpu, n, k):
-    """Q6_K (layout 0x0241): streaming GEMV (M <= 2), int8-MFMA decode (M 3..8)
-    and the MMQ (M = 9, 40, 130, 512; M = 9 runs the eight-wave 128x32 tile,
-    and on 5120 rows M = 130 and 512 the eight-wave 80x128 tile)."""
+    """Q6_K (layout 0x0241): streaming GEMV (M <= 2), int8-MFMA decode (M 3..8,
+    and M = 9 as two such passes where the cost model picks them) and the MMQ
+    (M = 40, 130, 512: split tiles up to M = 128, the direct-copy 160x128 tile
+    above)."""
     torch = torch_gpu
     import qw38_amd.ops as ops
     w, weff = integer_q6k(n, k, 3 * n, 16)
