@@ -211,6 +211,13 @@ def test_decode_passes_rows_match_decode(torch_gpu, fmt, n, k):
             if hi > t0:
                 assert np.array_equal(y[t0:hi].view(np.uint32), y8[:hi - t0].view(np.uint32)), \
                     f"{fmt} M={m}: tokens {t0}..{hi - 1} differ from the M=8 call"
+        if m == 16:  # the passes' residual epilogue adds exactly
+            res = torch.from_numpy(normal((16, n), 355)).cuda()
+            yr = torch.full((16, n), float("nan"), device="cuda")
+            ops.q4k_q8_project(w, sub(0, 16), yr, residual=res)
+            torch.cuda.synchronize()
+            want = (y + res.cpu().numpy()).astype(np.float32)
+            assert np.array_equal(yr.cpu().numpy().view(np.uint32), want.view(np.uint32)), f"{fmt} passes residual"
         if m == 9:
             q9 = oracle.Q8(ob.codes[:9], ob.scales[:9], ob.sums[:9], 9, k, ob.pk)
             if fmt == "q4k":

@@ -158,12 +158,13 @@ def test_mmq_q4k_integer_exact(torch_gpu, layout, n, m):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n,k", [(264, 2048), (5120, 2048)])
+@pytest.mark.parametrize("n,k", [(264, 2048), (5120, 2048), (776, 2304)])
 def test_q6k_integer_exact(torch_gpu, n, k):
     """Q6_K (layout 0x0241): streaming GEMV (M <= 2), int8-MFMA decode (M 3..8,
     and M = 9 as two such passes where the cost model picks them) and the MMQ
     (M = 40, 130, 512: split tiles up to M = 128, the direct-copy 160x128 tile
-    above)."""
+    above; K = 2304 gives it an odd super-block count in one K segment and a
+    partial last row tile)."""
     torch = torch_gpu
     import qw38_amd.ops as ops
     w, weff = integer_q6k(n, k, 3 * n, 16)
