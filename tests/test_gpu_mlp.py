@@ -184,7 +184,7 @@ def test_gate_up_swiglu_fused_bitwise(torch_gpu, mlp_weights, layout):
     """The fused gate+up launch (SwiGLU->Q8 in the projection's epilogue)
     equals the unfused chain -- two projections, then the oracle-pinned
     SwiGLU->Q8 pack -- bit for bit: the decode kernel at m = 1 on 0x020D, and
-    the MMQ at m covering every tile shape and the big-tile + tail split; a
+    the MMQ at m > 24 covering every tile shape and the big-tile + tail split; a
     group whose input scale is NaN is flagged in both."""
     torch = torch_gpu
     import qw38_amd.ops as ops
@@ -195,8 +195,10 @@ def test_gate_up_swiglu_fused_bitwise(torch_gpu, mlp_weights, layout):
     gamma = oracle.fp32_to_bf16(normal(5120, 80, 0.1))
     dgam = _dev(torch, gamma.view(np.int16))
     # m = 1 on 0x020D: the streaming-GEMV family (fused: one wave per strip,
-    # unfused: four waves split K); m > 8: the MMQ family
-    ms = ((1,) if layout == oracle.LAYOUT_Q4K_SEQ else ()) + (9, 40, 64, 130, 512)
+    # unfused: four waves split K); m > 24: the MMQ family on both sides (at
+    # m = 9..24 an unfused projection may run as batched-decode passes, a
+    # different family, while the fused launch stays on the MMQ)
+    ms = ((1,) if layout == oracle.LAYOUT_Q4K_SEQ else ()) + (25, 40, 64, 130, 512)
     for m in ms:
         print(f"gate_up layout=0x{layout:04x} m={m}", flush=True)
         res = normal((m, 5120), 90 + m) * 2
