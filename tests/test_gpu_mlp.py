@@ -225,6 +225,17 @@ def test_gate_up_swiglu_fused_bitwise(torch_gpu, mlp_weights, layout):
         assert torch.equal(out.codes, ref.codes)
         assert torch.equal(out.scales.view(torch.int32), ref.scales.view(torch.int32))
         assert torch.equal(out.sums, ref.sums)
+        if m == 40:  # the fused launch's small-M tiles (m = 9): its rows are the m = 40 rows
+            q9 = ops.Q8Input.empty(9, 5120)
+            q9.codes.copy_(qx.codes[:9]); q9.scales.copy_(qx.scales[:9]); q9.sums.copy_(qx.sums[:9])
+            o9 = ops.Q8Input.empty(9, 17408)
+            f9 = torch.zeros(1, dtype=torch.int32, device="cuda")
+            ops.q4k_q8_gate_up_swiglu(gate, up, q9, o9, f9)
+            torch.cuda.synchronize()
+            assert int(f9.item()) == 0
+            assert torch.equal(o9.codes, out.codes[:9])
+            assert torch.equal(o9.scales.view(torch.int32), out.scales[:9].view(torch.int32))
+            assert torch.equal(o9.sums, out.sums[:9])
 
 
 def test_gate_up_swiglu_rejections(torch_gpu, mlp_weights):
