@@ -82,29 +82,27 @@ __global__ __launch_bounds__(kWaves * 64) void q4k_mfma_decode_kernel(
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
 
   // ---- stage the activations once per block ----
+  // Loads are unconditional (clamped token) with a select after: a
+  // conditional load becomes a branch with its own wait.
   for (uint32_t e = tid; e < chunks * T; e += blockDim.x) {
     const uint32_t c = e / T, t = e % T;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (t < m) {
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(xc + size_t(t) * pk + c * 16);
-      const uint32_t z0 = src[0], z1 = src[1], z2 = src[2], z3 = src[3];
-      v.x = perm(z1, z0, 0x06040200u);
-      v.y = perm(z1, z0, 0x07050301u);
-      v.z = perm(z3, z2, 0x06040200u);
-      v.w = perm(z3, z2, 0x07050301u);
-    }
-    zs[e] = v;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(xc + size_t(min(t, m - 1)) * pk + c * 16);
+    const uint32_t z0 = src[0], z1 = src[1], z2 = src[2], z3 = src[3];
+    uint4 v;
+    v.x = perm(z1, z0, 0x06040200u);
+    v.y = perm(z1, z0, 0x07050301u);
+    v.z = perm(z3, z2, 0x06040200u);
+    v.w = perm(z3, z2, 0x07050301u);
+    zs[e] = t < m ? v : make_uint4(0, 0, 0, 0);
   }
   if (tid == 0) *zero = make_uint4(0, 0, 0, 0);
   for (uint32_t e = tid; e < groups * T; e += blockDim.x) {
     const uint32_t g = e / T, t = e % T;
-    float a = 0.f, u = 0.f;
-    if (t < m) {
-      a = xa[size_t(t) * groups + g];
-      u = a * float(xs[size_t(t) * groups + g]);
-    }
-    as[e] = a;
-    us[e] = u;
+    const size_t gi = size_t(min(t, m - 1)) * groups + g;
+    const float a = xa[gi];
+    const float u = a * float(xs[gi]);
+    as[e] = t < m ? a : 0.f;
+    us[e] = t < m ? u : 0.f;
   }
   __syncthreads();
 
