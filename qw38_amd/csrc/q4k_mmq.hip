@@ -874,6 +874,16 @@ constexpr double kQ6Step160 = 1.71;
 
 // Glu: the tile cost model runs over the 2 n virtual rows of gate and up, and
 // the launches get feature ranges (virtual rows / 2).
+// QW38_MMQ_I8=1: the direct-copy 256 x 128 tiles on the int8 matrix cores
+// (unfused calls; the same bits).
+static bool mmq_i8_env() {
+  static const bool v = [] {
+    const char* e = std::getenv("QW38_MMQ_I8");
+    return e && std::atoi(e) == 1;
+  }();
+  return v;
+}
+
 // QW38_MMQ_DMA: 0 turns the direct-copy tiles off, 2 keeps them off the
 // 128 x 32 tiles (tuning aids: every setting gives the same bits).
 static int mmq_dma_env() {
@@ -1106,13 +1116,17 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   // library scratch holds its pre-pass: rows [0, big) on the big tile, [big,
   // end) on the small one. hipErrorNotReady when it does not apply.
   const int dma_env = mmq_dma_env();
+  // QW38_MMQ_DMA=2, or the int8 form (QW38_MMQ_I8=1, unfused; it has no tail
+  // tiles): the direct-copy launch stops at the big tiles and mmq_kernel runs
+  // the rest
+  const bool dma_end_at_big = dma_env == 2 || (mmq_i8_env() && !Glu);
   auto try_dma = [&](uint32_t big, uint32_t tail_end, int tail_nj = 2) -> hipError_t {
     if constexpr (Layout == QW38_LAYOUT_Q4K_CANDIDATE_V2) {
       const bool aligned = ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
                              reinterpret_cast<uintptr_t>(x.codes) | reinterpret_cast<uintptr_t>(glu.codes2) |
                              reinterpret_cast<uintptr_t>(glu.meta2)) % 16) == 0;
       if (!dma_env || !aligned || x.pk != w.pk || (w.pk / 256) % 2 != 0) return hipErrorNotReady;
-      if (dma_env == 2) tail_end = big;
+      if (dma_end_at_big) tail_end = big;
       if (tail_end == 0) return hipErrorNotReady;
       int dev = 0;
       void* sc = scratch_acquire(s, mmq_dma_scratch_bytes(x.m, x.pk), &dev);
@@ -1144,7 +1158,7 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
   } else {
     if (bt == 128) return launch_cfg<Layout, 2, 2, 4, 4, Glu>(w, x, out, residual, s, 0, end, glu);  // 128 x 128
     if (forced) big_rows = pn;
-    const uint32_t dma_end = dma_env == 2 ? big_rows / kv : end;
+    const uint32_t dma_end = dma_end_at_big ? big_rows / kv : end;
     hipError_t e = try_dma(big_rows / kv, dma_end, dma_env == 3 ? 1 : 2);
     if (e == hipSuccess && dma_end == end) return e;
     if (e == hipErrorNotReady) e = launch_cfg<Layout, 4, 2, 4, 4, Glu>(w, x, out, residual, s, 0, big_rows / kv, glu);

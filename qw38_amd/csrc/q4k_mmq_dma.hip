@@ -39,6 +39,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 // The pre-pass writes the activations in blocks of kPB = 128 tokens. Its token
 // data block per (token block, super-block) is a' as [8 groups][128 tokens]
@@ -54,10 +55,11 @@ constexpr uint32_t kPB = 128, kTSlot = 8192, kTokU = 4096;
 // metadata (BR x 16 B) + token data (a' [8][BT] fp32, min-term operands
 // [BT][32 B]); metadata and token data of one super-block share a region
 // (the compiler tracks at most eight regions of copies in flight).
-template <int NW, int NJ>
+template <int NW, int NJ, bool I8 = false>
 struct Geo {
   static constexpr uint32_t BR = 32 * NW, BT = 16 * NJ;
-  static constexpr uint32_t BSL = BT * 128, ASL = BR * 128, MSL = BR * 16, TSL = BT * 64;
+  // B of one K step: 64 codes per token, FP16 (int8 in the I8 form)
+  static constexpr uint32_t BSL = BT * (I8 ? 64 : 128), ASL = BR * 128, MSL = BR * 16, TSL = BT * 64;
   static constexpr uint32_t OffA = 4 * BSL, OffM = OffA + 2 * ASL, MTS = MSL + TSL;
   static constexpr uint32_t Lds = OffM + 2 * MTS;  // 155648 B for 256 x 128, 57344 B for 128 x 32
   static constexpr uint32_t TokU = 32 * BT;         // min-term operands in the tile's token data
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restr
                                                            const int32_t* __restrict__ xs, uint32_t m,
                                                            uint32_t pk, uint8_t* __restrict__ bq,
                                                            uint8_t* __restrict__ tq, float* __restrict__ ti,
-                                                           bool unit_scale) {
+                                                           bool unit_scale, bool int8_b) {
   const uint32_t groups = pk / 32, kbs = pk / 256, steps = kbs * 4;
   const uint32_t t0 = blockIdx.x * 64, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
   if (blockIdx.y < kbs) {
@@ -150,6 +152,12 @@ __global__ __launch_bounds__(256) void mmq_dma_prep_kernel(const int8_t* __restr
     for (uint32_t i = 0; i < 8; ++i) {
       const uint32_t ch = w * 8 + i;  // 8-code chunk of the super-block (0..31)
       const uint32_t g = kb * 8 + ch / 4, lk = ch % 4, st = g / 2, c = (g % 2) * 4 + lk;
+      if (int8_b) {  // the int8 form: the same slot order, 8 B per (chunk, token)
+        const uint32_t z0 = rows[lane][ch * 2], z1 = rows[lane][ch * 2 + 1];
+        *reinterpret_cast<uint2*>(bq + ((size_t(tb) * steps + st) * 8 + c) * (kPB * 8) + tl * 8) =
+            make_uint2(perm(z1, z0, 0x06040200u), perm(z1, z0, 0x07050301u));  // z0 z2 z4 z6 | z1 z3 z5 z7
+        continue;
+      }
       const uint32_t u0 = rows[lane][ch * 2] ^ 0x80808080u, u1 = rows[lane][ch * 2 + 1] ^ 0x80808080u;
       uint4 o;
       o.x = as_u32(as_h2(perm(0x64646464u, u0, 0x04020400u)) + off);  // z0, z2
@@ -223,13 +231,21 @@ struct GluDma {
   int* failure;
 };
 
-template <int NW, int NJ, bool Glu>
+// I8 (256 x 128, unfused; opt-in, QW38_MMQ_I8=1): the same per-(row, token)
+// operations on the int8 matrix cores. The A operand is the raw codes (no
+// dequantization), B the pre-pass's int8 codes in the same slot order, one
+// v_mfma_i32_16x16x32_i8 per (row tile, token tile, group) gives the exact
+// dot, and P = f32(s * dot) -- the value the FP16 form's MFMA returns -- goes
+// into the same X chain, so the outputs are the same bits. It costs a
+// multiply and a convert per output and group beyond the FP16 form.
+template <int NW, int NJ, bool Glu, bool I8 = false>
 __global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n, uint32_t pn,
     uint32_t kbs, const uint8_t* __restrict__ bq, const uint8_t* __restrict__ tq,
     const float* __restrict__ ti, uint32_t m, float* __restrict__ out, const float* __restrict__ residual,
     uint32_t row_begin, uint32_t row_blocks, uint32_t tok_blocks, GluDma glu) {
-  using G = Geo<NW, NJ>;
+  using G = Geo<NW, NJ, I8>;
+  static_assert(!I8 || (!Glu && NJ == 8), "int8 form: the unfused 256 x 128 tile");
   constexpr uint32_t BR = G::BR, BT = G::BT, NH = NW / 2;
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t tiles_n = row_blocks * tok_blocks;
@@ -289,6 +305,13 @@ __global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
   auto issue_step = [&](uint32_t s_in, uint8_t* wB) __attribute__((always_inline)) {
     constexpr uint32_t units = BT / 8, CPW = units / NW;  // 1 KB copies per step; per wave
     const uint32_t s = min(s_in, steps - 1);
+    if constexpr (I8) {  // [8 chunks][BT tokens][8 B]: 64 16-byte positions per wave
+      static_assert(BT * 4 == 64 * NW, "int8 B copy share");
+      const uint8_t* row8 = bq + (uint64_t(pb) * steps + s) * 8 * (kPB * 8);
+      const uint32_t pos = wave * 64 + lane, c = pos / (BT / 2), tp = (pos % (BT / 2)) * 2;
+      dma16(row8 + c * (kPB * 8) + (toff + tp) * 8, wB + wave * 1024);
+      return;
+    }
     const uint8_t* row = bq + (uint64_t(pb) * steps + s) * 8 * (kPB * 16);
     if constexpr (CPW >= 1) {
 #pragma unroll
@@ -317,6 +340,9 @@ __global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
   // per super-block row data of this lane's A rows (32 wave + 16 i + lr)
   uint32_t S[2][2];  // scale bytes of groups 0-3 and 4-7
   half4 mf[2];       // min-term A operand (m of groups 4 lk .. 4 lk + 3; zero for lk >= 2)
+  // I8: the 6-bit scales of this lane's output rows 32 wave + 16 i + 4 lk + v,
+  // groups 0-3 and 4-7 as bytes
+  uint32_t Sx[I8 ? 2 : 1][I8 ? 4 : 1][2];
 
   auto compute = [&](auto qc, const uint8_t* Bs, const uint8_t* As, const uint8_t* Ms, const uint8_t* Ts) __attribute__((always_inline)) {
     constexpr uint32_t q = decltype(qc)::value;
@@ -333,6 +359,24 @@ __global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
         const h2 m01 = as_h2(perm(0x64646464u, mm, 0x04010400u)) + k1024;
         const h2 m23 = as_h2(perm(0x64646464u, mm, 0x04030402u)) + k1024;
         mf[i] = lk < 2 ? half4{m01.x, m01.y, m23.x, m23.y} : half4{0, 0, 0, 0};
+      }
+      if constexpr (I8) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          uint4 r4[4];
+          const uint32_t a0 = lds_addr(Ms + (wave * 32 + i * 16 + lk * 4) * 16);
+          asm volatile(
+              "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:16\n\tds_read_b128 %2, %4 offset:32\n\t"
+              "ds_read_b128 %3, %4 offset:48\n\ts_waitcnt lgkmcnt(0)"
+              : "=&v"(r4[0]), "=&v"(r4[1]), "=&v"(r4[2]), "=&v"(r4[3])
+              : "v"(a0)
+              : "memory");
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            Sx[i][v][0] = r4[v].y & 0x3f3f3f3fu;
+            Sx[i][v][1] = (r4[v].w & 0x0f0f0f0fu) | ((r4[v].y >> 2) & 0x30303030u);
+          }
+        }
       }
     }
     // A fragments of row tiles 0, 1 for group g = 2 q + gsel: codes
@@ -358,6 +402,68 @@ __global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
       const h2 p3 = __builtin_elementwise_fma(as_h2(perm(0x64646464u, hi, 0x04030402u)), s2, b2);
       return half8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
     };
+    if constexpr (I8) {
+      // The FP16 form's pipeline with int8 operands: A = the raw codes in the
+      // slot order, B from the int8 pre-pass, D = the exact dot; the scaling
+      // takes P = f32(s * D) (s * |D| < 2^22, so exact).
+      auto bfrag8 = [&](int u) __attribute__((always_inline)) {
+        return *reinterpret_cast<const long*>(Bs + (((u / NJ) * 4 + lk) * BT + (u % NJ) * 16 + lr) * 8);
+      };
+      auto afac8 = [&](int u) __attribute__((always_inline)) {
+        return *reinterpret_cast<const float*>(Ts + ((2 * q + u / NJ) * BT + (u % NJ) * 16 + lr) * 4);
+      };
+      long a8[2][2];
+#pragma unroll
+      for (int gs = 0; gs < 2; ++gs)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t w = wraw[gs][i];
+          a8[gs][i] = long((uint64_t((w >> 4) & 0x0f0f0f0fu) << 32) | (w & 0x0f0f0f0fu));
+        }
+      constexpr int kPF8 = 2;
+      long b8_[kPF8 + 1];
+      float a8q_[kPF8 + 1];
+#pragma unroll
+      for (int u = 0; u < kPF8; ++u) {
+        b8_[u] = bfrag8(u);
+        a8q_[u] = afac8(u);
+      }
+      v4i Dp[2];
+      float ap = 0.f;
+#pragma unroll
+      for (int u = 0; u <= 2 * NJ; ++u) {
+        v4i Dc[2];
+        float ac = 0.f;
+        if (u < 2 * NJ) {
+          if (u + kPF8 < 2 * NJ) {
+            b8_[(u + kPF8) % (kPF8 + 1)] = bfrag8(u + kPF8);
+            a8q_[(u + kPF8) % (kPF8 + 1)] = afac8(u + kPF8);
+          }
+          const long bf = b8_[u % (kPF8 + 1)];
+          ac = a8q_[u % (kPF8 + 1)];
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            Dc[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a8[u / NJ][i], bf, v4i{0, 0, 0, 0}, 0, 0, 0);
+        }
+        if (u > 0) {
+          const int pu = u - 1, pj = pu % NJ;
+          const uint32_t g = 2 * q + pu / NJ;
+          const bool first = q == 0 && pu < NJ;  // the super-block's first group
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int sv = int((Sx[i][v][g >> 2] >> (8 * (g & 3u))) & 0xffu);
+              const float P = float(__mul24(sv, Dp[i][v]));
+              X[i][pj][v] = first ? ap * P : fmaf(ap, P, X[i][pj][v]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        Dp[0] = Dc[0];
+        Dp[1] = Dc[1];
+        ap = ac;
+      }
+    } else {
     // Software pipeline over the step's 2 NJ items u = (group gsel = u / NJ,
     // token tile j = u % NJ): item u's MFMAs are issued after the B fragment
     // and a' of item u + kPF are requested and before item u - 1's results
@@ -410,6 +516,7 @@ __global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
       Pp[0] = Pc[0];
       Pp[1] = Pc[1];
       ap = ac;
+    }
     }
     // Pin X: otherwise the compiler defers the scaling FMAs and keeps
     // (spills) the MFMA results.
@@ -923,13 +1030,15 @@ uint64_t mmq_dma_scratch_bytes(uint32_t m, uint32_t pk) {
 
 namespace {
 
-template <int NW, int NJ>
+template <int NW, int NJ, bool I8 = false>
 hipError_t launch_dma_tiles(const WeightView& w, const Q8View& x, float* out, const float* residual, hipStream_t s,
                             uint32_t row_begin, uint32_t rows, const uint8_t* bq, const uint8_t* tq,
                             const float* ti, const WeightView* up, const GluDma& g) {
-  using G = Geo<NW, NJ>;
+  using G = Geo<NW, NJ, I8>;
   const bool glu = up != nullptr;
-  auto kern = glu ? mmq_dma_kernel<NW, NJ, true> : mmq_dma_kernel<NW, NJ, false>;
+  auto kern = mmq_dma_kernel<NW, NJ, false, I8>;
+  if constexpr (!I8)
+    if (glu) kern = mmq_dma_kernel<NW, NJ, true>;
   if (G::Lds > 64 * 1024) {
     const hipError_t e = set_max_lds(reinterpret_cast<const void*>(kern), int(G::Lds));
     if (e != hipSuccess) return e;
@@ -955,6 +1064,13 @@ hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, cons
                           hipStream_t s, uint32_t rows, uint32_t tail_end, void* scratch, const WeightView* up,
                           int8_t* qc, float* qa, int32_t* qs, int* failure, int tail_nj) {
   const bool glu = up != nullptr;
+  // QW38_MMQ_I8=1: the 256 x 128 tiles on the int8 matrix cores (same bits),
+  // for unfused calls without a tail (the tail tiles read the FP16 pre-pass)
+  static const bool i8_env = [] {
+    const char* v = std::getenv("QW38_MMQ_I8");
+    return v && std::atoi(v) == 1;
+  }();
+  const bool i8 = i8_env && !glu && tail_end == rows;
   if (w.layout != QW38_LAYOUT_Q4K_CANDIDATE_V2 || tail_end < rows || tail_end == 0 || x.pk != w.pk ||
       ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
         reinterpret_cast<uintptr_t>(x.codes) | reinterpret_cast<uintptr_t>(glu ? up->codes : nullptr) |
@@ -969,11 +1085,13 @@ hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, cons
   uint8_t* tq = bq + uint64_t(mp) * w.pk * 2;
   float* ti = reinterpret_cast<float*>(tq + uint64_t(mp / kPB) * (w.pk / 256) * kTSlot);
   hipLaunchKernelGGL(mmq_dma_prep_kernel, dim3(mp / 64, w.pk / 256 + 16), dim3(256), 0, s, x.codes, x.scales,
-                     x.sums, x.m, x.pk, bq, tq, ti, false);
+                     x.sums, x.m, x.pk, bq, tq, ti, false, i8);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const GluDma g{glu ? up->codes : nullptr, glu ? up->scales : nullptr, qc, qa, qs, failure};
-  if (rows > 0) e = launch_dma_tiles<8, 8>(w, x, out, residual, s, 0, rows, bq, tq, ti, up, g);
+  if (rows > 0)
+    e = i8 ? launch_dma_tiles<8, 8, true>(w, x, out, residual, s, 0, rows, bq, tq, ti, up, g)
+           : launch_dma_tiles<8, 8>(w, x, out, residual, s, 0, rows, bq, tq, ti, up, g);
   if (e == hipSuccess && tail_end > rows)
     e = tail_nj == 1 ? launch_dma_tiles<4, 1>(w, x, out, residual, s, rows, tail_end - rows, bq, tq, ti, up, g)
                      : launch_dma_tiles<4, 2>(w, x, out, residual, s, rows, tail_end - rows, bq, tq, ti, up, g);
@@ -1017,7 +1135,7 @@ hipError_t launch_q6_mmq_dma(const WeightView& w, const Q8View& x, float* out, c
     uint8_t* tq = bq + uint64_t(mp) * w.pk * 2;
     float* ti = reinterpret_cast<float*>(tq + uint64_t(mp / kPB) * kbs * kTSlot);
     hipLaunchKernelGGL(mmq_dma_prep_kernel, dim3(mp / 64, kbs + 16), dim3(256), 0, s, x.codes + size_t(t0) * x.pk,
-                       x.scales + size_t(t0) * groups, x.sums + size_t(t0) * groups, m, x.pk, bq, tq, ti, true);
+                       x.scales + size_t(t0) * groups, x.sums + size_t(t0) * groups, m, x.pk, bq, tq, ti, true, false);
     e = hipGetLastError();
     if (e != hipSuccess) break;
     float* o = out + size_t(t0) * w.n;

@@ -347,8 +347,9 @@ def test_q4k_mmq_direct_copy_rows_independent_of_m(torch_gpu, tmp_path):
     bitwise the same at every M (the reference's schedule invariance,
     tests/q4k_q8_test.cpp:118-120), the launches that take the direct-copy
     kernel must have got the scratch, M = 40 matches the oracle, and the
-    same M = 512 call with the kernel switched off (QW38_MMQ_DMA=0, a child
-    process since the switch is read once) must give the same bits."""
+    same M = 512 call with the kernel switched off (QW38_MMQ_DMA=0) and on its
+    int8 form (QW38_MMQ_I8=1; child processes, since the switches are read
+    once) must give the same bits."""
     import os
     import subprocess
     import sys
@@ -388,14 +389,18 @@ def test_q4k_mmq_direct_copy_rows_independent_of_m(torch_gpu, tmp_path):
             sub = oracle.Q4K(wl.codes[rows], wl.meta[rows], len(rows), k)
             ref, _, _ = oracle.q4k_q8_contract(sub, oracle.Q8(ob.codes[:m], ob.scales[:m], ob.sums[:m], m, k, ob.pk))
             _check(yn[:, rows], ref, "Q4_K MMQ M=40")
-    out = str(tmp_path / "dma_off.npy")
-    env = dict(os.environ, QW38_MMQ_DMA="0")
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    r = subprocess.run([sys.executable, "-c", _DMA_OFF_SCRIPT, root, out], env=env, timeout=110,
-                       capture_output=True, text=True)
-    assert r.returncode == 0, r.stderr[-2000:]
-    off = np.load(out)
-    assert np.array_equal(off.view(np.uint32), full.view(np.uint32)), "QW38_MMQ_DMA=0 differs from the direct-copy kernel"
+    # the same call with the direct-copy kernel off, and on its int8 form
+    # (QW38_MMQ_I8=1: v_mfma_i32_16x16x32_i8 on the raw codes, P = f32(s dot))
+    for var, val in (("QW38_MMQ_DMA", "0"), ("QW38_MMQ_I8", "1")):
+        print(f"Q4_K MMQ M=512 with {var}={val}", flush=True)
+        out = str(tmp_path / f"{var}.npy")
+        env = dict(os.environ, **{var: val})
+        r = subprocess.run([sys.executable, "-c", _DMA_OFF_SCRIPT, root, out], env=env, timeout=110,
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr[-2000:]
+        other = np.load(out)
+        assert np.array_equal(other.view(np.uint32), full.view(np.uint32)), f"{var}={val} differs from the direct-copy kernel"
 
 
 @pytest.mark.parametrize("layout", [oracle.LAYOUT_Q4K_SEQ, oracle.LAYOUT_Q4K_W64], ids=["020D", "0240"])
