@@ -22,6 +22,8 @@
 //   fragment reads are conflict-free) and each wave owns 32 rows x all 128 tokens: it
 //   dequantizes its own A fragments straight from the raw bytes, so A never
 //   makes an FP16 round trip through LDS.
+// - An opt-in int8 form of the 256 x 128 tile (QW38_MMQ_I8=1) runs the same
+//   arithmetic on v_mfma_i32_16x16x32_i8 (see mmq_dma_kernel's I8).
 // - All staging is global_load_lds_dwordx4 (no VGPRs, no VALU). A ring of four
 //   K-step slots for B and two super-block slots for A and the token data is
 //   filled two steps ahead; one barrier per pair of K steps, with explicit
