@@ -310,7 +310,7 @@ using Q6SegReduce = hipError_t (*)(const float* part, uint32_t segs, uint32_t m,
                                    const float* residual, float* out, hipStream_t s);
 uint64_t q6_mmq_dma_scratch_bytes(uint32_t mc, uint32_t n, uint32_t pk);
 hipError_t launch_q6_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
-                             hipStream_t s, void* scratch, int nw, uint32_t mc, Q6SegReduce reduce);
+                             hipStream_t s, void* scratch, int nw, int nj, uint32_t mc, Q6SegReduce reduce);
 
 // ---- launchers (defined in the .hip files) ---------------------------------
 hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t pk,

@@ -1052,31 +1052,39 @@ hipError_t mmq_dispatch(const WeightView& w, const Q8View& x, float* out, const 
       if ((!forced && c < c_best) || forced == id) c_best = c, pick = id;
     };
     consider(160, rounds(160, 1) * kbs * 4 * kQ6Step160);
-    // The direct-copy 160 x 128 tile (q4k_mmq_dma.hip; one fixed segment per
-    // block, tokens in chunks the scratch holds) measured faster than every
-    // tile above for all M > 128 at 5120 x 17408 (M = 160: 132 against
-    // 146 us; 512: 230 / 260; 1536: 668 / 853; 2048: 887 / 924) and slower
-    // at M = 128 (126 / 95), where one token tile leaves half the CUs idle.
-    // 171 (80 x 128) is a tuning id only.
-    if (mmq_dma_env() != 0 && x.pk == w.pk && w.pn % 8 == 0) {
-      consider(170, x.m > 128 ? 0.0 : 1e30);
-      consider(171, 1e30);
-    }
     if (split_env && segs > 1) {
       consider(82, rounds(80, segs) * seg * 4 * 1.07 + c_sum);
       consider(162, rounds(160, segs) * seg * 4 * kQ6Step160 + c_sum);
       if (segs % 2 == 0)  // runs of two segments
         consider(163, rounds(160, segs / 2) * 2 * seg * 4 * kQ6Step160 + c_sum);
     }
+    // The direct-copy 160 x 128 tile (q4k_mmq_dma.hip; one fixed segment per
+    // block, tokens in chunks the scratch holds) measured faster than every
+    // tile above for all M > 128 at 5120 x 17408 (M = 160: 132 against
+    // 146 us; 512: 230 / 260; 1536: 668 / 853; 2048: 887 / 924) and slower
+    // at M = 128 (126 / 95), where one token tile leaves half the CUs idle.
+    // M <= 128 with several K segments takes its 160 x 64 form (172: two
+    // token tiles per 128 tokens, two blocks per CU): 5120 x 17408 at
+    // M = 64 / 96 / 128 81 / 86 / 88 us against 90 / 92 / 92 for the split
+    // tiles; 776 rows at M = 130 77 against 116. One segment (K = 2304,
+    // M = 96): 45 against 32, so not there. M = 9..24 keeps the decode
+    // passes (5120 rows, M = 24: 65.5 against 73.5 us for 172). 171 (80 x 128)
+    // is a tuning id only. Each is priced just under the best tile above.
+    if (mmq_dma_env() != 0 && x.pk == w.pk && w.pn % 8 == 0) {
+      consider(170, x.m > 128 ? c_best * 0.9 : 1e30);
+      consider(171, 1e30);
+      consider(172, (x.m > 24 && x.m <= 128 && segs > 1) ? c_best * 0.95 : 1e30);
+    }
     if (!forced && decode_passes_us(w, x) < c_best) return run_decode_passes(w, x, out, residual, s);
-    if (pick == 170 || pick == 171) {  // direct-copy 160 x 128 / 80 x 128, one segment per block
+    if (pick == 170 || pick == 171 || pick == 172) {  // direct-copy 160 x 128 / 80 x 128 / 160 x 64, one segment per block
       const uint32_t cap = (x.m + 127) / 128 * 128;
       uint32_t mc = 0;
       for (uint32_t c = 128; c <= cap; c += 128)
         if (q6_mmq_dma_scratch_bytes(c, w.n, w.pk) <= kScratchBytes) mc = c;
       int dev = 0;
       if (void* sc = mc ? scratch_acquire(s, q6_mmq_dma_scratch_bytes(mc, w.n, w.pk), &dev) : nullptr) {
-        const hipError_t e = launch_q6_mmq_dma(w, x, out, residual, s, sc, pick == 170 ? 10 : 5, mc, q6_seg_reduce);
+        const hipError_t e = launch_q6_mmq_dma(w, x, out, residual, s, sc, pick == 171 ? 5 : 10, pick == 172 ? 4 : 8, mc,
+                                               q6_seg_reduce);
         scratch_release(dev, s, e == hipSuccess);
         return e;
       }

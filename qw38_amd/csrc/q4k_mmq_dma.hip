@@ -765,9 +765,9 @@ __global__ __launch_bounds__(NW * 64) void mmq_dma_kernel(
 // low nibbles, 128 B of high pairs), so a wave's codes of one step are one
 // 768 B copy. The step ring holds B (16 KB) and the NW waves' codes; a
 // super-block slot holds the waves' scales and d and the tokens' a (fp32).
-template <int NW>
+template <int NW, int NJ = 8>
 struct Geo6 {
-  static constexpr uint32_t BR = 16 * NW, BT = 128;
+  static constexpr uint32_t BR = 16 * NW, BT = 16 * NJ;
   static constexpr uint32_t BSL = BT * 128, AW = 768, SSL = BSL + NW * AW;  // one K step
   static constexpr uint32_t MW = 288, TSL = 8 * BT * 4, MTS = NW * MW + TSL;  // one super-block
   static constexpr uint32_t OffM = 4 * SSL, Lds = OffM + 2 * MTS;
@@ -781,20 +781,21 @@ __device__ __attribute__((always_inline)) inline void q6_regions(uint8_t* __rest
   f(b0, b1, b2, b3, mt0, mt1);
 }
 
-template <int NW>
+template <int NW, int NJ = 8>
 __global__ __launch_bounds__(NW * 64) void q6_mmq_dma_kernel(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ meta, uint32_t n, uint32_t pn,
     uint32_t kbs, const uint8_t* __restrict__ bq, const uint8_t* __restrict__ tq, uint32_t m,
     float* __restrict__ out, const float* __restrict__ residual, uint32_t row_blocks, uint32_t tok_blocks,
     uint32_t seg_kb, uint32_t segs, float* __restrict__ part) {
-  using G = Geo6<NW>;
-  constexpr uint32_t BT = G::BT, NJ = 8;
+  using G = Geo6<NW, NJ>;
+  constexpr uint32_t BT = G::BT;
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t tiles_n = row_blocks * tok_blocks;
   // segs > 1: block b runs segment b / tiles_n and writes its sum to part
   const uint32_t sgm = blockIdx.x / tiles_n, bx = blockIdx.x % tiles_n;
   const uint32_t tile = (tiles_n % 8 == 0) ? (bx % 8) * (tiles_n / 8) + bx / 8 : bx;
   const uint32_t rb = tile / tok_blocks, tb = tile % tok_blocks;
+  const uint32_t pb = tb * BT / kPB, toff = tb * BT % kPB;  // pre-pass token block and offset
   const uint32_t kb_lo = sgm * seg_kb, kb_hi = min(kbs, kb_lo + seg_kb);
   if (segs > 1) {
     out = part + size_t(sgm) * m * n;
@@ -809,8 +810,9 @@ __global__ __launch_bounds__(NW * 64) void q6_mmq_dma_kernel(
 
   // ---- copy issue ----
   // Super-block: lanes 0..15 the scale rows of the wave's two 8-row tiles,
-  // lanes 16, 17 their d (8 x fp16 each); waves 0..3 also 1 KB each of the
-  // tokens' a [8 groups][128 tokens] (pre-pass block tb, super-block kb).
+  // lanes 16, 17 their d (8 x fp16 each); waves 0 .. BT / 32 - 1 also 1 KB
+  // each of the tokens' a [8 groups][BT tokens], gathered from the pre-pass
+  // block pb at token offset toff.
   auto issue_super = [&](uint32_t kb_in, uint8_t* MT) __attribute__((always_inline)) {
     const uint32_t kb = min(kb_in, kbs - 1);
     if (lane < 18) {
@@ -819,13 +821,17 @@ __global__ __launch_bounds__(NW * 64) void q6_mmq_dma_kernel(
       const uint8_t* src = lane < 16 ? meta + (tr + (lane & 7u)) * 16 : meta + trows * 16 + tr * 2;
       dma16(src, MT + wave * G::MW);
     }
-    if (wave < 4) dma16(tq + (uint64_t(tb) * kbs + kb) * kTSlot + wave * 1024 + lane * 16, MT + NW * G::MW + wave * 1024);
+    if (wave < BT / 32) {
+      const uint32_t p = wave * 64 + lane, g = p / (BT / 4), tp = p % (BT / 4);
+      dma16(tq + (uint64_t(pb) * kbs + kb) * kTSlot + g * (kPB * 4) + (toff + tp * 4) * 4,
+            MT + NW * G::MW + wave * 1024);
+    }
   };
   // K step s: the wave's codes (lanes 0..31 low nibbles of tiles 0, 1 -- the
   // second tile's 16-byte chunks in the order p ^ 1, so the two tiles'
   // fragment reads use different banks -- lanes 32..47 the high pairs) and B
-  // units k = wave, wave + NW, ... of 1 KB (the pre-pass block's K step is
-  // one contiguous 16 KB run: [8 chunks][128 tokens][16 B]).
+  // units k = wave, wave + NW, ... of 1 KB (64 tokens of one chunk of the
+  // pre-pass block's K step [8 chunks][128 tokens][16 B]).
   auto issue_step = [&](uint32_t s_in, uint8_t* SL) __attribute__((always_inline)) {
     const uint32_t s = min(s_in, steps - 1), kb = s / 4, q = s % 4;
     if (lane < 48) {
@@ -835,11 +841,12 @@ __global__ __launch_bounds__(NW * 64) void q6_mmq_dma_kernel(
                                      : base + kQ6HiPlane + q * 128 + ((lane - 32) & 7u) * 16;
       dma16(src, SL + G::BSL + wave * G::AW);
     }
-    const uint8_t* row = bq + (uint64_t(tb) * steps + s) * G::BSL;
+    const uint8_t* row = bq + (uint64_t(pb) * steps + s) * (8 * kPB * 16);
+    constexpr uint32_t units = BT / 8, upc = BT / 64;  // 1 KB units per step, per chunk
 #pragma unroll
-    for (uint32_t k0 = 0; k0 < 16; k0 += NW) {
+    for (uint32_t k0 = 0; k0 < units; k0 += NW) {
       const uint32_t k = k0 + wave;
-      if (k < 16) dma16(row + k * 1024 + lane * 16, SL + k * 1024);
+      if (k < units) dma16(row + (k / upc) * (kPB * 16) + (toff + (k % upc) * 64) * 16 + lane * 16, SL + k * 1024);
     }
   };
 
@@ -1104,7 +1111,8 @@ hipError_t launch_mmq_dma(const WeightView& w, const Q8View& x, float* out, cons
 
 namespace qw38hip {
 
-// Q6_K 0x0241 on the direct-copy tiles, NW = 10 (160 x 128) or 5 (80 x 128):
+// Q6_K 0x0241 on the direct-copy tiles, NW = 10 (160 x 128, or 160 x 64 with
+// nj = 4) or 5 (80 x 128):
 // one block per (tile, fixed K segment). With several segments the tokens run
 // in chunks of mc (a multiple of 128): the chunk's pre-pass and segment sums
 // (one mc x n array per segment) share the scratch, and reduce(part, segs,
@@ -1117,9 +1125,10 @@ uint64_t q6_mmq_dma_scratch_bytes(uint32_t mc, uint32_t n, uint32_t pk) {
 }
 
 hipError_t launch_q6_mmq_dma(const WeightView& w, const Q8View& x, float* out, const float* residual,
-                             hipStream_t s, void* scratch, int nw, uint32_t mc, Q6SegReduce reduce) {
+                             hipStream_t s, void* scratch, int nw, int nj, uint32_t mc, Q6SegReduce reduce) {
   const uint32_t kbs = w.pk / 256, seg_kb = q6_seg_kb(kbs), segs = (kbs + seg_kb - 1) / seg_kb;
-  if (w.layout != QW38_LAYOUT_Q6K_WAVE64 || x.pk != w.pk || w.pn % 8 != 0 || (nw != 10 && nw != 5) ||
+  if (w.layout != QW38_LAYOUT_Q6K_WAVE64 || x.pk != w.pk || w.pn % 8 != 0 ||
+      !((nw == 10 && (nj == 8 || nj == 4)) || (nw == 5 && nj == 8)) ||
       mc == 0 || mc % kPB != 0 || x.m == 0 ||
       ((reinterpret_cast<uintptr_t>(w.codes) | reinterpret_cast<uintptr_t>(w.scales) |
         reinterpret_cast<uintptr_t>(x.codes)) % 16) != 0 ||
@@ -1128,9 +1137,9 @@ hipError_t launch_q6_mmq_dma(const WeightView& w, const Q8View& x, float* out, c
   const uint32_t groups = x.pk / 32;
   uint8_t* bq = static_cast<uint8_t*>(scratch);
   float* part = reinterpret_cast<float*>(bq + (mmq_dma_scratch_bytes(mc, w.pk) + 255) / 256 * 256);
-  auto kern = nw == 10 ? q6_mmq_dma_kernel<10> : q6_mmq_dma_kernel<5>;
-  const uint32_t br = nw == 10 ? Geo6<10>::BR : Geo6<5>::BR;
-  const uint32_t lds_bytes = nw == 10 ? Geo6<10>::Lds : Geo6<5>::Lds;
+  auto kern = nw == 5 ? q6_mmq_dma_kernel<5> : nj == 4 ? q6_mmq_dma_kernel<10, 4> : q6_mmq_dma_kernel<10>;
+  const uint32_t br = nw == 10 ? Geo6<10>::BR : Geo6<5>::BR, bt = 16u * uint32_t(nj);
+  const uint32_t lds_bytes = nw == 5 ? Geo6<5>::Lds : nj == 4 ? Geo6<10, 4>::Lds : Geo6<10>::Lds;
   hipError_t e = set_max_lds(reinterpret_cast<const void*>(kern), int(lds_bytes));
   for (uint32_t t0 = 0; e == hipSuccess && t0 < x.m; t0 += mc) {
     const uint32_t m = std::min(mc, x.m - t0), mp = (m + kPB - 1) / kPB * kPB;
@@ -1142,7 +1151,7 @@ hipError_t launch_q6_mmq_dma(const WeightView& w, const Q8View& x, float* out, c
     if (e != hipSuccess) break;
     float* o = out + size_t(t0) * w.n;
     const float* res = residual ? residual + size_t(t0) * w.n : nullptr;
-    const uint32_t row_blocks = (w.pn + br - 1) / br, tok_blocks = mp / kPB;
+    const uint32_t row_blocks = (w.pn + br - 1) / br, tok_blocks = (m + bt - 1) / bt;
     hipLaunchKernelGGL(kern, dim3(row_blocks * tok_blocks * segs), dim3(nw * 64), lds_bytes, s, w.codes, w.scales,
                        w.n, w.pn, kbs, bq, tq, m, o, res, row_blocks, tok_blocks, seg_kb, segs, part);
     e = hipGetLastError();

@@ -147,14 +147,44 @@ def test_q6k_split_k_rows_independent_of_m(torch_gpu):
             _check(yn, ref, "Q6_K split-K M=40")
 
 
+_Q6_SPLIT_SCRIPT = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
+import oracle, qw38_amd.ops as ops
+from _fix import silu_rows
+n, m, out = int(sys.argv[2]), int(sys.argv[3]), sys.argv[4]
+k = 17408
+g = torch.Generator(device="cuda"); g.manual_seed(341)
+x = torch.randn(n, k, generator=g, device="cuda") * 0.02
+w = ops.upload_q6k_blocks(ops.quantize_q6k_blocks(x, n, k), n, k)
+bf = oracle.fp32_to_bf16(silu_rows(m, k, 342))
+q = ops.Q8Input.empty(m, k)
+flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+ops.pack_q8(torch.from_numpy(bf.view(np.int16)).cuda(), q, flag)
+rows = []
+for t0 in ((0, 560) if m == 700 else (0, 34)):
+    qm = ops.Q8Input.empty(96, k)
+    qm.codes.copy_(q.codes[t0:t0 + 96]); qm.scales.copy_(q.scales[t0:t0 + 96]); qm.sums.copy_(q.sums[t0:t0 + 96])
+    y = torch.empty(96, n, device="cuda")
+    ops.q4k_q8_project(w, qm, y)
+    torch.cuda.synchronize()
+    rows.append(y.cpu().numpy())
+np.save(out, np.concatenate(rows))
+"""
+
+
 @pytest.mark.parametrize("n", [5120, 776])
-def test_q6k_mmq_direct_copy_matches_tiles(torch_gpu, n):
-    """Q6_K MMQ for M > 128 runs the direct-copy 160 x 128 tile
-    (q4k_mmq_dma.hip: one fixed K segment per block, tokens in chunks of at
-    most what the scratch holds, here 512 + 188 at M = 700). Its rows, with a
-    residual, must equal bitwise the rows of mmq_kernel's split tiles (M = 96
-    calls on token windows of the first and the second chunk) plus the same
-    residual. n = 776: a partial last row tile (776 = 4 x 160 + 136)."""
+def test_q6k_mmq_direct_copy_matches_tiles(torch_gpu, n, tmp_path):
+    """Q6_K MMQ runs the direct-copy kernel (q4k_mmq_dma.hip: one fixed K
+    segment per block): 160 x 128 tiles for M > 128, in token chunks of at
+    most what the scratch holds (512 + 188 at M = 700), and 160 x 64 tiles
+    for M <= 128 (the M = 96 calls here). Its rows, with a residual, must equal
+    bitwise the direct-copy M = 96 rows of the same tokens plus the residual,
+    and those equal mmq_kernel's split tiles (a child process with
+    QW38_MMQ_DMA=0). n = 776: a partial last row tile (776 = 4 x 160 + 136)."""
+    import os
+    import subprocess
+    import sys
     torch = torch_gpu
     import qw38_amd.ops as ops
     k = 17408
@@ -171,13 +201,24 @@ def test_q6k_mmq_direct_copy_matches_tiles(torch_gpu, n):
     after = ops.scratch_stats()
     assert after[0] == before[0] + 1 and after[1:] == before[1:], f"scratch not granted ({before} -> {after})"
     yn, rn = y.cpu().numpy(), res.cpu().numpy()
+    windows = []
     for t0 in ((0, 560) if m == 700 else (0, 34)):
-        print(f"Q6_K split tiles n={n} tokens {t0}..{t0 + 95}", flush=True)
+        print(f"Q6_K M=96 n={n} tokens {t0}..{t0 + 95}", flush=True)
         qm = ops.Q8Input.empty(96, k)
         qm.codes.copy_(q.codes[t0:t0 + 96]); qm.scales.copy_(q.scales[t0:t0 + 96]); qm.sums.copy_(q.sums[t0:t0 + 96])
         ym = _project(torch, ops, w, qm, 96, n)
+        windows.append(ym)
         want = (ym + rn[t0:t0 + 96]).astype(np.float32)
         assert np.array_equal(yn[t0:t0 + 96].view(np.uint32), want.view(np.uint32)), f"tokens {t0}.. differ"
+    print(f"Q6_K M=96 n={n} with QW38_MMQ_DMA=0", flush=True)
+    out = str(tmp_path / "q6_split.npy")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _Q6_SPLIT_SCRIPT, root, str(n), str(m), out],
+                       env=dict(os.environ, QW38_MMQ_DMA="0"), timeout=110, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    split = np.load(out)
+    assert np.array_equal(split.view(np.uint32), np.concatenate(windows).view(np.uint32)), \
+        "mmq_kernel's split tiles differ from the direct-copy rows"
 
 
 @pytest.mark.parametrize("fmt,n,k", [("q4k", 5120, 5120), ("q6k", 5120, 17408)])
