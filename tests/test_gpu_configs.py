@@ -495,7 +495,7 @@ def test_config4_mmq_outlier_rows(torch_gpu, m, layout):
     _check(y[:, rows], ref, f"config4 outlier rows N={n} M={m}")
 
 
-def test_config5_qkv_decode(torch_gpu):
+def test_config5_qkv_decode(torch_gpu, tmp_path):
     """Config-5 QKV/gate projection (12288x5120, Q4_K on 0x020D) at M=1, the
     full output against the oracle."""
     torch = torch_gpu
@@ -506,6 +506,31 @@ def test_config5_qkv_decode(torch_gpu):
     y = _project(torch, ops, w, q, 1, n)
     ref, _, _ = oracle.q4k_q8_contract(wl, ob)
     _check(y, ref, "config5 QKV M=1")
+    # 1536 strips run one block each (six per CU); the persistent grid of
+    # four blocks per CU (QW38_GEMV_STREAM_BLOCKS=1024, child process: the
+    # switch is read once) must give the same bits
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = str(tmp_path / "persistent.npy")
+    env = dict(os.environ, QW38_GEMV_STREAM_BLOCKS="1024")
+    r = subprocess.run([sys.executable, "-c", _QKV_SCRIPT, root, out], env=env, timeout=110,
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert np.array_equal(np.load(out).view(np.uint32), y.view(np.uint32)), "persistent grid rows differ"
+
+
+_QKV_SCRIPT = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
+import oracle, qw38_amd.ops as ops
+from _fix import normal
+from test_gpu_configs import _fit_q4k, _q8, _project
+w, wl = _fit_q4k(torch, ops, 12288, 5120, 901, oracle.LAYOUT_Q4K_SEQ)
+q, ob = _q8(torch, ops, normal((1, 5120), 902))
+np.save(sys.argv[2], _project(torch, ops, w, q, 1, 12288))
+"""
 
 
 @pytest.mark.parametrize("m", [1, 8, 128, 512])
