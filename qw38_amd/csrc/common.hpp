@@ -204,10 +204,6 @@ __device__ __forceinline__ void rms_q8_row(const float* __restrict__ x, const ui
     xv[st] = x[i];
     gv[st] = bf16_to_f32(gamma[i]);
   }
-  // The row also goes to LDS (xs, kRmsHidden floats), so the sum of squares
-  // below reads its strided elements there instead of from memory again.
-#pragma unroll
-  for (int st = 0; st < kSteps; ++st) xs[(half + kHalves * st) * 32 + lane32] = xv[st];
   float s = 0.f;
 #pragma unroll
   for (int st = 0; st < kSteps; ++st) s = fmaxf(s, fabsf(xv[st]));
@@ -215,20 +211,25 @@ __device__ __forceinline__ void rms_q8_row(const float* __restrict__ x, const ui
   for (int off = 32; off; off >>= 1) s = fmaxf(s, __shfl_xor(s, off));
   if ((tid & 63u) == 0) sm[tid >> 6] = s;
   __syncthreads();
-  if (tid == 0) {
-    float t = 0.f;
-    for (int w = 0; w < kWaves; ++w) t = fmaxf(t, sm[w]);
-    sm[16] = t;
-  }
-  __syncthreads();
-  const float scale = sm[16];
+  // every thread takes the block maximum itself (fmaxf is order-free)
+  float scale = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) scale = fmaxf(scale, sm[w]);
   const float safe = scale == 0.f ? 1.f : scale;
-  __syncthreads();  // sm[0..7] is rewritten below
+  // Each thread divides its own elements once; the quotients go to LDS (xs,
+  // kRmsHidden floats), where the sum of squares below reads them in the
+  // reference's strided order, and stay in registers for the output.
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    xv[st] = xv[st] / safe;
+    xs[(half + kHalves * st) * 32 + lane32] = xv[st];
+  }
+  __syncthreads();  // xs complete; every thread has read sm[0..kWaves)
   if (tid < 256) {
     float sq = 0.f;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
-      const float q = xs[tid + 256 * j] / safe;
+      const float q = xs[tid + 256 * j];
       sq = fmaf(q, q, sq);
     }
     sq = tree32_sum(sq);
@@ -246,7 +247,7 @@ __device__ __forceinline__ void rms_q8_row(const float* __restrict__ x, const ui
   const float inv = 1.0f / sqrtf(fmaf(se, se, sumsq / float(kRmsHidden)));
 #pragma unroll
   for (int st = 0; st < kSteps; ++st) {
-    const float y = bf16_to_f32(f32_to_bf16_rne((1.0f + gv[st]) * ((xv[st] / safe) * inv)));
+    const float y = bf16_to_f32(f32_to_bf16_rne((1.0f + gv[st]) * (xv[st] * inv)));
     q8_group32(y, codes, scales, sums, half + kHalves * st, failure);
   }
   __syncthreads();
