@@ -737,11 +737,15 @@ int mlp_run(const qw38_weight* gate, const qw38_weight* up, const qw38_weight* d
     return hip_fail(e, what);
   };
   hipError_t e = hipSuccess;
-  if (!pending_failure) {
+  // The internal flag is cleared on every call: at m = 1 by the RMS->Q8
+  // launch itself (one block), otherwise by a fill kernel first.
+  const bool clear_in_rms = !pending_failure && m == 1;
+  if (!pending_failure && !clear_in_rms) {
     profiling::ScopedRange range("qw38:op name=q8_clear_failure bytes=4");
     if ((e = launch_fill_zero_i32(flag, 1, s)) != hipSuccess) return bail(e, "q8.clear_failure");
   }
-  if ((e = launch_rms_q8(residual, gamma, eps, m, in_codes, in_scales, in_sums, flag, s)) != hipSuccess)
+  if ((e = launch_rms_q8(residual, gamma, eps, m, in_codes, in_scales, in_sums, flag, s, clear_in_rms)) !=
+      hipSuccess)
     return bail(e, "q8.rms_pack");
   Q8View x{in_codes, in_scales, in_sums, m, 5120, 5120};
   if (fused) {

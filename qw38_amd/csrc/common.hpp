@@ -317,9 +317,11 @@ hipError_t launch_q6_mmq_dma(const WeightView& w, const Q8View& x, float* out, c
 hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t pk,
                           int8_t* codes, float* scales, int32_t* sums, int* failure,
                           hipStream_t s);
+// clear_failure (m = 1 only): the kernel zeroes *failure before it can set
+// it, in place of a separate clearing launch.
 hipError_t launch_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
                          int8_t* codes, float* scales, int32_t* sums, int* failure,
-                         hipStream_t s);
+                         hipStream_t s, bool clear_failure = false);
 hipError_t launch_rms_bf16(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
                            uint16_t* out, hipStream_t s);
 hipError_t launch_swiglu_q8(const float* gate, const float* up, uint32_t m, uint32_t n,

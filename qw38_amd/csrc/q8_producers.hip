@@ -154,10 +154,13 @@ __global__ __launch_bounds__(256) void rms_kernel(const float* __restrict__ resi
 __global__ __launch_bounds__(1024) void rms_q8_wide_kernel(const float* __restrict__ residual,
                                                            const uint16_t* __restrict__ gamma, float eps,
                                                            int8_t* codes, float* scales, int32_t* sums,
-                                                           int* failure) {
+                                                           int* failure, int clear_failure) {
   __shared__ float sm[18];
   __shared__ float xs[kRmsHidden];
   const size_t row = blockIdx.x;
+  // one-block grid: the flag is cleared before the row's barriers, so every
+  // store that sets it comes after (plain vector store)
+  if (clear_failure && threadIdx.x == 0) *failure = 0;
   rms_q8_row<1024>(residual + row * kRmsHidden, gamma, eps, codes + row * kRmsHidden,
                    scales + row * (kRmsHidden / 32), sums + row * (kRmsHidden / 32), failure, sm, xs);
 }
@@ -188,9 +191,10 @@ hipError_t launch_pack_q8(const uint16_t* in, uint32_t m, uint32_t k, uint32_t p
 
 hipError_t launch_rms_q8(const float* residual, const uint16_t* gamma, float eps, uint32_t m,
                          int8_t* codes, float* scales, int32_t* sums, int* failure,
-                         hipStream_t s) {
+                         hipStream_t s, bool clear_failure) {
+  if (clear_failure && m != 1) return hipErrorInvalidValue;  // other blocks could set it first
   hipLaunchKernelGGL(rms_q8_wide_kernel, dim3(m), dim3(1024), 0, s, residual, gamma, eps, codes, scales, sums,
-                     failure);
+                     failure, clear_failure ? 1 : 0);
   return hipGetLastError();
 }
 

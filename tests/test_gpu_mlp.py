@@ -301,3 +301,8 @@ def test_q8_mlp_m1_fused_equals_chain(torch_gpu, mlp_weights, down):
     with pytest.raises(Qw38Error) as e:
         ops.q4k_q8_mlp(gate, up, dn, bad, dgam, 1e-6, out, 1, ws)
     assert e.value.operation == "q8.producer"
+    # the next call clears the flag again (at M=1 the RMS->Q8 launch does it)
+    again = torch.empty(1, 5120, device="cuda")
+    ops.q4k_q8_mlp(gate, up, dn, res, dgam, 1e-6, again, 1, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(again, ref)
